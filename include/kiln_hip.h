@@ -1,0 +1,193 @@
+/*
+ * kiln_hip.h - C ABI of Kiln's MI355X (gfx950) backend library, libkiln_hip.so.
+ *
+ * The library replaces the reference's generated-Triton GPU backend:
+ *   kiln/gpu/codegen.py   (Triton source per fused kernel, Launch list)
+ *   kiln/gpu/runtime.py   (launching, CUDA-graph capture/replay)
+ *   kiln/gpu/autotune.py  (timed matmul configs; the host side stays in Python
+ *                          and times plans built through this ABI)
+ * Every fused Kiln kernel is lowered (in Python, kiln/hip/lowering.py) to one or
+ * more kh_launch descriptors that name a hand-written HIP kernel family, its
+ * operands as (buffer slot, element offset, element strides) and, for fused
+ * elementwise work, an instruction tape. A plan is an ordered array of
+ * descriptors; one ctypes call runs a whole compiled graph, and a plan can be
+ * captured once into a hipGraph and replayed.
+ *
+ * Conventions
+ *   - Every function returns KH_OK (0) or a KH_ERR_* code; kh_last_error()
+ *     returns a thread-local message for the last failure.
+ *   - The library allocates no user-visible device memory. Arena, constants,
+ *     inputs, outputs and the workspace are device pointers owned by the
+ *     caller (torch tensors) and borrowed for the plan's lifetime.
+ *   - Kernels are launched on the hipStream_t the caller passes (torch's
+ *     current stream), so ordering with the caller's own work is preserved.
+ *   - A plan is not reentrant: calls share one arena and one workspace
+ *     (as in the reference, kiln/gpu/runtime.py:136).
+ *   - No HIP/torch types appear in signatures: streams are passed as void*.
+ */
+#ifndef KILN_HIP_H
+#define KILN_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KH_ABI_VERSION 1
+
+#define KH_MAX_RANK 6     /* iteration-space rank of one launch              */
+#define KH_MAX_REFS 12    /* operands (loads and stores) of one launch        */
+#define KH_MAX_INSNS 96   /* tape length                                      */
+#define KH_NREGS 16       /* tape registers                                   */
+#define KH_MAX_PASSES 8   /* row-kernel passes (reduction levels + output)    */
+
+/* status codes */
+enum {
+  KH_OK = 0,
+  KH_ERR_INVALID = 1,     /* malformed descriptor or argument -> ValueError          */
+  KH_ERR_UNSUPPORTED = 2, /* no kernel for this descriptor -> NotImplementedError    */
+  KH_ERR_HIP = 3,         /* a HIP runtime call failed -> RuntimeError               */
+  KH_ERR_NO_DEVICE = 4,   /* no usable gfx950 device -> RuntimeError                 */
+  KH_ERR_CAPACITY = 5     /* workspace too small for the plan -> MemoryError         */
+};
+
+/* buffer slots an operand can live in (reference Launch.bases, codegen.py:106-117) */
+enum { KH_BASE_INPUT = 0, KH_BASE_OUTPUT = 1, KH_BASE_CONST = 2, KH_BASE_ARENA = 3, KH_BASE_WORKSPACE = 4 };
+
+/* kernel families (reference _KernelWriter.write dispatch, codegen.py:532-542) */
+enum {
+  KH_FAM_EW = 1,   /* elementwise DAG / copy over one output shape            */
+  KH_FAM_ROW = 2,  /* innermost-dim reductions + elementwise (LN, softmax...) */
+  KH_FAM_GEMM = 3, /* [batched] matmul + epilogue tape, MFMA                  */
+  KH_FAM_GEMV = 4, /* M = 1 matmul + epilogue tape                            */
+  KH_FAM_RED = 5   /* reduction over non-innermost dims                       */
+};
+
+/* row-family variants chosen by the host pattern matcher */
+enum { KH_ROW_GENERIC = 0, KH_ROW_LAYERNORM = 1, KH_ROW_SOFTMAX = 2 };
+
+/* GEMM precisions */
+enum { KH_PREC_FP32 = 0, KH_PREC_BF16 = 1, KH_PREC_BF16X3 = 2 };
+
+/*
+ * Tape: a straight-line program over KH_NREGS slots, each slot holding the
+ * values of 4 adjacent elements of the iteration space (a per-row scalar or
+ * broadcast value is the same in all 4). Operands a/b are slot numbers or
+ * KH_SRC_IMM (the instruction's immediate).
+ *   LOAD  dst slot <- operand ref `a` at the current elements
+ *   STORE operand ref `dst` <- slot `a`
+ *   RSUM / RMAX (row family): slot `dst` accumulates the sum / max of slot `a`
+ *         over the valid columns of the current chunk
+ *   other ops: dst slot <- op(a, b)
+ * Loads at the start of a tape (or of a row pass) are issued together.
+ * Tapes that use at most 8 slots run with the slots in VGPRs.
+ */
+enum {
+  KH_OP_MOV = 0,  KH_OP_ADD, KH_OP_SUB, KH_OP_MUL, KH_OP_DIV, KH_OP_MAX, KH_OP_MIN,
+  KH_OP_NEG, KH_OP_RELU, KH_OP_EXP, KH_OP_TANH, KH_OP_SIGMOID, KH_OP_ERF,
+  KH_OP_GELU_TANH, KH_OP_GELU_ERF, KH_OP_RSQRT, KH_OP_SQRT,
+  KH_OP_RSUM, KH_OP_RMAX, KH_OP_LOAD, KH_OP_STORE,
+  KH_OP_COUNT
+};
+
+#define KH_SRC_IMM 0xFF
+
+typedef struct kh_ref {
+  int32_t base;                 /* KH_BASE_*                                    */
+  int32_t index;                /* input/output/const slot (0 for arena/ws)     */
+  int64_t offset;               /* element offset from the slot's pointer       */
+  int64_t strides[KH_MAX_RANK]; /* element stride per iteration dim; 0 = broadcast */
+} kh_ref;
+
+typedef struct kh_insn {
+  uint8_t op, dst, a, b;
+  float imm;
+} kh_insn;
+
+typedef struct kh_pass {
+  int16_t vec_begin, vec_end;   /* tape range run for every column chunk        */
+  int16_t post_begin, post_end; /* tape range run once per row after reductions */
+  uint16_t acc_mask;            /* slots that are reduction accumulators        */
+  uint16_t max_mask;            /* ... of which these reduce with max           */
+  int16_t single_chunk;         /* 1: row fits one chunk, slots persist         */
+  int16_t pad;
+} kh_pass;
+
+/*
+ * One kernel launch. Iteration spaces (rank / shape) and operand meaning:
+ *   EW   shape = output shape; refs strides over shape.
+ *   ROW  shape = row dims + [inner]; refs strides over that space; a per-row
+ *        scalar operand has inner stride 0. passes[] splits the tape.
+ *        variant KH_ROW_LAYERNORM / KH_ROW_SOFTMAX asks for the one-wave-per-row
+ *        fast path (cfg[4], cfg[5], fparams describe it); the tape must still
+ *        be complete, it runs when the fast path does not apply.
+ *   GEMM gemm = {batch, M, N, K}. refs[0] = A with strides over (b, m, k),
+ *        refs[1] = B over (b, k, n); refs[2..] are the epilogue's operands with
+ *        strides over (b, m, n). The tape starts with the accumulator in slot 0.
+ *        cfg[1] = tile configuration id, cfg[2] = split-K (0: library picks),
+ *        cfg[3] = precision.
+ *   GEMV as GEMM with M = 1.
+ *   RED  shape = input shape; refs[0] = input, refs[1] = output, both with
+ *        strides over the input shape (the output's reduced dims stride 0);
+ *        cfg[0] = bitmask of reduced dims, cfg[1] = 1 for max else sum.
+ * cfg[] holds the family configuration (GEMM: tile id, split-K, precision).
+ */
+typedef struct kh_launch {
+  int32_t family;
+  int32_t variant;
+  int32_t rank;
+  int32_t n_refs;
+  int32_t n_insns;
+  int32_t n_passes;
+  int32_t cfg[8];
+  float fparams[4];
+  int64_t shape[KH_MAX_RANK];
+  int64_t gemm[4];
+  kh_ref refs[KH_MAX_REFS];
+  kh_insn insns[KH_MAX_INSNS];
+  kh_pass passes[KH_MAX_PASSES];
+  char name[32];
+} kh_launch;
+
+typedef struct kh_plan kh_plan;
+
+/* library -------------------------------------------------------------------- */
+int kh_version(void);
+/* sizeof(kh_launch), sizeof(kh_ref), sizeof(kh_insn), sizeof(kh_pass): lets a
+ * binding check its struct mirrors against the compiled library. */
+int kh_abi_sizes(size_t *sizes4);
+const char *kh_last_error(void);
+/* Select `device`, check it is gfx950, cache CU count. */
+int kh_init(int device);
+/* Device facts: compute units, LDS bytes per CU, gfx arch string (>= 16 bytes). */
+int kh_device_info(int *cus, int *lds_bytes, char *arch, int arch_len);
+/* Number of GEMM tile configurations compiled into the library, and their shape:
+ * out[0..7] = {BM, BN, BK, WM, WN, WK, MFMA, precision}. */
+int kh_gemm_config_count(void);
+int kh_gemm_config(int id, int32_t *out8);
+
+/* plans: replace generate() + GPUExecutable (codegen.py:601-614, runtime.py:135-217) */
+int kh_plan_create(const kh_launch *launches, int n_launches, kh_plan **out);
+/* Workspace bytes the plan needs (split-K partials + tile counters); the caller
+ * allocates it zero-filled and passes it to kh_plan_bind. */
+int kh_plan_workspace_bytes(const kh_plan *plan, size_t *bytes);
+int kh_plan_bind(kh_plan *plan, void *const *consts, int n_consts, void *arena, void *workspace,
+                 size_t workspace_bytes);
+/* Run every launch in order on `stream` (GPUExecutable._run, runtime.py:164-179). */
+int kh_plan_run(kh_plan *plan, void *const *inputs, int n_inputs, void *const *outputs, int n_outputs,
+                void *stream);
+/* Run one launch (per-kernel profiling). */
+int kh_plan_run_one(kh_plan *plan, int index, void *const *inputs, int n_inputs, void *const *outputs,
+                    int n_outputs, void *stream);
+/* Capture the whole plan over fixed input/output buffers into a hipGraph
+ * (GPUExecutable._capture, runtime.py:191-204) and replay it on `stream`. */
+int kh_plan_capture(kh_plan *plan, void *const *inputs, int n_inputs, void *const *outputs, int n_outputs);
+int kh_plan_replay(kh_plan *plan, void *stream);
+int kh_plan_destroy(kh_plan *plan);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* KILN_HIP_H */

@@ -1,0 +1,191 @@
+// kh_common.hpp - device helpers shared by Kiln's gfx950 kernel families:
+// scalar math of the fused op set, the instruction-tape interpreter, wave64
+// reductions and fast integer division for index decomposition.
+//
+// The op semantics follow the reference's op table (kiln/ir/ops.py:48-97) and
+// its GPU forms (kiln/gpu/codegen.py:53-88, 223-248). Where this file uses a
+// different but more accurate formula it says so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "kiln_hip.h"
+
+namespace kh {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------------------
+// Fast unsigned division by a runtime constant (n, d < 2^31), the round-up
+// multiply-high method (Granlund & Montgomery 1994): q = (umulhi(n, m) + n) >> s.
+struct FastDiv {
+  uint32_t d, m, s;
+};
+
+inline FastDiv make_fastdiv(uint32_t d) {
+  FastDiv f;
+  f.d = d;
+  uint32_t s = 0;
+  while ((1ull << s) < d) ++s;
+  f.s = s;
+  f.m = (uint32_t)(((1ull << 32) * ((1ull << s) - d)) / d + 1);
+  return f;
+}
+
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv &f) {
+  return (__umulhi(n, f.m) + n) >> f.s;
+}
+
+// ---------------------------------------------------------------------------
+// Scalar math. exp/erf/tanh use the device library's accurate forms.
+// GELU(tanh) is evaluated as x * sigmoid(2u) = x / (1 + exp(-2u)),
+// u = sqrt(2/pi) (x + 0.044715 x^3): algebraically equal to
+// 0.5 x (1 + tanh(u)) but free of the 1 - e cancellation of the tanh form.
+__device__ __forceinline__ float op_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+__device__ __forceinline__ float op_gelu_tanh(float x) {
+  const float u = 0.7978845608028654f * fmaf(0.044715f * x, x * x, x);
+  return x / (1.0f + expf(-2.0f * u));
+}
+
+__device__ __forceinline__ float op_gelu_erf(float x) {
+  return 0.5f * x * (1.0f + erff(x * 0.7071067811865476f));
+}
+
+__device__ __forceinline__ float nan_max(float a, float b) {
+  return (a != a) ? a : ((b != b) ? b : fmaxf(a, b));
+}
+__device__ __forceinline__ float nan_min(float a, float b) {
+  return (a != a) ? a : ((b != b) ? b : fminf(a, b));
+}
+
+// ---------------------------------------------------------------------------
+// wave64 all-reductions: DPP within rows of 16 lanes, then cross-row swizzles.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp<0x141>(v);  // row_half_mirror
+  v += dpp<0x140>(v);  // row_mirror
+  v += __shfl_xor(v, 16, kWave);
+  v += __shfl_xor(v, 32, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp<0xB1>(v));
+  v = fmaxf(v, dpp<0x4E>(v));
+  v = fmaxf(v, dpp<0x141>(v));
+  v = fmaxf(v, dpp<0x140>(v));
+  v = fmaxf(v, __shfl_xor(v, 16, kWave));
+  v = fmaxf(v, __shfl_xor(v, 32, kWave));
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// Instruction-tape interpreter pieces. A thread evaluates a tape on a group of
+// 4 adjacent elements, so each (wave-uniform) instruction is decoded once per
+// 4 elements. Kernels keep registers and prefetched operands in small arrays
+// indexed by wave-uniform numbers.
+template <int V>
+struct Vec {
+  float v[V];
+};
+
+__device__ __forceinline__ Vec<4> splat4(float s) {
+  Vec<4> o;
+  o.v[0] = o.v[1] = o.v[2] = o.v[3] = s;
+  return o;
+}
+
+// Slot bank: NS slots of 4 floats in one flat array. With NS = 8 LLVM keeps
+// the array in VGPRs and indexes it with s_set_gpr_idx for a wave-uniform slot
+// number; a larger bank (or two banks) is placed in scratch memory, so tapes
+// that fit 8 slots use the VGPR variant.
+constexpr int kFastSlots = 8;
+
+template <int N>
+__device__ __forceinline__ Vec<4> bank_get(const float (&b)[N], int s) {
+  Vec<4> o;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o.v[i] = b[(s & (N / 4 - 1)) * 4 + i];
+  return o;
+}
+
+template <int N>
+__device__ __forceinline__ void bank_set(float (&b)[N], int s, const Vec<4> &v) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) b[(s & (N / 4 - 1)) * 4 + i] = v.v[i];
+}
+
+// One tape instruction (not STORE/RSUM/RMAX) on 4 lanes of data.
+__device__ __forceinline__ Vec<4> apply4(int op, const Vec<4> &x, const Vec<4> &y) {
+  Vec<4> r;
+#define KH_EACH(expr)                             \
+  _Pragma("unroll") for (int i = 0; i < 4; ++i) { \
+    const float u = x.v[i], w = y.v[i];           \
+    (void)w;                                      \
+    r.v[i] = (expr);                              \
+  }                                               \
+  break;
+  switch (op) {
+    case KH_OP_ADD: KH_EACH(u + w)
+    case KH_OP_SUB: KH_EACH(u - w)
+    case KH_OP_MUL: KH_EACH(u * w)
+    case KH_OP_DIV: KH_EACH(u / w)
+    case KH_OP_MAX: KH_EACH(nan_max(u, w))
+    case KH_OP_MIN: KH_EACH(nan_min(u, w))
+    case KH_OP_NEG: KH_EACH(-u)
+    case KH_OP_RELU: KH_EACH(u != u ? u : fmaxf(u, 0.0f))
+    case KH_OP_EXP: KH_EACH(expf(u))
+    case KH_OP_TANH: KH_EACH(tanhf(u))
+    case KH_OP_SIGMOID: KH_EACH(op_sigmoid(u))
+    case KH_OP_ERF: KH_EACH(erff(u))
+    case KH_OP_GELU_TANH: KH_EACH(op_gelu_tanh(u))
+    case KH_OP_GELU_ERF: KH_EACH(op_gelu_erf(u))
+    case KH_OP_RSQRT: KH_EACH(rsqrtf(u))
+    case KH_OP_SQRT: KH_EACH(sqrtf(u))
+    default: KH_EACH(u)
+  }
+#undef KH_EACH
+  return r;
+}
+
+// Execute tape[begin, end) on slot bank `f` (NS slots). The first `n_pre`
+// instructions are LOADs: they are issued together before any result is
+// needed. `load(ref)` returns the 4 values of operand ref at the current
+// elements, `store(ref, v)` writes them, `reduce(insn, v)` handles RSUM/RMAX.
+template <int NS, class Load, class Store, class Reduce>
+__device__ __forceinline__ void exec_tape(const kh_insn *tape, int begin, int end, int n_pre, float (&f)[NS * 4],
+                                          Load &&load, Store &&store, Reduce &&reduce) {
+  Vec<4> pre[kFastSlots];
+#pragma unroll
+  for (int i = 0; i < kFastSlots; ++i)
+    if (i < n_pre) pre[i] = load(tape[begin + i].a);
+#pragma unroll
+  for (int i = 0; i < kFastSlots; ++i)
+    if (i < n_pre) bank_set(f, tape[begin + i].dst, pre[i]);
+  for (int pc = begin + n_pre; pc < end; ++pc) {
+    const kh_insn in = tape[pc];
+    if (in.op == KH_OP_LOAD) {
+      bank_set(f, in.dst, load(in.a));
+      continue;
+    }
+    const Vec<4> x = in.a == KH_SRC_IMM ? splat4(in.imm) : bank_get(f, in.a);
+    if (in.op == KH_OP_STORE) {
+      store(in.dst, x);
+    } else if (in.op == KH_OP_RSUM || in.op == KH_OP_RMAX) {
+      reduce(in, x);
+    } else {
+      const Vec<4> y = in.b == KH_SRC_IMM ? splat4(in.imm) : bank_get(f, in.b);
+      bank_set(f, in.dst, apply4(in.op, x, y));
+    }
+  }
+}
+
+}  // namespace kh

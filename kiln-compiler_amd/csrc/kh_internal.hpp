@@ -1,0 +1,61 @@
+// kh_internal.hpp - host-side interface between the plan executor and the
+// kernel families. Each family validates a kh_launch once, at plan creation,
+// into an Op that keeps its precomputed kernel arguments; running the op only
+// patches the resolved device pointers and launches.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <memory>
+#include <string>
+
+#include "kiln_hip.h"
+
+namespace kh {
+
+struct Device {
+  int id = -1;
+  int cus = 256;
+  int lds_bytes = 160 * 1024;
+  char arch[64] = {0};
+};
+const Device &current_device();
+
+class Op {
+ public:
+  virtual ~Op() = default;
+  // ptrs[j] = device address of element 0 of ref j (slot pointer + offset).
+  // counters: this op's own zero-initialised uint32 counters (kernels leave
+  // them at zero), partials: scratch shared by every op of the plan (ops run
+  // one after another on one stream). Either may be null if not requested.
+  virtual hipError_t launch(float *const *ptrs, uint32_t *counters, float *partials, hipStream_t stream) = 0;
+  virtual size_t counter_count() const { return 0; }
+  virtual size_t partial_floats() const { return 0; }
+};
+
+// Each factory returns nullptr and sets `err` when the descriptor is invalid or
+// unsupported; `unsupported` distinguishes the two for the status code.
+std::unique_ptr<Op> make_ew(const kh_launch &L, std::string &err, bool &unsupported);
+std::unique_ptr<Op> make_row(const kh_launch &L, std::string &err, bool &unsupported);
+std::unique_ptr<Op> make_gemm(const kh_launch &L, std::string &err, bool &unsupported);
+std::unique_ptr<Op> make_gemv(const kh_launch &L, std::string &err, bool &unsupported);
+std::unique_ptr<Op> make_red(const kh_launch &L, std::string &err, bool &unsupported);
+
+int gemm_config_count();
+bool gemm_config(int id, int32_t out8[8]);
+
+// Shared descriptor checks.
+// Facts about a validated tape range.
+struct TapeInfo {
+  int slots = 0;          // highest slot used + 1
+  int leading_loads = 0;  // LOADs at the start of the range (at most 8)
+  uint32_t loaded = 0;    // refs read by LOAD
+  uint32_t stored = 0;    // refs written by STORE
+};
+
+// Validate tape[begin, end): opcodes, slot numbers, and that LOAD/STORE name
+// refs in [first_ref, n_refs) (GEMM epilogues start at ref 2).
+bool check_tape(const kh_launch &L, int begin, int end, bool allow_row_ops, TapeInfo &info, std::string &err,
+                int first_ref = 0);
+
+}  // namespace kh

@@ -1,0 +1,258 @@
+"""GEMM tile configurations: a default heuristic and a measured autotuner.
+
+Replaces the reference's Triton config heuristic and tuner
+(kiln/gpu/codegen.py:552-598, kiln/gpu/autotune.py:40-193). The knobs are
+the MI355X GEMM family's: the compiled tile configurations (macro-tile
+BM x BN x BK, waves along M / N / K, MFMA shape; ``kh_gemm_config``) and the
+split-K factor. The policy follows the reference tuner:
+
+  * candidates are filtered to the problem (no tile far larger than it);
+  * each candidate is compiled as a one-matmul plan, checked against a
+    float64 result (relative-to-max error <= 1e-4; rejected otherwise) and
+    timed as GPU time of a 20-call graph replay (runtime.kernel_seconds);
+  * the fastest few and the default are re-timed interleaved, and the default
+    is kept unless beaten by more than MIN_GAIN;
+  * results are cached by device, CU count, precision and shape in
+    $KILN_CACHE_DIR/hip_autotune.json (a corrupt cache is ignored).
+"""
+
+from __future__ import annotations
+
+import json
+import math
+import os
+import time
+import warnings
+from pathlib import Path
+
+MIN_GAIN = 1.03
+FINALISTS = 3
+SPLITS = (1, 2, 3, 4, 6, 8)
+
+# (BM, BN, BK, WM, WN, WK, MFMA) of the compiled configurations, by id; must
+# match the table in csrc/kh_gemm.hip (tests check it against kh_gemm_config).
+TILES = {
+    0: (128, 128, 32, 2, 2, 1, 32),
+    1: (128, 192, 32, 2, 2, 1, 32),
+    2: (256, 128, 32, 2, 2, 1, 32),
+    3: (64, 64, 32, 2, 2, 1, 32),
+    4: (64, 128, 32, 2, 2, 1, 32),
+    5: (128, 64, 32, 2, 2, 1, 32),
+    6: (32, 64, 32, 1, 2, 2, 32),
+    7: (32, 32, 32, 1, 1, 4, 32),
+    8: (64, 64, 32, 1, 1, 4, 32),
+    9: (32, 32, 32, 2, 2, 1, 16),
+    10: (16, 64, 32, 1, 4, 1, 16),
+    11: (64, 32, 32, 2, 2, 1, 16),
+}
+DEFAULT_CUS = 256
+
+
+def device_cus() -> int:
+    try:
+        from kiln.hip import lib as kl
+
+        return kl.device_info()["cus"]
+    except Exception:  # library not built: the heuristic still works with MI355X's count
+        return DEFAULT_CUS
+
+
+def matmul_shape(kernel):
+    mm = next(n for n in kernel.nodes if n.op == "matmul")
+    a, b = mm.inputs
+    batch = math.prod(a.shape[:-2]) if a.type.rank == 3 else 1
+    return batch, a.shape[-2], b.shape[-1], a.shape[-1]
+
+
+def fits(tile, m, n, k) -> bool:
+    bm, bn = TILES[tile][:2]
+    p2 = lambda x: 1 << max(0, (x - 1).bit_length())
+    return bm <= max(16, p2(m)) and bn <= max(16, p2(n))
+
+
+def estimate(tile, splitk, batch, m, n, k, cus) -> float:
+    """Relative time model: rounds of workgroups over the CUs x per-tile work,
+    with a penalty for small (inefficient) tiles and for split-K traffic."""
+    bm, bn, bk, wm, wn, wk, mt = TILES[tile]
+    units = math.ceil(m / bm) * math.ceil(n / bn) * batch * splitk
+    rounds = math.ceil(units / cus)
+    kper = math.ceil(k / splitk / bk) * bk
+    waves = wm * wn * wk
+    efficiency = min(1.0, (bm * bn) / (128 * 128)) ** 0.25 * (1.0 if waves == 4 else 0.9)
+    return rounds * bm * bn * kper / efficiency + (splitk > 1) * bm * bn * splitk * 8
+
+
+def default_matmul_config(graph, kernel, cus=None) -> dict:
+    """Tile and split-K for a matmul kernel, without measuring.
+
+    Prefer the largest tile that gives every CU a workgroup; when no tile can
+    (M = 128 shapes on 256 CUs), pick the tile / split-K pair with the lowest
+    modelled time.
+    """
+    batch, m, n, k = matmul_shape(kernel)
+    return default_config_for(batch, m, n, k, cus)
+
+
+def default_config_for(batch, m, n, k, cus=None) -> dict:
+    cus = cus or device_cus()
+    best = None
+    for tile in TILES:
+        if not fits(tile, m, n, k):
+            continue
+        for s in SPLITS:
+            if s > 1 and k // s < 128:
+                continue
+            t = estimate(tile, s, batch, m, n, k, cus)
+            if best is None or t < best[0]:
+                best = (t, tile, s)
+    if best is None:
+        return {"tile": 9, "splitk": 1}
+    return {"tile": best[1], "splitk": best[2]}
+
+
+def candidates(batch, m, n, k, cus=None) -> list:
+    cus = cus or device_cus()
+    out = []
+    for tile in TILES:
+        if not fits(tile, m, n, k):
+            continue
+        for s in SPLITS:
+            if s > 1 and k // s < 64:
+                continue
+            units = math.ceil(m / TILES[tile][0]) * math.ceil(n / TILES[tile][1]) * batch * s
+            if s > 1 and units > 4 * cus:
+                continue
+            out.append({"tile": tile, "splitk": s})
+    return out
+
+
+def cache_path() -> Path:
+    base = os.environ.get("KILN_CACHE_DIR") or os.path.join(Path.home(), ".cache", "kiln")
+    return Path(base) / "hip_autotune.json"
+
+
+def _matmul_graph(batch, m, n, k):
+    from kiln.ir import Graph, TensorType
+
+    g = Graph("matmul")
+    lead = (batch,) if batch > 1 else ()
+    a = g.add_arg(TensorType((*lead, m, k)), "a")
+    b = g.add_arg(TensorType((*lead, k, n)), "b")
+    g.results = [g.add_node("matmul", [a, b])]
+    return g
+
+
+class GPUAutotuner:
+    """Chooses GEMM configurations by measurement, with an on-disk cache."""
+
+    def __init__(self, precision="fp32", use_cache=True):
+        self.precision = precision
+        self.use_cache = use_cache
+        self.log = []
+        self._cache = self._load() if use_cache else {}
+
+    def _load(self):
+        try:
+            data = json.loads(cache_path().read_text())
+            return data if isinstance(data, dict) else {}
+        except (OSError, ValueError):
+            return {}
+
+    def _save(self):
+        if not self.use_cache:
+            return
+        path = cache_path()
+        try:
+            path.parent.mkdir(parents=True, exist_ok=True)
+            tmp = path.with_suffix(".tmp")
+            tmp.write_text(json.dumps(self._cache, indent=1, sort_keys=True))
+            tmp.replace(path)
+        except OSError as err:
+            warnings.warn(f"Kiln: couldn't write the GPU autotune cache ({err})")
+
+    @staticmethod
+    def device_key():
+        from kiln.hip import lib as kl
+
+        info = kl.device_info()
+        return f"{info['arch']}|{info['cus']}"
+
+    def config_for(self, graph, kernel):
+        batch, m, n, k = matmul_shape(kernel)
+        key = f"{self.device_key()}|{self.precision}|{batch}x{m}x{n}x{k}"
+        entry = self._cache.get(key)
+        if not isinstance(entry, dict) or "config" not in entry:
+            entry = self.tune(batch, m, n, k, default_config_for(batch, m, n, k))
+            if entry["candidates"]:
+                self._cache[key] = entry
+                self._save()
+            source = "tuned"
+        else:
+            source = "cache"
+        self.log.append({"shape": (batch, m, n, k), "source": source, **entry})
+        return dict(entry["config"])
+
+    def _compile(self, batch, m, n, k, config):
+        from kiln.api import Options, compile_graph
+
+        opts = Options(device="cuda", cuda_graphs=False, matmul_precision=self.precision,
+                       gpu_matmul_config=lambda *_: dict(config))
+        exe, _ = compile_graph(_matmul_graph(batch, m, n, k), opts)
+        return exe
+
+    def tune(self, batch, m, n, k, default):
+        import torch
+
+        from kiln.hip.runtime import device, kernel_seconds
+
+        start = time.perf_counter()
+        dev = device()
+        gen = torch.Generator(device="cpu").manual_seed(0)
+        lead = (batch,) if batch > 1 else ()
+        a = torch.randn(*lead, m, k, generator=gen).to(dev)
+        b = (torch.randn(*lead, k, n, generator=gen) / k ** 0.5).to(dev)
+        expected = (a.double() @ b.double()).float()
+        tol = 1e-4 if self.precision == "fp32" else 2e-2
+        scale = expected.abs().max().item() or 1.0
+        runs, seconds, rejected = {}, {}, []
+        configs = [default] + [c for c in candidates(batch, m, n, k) if c != default]
+        for cfg in configs:
+            key = (cfg["tile"], cfg["splitk"])
+            try:
+                exe = self._compile(batch, m, n, k, cfg)
+                (out,) = exe(a, b)
+                err = (out - expected).abs().max().item() / scale
+                if not err <= tol:
+                    rejected.append(f"{cfg}: relative error {err:.1e}")
+                    continue
+            except Exception as e:  # noqa: BLE001 - a failing candidate is dropped, never fatal
+                rejected.append(f"{cfg}: {type(e).__name__}: {str(e).splitlines()[0][:80] if str(e) else ''}")
+                continue
+            outs = [torch.empty_like(expected)]
+            runs[key] = lambda exe=exe, outs=outs: exe.run_into([a, b], outs)
+            seconds[key] = kernel_seconds(runs[key], rounds=3)
+        default_key = (default["tile"], default["splitk"])
+        if not seconds:
+            warnings.warn(f"Kiln: no GEMM config passed for {batch}x{m}x{n}x{k}; keeping the default. "
+                          + "; ".join(rejected[:3]))
+            return {"config": dict(default), "default_config": dict(default), "tflops": None,
+                    "default_tflops": None, "candidates": 0, "seconds": round(time.perf_counter() - start, 1)}
+        ranked = sorted(seconds, key=seconds.get)[:FINALISTS]
+        if default_key in seconds and default_key not in ranked:
+            ranked.append(default_key)
+        final = {}
+        for _ in range(3):
+            for key in ranked:
+                final[key] = min(final.get(key, float("inf")), kernel_seconds(runs[key], rounds=2))
+        winner = min(final, key=final.get)
+        if default_key in final and final[default_key] <= final[winner] * MIN_GAIN:
+            winner = default_key
+        flops = 2 * batch * m * n * k
+        return {
+            "config": {"tile": winner[0], "splitk": winner[1]},
+            "default_config": dict(default),
+            "tflops": round(flops / final[winner] / 1e12, 2),
+            "default_tflops": round(flops / final[default_key] / 1e12, 2) if default_key in final else None,
+            "candidates": len(seconds),
+            "seconds": round(time.perf_counter() - start, 1),
+        }

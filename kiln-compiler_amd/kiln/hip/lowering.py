@@ -1,0 +1,720 @@
+"""Lower an optimised Kiln graph to kernel-family launch descriptors.
+
+Replaces the reference's Triton code generator (kiln/gpu/codegen.py:145-614).
+Instead of writing a kernel's source, each fused Kiln kernel becomes one (or,
+for elementwise kernels with outputs of several shapes, a few) ``kh_launch``
+descriptors naming a hand-written HIP kernel family:
+
+  matmul kernel           -> GEMM (MFMA) or, for M = 1, GEMV; the fused
+                             epilogue becomes a tape over the accumulator
+  reduction, innermost    -> ROW; LayerNorm / softmax in the exact form the
+                             frontend emits also request the one-wave-per-row
+                             fast path
+  reduction, other dims   -> RED
+  elementwise / copy      -> EW, one launch per distinct output shape
+
+Operands are (buffer slot, element offset, element strides over the launch's
+iteration space): views never cost a copy, broadcasts are stride 0 - the
+same addressing the reference computes in codegen.py:185-219.
+
+Tapes are built over virtual registers, then assigned to the kernels' slots by
+linear scan. A tape that fits 8 slots runs with its slots in VGPRs.
+"""
+
+from __future__ import annotations
+
+import hashlib
+import math
+from dataclasses import dataclass, field
+
+from kiln.hip import lib as kl
+from kiln.ir import ops
+from kiln.ir.core import Graph, Kernel
+from kiln.passes.buffers import compute_layouts, kernel_inputs, kernel_outputs
+from kiln.passes.fusion import is_row_reduction
+
+ROW_SINGLE_CHUNK = 1024   # rows up to this length are held in registers (workgroup x 4)
+
+_UNARY_OP = {"neg": "neg", "exp": "exp", "tanh": "tanh", "sigmoid": "sigmoid", "relu": "relu",
+             "rsqrt": "rsqrt", "sqrt": "sqrt", "erf": "erf", "copy": "mov"}
+_BINARY_OP = {"add": "add", "sub": "sub", "mul": "mul", "div": "div", "maximum": "max", "minimum": "min"}
+
+
+@dataclass
+class Launch:
+    """One kernel launch of the plan (host-side record + its C descriptor)."""
+
+    name: str
+    kernel: str
+    family: int
+    desc: kl.LaunchDesc
+    summary: str
+    flops: int = 0
+    bytes: int = 0
+
+
+@dataclass
+class Program:
+    launches: list = field(default_factory=list)
+    consts: list = field(default_factory=list)   # const slot -> constant name
+    precision: str = "fp32"
+
+    @property
+    def source(self) -> str:
+        """Human-readable plan listing (the analogue of the reference's
+        generated Triton source, codegen.py:601-614)."""
+        lines = [f"// Kiln HIP plan: {len(self.launches)} launches, precision {self.precision}"]
+        for i, l in enumerate(self.launches):
+            lines.append(f"launch {i} {l.name} [{l.kernel}] {kl.FAMILY_NAMES[l.family]}: {l.summary}")
+            d = l.desc
+            for j in range(d.n_refs):
+                r = d.refs[j]
+                base = ["input", "output", "const", "arena", "workspace"][r.base]
+                lines.append(f"    ref {j}: {base}[{r.index}] +{r.offset} strides {list(r.strides)[:max(d.rank, 3)]}")
+            for j in range(d.n_insns):
+                ins = d.insns[j]
+                lines.append(f"    {j:3d} {kl.OPCODES[ins.op]:<9} dst={ins.dst} a={ins.a} b={ins.b} imm={ins.imm!r}")
+        return "\n".join(lines) + "\n"
+
+    def digest(self) -> str:
+        return hashlib.sha256(self.source.encode()).hexdigest()[:16]
+
+
+# ----------------------------------------------------------------------------------
+# Tapes over virtual registers.
+
+class _Tape:
+    """A straight-line tape over virtual registers, allocated to slots later."""
+
+    def __init__(self):
+        self.insns = []          # [op, dst, a, b, imm]; dst/a/b: virtual id, ref index, or None (imm)
+        self.n_virt = 0
+        self.marks = {}          # virtual -> position it must be live from (row accumulators)
+
+    def virt(self):
+        self.n_virt += 1
+        return self.n_virt - 1
+
+    def emit(self, op, dst=None, a=None, b=None, imm=0.0):
+        self.insns.append([op, dst, a, b, float(imm)])
+        return dst
+
+    # operand kinds per opcode
+    @staticmethod
+    def reads(ins):
+        op = ins[0]
+        if op == "load":
+            return []
+        if op == "store":
+            return [ins[2]] if ins[2] is not None else []
+        if op in ("rsum", "rmax"):
+            return [ins[1], ins[2]]
+        return [x for x in (ins[2], ins[3]) if x is not None]
+
+    @staticmethod
+    def writes(ins):
+        return [] if ins[0] == "store" else [ins[1]]
+
+
+def _allocate(tape: _Tape, loops, limit=kl.NREGS):
+    """Linear-scan slot assignment. ``loops`` lists (begin, end) insn ranges
+    that execute repeatedly: a value live into a loop stays live through it."""
+    first, last = {}, {}
+    for i, ins in enumerate(tape.insns):
+        for v in tape.writes(ins) + tape.reads(ins):
+            first.setdefault(v, i)
+            last[v] = i
+    for v, pos in tape.marks.items():
+        first[v] = min(first.get(v, pos), pos)
+        last.setdefault(v, pos)
+    for b, e in loops:
+        for v in list(first):
+            if first[v] < b <= last[v] < e:
+                last[v] = e - 1       # defined before the loop, read inside: live to its end
+    order = sorted(first, key=lambda v: (first[v], last[v]))
+    slot, active, free = {}, [], list(range(limit))
+    for v in order:
+        start = first[v]
+        for u in list(active):
+            if last[u] < start:
+                active.remove(u)
+                free.append(slot[u])
+        if not free:
+            return None
+        free.sort()
+        slot[v] = free.pop(0)
+        active.append(v)
+    return slot
+
+
+def _encode(tape: _Tape, slot, desc: kl.LaunchDesc, ref_offset=0):
+    if len(tape.insns) > kl.MAX_INSNS:
+        raise NotImplementedError(f"HIP backend: tape of {len(tape.insns)} instructions exceeds {kl.MAX_INSNS}")
+    for i, (op, dst, a, b, imm) in enumerate(tape.insns):
+        ins = desc.insns[i]
+        ins.op = kl.OP[op]
+        ins.imm = imm
+        if op == "load":
+            ins.dst, ins.a, ins.b = slot[dst], a + ref_offset, 0
+        elif op == "store":
+            ins.dst, ins.a, ins.b = dst + ref_offset, slot[a], 0
+        else:
+            ins.dst = slot[dst]
+            ins.a = kl.SRC_IMM if a is None else slot[a]
+            ins.b = kl.SRC_IMM if b is None else slot[b]
+    desc.n_insns = len(tape.insns)
+    return max(slot.values(), default=-1) + 1
+
+
+# ----------------------------------------------------------------------------------
+
+class _Lowerer:
+    def __init__(self, graph: Graph, precision: str, matmul_config):
+        self.g = graph
+        self.layouts = compute_layouts(graph)
+        self.users = graph.users()
+        self.precision = precision
+        self.matmul_config = matmul_config
+        self.program = Program(precision=precision)
+        self.const_slot = {}
+
+    # operands ---------------------------------------------------------------------
+
+    def slot_of(self, base):
+        kind = base[0]
+        if kind == "input":
+            return kl.BASE_INPUT, base[1]
+        if kind == "output":
+            return kl.BASE_OUTPUT, base[1]
+        if kind == "const":
+            name = base[1]
+            if name not in self.const_slot:
+                self.const_slot[name] = len(self.program.consts)
+                self.program.consts.append(name)
+            return kl.BASE_CONST, self.const_slot[name]
+        return kl.BASE_ARENA, 0
+
+    def element_offset(self, v):
+        lay = self.layouts[v]
+        if lay.base[0] == "arena":
+            byte_offset = lay.base[1].node.attrs.get("offset", 0)
+            assert byte_offset % 4 == 0
+            return byte_offset // 4 + lay.offset
+        return lay.offset
+
+    def ref(self, v, space):
+        """kh_ref for value v read over iteration space `space` (right-aligned
+        broadcasting: size-1 dims of v get stride 0)."""
+        if v not in self.layouts:
+            raise NotImplementedError(f"HIP backend: value {v} has no storage")
+        lay = self.layouts[v]
+        r = kl.Ref()
+        r.base, r.index = self.slot_of(lay.base)
+        r.offset = self.element_offset(v)
+        rank = len(space)
+        lead = rank - len(lay.shape)
+        if lead < 0:
+            raise NotImplementedError(f"HIP backend: operand {v} has higher rank than its kernel")
+        for i, (s, st) in enumerate(zip(lay.shape, lay.strides)):
+            r.strides[lead + i] = 0 if s == 1 else st
+        return r
+
+    def new_desc(self, family, name, kernel, space):
+        d = kl.LaunchDesc()
+        d.family = family
+        d.rank = len(space)
+        if d.rank > kl.MAX_RANK:
+            raise NotImplementedError(f"HIP backend: rank {d.rank} > {kl.MAX_RANK}")
+        for i, s in enumerate(space):
+            d.shape[i] = s
+        d.name = f"{kernel.name}_{name}".encode()[:31]
+        return d
+
+    def add(self, d, kernel, summary, flops=0, nbytes=0):
+        self.program.launches.append(Launch(d.name.decode(), kernel.name, d.family, d, summary, flops, nbytes))
+
+    def is_imm(self, v):
+        return self.g.is_scalar_const(v)
+
+    def imm(self, v):
+        return float(self.g.const_data(v))
+
+    # elementwise ---------------------------------------------------------------------------
+
+    def lower_elementwise(self, k: Kernel):
+        outs = kernel_outputs(self.g, k, self.users)
+        by_shape = {}
+        for v in outs:
+            by_shape.setdefault(tuple(v.shape), []).append(v)
+        members = set(k.nodes)
+        for i, (shape, group) in enumerate(by_shape.items()):
+            d = self.new_desc(kl.FAM_EW, f"ew{i}", k, shape)
+            refs, ref_of = [], {}
+            needed = self._needed(group, members)
+            externals = []
+            for n in k.nodes:
+                if n.out in needed:
+                    for v in n.inputs:
+                        if (v.node not in members or v.node is None) and not self.is_imm(v) and v not in externals:
+                            externals.append(v)
+            for v in externals:
+                ref_of[v] = len(refs)
+                refs.append(self.ref(v, shape))
+            out_ref = {}
+            for v in group:
+                out_ref[v] = len(refs)
+                refs.append(self.ref(v, shape))
+            self._check_refs(refs)
+            for j, r in enumerate(refs):
+                d.refs[j] = r
+            d.n_refs = len(refs)
+
+            def build(eager_loads):
+                t = _Tape()
+                env = {}
+                if eager_loads:
+                    for v in externals:
+                        env[v] = t.emit("load", t.virt(), ref_of[v])
+                self._emit_dag(t, env, group, members, k.nodes, ref_of)
+                for v in group:
+                    t.emit("store", out_ref[v], env[v])
+                return t
+
+            self._finish_tape(d, build, loops=[])
+            nbytes = 4 * (sum(math.prod(v.shape) for v in externals) + len(group) * math.prod(shape))
+            ops_list = " ".join(n.op for n in k.nodes if n.out in needed)
+            self.add(d, k, f"shape {list(shape)}: {ops_list}", nbytes=nbytes)
+
+    @staticmethod
+    def _needed(wanted, members, stop=()):
+        """Member values `wanted` depends on, not looking past values in `stop`."""
+        need, todo = set(), list(wanted)
+        while todo:
+            v = todo.pop()
+            if v in need or v.node not in members or v in stop:
+                continue
+            need.add(v)
+            todo.extend(v.node.inputs)
+        return need
+
+    def _emit_dag(self, t, env, wanted, members, order, ref_of, node_ok=None):
+        """Emit the members needed for `wanted` (program order), loading
+        externals on first use when not already in env."""
+        need = self._needed(wanted, members, stop=env)
+
+        def operand(v):
+            if v in env:
+                return env[v]
+            if self.is_imm(v):
+                return None
+            if v.node in members and v.node is not None:
+                raise AssertionError(f"value {v} used before it is computed")
+            env[v] = t.emit("load", t.virt(), ref_of[v])
+            return env[v]
+
+        for n in order:
+            if n.out not in need or n.out in env:
+                continue
+            if node_ok is not None and not node_ok(n):
+                continue
+            self._emit_node(t, env, n, operand)
+
+    def _emit_node(self, t, env, n, operand):
+        op = n.op
+        if op in _BINARY_OP:
+            a, b = n.inputs
+            ra, rb = operand(a), operand(b)
+            if ra is None and rb is None:       # both scalar constants: materialise one
+                ra = t.emit("mov", t.virt(), None, None, self.imm(a))
+            imm = self.imm(a) if ra is None else (self.imm(b) if rb is None else 0.0)
+            env[n.out] = t.emit(_BINARY_OP[op], t.virt(), ra, rb, imm)
+        elif op == "gelu":
+            ra = operand(n.inputs[0])
+            opname = "gelu_tanh" if n.attrs.get("approximate", "none") == "tanh" else "gelu_erf"
+            imm = self.imm(n.inputs[0]) if ra is None else 0.0
+            env[n.out] = t.emit(opname, t.virt(), ra, None, imm)
+        elif op in _UNARY_OP:
+            ra = operand(n.inputs[0])
+            imm = self.imm(n.inputs[0]) if ra is None else 0.0
+            env[n.out] = t.emit(_UNARY_OP[op], t.virt(), ra, None, imm)
+        else:
+            raise NotImplementedError(f"GPU backend: no lowering for '{op}'")
+
+    def _finish_tape(self, d, build, loops, limit=kl.NREGS, ref_offset=0, preset=None):
+        """Build the tape (loads first, else loads on demand), allocate, encode.
+        Returns the slot count."""
+        best = None
+        for eager in (True, False):
+            t = build(eager)
+            lp = loops(t) if callable(loops) else loops
+            slot = _allocate(t, lp, limit)
+            if preset is not None and slot is not None:
+                slot = self._pin(t, slot, preset, lp, limit)
+            if slot is None:
+                continue
+            used = max(slot.values(), default=-1) + 1
+            if best is None or used < best[0] or (used <= kl.FAST_SLOTS and eager):
+                best = (used, t, slot)
+            if used <= kl.FAST_SLOTS:
+                break
+        if best is None:
+            raise NotImplementedError(f"HIP backend: fused kernel needs more than {limit} registers")
+        return _encode(best[1], best[2], d, ref_offset)
+
+    @staticmethod
+    def _pin(t, slot, preset, loops, limit):
+        """Re-run allocation with virtual `preset[0]` forced into slot preset[1]."""
+        v0, s0 = preset
+        if slot.get(v0) == s0:
+            return slot
+        # swap slots s0 and slot[v0] globally (valid: a permutation of slots)
+        other = slot.get(v0)
+        out = {}
+        for v, s in slot.items():
+            out[v] = other if s == s0 else (s0 if s == other else s)
+        return out
+
+    @staticmethod
+    def _check_refs(refs):
+        if len(refs) > kl.MAX_REFS:
+            raise NotImplementedError(f"HIP backend: kernel has {len(refs)} operands (max {kl.MAX_REFS})")
+
+    # row kernels ------------------------------------------------------------------------------
+
+    def lower_reduction(self, k: Kernel):
+        reds = [n for n in k.nodes if n.op.startswith("reduce_")]
+        if all(is_row_reduction(n) for n in reds):
+            return self.lower_row(k, reds)
+        if len(k.nodes) != 1:
+            raise NotImplementedError("GPU backend: a non-innermost reduction must be alone in its kernel")
+        return self.lower_red(k, reds[0])
+
+    def lower_red(self, k, n):
+        x, out = n.inputs[0], n.out
+        space = tuple(x.shape)
+        d = self.new_desc(kl.FAM_RED, "reduce", k, space)
+        outs = kernel_outputs(self.g, k, self.users)
+        if outs != [out]:
+            raise NotImplementedError("GPU backend: reduction kernel with extra outputs")
+        d.refs[0] = self.ref(x, space)
+        lay = self.layouts[out]
+        r = kl.Ref()
+        r.base, r.index = self.slot_of(lay.base)
+        r.offset = self.element_offset(out)
+        for i, (s, st) in enumerate(zip(lay.shape, lay.strides)):
+            r.strides[i] = 0 if s == 1 else st
+        d.refs[1] = r
+        d.n_refs = 2
+        dims = {dd % x.type.rank for dd in n.attrs["dims"]}
+        d.cfg[0] = sum(1 << dd for dd in dims)
+        d.cfg[1] = 1 if n.op == "reduce_max" else 0
+        nbytes = 4 * (math.prod(x.shape) + math.prod(out.shape))
+        self.add(d, k, f"{n.op} dims {sorted(dims)} of {list(x.shape)}", nbytes=nbytes)
+
+    def lower_row(self, k, reds):
+        shape = tuple(reds[0].inputs[0].shape)
+        rows, inner = shape[:-1], shape[-1]
+        members = set(k.nodes)
+        outs = kernel_outputs(self.g, k, self.users)
+        single = inner <= ROW_SINGLE_CHUNK
+
+        def is_vec(v):
+            return v.type.rank > 0 and v.shape[-1] == inner
+
+        # levels: reductions completed before a value is available
+        level = {}
+        for n in k.nodes:
+            lv = max([level[v] for v in n.inputs if v in level], default=0)
+            level[n.out] = lv + (1 if n.op.startswith("reduce_") else 0)
+        depth = max(level[n.out] for n in reds)
+
+        externals = []
+        for n in k.nodes:
+            for v in n.inputs:
+                if (v.node not in members or v.node is None) and not self.is_imm(v) and v not in externals:
+                    externals.append(v)
+        variant, fparams, cfg45, ordered = self._row_pattern(k, reds, outs, externals)
+        if ordered is not None:
+            externals = ordered
+        refs, ref_of = [], {}
+        for v in externals:
+            ref_of[v] = len(refs)
+            refs.append(self.ref(v, shape))
+        out_ref = {}
+        for v in outs:
+            out_ref[v] = len(refs)
+            refs.append(self.ref(v, shape))
+        self._check_refs(refs)
+
+        d = self.new_desc(kl.FAM_ROW, "row", k, shape)
+        for j, r in enumerate(refs):
+            d.refs[j] = r
+        d.n_refs = len(refs)
+        d.variant = variant
+        for i, f in enumerate(fparams):
+            d.fparams[i] = f
+        d.cfg[4], d.cfg[5] = cfg45
+
+        def build(_eager):
+            t = _Tape()
+            persist = {}      # values whose slots stay valid for the rest of the row
+            segments = []     # per pass: (vec_begin, vec_end, post_begin, post_end, accs, maxs)
+            for p in range(depth + 1):
+                final = p == depth
+                seg_reds = [n for n in reds if level[n.out] == p + 1]
+                # accumulators live from the pass start
+                accs = {}
+                for n in seg_reds:
+                    v = t.virt()
+                    t.marks[v] = len(t.insns)
+                    accs[n.out] = v
+                vb = len(t.insns)
+                env = dict(persist)
+                # leading loads: externals this segment reads directly
+                wanted = [n.inputs[0] for n in seg_reds]
+                if final:
+                    wanted = [v for v in outs if is_vec(v)]
+
+                def vec_ok(n):
+                    return is_vec(n.out) or level[n.out] == 0
+
+                need = self._needed(wanted, members, stop=env)
+                for v in wanted:
+                    if v not in env and (v.node not in members or v.node is None):
+                        env[v] = t.emit("load", t.virt(), ref_of[v])
+                for n in k.nodes:
+                    if n.out in need and vec_ok(n):
+                        for v in n.inputs:
+                            if v not in env and not self.is_imm(v) and (v.node not in members or v.node is None):
+                                env[v] = t.emit("load", t.virt(), ref_of[v])
+                self._emit_dag(t, env, wanted, members, k.nodes, ref_of, node_ok=vec_ok)
+                for n in seg_reds:
+                    t.emit("rsum" if n.op == "reduce_sum" else "rmax", accs[n.out], env[n.inputs[0]])
+                if final:
+                    for v in outs:
+                        if is_vec(v):
+                            t.emit("store", out_ref[v], env[v])
+                ve = len(t.insns)
+                if single:
+                    persist.update(env)
+                for n in seg_reds:
+                    persist[n.out] = accs[n.out]
+                # post segment: per-row scalars at the next level (and scalar outputs at the end)
+                pb = len(t.insns)
+                penv = dict(persist)
+                if final:
+                    scalars = [v for v in outs if not is_vec(v)]
+                else:
+                    scalars = [n.out for n in k.nodes if level[n.out] == p + 1 and not is_vec(n.out)
+                               and not n.op.startswith("reduce_")]
+                self._emit_dag(t, penv, scalars, members, k.nodes, ref_of,
+                               node_ok=lambda n: not is_vec(n.out))
+                if final:
+                    for v in outs:
+                        if not is_vec(v):
+                            t.emit("store", out_ref[v], penv[v])
+                pe = len(t.insns)
+                for v in scalars:
+                    persist[v] = penv[v]
+                for v, r in penv.items():
+                    if v.node is not None and v.node in members and not is_vec(v):
+                        persist.setdefault(v, r)
+                acc_list = [accs[n.out] for n in seg_reds]
+                max_list = [accs[n.out] for n in seg_reds if n.op == "reduce_max"]
+                segments.append((vb, ve, pb, pe, acc_list, max_list))
+            t.segments = segments
+            return t
+
+        def loops(t):
+            return [] if single else [(s[0], s[1]) for s in t.segments]
+
+        # loads are placed at the start of the segment that reads them
+        t = build(True)
+        slot = _allocate(t, loops(t), kl.NREGS)
+        if slot is None:
+            raise NotImplementedError("HIP backend: row kernel needs more than 16 registers")
+        _encode(t, slot, d)
+        if len(t.segments) > kl.MAX_PASSES:
+            raise NotImplementedError(f"HIP backend: row kernel with {len(t.segments)} passes")
+        for i, (vb, ve, pb, pe, accs, maxs) in enumerate(t.segments):
+            P = d.passes[i]
+            P.vec_begin, P.vec_end, P.post_begin, P.post_end = vb, ve, pb, pe
+            P.acc_mask = sum(1 << slot[v] for v in accs)
+            P.max_mask = sum(1 << slot[v] for v in maxs)
+            P.single_chunk = 1 if single else 0
+        d.n_passes = len(t.segments)
+        nbytes = 4 * (sum(math.prod(v.shape) for v in externals) + sum(math.prod(v.shape) for v in outs))
+        kind = {kl.ROW_LAYERNORM: "layernorm", kl.ROW_SOFTMAX: "softmax"}.get(variant, "generic")
+        self.add(d, k, f"{kind} rows {list(rows)} x {inner}, {len(t.segments)} passes"
+                       f"{'' if single else ' (chunked)'}: {' '.join(n.op for n in k.nodes)}", nbytes=nbytes)
+
+    def _row_pattern(self, k, reds, outs, externals):
+        """Recognise the frontend's LayerNorm / softmax decompositions
+        (kiln/frontend/fx_import.py:212-230). Returns (variant, fparams,
+        (cfg4, cfg5), ordered externals or None)."""
+        nodes = k.nodes
+        none = (kl.ROW_GENERIC, [], (0, 0), None)
+        if len(outs) != 1 or outs[0].node not in set(nodes):
+            return none
+        out = outs[0]
+        imm = lambda v: self.imm(v) if self.is_imm(v) else None
+        ops_ = [n.op for n in nodes]
+        # softmax: [pre] reduce_max, sub, exp, reduce_sum, div
+        if ops_[-5:] == ["reduce_max", "sub", "exp", "reduce_sum", "div"] and len(nodes) in (5, 6):
+            mx, sub, ex, sm, dv = nodes[-5:]
+            pre, pre_scale, x = 0, 0.0, mx.inputs[0]
+            if len(nodes) == 6:
+                p = nodes[0]
+                if p.op not in ("mul", "div") or p.out is not x or imm(p.inputs[1]) is None:
+                    return none
+                pre, pre_scale, x = (1 if p.op == "mul" else 2), imm(p.inputs[1]), p.inputs[0]
+            ok = (sub.inputs == [mx.inputs[0], mx.out] and ex.inputs == [sub.out] and sm.inputs == [ex.out]
+                  and dv.inputs == [ex.out, sm.out] and dv.out is out and x not in set(n.out for n in nodes))
+            if ok and externals == [x]:
+                return kl.ROW_SOFTMAX, [pre_scale], (pre, 0), [x]
+            return none
+        # layernorm: reduce_sum, mul c, sub, mul, reduce_sum, mul c, add eps, rsqrt, mul, [mul g], [add b]
+        if len(nodes) >= 9 and ops_[:9] == ["reduce_sum", "mul", "sub", "mul", "reduce_sum", "mul", "add",
+                                            "rsqrt", "mul"]:
+            s1, m1, xc, sq, s2, m2, ad, rs, y = nodes[:9]
+            x = s1.inputs[0]
+            c1, c2, eps = imm(m1.inputs[1]), imm(m2.inputs[1]), imm(ad.inputs[1])
+            ok = (None not in (c1, c2, eps) and m1.inputs[0] is s1.out and xc.inputs == [x, m1.out]
+                  and sq.inputs == [xc.out, xc.out] and s2.inputs == [sq.out] and m2.inputs[0] is s2.out
+                  and ad.inputs[0] is m2.out and rs.inputs == [ad.out] and y.inputs == [xc.out, rs.out])
+            if not ok:
+                return none
+            rest, cur, gamma, beta = nodes[9:], y.out, None, None
+            if rest and rest[0].op == "mul" and rest[0].inputs[0] is cur and not self.is_imm(rest[0].inputs[1]):
+                gamma, cur, rest = rest[0].inputs[1], rest[0].out, rest[1:]
+            if rest and rest[0].op == "add" and rest[0].inputs[0] is cur and not self.is_imm(rest[0].inputs[1]):
+                beta, cur, rest = rest[0].inputs[1], rest[0].out, rest[1:]
+            if rest or cur is not out:
+                return none
+            inner = x.shape[-1]
+            for p in (gamma, beta):
+                if p is not None and (p.type.rank < 1 or p.shape[-1] != inner
+                                      or any(s != 1 for s in p.shape[:-1])):
+                    return none
+            ordered = [x] + [p for p in (gamma, beta) if p is not None]
+            if sorted(map(id, ordered)) != sorted(map(id, externals)) or len(set(map(id, ordered))) != len(ordered):
+                return none
+            return kl.ROW_LAYERNORM, [c1, c2, eps], (int(gamma is not None), int(beta is not None)), ordered
+        return none
+
+    # matmul -----------------------------------------------------------------------------------
+
+    def lower_matmul(self, k: Kernel):
+        mm = next(n for n in k.nodes if n.op == "matmul")
+        a, b = mm.inputs
+        out_shape = tuple(mm.out.shape)
+        batch = math.prod(a.shape[:-2]) if a.type.rank == 3 else 1
+        m, kk, n = a.shape[-2], a.shape[-1], b.shape[-1]
+        members = set(k.nodes)
+        outs = kernel_outputs(self.g, k, self.users)
+        space3 = (batch, m, n)
+
+        def ref3(v, dims):
+            """Strides of v over a 3-d space named by `dims` (v's own dims right-aligned)."""
+            lay = self.layouts[v]
+            r = kl.Ref()
+            r.base, r.index = self.slot_of(lay.base)
+            r.offset = self.element_offset(v)
+            lead = 3 - len(lay.shape)
+            for i, (s, st) in enumerate(zip(lay.shape, lay.strides)):
+                r.strides[lead + i] = 0 if s == 1 and dims[lead + i] != 1 else st
+            return r
+
+        gemv = m == 1
+        d = self.new_desc(kl.FAM_GEMV if gemv else kl.FAM_GEMM, "gemv" if gemv else "matmul", k, space3)
+        d.gemm[0], d.gemm[1], d.gemm[2], d.gemm[3] = batch, m, n, kk
+        if a not in self.layouts or b not in self.layouts:
+            raise NotImplementedError("HIP backend: matmul operand has no storage")
+        d.refs[0] = ref3(a, (batch, m, kk))
+        d.refs[1] = ref3(b, (batch, kk, n))
+        externals = []
+        for nd in k.nodes:
+            if nd is mm:
+                continue
+            for v in nd.inputs:
+                if v is not mm.out and (v.node not in members or v.node is None) and not self.is_imm(v) \
+                        and v not in externals:
+                    externals.append(v)
+        refs, ref_of = [], {}
+        for v in externals:
+            ref_of[v] = len(refs)
+            refs.append(ref3(v, space3))
+        out_ref = {}
+        for v in outs:
+            out_ref[v] = len(refs)
+            refs.append(ref3(v, space3))
+        self._check_refs(refs + [None, None])
+        for j, r in enumerate(refs):
+            d.refs[2 + j] = r
+        d.n_refs = 2 + len(refs)
+
+        def build(eager):
+            t = _Tape()
+            acc = t.virt()
+            t.marks[acc] = 0
+            env = {mm.out: acc}
+            if eager:
+                for v in externals:
+                    env[v] = t.emit("load", t.virt(), ref_of[v])
+            self._emit_dag(t, env, outs, members, k.nodes, ref_of)
+            for v in outs:
+                t.emit("store", out_ref[v], env[v])
+            t.acc = acc
+            return t
+
+        # slot 0 must hold the accumulator on entry
+        best = None
+        for eager in (True, False):
+            t = build(eager)
+            slot = _allocate(t, [], kl.FAST_SLOTS)
+            if slot is None:
+                continue
+            slot = self._pin(t, slot, (t.acc, 0), [], kl.FAST_SLOTS)
+            best = (t, slot)
+            break
+        if best is None:
+            raise NotImplementedError("HIP backend: matmul epilogue needs more than 8 registers")
+        _encode(best[0], best[1], d, ref_offset=2)
+        cfg = dict(self.matmul_config(self.g, k)) if not gemv else {"tile": 0, "splitk": 0}
+        d.cfg[1] = int(cfg.get("tile", 0))
+        d.cfg[2] = int(cfg.get("splitk", 1))
+        d.cfg[3] = {"fp32": kl.PREC_FP32, "bf16": kl.PREC_BF16, "bf16x3": kl.PREC_BF16X3}[
+            cfg.get("precision", self.precision)]
+        flops = 2 * batch * m * n * kk
+        nbytes = 4 * (math.prod(a.shape) + math.prod(b.shape) + sum(math.prod(v.shape) for v in externals)
+                      + len(outs) * math.prod(out_shape))
+        epi = " ".join(nd.op for nd in k.nodes if nd is not mm)
+        summary = f"{batch}x{m}x{n}x{kk}"
+        if not gemv:
+            summary += f" tile {d.cfg[1]} splitk {d.cfg[2]}"
+        if epi:
+            summary += f" epilogue: {epi}"
+        self.add(d, k, summary, flops=flops, nbytes=nbytes)
+
+    # driver --------------------------------------------------------------------------------------
+
+    def run(self) -> Program:
+        for k in self.g.kernels:
+            for n in k.nodes:
+                if ops.kind(n.op) not in ("elementwise", "reduction", "matmul"):
+                    raise NotImplementedError(f"GPU backend: unexpected op '{n.op}' in a kernel")
+        for k in self.g.kernels:
+            if k.kind == "matmul":
+                self.lower_matmul(k)
+            elif k.kind == "reduction":
+                self.lower_reduction(k)
+            else:
+                self.lower_elementwise(k)
+        return self.program
+
+
+def lower_graph(graph: Graph, precision: str = "fp32", matmul_config=None) -> Program:
+    """Fused, buffer-assigned, memory-planned graph -> Program (launch list)."""
+    from kiln.hip.autotune import default_matmul_config
+
+    return _Lowerer(graph, precision, matmul_config or default_matmul_config).run()
