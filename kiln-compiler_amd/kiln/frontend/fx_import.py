@@ -178,6 +178,13 @@ class _Importer:
             start = start + size if start < 0 else start
             end = end + size if end < 0 else end
             return self.emit("slice", x, dim=dim, start=max(0, start), end=min(end, size), step=step)
+        if t is aten.select.int:
+            # x[..., i, ...]: a one-element slice, then the dim dropped (both views)
+            x = self.val(args[0])
+            dim = args[1] % x.type.rank
+            i = args[2] + x.shape[dim] if args[2] < 0 else args[2]
+            one = self.emit("slice", x, dim=dim, start=i, end=i + 1, step=1)
+            return self.drop_dims(one, [dim])
         if t in (aten.split_with_sizes.default, aten.split.Tensor):
             x = self.val(args[0])
             dim = (args[2] if len(args) > 2 else kw.get("dim", 0)) % x.type.rank

@@ -1,0 +1,190 @@
+"""The HIP backend's host side on the CPU: the C-ABI library loads and exports
+every entry point of include/kiln_hip.h, descriptors are validated by the
+library (kh_plan_create runs without a GPU: it only prepares kernel
+arguments), and the lowering picks the intended kernel families."""
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from kiln.api import Options, build_passes, compile_graph
+from kiln.frontend.fx_import import import_exported
+from kiln.hip import autotune, lib as kl
+from kiln.hip.lowering import lower_graph
+from kiln.ir import parse
+from kiln.passes.manager import PassManager
+from models.transformer import Block, Stack
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "kiln_hip.h")
+
+
+def lowered(fn, *xs, **opts):
+    module = fn if isinstance(fn, torch.nn.Module) else type("F", (torch.nn.Module,), {
+        "forward": lambda self, *a: fn(*a)})()
+    g = import_exported(torch.export.export(module.eval(), xs).run_decompositions())
+    PassManager(build_passes(Options(**opts))).run(g)
+    return g, lower_graph(g)
+
+
+def test_library_exports_every_header_symbol():
+    lib = kl.load()
+    declared = set(re.findall(r"^\s*(?:int|const char \*)\s*(kh_\w+)\s*\(", open(HEADER).read(), re.M))
+    assert declared == set(kl.EXPORTED)
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert lib.kh_version() == kl.ABI_VERSION
+
+
+def test_struct_sizes_match_the_library():
+    sizes = (ctypes.c_size_t * 4)()
+    kl.load().kh_abi_sizes(sizes)
+    assert tuple(sizes) == (ctypes.sizeof(kl.LaunchDesc), ctypes.sizeof(kl.Ref), ctypes.sizeof(kl.Insn),
+                            ctypes.sizeof(kl.PassDesc))
+
+
+def test_gemm_config_table_matches_the_tuner():
+    cfgs = kl.gemm_configs()
+    assert len(cfgs) == len(autotune.TILES)
+    for i, c in enumerate(cfgs):
+        assert tuple(c[:7]) == autotune.TILES[i]
+
+
+def test_block_lowers_to_the_expected_families():
+    g, prog = lowered(Block(768, 12, 128), torch.randn(128, 768))
+    fams = [kl.FAMILY_NAMES[l.family] for l in prog.launches]
+    assert fams == ["row", "gemm", "elementwise", "gemm", "row", "gemm", "elementwise", "gemm", "row", "gemm",
+                    "gemm"]
+    variants = [l.desc.variant for l in prog.launches if l.family == kl.FAM_ROW]
+    assert variants == [kl.ROW_LAYERNORM, kl.ROW_SOFTMAX, kl.ROW_LAYERNORM]
+    plan = kl.Plan([l.desc for l in prog.launches])
+    assert plan.n_launches == 11
+
+
+def test_decode_uses_the_gemv_family():
+    _, prog = lowered(torch.nn.Linear(768, 3072), torch.randn(1, 768))
+    assert [l.family for l in prog.launches] == [kl.FAM_GEMV]
+
+
+def test_long_rows_are_chunked_and_short_rows_fast():
+    _, prog = lowered(torch.nn.LayerNorm(10000), torch.randn(2, 10000))
+    assert "(chunked)" in prog.launches[0].summary
+    _, prog = lowered(torch.nn.LayerNorm(768), torch.randn(4, 768))
+    assert prog.launches[0].desc.variant == kl.ROW_LAYERNORM
+    _, prog = lowered(lambda x: F.softmax(x * 0.125, -1), torch.randn(2, 8, 64))
+    d = prog.launches[0].desc
+    assert d.variant == kl.ROW_SOFTMAX and d.cfg[4] == 1 and d.fparams[0] == 0.125
+
+
+def test_column_reductions_use_the_reduce_family():
+    _, prog = lowered(lambda x: x.sum(0, keepdim=True) * 2.0, torch.randn(6, 10))
+    assert kl.FAM_RED in [l.family for l in prog.launches]
+
+
+def test_bias_gelu_is_one_elementwise_launch_with_vector_operands():
+    b = torch.randn(3072)
+    _, prog = lowered(lambda t: F.gelu(t + b, approximate="tanh"), torch.randn(64, 3072))
+    (launch,) = prog.launches
+    assert launch.family == kl.FAM_EW
+    ops = [kl.OPCODES[launch.desc.insns[i].op] for i in range(launch.desc.n_insns)]
+    assert ops == ["load", "load", "add", "gelu_tanh", "store"]
+    bias = launch.desc.refs[1] if launch.desc.refs[0].strides[0] else launch.desc.refs[0]
+    assert list(bias.strides[:2]) == [0, 1]
+
+
+def test_stack_decode_plan():
+    _, prog = lowered(Stack(12, 768, 12, 1), torch.randn(1, 768))
+    assert len(prog.launches) == 12 * 9 + 1
+    kl.Plan([l.desc for l in prog.launches])
+
+
+@pytest.mark.parametrize("mutate, err", [
+    (lambda d: setattr(d.insns[0], "op", 99), ValueError),
+    (lambda d: setattr(d.insns[0], "dst", 40), ValueError),
+    (lambda d: setattr(d, "family", 42), ValueError),
+    (lambda d: setattr(d, "n_refs", 13), ValueError),
+    (lambda d: d.cfg.__setitem__(1, 77), ValueError),
+])
+def test_library_rejects_bad_descriptors(mutate, err):
+    _, prog = lowered(lambda a, b: a @ b + 1.0, torch.randn(8, 16), torch.randn(16, 4))
+    d = kl.LaunchDesc.from_buffer_copy(prog.launches[0].desc)
+    mutate(d)
+    with pytest.raises(err):
+        kl.Plan([d])
+
+
+def test_unknown_precision_is_not_implemented():
+    _, prog = lowered(lambda a, b: a @ b, torch.randn(8, 16), torch.randn(16, 4))
+    d = kl.LaunchDesc.from_buffer_copy(prog.launches[0].desc)
+    d.cfg[3] = 7
+    with pytest.raises(NotImplementedError):
+        kl.Plan([d])
+
+
+def test_split_k_workspace_is_reported():
+    _, prog = lowered(lambda a, b: a @ b, torch.randn(128, 3072), torch.randn(3072, 768))
+    d = kl.LaunchDesc.from_buffer_copy(prog.launches[0].desc)
+    d.cfg[1], d.cfg[2] = 3, 4          # 64x64 tiles, split-K 4
+    plan = kl.Plan([d])
+    tiles = (128 // 64) * (768 // 64)
+    assert plan.workspace_bytes == 256 * ((tiles * 4 + 255) // 256) + 4 * tiles * 64 * 64 * 4
+
+
+def test_plan_listing_is_stable():
+    g = parse(open(os.path.join(os.path.dirname(__file__), "lit", "fusion.kir")).read())
+    PassManager(build_passes(Options())).run(g)
+    a, b = lower_graph(g), lower_graph(g)
+    assert a.source == b.source and a.digest() == b.digest()
+
+
+def test_default_tiles_fill_the_gpu():
+    cfg = autotune.default_config_for(1, 2048, 3072, 768, cus=256)
+    bm, bn = autotune.TILES[cfg["tile"]][:2]
+    assert (2048 // bm) * (3072 // bn) * cfg["splitk"] >= 256
+    small = autotune.default_config_for(1, 128, 768, 768, cus=256)
+    bm, bn = autotune.TILES[small["tile"]][:2]
+    assert -(-128 // bm) * -(-768 // bn) * small["splitk"] >= 64
+
+
+def test_candidates_fit_the_problem():
+    for m, n, k in [(128, 3072, 768), (1, 768, 768), (7, 13, 5)]:
+        for c in autotune.candidates(1, m, n, k, cus=256):
+            bm, bn = autotune.TILES[c["tile"]][:2]
+            assert bm <= max(16, 2 * m) and bn <= max(16, 2 * n)
+
+
+def test_options_and_errors():
+    g = parse("graph @f(%arg0: f32[2]) -> (f32[2]) {\n %0 = exp %arg0 : f32[2]\n return %0\n}")
+    with pytest.raises(ValueError):
+        compile_graph(g, Options(device="tpu"))
+    with pytest.raises(NotImplementedError):
+        compile_graph(g, Options(device="cpu"))
+    import kiln
+
+    with pytest.raises(TypeError):
+        kiln.compile(torch.nn.Linear(2, 2), (torch.randn(1, 2),), not_an_option=1)
+
+
+def test_memory_check_gives_a_clear_error(monkeypatch):
+    from kiln.hip.runtime import check_memory
+
+    monkeypatch.setattr(torch.cuda, "mem_get_info", lambda dev=None: (10 * 2**20, 32 * 2**30))
+    with pytest.raises(MemoryError, match="only 10.0 MiB"):
+        check_memory(torch.device("cuda"), 64 * 2**20, "the arena")
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(kl, "_lib", None)
+    monkeypatch.setenv("KILN_HIP_LIB", str(tmp_path / "missing.so"))
+    with pytest.raises(RuntimeError, match="not built"):
+        kl.load()
+
+
+def test_autotune_cache_is_ignored_when_corrupt(tmp_path):
+    autotune.cache_path().parent.mkdir(parents=True, exist_ok=True)
+    autotune.cache_path().write_text("{not json")
+    assert autotune.GPUAutotuner()._cache == {}
