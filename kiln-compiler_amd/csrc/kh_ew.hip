@@ -114,6 +114,172 @@ class EwOp final : public Op {
   }
 };
 
+// ---------------------------------------------------------------------------
+// Fast path: out = act(a op b) (or act(a)) on a rows x inner space whose
+// operands are contiguous along inner, per-row broadcast or a bias row. No
+// tape: the op pair is a template, each thread keeps 4 groups of 4 in flight
+// (all loads issued first), and registers stay low so waves stay resident.
+enum { kFastAdd = 0, kFastSub, kFastMul, kFastNone };
+enum { kActNone = 0, kActGeluTanh, kActGeluErf, kActRelu };
+
+struct EwFastArgs {
+  const float *a, *b;
+  float *out;
+  int64_t a_os, b_os, out_os;  // row strides (elements)
+  int32_t a_bc, b_bc;          // 1: one value per row (inner stride 0)
+  int32_t b_imm, imm_left;     // b is the immediate; the immediate is the left operand
+  float imm;
+  uint32_t inner4, total4;
+  FastDiv div;
+};
+
+constexpr int kFastUnroll = 4;
+
+template <int OP, int ACT>
+__global__ __launch_bounds__(kEwThreads) void ew_fast_kernel(const EwFastArgs a) {
+  const uint32_t stride = gridDim.x * kEwThreads;
+  for (uint32_t g0 = blockIdx.x * kEwThreads + threadIdx.x; g0 < a.total4; g0 += stride * kFastUnroll) {
+    float4 xa[kFastUnroll], xb[kFastUnroll];
+    uint32_t row[kFastUnroll], col[kFastUnroll];
+#pragma unroll
+    for (int u = 0; u < kFastUnroll; ++u) {
+      const uint32_t g = g0 + u * stride;
+      row[u] = fdiv(g, a.div);
+      col[u] = (g - row[u] * a.inner4) * 4;
+      if (g < a.total4) {
+        const float *pa = a.a + (int64_t)row[u] * a.a_os;
+        if (a.a_bc) {
+          const float s = pa[0];
+          xa[u] = make_float4(s, s, s, s);
+        } else {
+          xa[u] = *reinterpret_cast<const float4 *>(pa + col[u]);
+        }
+        if (OP != kFastNone && !a.b_imm) {
+          const float *pb = a.b + (int64_t)row[u] * a.b_os;
+          if (a.b_bc) {
+            const float s = pb[0];
+            xb[u] = make_float4(s, s, s, s);
+          } else {
+            xb[u] = *reinterpret_cast<const float4 *>(pb + col[u]);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kFastUnroll; ++u) {
+      const uint32_t g = g0 + u * stride;
+      if (g >= a.total4) break;
+      float v[4] = {xa[u].x, xa[u].y, xa[u].z, xa[u].w};
+      const float w[4] = {xb[u].x, xb[u].y, xb[u].z, xb[u].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float l = v[i], r = a.b_imm ? a.imm : w[i];
+        if (a.b_imm && a.imm_left) r = v[i], l = a.imm;
+        float x = OP == kFastAdd ? l + r : OP == kFastSub ? l - r : OP == kFastMul ? l * r : v[i];
+        if (ACT == kActGeluTanh) x = op_gelu_tanh(x);
+        if (ACT == kActGeluErf) x = op_gelu_erf(x);
+        if (ACT == kActRelu) x = x != x ? x : fmaxf(x, 0.0f);
+        v[i] = x;
+      }
+      *reinterpret_cast<float4 *>(a.out + (int64_t)row[u] * a.out_os + col[u]) = make_float4(v[0], v[1], v[2], v[3]);
+    }
+  }
+}
+
+class EwFastOp final : public Op {
+ public:
+  EwFastArgs args{};
+  int op = kFastAdd, act = kActNone, ra = 0, rb = -1, ro = 0, grid = 1;
+  hipError_t launch(float *const *ptrs, uint32_t *, float *, hipStream_t stream) override {
+    EwFastArgs x = args;
+    x.a = ptrs[ra];
+    x.b = rb >= 0 ? ptrs[rb] : nullptr;
+    x.out = ptrs[ro];
+    for (int j : {ra, rb, ro})
+      if (j >= 0 && (reinterpret_cast<uintptr_t>(ptrs[j]) & 15) != 0 &&
+          !(j == ra && x.a_bc) && !(j == rb && x.b_bc))
+        return fallback->launch(ptrs, nullptr, nullptr, stream);  // unaligned buffer: tape path
+    if (x.total4 == 0) return hipSuccess;
+#define KH_FAST_CASE(O, A) \
+  if (op == O && act == A) hipLaunchKernelGGL((ew_fast_kernel<O, A>), dim3(grid), dim3(kEwThreads), 0, stream, x);
+#define KH_FAST_ACTS(O) KH_FAST_CASE(O, kActNone) KH_FAST_CASE(O, kActGeluTanh) KH_FAST_CASE(O, kActGeluErf) \
+  KH_FAST_CASE(O, kActRelu)
+    KH_FAST_ACTS(kFastAdd)
+    KH_FAST_ACTS(kFastSub)
+    KH_FAST_ACTS(kFastMul)
+    KH_FAST_ACTS(kFastNone)
+#undef KH_FAST_ACTS
+#undef KH_FAST_CASE
+    return hipGetLastError();
+  }
+  std::unique_ptr<Op> fallback;
+};
+
+// Recognise LOAD a; [LOAD b]; [add|sub|mul]; [gelu|relu]; STORE over a space
+// that coalesces to (rows, inner) with inner % 4 == 0 and vector-friendly
+// operands. Returns nullptr when the descriptor does not qualify.
+std::unique_ptr<Op> try_fast_ew(const kh_launch &L, EwOp &generic, int rank, int outer_rank) {
+  const EwArgs &g = generic.args;
+  if (rank < 1 || outer_rank > 1 || g.inner % 4 != 0 || g.total_groups == 0) return nullptr;
+  const kh_insn *t = L.insns;
+  int n = L.n_insns, pc = 0;
+  int slot_a = -1, slot_b = -1, ra = -1, rb = -1;
+  if (pc < n && t[pc].op == KH_OP_LOAD) slot_a = t[pc].dst, ra = t[pc].a, ++pc;
+  if (pc < n && t[pc].op == KH_OP_LOAD) slot_b = t[pc].dst, rb = t[pc].a, ++pc;
+  if (ra < 0) return nullptr;
+  int op = kFastNone, act = kActNone, cur = slot_a;
+  bool b_imm = false, imm_left = false;
+  float imm = 0.0f;
+  if (pc < n && (t[pc].op == KH_OP_ADD || t[pc].op == KH_OP_SUB || t[pc].op == KH_OP_MUL)) {
+    const kh_insn &in = t[pc++];
+    op = in.op == KH_OP_ADD ? kFastAdd : in.op == KH_OP_SUB ? kFastSub : kFastMul;
+    if (slot_b >= 0 && in.a == slot_a && in.b == slot_b) {
+    } else if (slot_b >= 0 && in.a == slot_b && in.b == slot_a) {
+      std::swap(ra, rb);
+      std::swap(slot_a, slot_b);
+    } else if (slot_b < 0 && in.a == slot_a && in.b == KH_SRC_IMM) {
+      b_imm = true, imm = in.imm;
+    } else if (slot_b < 0 && in.b == slot_a && in.a == KH_SRC_IMM) {
+      b_imm = true, imm_left = true, imm = in.imm;
+    } else {
+      return nullptr;
+    }
+    cur = in.dst;
+  } else if (slot_b >= 0) {
+    return nullptr;
+  }
+  if (pc < n && (t[pc].op == KH_OP_GELU_TANH || t[pc].op == KH_OP_GELU_ERF || t[pc].op == KH_OP_RELU ||
+                 t[pc].op == KH_OP_MOV)) {
+    const kh_insn &in = t[pc++];
+    if (in.a != cur) return nullptr;
+    act = in.op == KH_OP_GELU_TANH ? kActGeluTanh : in.op == KH_OP_GELU_ERF ? kActGeluErf
+                                                    : in.op == KH_OP_RELU ? kActRelu : kActNone;
+    cur = in.dst;
+  }
+  if (pc != n - 1 || t[pc].op != KH_OP_STORE || t[pc].a != cur) return nullptr;
+  const int ro = t[pc].dst;
+  auto vec = [&](int j) { return (generic.vec_candidates >> j & 1) != 0; };
+  auto bc = [&](int j) { return g.istride[j] == 0; };
+  if (!vec(ro) || (!vec(ra) && !bc(ra)) || (rb >= 0 && !vec(rb) && !bc(rb))) return nullptr;
+  auto fast = std::make_unique<EwFastOp>();
+  EwFastArgs &f = fast->args;
+  fast->op = op, fast->act = act, fast->ra = ra, fast->rb = rb, fast->ro = ro;
+  f.a_os = outer_rank ? g.ostride[ra][0] : 0;
+  f.b_os = (rb >= 0 && outer_rank) ? g.ostride[rb][0] : 0;
+  f.out_os = outer_rank ? g.ostride[ro][0] : 0;
+  f.a_bc = bc(ra);
+  f.b_bc = rb >= 0 && bc(rb);
+  f.b_imm = b_imm, f.imm_left = imm_left, f.imm = imm;
+  f.inner4 = g.inner / 4;
+  f.total4 = g.total_groups;
+  f.div = make_fastdiv(f.inner4);
+  const int64_t blocks = ((int64_t)f.total4 + kEwThreads * kFastUnroll - 1) / (kEwThreads * kFastUnroll);
+  fast->grid = (int)std::max<int64_t>(1, std::min<int64_t>(blocks, (int64_t)current_device().cus * 16));
+  auto copy = std::make_unique<EwOp>(generic);
+  fast->fallback = std::move(copy);
+  return fast;
+}
+
 }  // namespace
 
 std::unique_ptr<Op> make_ew(const kh_launch &L, std::string &err, bool &unsupported) {
@@ -192,6 +358,7 @@ std::unique_ptr<Op> make_ew(const kh_launch &L, std::string &err, bool &unsuppor
   op->slots = info.slots;
   const int64_t blocks = (total + kEwThreads - 1) / kEwThreads;
   op->grid = (int)std::max<int64_t>(1, std::min<int64_t>(blocks, (int64_t)current_device().cus * 16));
+  if (auto fast = try_fast_ew(L, *op, rank, outer_rank)) return fast;
   return op;
 }
 

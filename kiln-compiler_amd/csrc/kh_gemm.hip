@@ -19,14 +19,16 @@
 //     4, so bias, GELU, residual, scale and mask operands are read with
 //     coalesced 128-bit loads and the output is written with 128-bit stores;
 //   * split-K (for M = 128 shapes that cannot fill 256 CUs): each split writes
-//     its raw partial tile to the workspace; the last workgroup to finish a
-//     tile (device-scope counter) sums the partials in split order - the
-//     result does not depend on arrival order - runs the epilogue and resets
-//     the counter, so the next launch (or graph replay) starts from zero;
+//     its raw partial tile, dense [split][batch][M][N], to the workspace and
+//     a second kernel sums them in split order and runs the epilogue. The
+//     kernel boundary is the only synchronisation (a per-tile device-scope
+//     counter would need an L2 write-back per workgroup across 8 XCDs), and
+//     the fixed summation order keeps the result independent of scheduling;
 //   * workgroup ids are remapped so each XCD (own L2) receives a contiguous
 //     block of tiles.
 #include <algorithm>
 #include <cstring>
+#include <type_traits>
 
 #include "kh_common.hpp"
 #include "kh_gemm_args.hpp"
@@ -75,8 +77,11 @@ __global__ __launch_bounds__(64 * WM * WN * WK) void gemm_f32_kernel(const GemmA
   constexpr int G = 64 / MT;   // lane groups = K values one MFMA consumes
   constexpr int KW = BK / WK;  // K per wave per step
   constexpr int KG = KW / G;   // K per lane group per step
-  constexpr int A_STRIDE = BK + 4, B_STRIDE = BN + 4, C_STRIDE = BN + 4;
-  constexpr int A_FLOATS = BM * A_STRIDE, B_FLOATS = BK * B_STRIDE;
+  // LDS: A as [m][k] (row stride BK + 4: 16-byte aligned rows, conflict-free
+  // 128-bit reads), B transposed to [n][k] (row stride BK + 2: conflict-free
+  // 64-bit reads and conflict-free transposing writes), both double-buffered.
+  constexpr int A_STRIDE = BK + 4, B_STRIDE = BK + 2, C_STRIDE = BN + 4;
+  constexpr int A_FLOATS = BM * A_STRIDE, B_FLOATS = BN * B_STRIDE;
   constexpr int AB_FLOATS = 2 * (A_FLOATS + B_FLOATS);
   constexpr int C_FLOATS = BM * C_STRIDE;
   constexpr int LDS_FLOATS = AB_FLOATS > C_FLOATS ? AB_FLOATS : C_FLOATS;
@@ -85,12 +90,12 @@ __global__ __launch_bounds__(64 * WM * WN * WK) void gemm_f32_kernel(const GemmA
   constexpr int B_LOADS = (B_VECS + kThreads - 1) / kThreads;
   static_assert(TM % MT == 0 && TN % MT == 0, "wave tile must be a multiple of the MFMA tile");
   static_assert(KG % 4 == 0, "each lane group needs a multiple of 4 K values per step");
+  static_assert(BK % 8 == 0 && BN % 32 == 0 && B_VECS % 64 == 0, "B load mapping");
   static_assert(LDS_FLOATS * 4 <= 160 * 1024, "LDS");
   using M = Mfma<MT>;
   typedef typename M::acc_t acc_t;
 
   __shared__ __attribute__((aligned(16))) float lds[LDS_FLOATS];
-  __shared__ uint32_t last_flag;
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
@@ -106,15 +111,39 @@ __global__ __launch_bounds__(64 * WM * WN * WK) void gemm_f32_kernel(const GemmA
   const int k_end = min(a.K, k_begin + a.k_per_split);
   const float *Ab = a.A + (int64_t)bidx * a.sa_b;
   const float *Bb = a.B + (int64_t)bidx * a.sb_b;
+  // A float4 i of a step: row idx / (BK/4), k quad idx % (BK/4) (rows of BK
+  // contiguous floats). B float4 i: each wave covers 8 k-rows x 8 n-quads
+  // (128 contiguous bytes per row), so the transposing LDS writes hit 32
+  // distinct banks.
+  auto a_pos = [&](int i, int &r, int &kq) {
+    const int idx = tid + i * kThreads;
+    r = idx / (BK / 4), kq = idx % (BK / 4);
+  };
+  auto b_pos = [&](int i, int &kr, int &nq) {
+    const int idx = tid + i * kThreads;
+    const int c = idx >> 6;
+    kr = (c % (BK / 8)) * 8 + ((idx & 63) >> 3);
+    nq = (c / (BK / 8)) * 8 + (idx & 7);
+  };
+  const bool interior = m0 + BM <= a.M && n0 + BN <= a.N && a.a_vec && a.b_vec &&
+                        (k_end - k_begin) % BK == 0;
 
   float4 ra[A_LOADS], rb[B_LOADS];
-  auto load_step = [&](int k0) {
+  // `fast_tag` is std::true_type for interior tiles: unconditional 128-bit
+  // loads, no control flow between them, so every load of a step is in flight
+  // at once. Edge tiles use the guarded path.
+  auto load_step = [&](int k0, auto fast_tag) {
+    constexpr bool fast = decltype(fast_tag)::value;
 #pragma unroll
     for (int i = 0; i < A_LOADS; ++i) {
-      const int idx = tid + i * kThreads;
-      const int m = m0 + idx / (BK / 4), k = k0 + (idx % (BK / 4)) * 4;
+      int r, kq;
+      a_pos(i, r, kq);
+      const int m = m0 + r, k = k0 + kq * 4;
       float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if ((A_VECS % kThreads == 0 || idx < A_VECS) && m < a.M) {
+      const bool in_tile = A_VECS % kThreads == 0 || tid + i * kThreads < A_VECS;
+      if constexpr (fast) {
+        if (in_tile) v = *reinterpret_cast<const float4 *>(Ab + (int64_t)m * a.sa_m + k);
+      } else if (in_tile && m < a.M) {
         const float *p = Ab + (int64_t)m * a.sa_m;
         if (a.a_vec && k + 3 < k_end) {
           v = *reinterpret_cast<const float4 *>(p + k);
@@ -129,10 +158,14 @@ __global__ __launch_bounds__(64 * WM * WN * WK) void gemm_f32_kernel(const GemmA
     }
 #pragma unroll
     for (int i = 0; i < B_LOADS; ++i) {
-      const int idx = tid + i * kThreads;
-      const int k = k0 + idx / (BN / 4), n = n0 + (idx % (BN / 4)) * 4;
+      int kr, nq;
+      b_pos(i, kr, nq);
+      const int k = k0 + kr, n = n0 + nq * 4;
       float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-      if ((B_VECS % kThreads == 0 || idx < B_VECS) && k < k_end) {
+      const bool in_tile = B_VECS % kThreads == 0 || tid + i * kThreads < B_VECS;
+      if constexpr (fast) {
+        if (in_tile) v = *reinterpret_cast<const float4 *>(Bb + (int64_t)k * a.sb_k + n);
+      } else if (in_tile && k < k_end) {
         const float *p = Bb + (int64_t)k * a.sb_k;
         if (a.b_vec && n + 3 < a.N) {
           v = *reinterpret_cast<const float4 *>(p + n);
@@ -151,15 +184,22 @@ __global__ __launch_bounds__(64 * WM * WN * WK) void gemm_f32_kernel(const GemmA
     float *Bs = As + A_FLOATS;
 #pragma unroll
     for (int i = 0; i < A_LOADS; ++i) {
-      const int idx = tid + i * kThreads;
-      if (A_VECS % kThreads == 0 || idx < A_VECS)
-        *reinterpret_cast<float4 *>(As + (idx / (BK / 4)) * A_STRIDE + (idx % (BK / 4)) * 4) = ra[i];
+      int r, kq;
+      a_pos(i, r, kq);
+      if (A_VECS % kThreads == 0 || tid + i * kThreads < A_VECS)
+        *reinterpret_cast<float4 *>(As + r * A_STRIDE + kq * 4) = ra[i];
     }
 #pragma unroll
     for (int i = 0; i < B_LOADS; ++i) {
-      const int idx = tid + i * kThreads;
-      if (B_VECS % kThreads == 0 || idx < B_VECS)
-        *reinterpret_cast<float4 *>(Bs + (idx / (BN / 4)) * B_STRIDE + (idx % (BN / 4)) * 4) = rb[i];
+      int kr, nq;
+      b_pos(i, kr, nq);
+      if (B_VECS % kThreads == 0 || tid + i * kThreads < B_VECS) {
+        float *b = Bs + (nq * 4) * B_STRIDE + kr;
+        b[0] = rb[i].x;
+        b[B_STRIDE] = rb[i].y;
+        b[2 * B_STRIDE] = rb[i].z;
+        b[3 * B_STRIDE] = rb[i].w;
+      }
     }
   };
 
@@ -172,40 +212,57 @@ __global__ __launch_bounds__(64 * WM * WN * WK) void gemm_f32_kernel(const GemmA
       for (int r = 0; r < M::kRegs; ++r) acc[i][j][r] = 0.0f;
 
   const int g = lane / MT, li = lane % MT;
+  const int kb = wk * KW + g * KG;
   const int n_steps = k_end > k_begin ? (k_end - k_begin + BK - 1) / BK : 0;
+  auto main_loop = [&](auto fast_tag) {
   if (n_steps > 0) {
-    load_step(k_begin);
+    load_step(k_begin, fast_tag);
     store_step(0);
   }
   __syncthreads();
   for (int s = 0; s < n_steps; ++s) {
     const int buf = s & 1;
-    if (s + 1 < n_steps) load_step(k_begin + (s + 1) * BK);
-    const float *As = lds + buf * (A_FLOATS + B_FLOATS);
-    const float *Bs = As + A_FLOATS;
-    const int kb = wk * KW + g * KG;
-#pragma unroll
-    for (int j4 = 0; j4 < KG; j4 += 4) {
-      float4 av[FM];
+    if (s + 1 < n_steps) load_step(k_begin + (s + 1) * BK, fast_tag);
+    const float *As = lds + buf * (A_FLOATS + B_FLOATS) + (wm * TM + li) * A_STRIDE + kb;
+    const float *Bs = lds + buf * (A_FLOATS + B_FLOATS) + A_FLOATS + (wn * TN + li) * B_STRIDE + kb;
+    // fragments of 4 K values, double-buffered in registers
+    float4 av[2][FM];
+    float2 bv[2][FN][2];
+    auto read_frag = [&](int set, int j4) {
 #pragma unroll
       for (int fm = 0; fm < FM; ++fm)
-        av[fm] = *reinterpret_cast<const float4 *>(As + (wm * TM + fm * MT + li) * A_STRIDE + kb + j4);
+        av[set][fm] = *reinterpret_cast<const float4 *>(As + fm * MT * A_STRIDE + j4);
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn) {
+        bv[set][fn][0] = *reinterpret_cast<const float2 *>(Bs + fn * MT * B_STRIDE + j4);
+        bv[set][fn][1] = *reinterpret_cast<const float2 *>(Bs + fn * MT * B_STRIDE + j4 + 2);
+      }
+    };
+    read_frag(0, 0);
+#pragma unroll
+    for (int j4 = 0; j4 < KG; j4 += 4) {
+      const int cur = (j4 / 4) & 1;
+      if (j4 + 4 < KG) read_frag(cur ^ 1, j4 + 4);
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
-        float bv[FN];
-#pragma unroll
-        for (int fn = 0; fn < FN; ++fn) bv[fn] = Bs[(kb + j4 + jj) * B_STRIDE + wn * TN + fn * MT + li];
 #pragma unroll
         for (int fm = 0; fm < FM; ++fm) {
-          const float x = jj == 0 ? av[fm].x : jj == 1 ? av[fm].y : jj == 2 ? av[fm].z : av[fm].w;
+          const float4 A4 = av[cur][fm];
+          const float x = jj == 0 ? A4.x : jj == 1 ? A4.y : jj == 2 ? A4.z : A4.w;
 #pragma unroll
-          for (int fn = 0; fn < FN; ++fn) acc[fm][fn] = M::mma(x, bv[fn], acc[fm][fn]);
+          for (int fn = 0; fn < FN; ++fn) {
+            const float2 B2 = bv[cur][fn][jj >> 1];
+            acc[fm][fn] = M::mma(x, (jj & 1) ? B2.y : B2.x, acc[fm][fn]);
+          }
         }
       }
     }
     if (s + 1 < n_steps) store_step(buf ^ 1);
     __syncthreads();
   }
+  };
+  if (interior) main_loop(std::true_type{});
+  else main_loop(std::false_type{});
 
   // Stage the tile in LDS (the K-split wave groups add in a fixed order).
   float *Cs = lds;
@@ -226,47 +283,34 @@ __global__ __launch_bounds__(64 * WM * WN * WK) void gemm_f32_kernel(const GemmA
   }
 
   constexpr int GROUPS = BM * BN / 4;
-  const int64_t tile_id = (int64_t)bidx * n_tiles + tile;
   if (a.splitk > 1) {
-    float *part = a.ws_partial + ((int64_t)split * a.batch * n_tiles + tile_id) * (BM * BN);
+    // raw partial tile -> dense [split][batch][M][N]; the reduce kernel adds
+    // the splits and runs the epilogue
+    float *part = a.ws_partial + ((int64_t)split * a.batch + bidx) * (int64_t)a.M * a.N;
+    const bool vec = (a.N & 3) == 0;
     for (int q = tid; q < GROUPS; q += kThreads) {
       const int r = q / (BN / 4), c = (q % (BN / 4)) * 4;
-      *reinterpret_cast<float4 *>(part + r * BN + c) = *reinterpret_cast<const float4 *>(Cs + r * C_STRIDE + c);
+      const int m = m0 + r, n = n0 + c;
+      if (m >= a.M || n >= a.N) continue;
+      const float *src = Cs + r * C_STRIDE + c;
+      float *dst = part + (int64_t)m * a.N + n;
+      if (vec) {
+        *reinterpret_cast<float4 *>(dst) = *reinterpret_cast<const float4 *>(src);
+      } else {
+        for (int i = 0; i < 4 && n + i < a.N; ++i) dst[i] = src[i];
+      }
     }
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-      const uint32_t prior = atomicAdd(a.ws_count + tile_id, 1u);
-      last_flag = prior == (uint32_t)(a.splitk - 1);
-    }
-    __syncthreads();
-    if (!last_flag) return;
-    __threadfence();
+    return;
   }
   for (int q = tid; q < GROUPS; q += kThreads) {
     const int r = q / (BN / 4), c = (q % (BN / 4)) * 4;
     const int m = m0 + r, n = n0 + c;
     if (m >= a.M || n >= a.N) continue;
     Vec<4> v;
-    if (a.splitk > 1) {
-      v = splat4(0.0f);
-      for (int sp = 0; sp < a.splitk; ++sp) {
-        float4 p;
-        if (sp == split) {
-          p = *reinterpret_cast<const float4 *>(Cs + r * C_STRIDE + c);
-        } else {
-          p = *reinterpret_cast<const float4 *>(a.ws_partial +
-                                                ((int64_t)sp * a.batch * n_tiles + tile_id) * (BM * BN) + r * BN + c);
-        }
-        v.v[0] += p.x, v.v[1] += p.y, v.v[2] += p.z, v.v[3] += p.w;
-      }
-    } else {
-      const float4 p = *reinterpret_cast<const float4 *>(Cs + r * C_STRIDE + c);
-      v.v[0] = p.x, v.v[1] = p.y, v.v[2] = p.z, v.v[3] = p.w;
-    }
+    const float4 p = *reinterpret_cast<const float4 *>(Cs + r * C_STRIDE + c);
+    v.v[0] = p.x, v.v[1] = p.y, v.v[2] = p.z, v.v[3] = p.w;
     run_epilogue(a, bidx, m, n, min(4, a.N - n), v);
   }
-  if (a.splitk > 1 && tid == 0) atomicExch(a.ws_count + tile_id, 0u);
 }
 
 // ---------------------------------------------------------------------------
@@ -288,7 +332,13 @@ struct TileCfg {
   X(8, 64, 64, 32, 1, 1, 4, 32)   \
   X(9, 32, 32, 32, 2, 2, 1, 16)   \
   X(10, 16, 64, 32, 1, 4, 1, 16)  \
-  X(11, 64, 32, 32, 2, 2, 1, 16)
+  X(11, 64, 32, 32, 2, 2, 1, 16)  \
+  X(12, 128, 128, 32, 4, 2, 1, 32) \
+  X(13, 128, 192, 32, 4, 2, 1, 32) \
+  X(14, 256, 128, 32, 4, 2, 1, 32) \
+  X(15, 64, 128, 64, 2, 2, 1, 32)  \
+  X(16, 128, 64, 64, 2, 2, 1, 32)  \
+  X(17, 64, 64, 64, 2, 2, 1, 32)
 
 constexpr TileCfg kConfigs[] = {
 #define KH_CFG_ROW(id, bm, bn, bk, wm, wn, wk, mt) {bm, bn, bk, wm, wn, wk, mt},
@@ -316,7 +366,7 @@ class GemmOp final : public Op {
   GemmArgs args{};
   int cfg = 0;
   dim3 grid;
-  size_t n_counters = 0, n_partials = 0;
+  size_t n_partials = 0;
   bool a_vec_layout = false, b_vec_layout = false;
   uint32_t e_vec_candidates = 0;
 
@@ -333,12 +383,12 @@ class GemmOp final : public Op {
         a.e_vec_mask |= 1u << j;
     }
     a.ws_partial = partials;
-    a.ws_count = counters;
     if (a.M == 0 || a.N == 0 || a.batch == 0) return hipSuccess;
-    if (a.splitk > 1 && (!partials || !counters)) return hipErrorInvalidValue;
-    return launch_config(cfg, a, grid, stream);
+    if (a.splitk > 1 && !partials) return hipErrorInvalidValue;
+    const hipError_t e = launch_config(cfg, a, grid, stream);
+    if (e != hipSuccess || a.splitk == 1) return e;
+    return launch_splitk_reduce(a, current_device().cus, stream);
   }
-  size_t counter_count() const override { return n_counters; }
   size_t partial_floats() const override { return n_partials; }
 };
 
@@ -440,8 +490,7 @@ std::unique_ptr<Op> make_gemm(const kh_launch &L, std::string &err, bool &unsupp
   op->cfg = cfg;
   op->grid = dim3((unsigned)n_tiles, (unsigned)batch, (unsigned)splitk);
   if (splitk > 1) {
-    op->n_partials = (size_t)splitk * batch * n_tiles * t.bm * t.bn;
-    op->n_counters = (size_t)batch * n_tiles;
+    op->n_partials = (size_t)splitk * batch * M * N;
   }
   return op;
 }

@@ -2,6 +2,7 @@
 // GEMM and GEMV kernels (both end in epilogue(acc) over (batch, m, n)).
 #pragma once
 
+#include <algorithm>
 #include <string>
 
 #include "kh_common.hpp"
@@ -22,7 +23,6 @@ struct GemmArgs {
   int64_t estride[KH_MAX_REFS][3];
   kh_insn insns[KH_MAX_INSNS];        // LOAD/STORE operands renumbered to epilogue slots
   float *ws_partial;
-  uint32_t *ws_count;
 };
 
 // Run the epilogue tape for columns [n, n + valid) of output row (b, m);
@@ -59,6 +59,48 @@ __device__ __forceinline__ void run_epilogue(const GemmArgs &a, int64_t b, int64
   bank_set(f, 0, acc);
   exec_tape<kFastSlots>(a.insns, 0, a.n_insns, a.n_pre, f, load, store, [](const kh_insn &, const Vec<4> &) {});
 }
+
+// Split-K, second kernel: partials are dense [split][batch][M][N] fp32 in the
+// workspace (written by the first kernel without any cross-workgroup
+// synchronisation; the kernel boundary makes them visible to every XCD).
+// Each thread sums the splits of 4 adjacent columns in split order (the
+// result does not depend on scheduling) and runs the epilogue.
+namespace {
+constexpr int kReduceThreads = 256;
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmArgs a) {
+  const uint32_t n4 = (uint32_t)(a.N + 3) / 4;
+  const uint64_t rows = (uint64_t)a.batch * a.M;
+  const uint64_t total = rows * n4;
+  const uint64_t plane = rows * (uint64_t)a.N;
+  const bool vec = (a.N & 3) == 0;
+  for (uint64_t q = (uint64_t)blockIdx.x * 256 + threadIdx.x; q < total; q += (uint64_t)gridDim.x * 256) {
+    const uint64_t row = q / n4;
+    const int n = (int)(q - row * n4) * 4;
+    const int valid = min(4, a.N - n);
+    const float *p = a.ws_partial + row * a.N + n;
+    Vec<4> s = splat4(0.0f);
+    for (int sp = 0; sp < a.splitk; ++sp, p += plane) {
+      if (vec) {
+        const float4 v = *reinterpret_cast<const float4 *>(p);
+        s.v[0] += v.x, s.v[1] += v.y, s.v[2] += v.z, s.v[3] += v.w;
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (i < valid) s.v[i] += p[i];
+      }
+    }
+    run_epilogue(a, (int64_t)(row / a.M), (int64_t)(row % a.M), n, valid, s);
+  }
+}
+
+inline hipError_t launch_splitk_reduce(const GemmArgs &a, int cus, hipStream_t stream) {
+  const uint64_t total = (uint64_t)a.batch * a.M * (uint64_t)((a.N + 3) / 4);
+  const uint64_t blocks = (total + kReduceThreads - 1) / kReduceThreads;
+  const unsigned grid = (unsigned)std::max<uint64_t>(1, std::min<uint64_t>(blocks, (uint64_t)cus * 8));
+  hipLaunchKernelGGL(splitk_reduce_kernel, dim3(grid), dim3(kReduceThreads), 0, stream, a);
+  return hipGetLastError();
+}
+}  // namespace
 
 // Host: validate the epilogue refs/tape of a matmul descriptor into `a`.
 bool fill_epilogue(const kh_launch &L, GemmArgs &a, uint32_t &vec_candidates, std::string &err);

@@ -7,11 +7,12 @@
 // column quads of one weight row (1 KiB contiguous per k), 16 k-lanes walk
 // the K range four rows at a time so each thread has four loads in flight.
 // The 16 partial sums per column are combined through LDS in a fixed order.
-// When the column blocks cannot fill the GPU, K is split across workgroups
-// and the last one to finish a column block (device-scope counter) sums the
-// partials in split order and applies the epilogue, as in the GEMM family.
+// When the column blocks cannot fill the GPU, K is split across workgroups:
+// each writes a dense partial row and splitk_reduce_kernel (shared with the
+// GEMM family) sums them in split order and applies the epilogue.
 #include <algorithm>
 #include <cstring>
+#include <type_traits>
 
 #include "kh_common.hpp"
 #include "kh_gemm_args.hpp"
@@ -24,7 +25,6 @@ constexpr int kCols = 64;  // columns per workgroup
 
 __global__ __launch_bounds__(256) void gemv_kernel(const GemmArgs a) {
   __shared__ float4 part[16][16];
-  __shared__ uint32_t last_flag;
   const int cq = threadIdx.x & 15, kl = threadIdx.x >> 4;
   const int nb = blockIdx.x, b = blockIdx.y, split = blockIdx.z;
   const int n = nb * kCols + cq * 4;
@@ -32,19 +32,25 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemmArgs a) {
   const int k_end = min(a.K, k_begin + a.k_per_split);
   const float *x = a.A + (int64_t)b * a.sa_b;
   const float *W = a.B + (int64_t)b * a.sb_b;
-  const bool vec = a.b_vec && n + 3 < a.N;
-  auto row = [&](int k) -> float4 {
-    const float *p = W + (int64_t)k * a.sb_k;
-    if (vec) return *reinterpret_cast<const float4 *>(p + n);
-    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (n + 0 < a.N) v.x = p[(int64_t)(n + 0) * a.sb_n];
-    if (n + 1 < a.N) v.y = p[(int64_t)(n + 1) * a.sb_n];
-    if (n + 2 < a.N) v.z = p[(int64_t)(n + 2) * a.sb_n];
-    if (n + 3 < a.N) v.w = p[(int64_t)(n + 3) * a.sb_n];
-    return v;
-  };
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (n < a.N) {
+  // The vector/scalar choice is made once, outside the K loop, so the four
+  // row loads of an iteration carry no control flow between them and are all
+  // in flight together.
+  auto walk = [&](auto vec_tag) {
+    constexpr bool vec = decltype(vec_tag)::value;
+    auto row = [&](int k) -> float4 {
+      const float *p = W + (int64_t)k * a.sb_k;
+      if constexpr (vec) {
+        return *reinterpret_cast<const float4 *>(p + n);
+      } else {
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (n + 0 < a.N) v.x = p[(int64_t)(n + 0) * a.sb_n];
+        if (n + 1 < a.N) v.y = p[(int64_t)(n + 1) * a.sb_n];
+        if (n + 2 < a.N) v.z = p[(int64_t)(n + 2) * a.sb_n];
+        if (n + 3 < a.N) v.w = p[(int64_t)(n + 3) * a.sb_n];
+        return v;
+      }
+    };
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     int k = k_begin + kl;
     for (; k + 48 < k_end; k += 64) {
       const float4 w0 = row(k), w1 = row(k + 16), w2 = row(k + 32), w3 = row(k + 48);
@@ -60,7 +66,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemmArgs a) {
       const float xv = x[(int64_t)k * a.sa_k];
       acc.x = fmaf(xv, w.x, acc.x), acc.y = fmaf(xv, w.y, acc.y), acc.z = fmaf(xv, w.z, acc.z), acc.w = fmaf(xv, w.w, acc.w);
     }
-  }
+    return acc;
+  };
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (n < a.N) acc = (a.b_vec && n + 3 < a.N) ? walk(std::true_type{}) : walk(std::false_type{});
   part[kl][cq] = acc;
   __syncthreads();
   Vec<4> v = splat4(0.0f);
@@ -71,37 +80,21 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemmArgs a) {
       v.v[0] += p.x, v.v[1] += p.y, v.v[2] += p.z, v.v[3] += p.w;
     }
   }
-  const int n_blocks = gridDim.x;
-  const int64_t slot = (int64_t)b * n_blocks + nb;
+  if (kl != 0 || n >= a.N) return;
   if (a.splitk > 1) {
-    float *mine = a.ws_partial + ((int64_t)split * a.batch * n_blocks + slot) * kCols + cq * 4;
-    if (kl == 0) *reinterpret_cast<float4 *>(mine) = make_float4(v.v[0], v.v[1], v.v[2], v.v[3]);
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) last_flag = atomicAdd(a.ws_count + slot, 1u) == (uint32_t)(a.splitk - 1);
-    __syncthreads();
-    if (!last_flag) return;
-    __threadfence();
-    if (kl == 0) {
-      Vec<4> s = splat4(0.0f);
-      for (int sp = 0; sp < a.splitk; ++sp) {
-        float4 p;
-        if (sp == split) p = make_float4(v.v[0], v.v[1], v.v[2], v.v[3]);
-        else p = *reinterpret_cast<const float4 *>(a.ws_partial + ((int64_t)sp * a.batch * n_blocks + slot) * kCols + cq * 4);
-        s.v[0] += p.x, s.v[1] += p.y, s.v[2] += p.z, s.v[3] += p.w;
-      }
-      v = s;
-    }
-    if (threadIdx.x == 0) atomicExch(a.ws_count + slot, 0u);
+    // dense partial row [split][batch][N]; splitk_reduce_kernel finishes it
+    float *dst = a.ws_partial + ((int64_t)split * a.batch + b) * a.N + n;
+    for (int i = 0; i < 4 && n + i < a.N; ++i) dst[i] = v.v[i];
+    return;
   }
-  if (kl == 0 && n < a.N) run_epilogue(a, b, 0, n, min(4, a.N - n), v);
+  run_epilogue(a, b, 0, n, min(4, a.N - n), v);
 }
 
 class GemvOp final : public Op {
  public:
   GemmArgs args{};
   dim3 grid;
-  size_t n_counters = 0, n_partials = 0;
+  size_t n_partials = 0;
   bool b_vec_layout = false;
   uint32_t e_vec_candidates = 0;
 
@@ -117,13 +110,13 @@ class GemvOp final : public Op {
         a.e_vec_mask |= 1u << j;
     }
     a.ws_partial = partials;
-    a.ws_count = counters;
     if (a.N == 0 || a.batch == 0) return hipSuccess;
-    if (a.splitk > 1 && (!partials || !counters)) return hipErrorInvalidValue;
+    if (a.splitk > 1 && !partials) return hipErrorInvalidValue;
     hipLaunchKernelGGL(gemv_kernel, grid, dim3(256), 0, stream, a);
-    return hipGetLastError();
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess || a.splitk == 1) return e;
+    return launch_splitk_reduce(a, current_device().cus, stream);
   }
-  size_t counter_count() const override { return n_counters; }
   size_t partial_floats() const override { return n_partials; }
 };
 
@@ -164,8 +157,7 @@ std::unique_ptr<Op> make_gemv(const kh_launch &L, std::string &err, bool &unsupp
   a.splitk = splitk;
   op->grid = dim3((unsigned)n_blocks, (unsigned)std::max<int64_t>(batch, 1), (unsigned)splitk);
   if (splitk > 1) {
-    op->n_partials = (size_t)splitk * batch * n_blocks * kCols;
-    op->n_counters = (size_t)batch * n_blocks;
+    op->n_partials = (size_t)splitk * batch * N;
   }
   return op;
 }

@@ -44,6 +44,12 @@ TILES = {
     9: (32, 32, 32, 2, 2, 1, 16),
     10: (16, 64, 32, 1, 4, 1, 16),
     11: (64, 32, 32, 2, 2, 1, 16),
+    12: (128, 128, 32, 4, 2, 1, 32),
+    13: (128, 192, 32, 4, 2, 1, 32),
+    14: (256, 128, 32, 4, 2, 1, 32),
+    15: (64, 128, 64, 2, 2, 1, 32),
+    16: (128, 64, 64, 2, 2, 1, 32),
+    17: (64, 64, 64, 2, 2, 1, 32),
 }
 DEFAULT_CUS = 256
 

@@ -680,7 +680,10 @@ class _Lowerer:
         if best is None:
             raise NotImplementedError("HIP backend: matmul epilogue needs more than 8 registers")
         _encode(best[0], best[1], d, ref_offset=2)
-        cfg = dict(self.matmul_config(self.g, k)) if not gemv else {"tile": 0, "splitk": 0}
+        cfg = dict(self.matmul_config(self.g, k))
+        if gemv:
+            cfg = {"tile": 0, "splitk": int(cfg.get("gemv_splitk", 0)), "precision": cfg.get("precision",
+                                                                                             self.precision)}
         d.cfg[1] = int(cfg.get("tile", 0))
         d.cfg[2] = int(cfg.get("splitk", 1))
         d.cfg[3] = {"fp32": kl.PREC_FP32, "bf16": kl.PREC_BF16, "bf16x3": kl.PREC_BF16X3}[

@@ -206,7 +206,7 @@ def test_split_k_is_deterministic():
                                rtol=RTOL, atol=ATOL * 10)
 
 
-@pytest.mark.parametrize("tile", range(12))
+@pytest.mark.parametrize("tile", range(18))
 def test_every_gemm_tile_configuration(tile):
     # ragged sizes (no dimension a multiple of any tile), bias + residual epilogue
     M, N, K = 77, 133, 61
