@@ -170,8 +170,10 @@ int kh_gemm_config(int id, int32_t *out8);
 
 /* plans: replace generate() + GPUExecutable (codegen.py:601-614, runtime.py:135-217) */
 int kh_plan_create(const kh_launch *launches, int n_launches, kh_plan **out);
-/* Workspace bytes the plan needs (split-K partials + tile counters); the caller
- * allocates it zero-filled and passes it to kh_plan_bind. */
+/* Workspace bytes the plan needs (dense split-K partials, reused by every
+ * launch in turn); the caller allocates it and passes it to kh_plan_bind. Its
+ * contents need no initialisation: each split-K launch writes all the partials
+ * it reads back. */
 int kh_plan_workspace_bytes(const kh_plan *plan, size_t *bytes);
 int kh_plan_bind(kh_plan *plan, void *const *consts, int n_consts, void *arena, void *workspace,
                  size_t workspace_bytes);
