@@ -62,8 +62,13 @@ enum {
   KH_FAM_ROW = 2,  /* innermost-dim reductions + elementwise (LN, softmax...) */
   KH_FAM_GEMM = 3, /* [batched] matmul + epilogue tape, MFMA                  */
   KH_FAM_GEMV = 4, /* M = 1 matmul + epilogue tape                            */
-  KH_FAM_RED = 5   /* reduction over non-innermost dims                       */
+  KH_FAM_RED = 5,  /* reduction over non-innermost dims                       */
+  KH_FAM_ATTN = 6  /* fused scores -> softmax -> x V (the lowering's pattern)  */
 };
+
+/* attention family: how the scores are scaled and masked before the softmax */
+enum { KH_ATTN_MASK_NONE = 0, KH_ATTN_MASK_CAUSAL = 1, KH_ATTN_MASK_ADD = 2 };
+enum { KH_ATTN_SCALE_NONE = 0, KH_ATTN_SCALE_MUL = 1, KH_ATTN_SCALE_DIV = 2 };
 
 /* row-family variants chosen by the host pattern matcher */
 enum { KH_ROW_GENERIC = 0, KH_ROW_LAYERNORM = 1, KH_ROW_SOFTMAX = 2 };
@@ -132,6 +137,13 @@ typedef struct kh_pass {
  *   RED  shape = input shape; refs[0] = input, refs[1] = output, both with
  *        strides over the input shape (the output's reduced dims stride 0);
  *        cfg[0] = bitmask of reduced dims, cfg[1] = 1 for max else sum.
+ *   ATTN gemm = {batch, Tq, Tk, head dim (32 or 64)}. refs[0] = Q over
+ *        (b, query, d), refs[1] = K over (b, key, d), refs[2] = V over
+ *        (b, key, d), refs[3] = output over (b, query, d): unit d stride,
+ *        16-byte aligned rows. s = q.k, then (cfg[1]) s * fparams[0] or
+ *        s / fparams[0], then (cfg[0]) CAUSAL: -inf where key > query, or
+ *        ADD: s + refs[4] (strides over (b, query, key)); out = softmax(s) V.
+ *        cfg[2] = waves per workgroup splitting the keys (0: library picks).
  * cfg[] holds the family configuration (GEMM: tile id, split-K, precision).
  */
 typedef struct kh_launch {

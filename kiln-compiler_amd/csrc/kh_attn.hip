@@ -1,0 +1,331 @@
+// kh_attn.hip - the fused attention family: for every batch/head b and query
+// row i,
+//     s[j]  = (q[b,i,:] . k[b,j,:]) (* or / scale) (+ mask[b,i,j])
+//     o[b,i,:] = sum_j softmax(s)[j] * v[b,j,:]
+// in one kernel, with the scores never leaving the chip.
+//
+// This is the kernel the reference lists as its missing piece (README.md:185):
+// its backend runs the same computation as five launches (a K^T copy, the
+// scores matmul with scale and mask epilogue, a softmax row kernel, the
+// probabilities x V matmul and a head-merging copy; kiln/gpu/codegen.py
+// 484-530 and 312-430), moving the [B, Tq, Tk] scores through HBM three times.
+// The lowering recognises that five-kernel pattern and emits this family
+// instead; results agree with the unfused path within fp32 rounding (the
+// softmax is evaluated online, FlashAttention-2 style, so the exponentials are
+// taken against a running maximum and rescaled).
+//
+// gfx950 design (fp32 operands on v_mfma_f32_32x32x2_f32, wave64):
+//   * a workgroup owns 32 query rows of one head; its NW waves split the key
+//     blocks (32 keys each) round-robin and merge their partial results
+//     through LDS at the end, so short sequences still put NW waves per
+//     query block on the GPU;
+//   * the scores are computed transposed, S^T = K Q^T: an accumulator column
+//     is one query (lane % 32) and its 16 registers are 16 keys, so the
+//     softmax max/sum over keys is a per-lane loop plus one exchange with
+//     lane ^ 32. Each lane keeps its query's Q half-row (DH/2 floats) in
+//     registers for the whole kernel and reads K rows with 128-bit loads;
+//     the head dimension is split between the two lane halves (a dot product
+//     is order-free);
+//   * O^T += V^T P^T consumes the probabilities straight from the score
+//     registers: MFMA step r takes, from each lane half, the key held in
+//     accumulator register r, so the V^T operand is read with the same key
+//     permutation and P never moves through LDS or across lanes;
+//   * causal masks (the frozen upper-triangular -inf constant) are applied
+//     from indices: key blocks wholly above the diagonal are skipped and only
+//     the diagonal block is compared. Other additive masks are read from
+//     memory;
+//   * workgroups are issued longest-first (causal rows near the end of the
+//     sequence have the most key blocks).
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+
+#include "kh_common.hpp"
+#include "kh_internal.hpp"
+
+namespace kh {
+namespace {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kQB = 32;  // queries per workgroup
+constexpr int kKB = 32;  // keys per block
+
+struct AttnArgs {
+  const float *q, *k, *v;
+  float *o;
+  const float *mask;
+  int64_t q_b, q_t, k_b, k_t, v_b, v_t, o_b, o_t, m_b, m_q, m_k;
+  int32_t batch, tq, tk, n_qblocks;
+  int32_t mask_mode, scale_mode;
+  float scale;
+};
+
+template <int DH, int NW>
+__global__ __launch_bounds__(64 * NW) void attn_kernel(const AttnArgs a) {
+  constexpr int NT = DH / 32;  // 32-wide tiles of the head dimension in O^T
+  constexpr int QS = DH / 2;   // head-dim elements per lane half (= MFMA steps of S^T)
+  __shared__ float o_part[NW][kQB][DH + 4];
+  __shared__ float m_part[NW][kQB], l_part[NW][kQB];
+
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int col = lane & 31, half = lane >> 5;
+  const int b = blockIdx.x % a.batch;
+  const int qb = a.n_qblocks - 1 - (int)(blockIdx.x / a.batch);
+  const int q0 = qb * kQB;
+  const int qi = q0 + col;
+  const bool q_ok = qi < a.tq;
+
+  // this lane's Q half-row, kept for the whole kernel
+  float qf[QS];
+  {
+    const float *qp = a.q + b * a.q_b + (int64_t)min(qi, a.tq - 1) * a.q_t + half * QS;
+#pragma unroll
+    for (int j = 0; j < QS / 4; ++j) {
+      float4 t = *reinterpret_cast<const float4 *>(qp + 4 * j);
+      if (!q_ok) t = make_float4(0.f, 0.f, 0.f, 0.f);
+      qf[4 * j] = t.x, qf[4 * j + 1] = t.y, qf[4 * j + 2] = t.z, qf[4 * j + 3] = t.w;
+    }
+  }
+
+  int kend = a.tk;
+  if (a.mask_mode == KH_ATTN_MASK_CAUSAL) kend = min(a.tk, q0 + kQB);
+  const int nkb = (kend + kKB - 1) / kKB;
+
+  const float *kbase = a.k + b * a.k_b + half * QS;
+  const float *vbase = a.v + b * a.v_b + col;
+  auto load_k = [&](int kb, float4 (&kf)[QS / 4]) {
+    const int key = min(kb * kKB + col, a.tk - 1);
+    const float *kp = kbase + (int64_t)key * a.k_t;
+#pragma unroll
+    for (int j = 0; j < QS / 4; ++j) kf[j] = *reinterpret_cast<const float4 *>(kp + 4 * j);
+  };
+  // V^T operand of MFMA step r, tile t: V[key(r)][t*32 + col], key(r) the
+  // key held in accumulator register r of this lane half.
+  auto load_v = [&](int kb, float (&vf)[16 * NT]) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int key = min(kb * kKB + (r >> 2) * 8 + half * 4 + (r & 3), a.tk - 1);
+      const float *vp = vbase + (int64_t)key * a.v_t;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) vf[r * NT + t] = vp[t * 32];
+    }
+  };
+
+  f32x16 oacc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) oacc[t][r] = 0.0f;
+  float m_run = -INFINITY, l_run = 0.0f;
+
+  float4 kf[QS / 4], kn[QS / 4];
+  float vf[16 * NT], vn[16 * NT];
+  int kb = w;
+  if (kb < nkb) {
+    load_k(kb, kf);
+    load_v(kb, vf);
+  }
+  for (; kb < nkb; kb += NW) {
+    const int next = kb + NW;
+    if (next < nkb) {
+      load_k(next, kn);
+      load_v(next, vn);
+    }
+    // S^T block: 32 keys x 32 queries
+    f32x16 s;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[r] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < QS / 4; ++j) {
+      s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[j].x, qf[4 * j + 0], s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[j].y, qf[4 * j + 1], s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[j].z, qf[4 * j + 2], s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[j].w, qf[4 * j + 3], s, 0, 0, 0);
+    }
+    const int key0 = kb * kKB;
+    const bool edge = key0 + kKB > a.tk || (a.mask_mode == KH_ATTN_MASK_CAUSAL && key0 + kKB - 1 > q0);
+    float p[16];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int key = key0 + (r >> 2) * 8 + half * 4 + (r & 3);
+      float x = s[r];
+      if (a.scale_mode == KH_ATTN_SCALE_MUL) x = x * a.scale;
+      else if (a.scale_mode == KH_ATTN_SCALE_DIV) x = x / a.scale;
+      if (a.mask_mode == KH_ATTN_MASK_ADD) {
+        const int kc = min(key, a.tk - 1), qc = min(qi, a.tq - 1);
+        x = x + a.mask[b * a.m_b + (int64_t)qc * a.m_q + (int64_t)kc * a.m_k];
+      }
+      if (edge && (key >= a.tk || (a.mask_mode == KH_ATTN_MASK_CAUSAL && key > qi))) x = -INFINITY;
+      p[r] = x;
+      mx = fmaxf(mx, x);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(m_run, mx);
+    // a row with no finite score so far keeps m = -inf; exponentials are then
+    // taken against 0 so they stay 0 instead of becoming NaN
+    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+    const float alpha = expf(m_run - m_use);
+    float sum = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      p[r] = expf(p[r] - m_use);
+      sum += p[r];
+    }
+    sum += __shfl_xor(sum, 32);
+    l_run = l_run * alpha + sum;
+    m_run = m_new;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) oacc[t] *= alpha;
+    // O^T += V^T P^T, key order permuted to match the score registers
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+#pragma unroll
+      for (int t = 0; t < NT; ++t) oacc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[r * NT + t], p[r], oacc[t], 0, 0, 0);
+    if (next < nkb) {
+#pragma unroll
+      for (int j = 0; j < QS / 4; ++j) kf[j] = kn[j];
+#pragma unroll
+      for (int j = 0; j < 16 * NT; ++j) vf[j] = vn[j];
+    }
+  }
+
+  // merge the NW key-split partials: o = sum_w e^(m_w - M) o_w / sum_w e^(m_w - M) l_w
+  if (half == 0) m_part[w][col] = m_run, l_part[w][col] = l_run;
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o_part[w][col][t * 32 + (r >> 2) * 8 + half * 4 + (r & 3)] = oacc[t][r];
+  __syncthreads();
+  constexpr int kChunks = kQB * DH / 4;
+  for (int c = threadIdx.x; c < kChunks; c += 64 * NW) {
+    const int qr = c / (DH / 4), d = (c % (DH / 4)) * 4;
+    if (q0 + qr >= a.tq) continue;
+    float mm = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < NW; ++u) mm = fmaxf(mm, m_part[u][qr]);
+    const float mu = mm == -INFINITY ? 0.0f : mm;
+    float l = 0.0f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int u = 0; u < NW; ++u) {
+      const float e = expf(m_part[u][qr] - mu);
+      l += l_part[u][qr] * e;
+      acc.x += o_part[u][qr][d] * e, acc.y += o_part[u][qr][d + 1] * e;
+      acc.z += o_part[u][qr][d + 2] * e, acc.w += o_part[u][qr][d + 3] * e;
+    }
+    acc.x /= l, acc.y /= l, acc.z /= l, acc.w /= l;
+    *reinterpret_cast<float4 *>(a.o + b * a.o_b + (int64_t)(q0 + qr) * a.o_t + d) = acc;
+  }
+}
+
+class AttnOp final : public Op {
+ public:
+  AttnArgs args{};
+  int dh = 64, nw = 4;
+  dim3 grid;
+
+  hipError_t launch(float *const *ptrs, uint32_t *, float *, hipStream_t stream) override {
+    AttnArgs a = args;
+    a.q = ptrs[0], a.k = ptrs[1], a.v = ptrs[2], a.o = ptrs[3];
+    a.mask = a.mask_mode == KH_ATTN_MASK_ADD ? ptrs[4] : nullptr;
+    for (int j = 0; j < 4; ++j)
+      if (reinterpret_cast<uintptr_t>(ptrs[j]) & 15) return hipErrorInvalidValue;
+    if (a.batch == 0 || a.tq == 0) return hipSuccess;
+#define KH_ATTN_LAUNCH(D, W)                                                                         \
+  if (dh == D && nw == W) {                                                                          \
+    hipLaunchKernelGGL((attn_kernel<D, W>), grid, dim3(64 * W), 0, stream, a);                      \
+    return hipGetLastError();                                                                        \
+  }
+    KH_ATTN_LAUNCH(64, 4)
+    KH_ATTN_LAUNCH(64, 2)
+    KH_ATTN_LAUNCH(64, 1)
+    KH_ATTN_LAUNCH(32, 4)
+    KH_ATTN_LAUNCH(32, 2)
+    KH_ATTN_LAUNCH(32, 1)
+#undef KH_ATTN_LAUNCH
+    return hipErrorInvalidValue;
+  }
+};
+
+bool aligned4(int64_t v) { return v % 4 == 0; }
+
+}  // namespace
+
+std::unique_ptr<Op> make_attn(const kh_launch &L, std::string &err, bool &unsupported) {
+  unsupported = false;
+  const int mask_mode = L.cfg[0], scale_mode = L.cfg[1];
+  if (mask_mode < KH_ATTN_MASK_NONE || mask_mode > KH_ATTN_MASK_ADD || scale_mode < KH_ATTN_SCALE_NONE ||
+      scale_mode > KH_ATTN_SCALE_DIV) {
+    err = "attention: bad mask or scale mode";
+    return nullptr;
+  }
+  const int want_refs = mask_mode == KH_ATTN_MASK_ADD ? 5 : 4;
+  if (L.n_refs != want_refs) {
+    err = "attention: expected q, k, v, out" + std::string(want_refs == 5 ? ", mask" : "") + " operands";
+    return nullptr;
+  }
+  const int64_t batch = L.gemm[0], tq = L.gemm[1], tk = L.gemm[2], dh = L.gemm[3];
+  if (batch < 0 || tq < 0 || tk < 0 || batch >= (1 << 20) || tq >= (1 << 24) || tk >= (1 << 24)) {
+    unsupported = true;
+    err = "attention: sizes out of range";
+    return nullptr;
+  }
+  if (tq > 0 && tk == 0) {
+    err = "attention: no keys";
+    return nullptr;
+  }
+  if (dh != 32 && dh != 64) {
+    unsupported = true;
+    err = "attention: head dimension must be 32 or 64";
+    return nullptr;
+  }
+  for (int j = 0; j < 4; ++j) {
+    const kh_ref &r = L.refs[j];
+    if (r.strides[2] != 1 || !aligned4(r.offset) || !aligned4(r.strides[0]) || !aligned4(r.strides[1])) {
+      unsupported = true;
+      err = "attention: q, k, v and out need unit head-dim stride and 16-byte aligned rows";
+      return nullptr;
+    }
+  }
+  if (scale_mode == KH_ATTN_SCALE_DIV && L.fparams[0] == 0.0f) {
+    err = "attention: division by a zero scale";
+    return nullptr;
+  }
+  auto op = std::make_unique<AttnOp>();
+  AttnArgs &a = op->args;
+  a.batch = (int)batch, a.tq = (int)tq, a.tk = (int)tk;
+  a.q_b = L.refs[0].strides[0], a.q_t = L.refs[0].strides[1];
+  a.k_b = L.refs[1].strides[0], a.k_t = L.refs[1].strides[1];
+  a.v_b = L.refs[2].strides[0], a.v_t = L.refs[2].strides[1];
+  a.o_b = L.refs[3].strides[0], a.o_t = L.refs[3].strides[1];
+  if (mask_mode == KH_ATTN_MASK_ADD)
+    a.m_b = L.refs[4].strides[0], a.m_q = L.refs[4].strides[1], a.m_k = L.refs[4].strides[2];
+  a.mask_mode = mask_mode, a.scale_mode = scale_mode, a.scale = L.fparams[0];
+  a.n_qblocks = (int)((tq + kQB - 1) / kQB);
+  op->dh = (int)dh;
+  // key-split waves per workgroup: enough workgroups x waves to cover the GPU
+  int nw = L.cfg[2];
+  if (nw <= 0) {
+    const int64_t groups = batch * a.n_qblocks;
+    const int64_t kblocks = (tk + kKB - 1) / kKB;
+    nw = groups >= 4ll * current_device().cus ? 1 : (groups >= 2ll * current_device().cus ? 2 : 4);
+    if (kblocks < nw) nw = kblocks >= 2 ? 2 : 1;
+  }
+  if (nw != 1 && nw != 2 && nw != 4) {
+    err = "attention: waves per workgroup must be 1, 2 or 4";
+    return nullptr;
+  }
+  op->nw = nw;
+  const int64_t n_groups = batch * (int64_t)a.n_qblocks;
+  if (n_groups >= (1ll << 31)) {
+    unsupported = true;
+    err = "attention: grid too large";
+    return nullptr;
+  }
+  op->grid = dim3((unsigned)std::max<int64_t>(1, n_groups));
+  return op;
+}
+
+}  // namespace kh

@@ -40,6 +40,7 @@ std::unique_ptr<Op> make_row(const kh_launch &L, std::string &err, bool &unsuppo
 std::unique_ptr<Op> make_gemm(const kh_launch &L, std::string &err, bool &unsupported);
 std::unique_ptr<Op> make_gemv(const kh_launch &L, std::string &err, bool &unsupported);
 std::unique_ptr<Op> make_red(const kh_launch &L, std::string &err, bool &unsupported);
+std::unique_ptr<Op> make_attn(const kh_launch &L, std::string &err, bool &unsupported);
 
 int gemm_config_count();
 bool gemm_config(int id, int32_t out8[8]);

@@ -259,6 +259,7 @@ int kh_plan_create(const kh_launch *launches, int n_launches, kh_plan **out) {
         case KH_FAM_GEMM: op = kh::make_gemm(L, err, unsupported); break;
         case KH_FAM_GEMV: op = kh::make_gemv(L, err, unsupported); break;
         case KH_FAM_RED: op = kh::make_red(L, err, unsupported); break;
+        case KH_FAM_ATTN: op = kh::make_attn(L, err, unsupported); break;
         default: err = "unknown kernel family " + std::to_string(L.family);
       }
     }

@@ -37,6 +37,7 @@ class Options:
     gpu_matmul_config: object = None  # advanced: fn(graph, kernel) -> {"tile": id, "splitk": s}
     matmul_precision: str = "fp32"    # GPU GEMMs: "fp32" | "bf16" (bf16 inputs, fp32 accumulate) | "bf16x3"
     debug: bool = False          # GPU: NaN-poison the arena and synchronise after every plan run
+    fused_attention: bool = True # GPU: scores -> softmax -> (x V) as one kernel (needs fusion)
 
     @classmethod
     def none(cls, **kw):
@@ -119,7 +120,12 @@ def _compile_graph_gpu(graph: Graph, options: Options):
     from kiln.passes.manager import PassManager
 
     start = time.perf_counter()
-    pm = PassManager(build_passes(options), print_after_all=options.print_ir)
+    passes = build_passes(options)
+    if options.fusion and options.fused_attention:
+        from kiln.hip.attention import FuseAttention
+
+        passes.insert(len(passes) - 1, FuseAttention())   # after buffer-assign, before memory-plan
+    pm = PassManager(passes, print_after_all=options.print_ir)
     pm.run(graph)
     precision = _precision(options)
     tuner = None

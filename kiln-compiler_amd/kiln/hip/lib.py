@@ -22,7 +22,9 @@ MAX_PASSES = 8
 
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP, ERR_NO_DEVICE, ERR_CAPACITY = range(6)
 BASE_INPUT, BASE_OUTPUT, BASE_CONST, BASE_ARENA, BASE_WORKSPACE = range(5)
-FAM_EW, FAM_ROW, FAM_GEMM, FAM_GEMV, FAM_RED = 1, 2, 3, 4, 5
+FAM_EW, FAM_ROW, FAM_GEMM, FAM_GEMV, FAM_RED, FAM_ATTN = 1, 2, 3, 4, 5, 6
+ATTN_MASK_NONE, ATTN_MASK_CAUSAL, ATTN_MASK_ADD = 0, 1, 2
+ATTN_SCALE_NONE, ATTN_SCALE_MUL, ATTN_SCALE_DIV = 0, 1, 2
 ROW_GENERIC, ROW_LAYERNORM, ROW_SOFTMAX = 0, 1, 2
 PREC_FP32, PREC_BF16, PREC_BF16X3 = 0, 1, 2
 
@@ -31,7 +33,8 @@ OPCODES = ["mov", "add", "sub", "mul", "div", "max", "min", "neg", "relu", "exp"
 OP = {name: i for i, name in enumerate(OPCODES)}
 SRC_IMM = 0xFF
 
-FAMILY_NAMES = {FAM_EW: "elementwise", FAM_ROW: "row", FAM_GEMM: "gemm", FAM_GEMV: "gemv", FAM_RED: "reduce"}
+FAMILY_NAMES = {FAM_EW: "elementwise", FAM_ROW: "row", FAM_GEMM: "gemm", FAM_GEMV: "gemv", FAM_RED: "reduce",
+                FAM_ATTN: "attention"}
 
 
 class Ref(ctypes.Structure):

@@ -12,6 +12,8 @@ descriptors naming a hand-written HIP kernel family:
                              fast path
   reduction, other dims   -> RED
   elementwise / copy      -> EW, one launch per distinct output shape
+  attention (merged by kiln.hip.attention.FuseAttention)
+                          -> ATTN: scores, softmax and (x V) in one launch
 
 Operands are (buffer slot, element offset, element strides over the launch's
 iteration space): views never cost a copy, broadcasts are stride 0 - the
@@ -699,15 +701,57 @@ class _Lowerer:
             summary += f" epilogue: {epi}"
         self.add(d, k, summary, flops=flops, nbytes=nbytes)
 
+    # attention --------------------------------------------------------------------------------
+
+    def lower_attention(self, k: Kernel):
+        from kiln.hip.attention import causal_or_none, match_kernel, operand_strides
+
+        m = match_kernel(self.g, k)
+        strides = operand_strides(m, self.layouts) if m is not None else None
+        if strides is None:
+            raise NotImplementedError(f"HIP backend: attention kernel {k.name} does not have the fused form")
+        batch, tq, dh = m.q.shape
+        tk = m.v.shape[1]
+        d = self.new_desc(kl.FAM_ATTN, "attn", k, (batch, tq, tk))
+        d.gemm[0], d.gemm[1], d.gemm[2], d.gemm[3] = batch, tq, tk, dh
+        for j, (v, (_, st)) in enumerate(zip((m.q, m.k, m.v, m.result), strides)):
+            r = kl.Ref()
+            r.base, r.index = self.slot_of(self.layouts[v].base)
+            r.offset = self.element_offset(v)
+            for i in range(3):
+                r.strides[i] = st[i]
+            d.refs[j] = r
+        d.n_refs = 4
+        mode = kl.ATTN_MASK_NONE
+        if m.mask is not None:
+            mode = causal_or_none(self.g, m.mask, batch, tq, tk)
+            if mode is None:
+                mode = kl.ATTN_MASK_ADD
+                d.refs[4] = self.ref(m.mask, (batch, tq, tk))
+                d.n_refs = 5
+        d.cfg[0], d.cfg[1] = mode, m.scale_mode
+        d.fparams[0] = m.scale
+        causal = mode == kl.ATTN_MASK_CAUSAL
+        pairs = sum(min(tk, i + 1) for i in range(tq)) if causal else tq * tk
+        flops = 4 * batch * pairs * dh
+        nbytes = 4 * batch * dh * (2 * tq + 2 * tk) + (4 * batch * tq * tk if mode == kl.ATTN_MASK_ADD else 0)
+        what = {kl.ATTN_MASK_NONE: "no mask", kl.ATTN_MASK_CAUSAL: "causal", kl.ATTN_MASK_ADD: "additive mask"}[mode]
+        scale = {kl.ATTN_SCALE_NONE: "", kl.ATTN_SCALE_MUL: f", scores * {m.scale:g}",
+                 kl.ATTN_SCALE_DIV: f", scores / {m.scale:g}"}[m.scale_mode]
+        self.add(d, k, f"{batch} heads x {tq} queries x {tk} keys, head dim {dh}, {what}{scale}",
+                 flops=flops, nbytes=nbytes)
+
     # driver --------------------------------------------------------------------------------------
 
     def run(self) -> Program:
         for k in self.g.kernels:
             for n in k.nodes:
-                if ops.kind(n.op) not in ("elementwise", "reduction", "matmul"):
+                if ops.kind(n.op) not in ("elementwise", "reduction", "matmul") and k.kind != "attention":
                     raise NotImplementedError(f"GPU backend: unexpected op '{n.op}' in a kernel")
         for k in self.g.kernels:
-            if k.kind == "matmul":
+            if k.kind == "attention":
+                self.lower_attention(k)
+            elif k.kind == "matmul":
                 self.lower_matmul(k)
             elif k.kind == "reduction":
                 self.lower_reduction(k)

@@ -1,0 +1,144 @@
+"""Parity of the fused attention family (kiln.hip.attention + kh_attn.hip).
+
+The fused kernel must give what the five-kernel path gives: every case is
+compared with the float64 oracle (interpreter over the imported graph, or the
+C oracle for the GPT-2 block) and with eager PyTorch fp32 at the fp32
+tolerance (rtol 1e-4, atol 1e-5), and checks that the fused launch was used.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import kiln
+import oracle
+from kiln.hip import lib as kl
+from models.transformer import Block, gpt2_init_
+from oracle import interp
+from test_gpu import ATOL, RTOL, as_tuple, imported
+
+pytestmark = pytest.mark.gpu
+
+
+def n_attention(compiled):
+    return sum(1 for l in compiled._exe.program.launches if l.family == kl.FAM_ATTN)
+
+
+def compare(fn, *xs, fused=1, rtol=RTOL, atol=ATOL, **flags):
+    compiled = kiln.compile(fn, xs, device="cuda", **flags)
+    assert n_attention(compiled) == fused, compiled._exe.program.source
+    ref = interp.run(imported(fn, xs), *[x.numpy() for x in xs])
+    with torch.no_grad():
+        eager = as_tuple(fn(*xs))
+    got = as_tuple(compiled(*xs))
+    for a, r, e in zip(got, ref, eager):
+        np.testing.assert_allclose(a.cpu().numpy().astype(np.float64), r, rtol=rtol, atol=atol)
+        torch.testing.assert_close(a.cpu(), e, rtol=rtol, atol=atol, equal_nan=True)
+    return compiled
+
+
+class Attn(torch.nn.Module):
+    """softmax(q k^T scale + mask) v over [B, T, D] inputs, heads merged into [Tq, B*D]."""
+
+    def __init__(self, mask=None, scale=0.125, divide=False, merge=True):
+        super().__init__()
+        self.scale, self.divide, self.merge = scale, divide, merge
+        if mask is not None:
+            self.register_buffer("mask", mask)
+        else:
+            self.mask = None
+
+    def forward(self, q, k, v):
+        s = q @ k.transpose(-2, -1)
+        s = s / self.scale if self.divide else s * self.scale
+        if self.mask is not None:
+            s = s + self.mask
+        o = F.softmax(s, dim=-1) @ v
+        if self.merge:
+            o = o.transpose(0, 1).contiguous().view(q.shape[1], -1)
+        return o
+
+
+def qkv(b, tq, tk, d, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(b, tq, d, generator=g), torch.randn(b, tk, d, generator=g),
+            torch.randn(b, tk, d, generator=g))
+
+
+@pytest.mark.parametrize("T", [1, 5, 32, 77, 128, 200])
+@pytest.mark.parametrize("d", [32, 64])
+def test_causal(T, d):
+    mask = torch.full((T, T), float("-inf")).triu(1)
+    c = compare(Attn(mask, scale=1 / math.sqrt(d)), *qkv(3, T, T, d, seed=T))
+    assert "causal" in c._exe.program.source
+
+
+@pytest.mark.parametrize("tq, tk", [(1, 40), (50, 90), (64, 64), (33, 7)])
+def test_no_mask_cross_attention(tq, tk):
+    compare(Attn(None, scale=0.125), *qkv(2, tq, tk, 64, seed=tq + tk))
+
+
+def test_divided_scale_and_no_head_merge():
+    c = compare(Attn(None, scale=8.0, divide=True, merge=False), *qkv(4, 70, 70, 64, seed=3))
+    assert "scores / 8" in c._exe.program.source
+
+
+def test_additive_mask():
+    g = torch.Generator().manual_seed(7)
+    mask = torch.randn(45, 60, generator=g)
+    mask[torch.rand(45, 60, generator=g) < 0.3] = float("-inf")
+    mask[:, 0] = 0.0                      # every row keeps a finite score
+    c = compare(Attn(mask), *qkv(3, 45, 60, 32, seed=1))
+    assert "additive mask" in c._exe.program.source
+
+
+def test_fully_masked_rows_are_nan_as_in_eager():
+    mask = torch.zeros(20, 20)
+    mask[3, :] = float("-inf")
+    mask[11, :] = float("-inf")
+    q, k, v = qkv(2, 20, 20, 64, seed=5)
+    fn = Attn(mask, merge=False)
+    compiled = kiln.compile(fn, (q, k, v), device="cuda")
+    assert n_attention(compiled) == 1
+    with torch.no_grad():
+        eager = fn(q, k, v)
+    got = compiled(q, k, v).cpu()
+    assert torch.isnan(eager[:, [3, 11]]).all()
+    torch.testing.assert_close(got, eager, rtol=RTOL, atol=ATOL, equal_nan=True)
+
+
+def test_unsupported_head_dim_is_not_fused():
+    compare(Attn(None, scale=0.25), *qkv(2, 24, 24, 16, seed=2), fused=0)
+
+
+def test_fusion_can_be_turned_off():
+    compare(Attn(None), *qkv(2, 40, 40, 64, seed=4), fused=0, fused_attention=False)
+
+
+@pytest.mark.parametrize("T", [1, 77, 128, 512])
+def test_block_uses_one_attention_launch(T):
+    model = gpt2_init_(Block(768, 12, T), seed=T).eval()
+    x = torch.randn(T, 768, generator=torch.Generator().manual_seed(T + 1))
+    c = kiln.compile(model, (x,), device="cuda")
+    assert c.report.lowering["launches"] == 7 and n_attention(c) == 1
+    # the scores never get arena memory: the peak is the MLP's (768 + 768 + 3072) T floats
+    assert c.report.arena_bytes == 4 * 4608 * T
+    params = {k: v.numpy() for k, v in model.state_dict().items()}
+    want = oracle.block(x.numpy(), params, 12)
+    got = c(x).cpu()
+    np.testing.assert_allclose(got.numpy().astype(np.float64), want, rtol=RTOL, atol=ATOL)
+    with torch.no_grad():
+        torch.testing.assert_close(got, model(x), rtol=RTOL, atol=ATOL)
+
+
+def test_fused_matches_unfused_at_1024():
+    T = 1024
+    model = gpt2_init_(Block(768, 12, T), seed=9).eval().cuda()
+    x = torch.randn(T, 768, device="cuda")
+    fused = kiln.compile(model, (x,), device="cuda")
+    plain = kiln.compile(model, (x,), device="cuda", fused_attention=False)
+    assert n_attention(fused) == 1 and n_attention(plain) == 0
+    torch.testing.assert_close(fused(x), plain(x), rtol=RTOL, atol=ATOL)

@@ -23,11 +23,16 @@ from models.transformer import Block, Stack
 HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "kiln_hip.h")
 
 
-def lowered(fn, *xs, **opts):
+def lowered(fn, *xs, fuse_attention=False, **opts):
     module = fn if isinstance(fn, torch.nn.Module) else type("F", (torch.nn.Module,), {
         "forward": lambda self, *a: fn(*a)})()
     g = import_exported(torch.export.export(module.eval(), xs).run_decompositions())
-    PassManager(build_passes(Options(**opts))).run(g)
+    passes = build_passes(Options(**opts))
+    if fuse_attention:
+        from kiln.hip.attention import FuseAttention
+
+        passes.insert(len(passes) - 1, FuseAttention())
+    PassManager(passes).run(g)
     return g, lower_graph(g)
 
 
@@ -63,6 +68,77 @@ def test_block_lowers_to_the_expected_families():
     assert variants == [kl.ROW_LAYERNORM, kl.ROW_SOFTMAX, kl.ROW_LAYERNORM]
     plan = kl.Plan([l.desc for l in prog.launches])
     assert plan.n_launches == 11
+
+
+def test_block_attention_becomes_one_launch():
+    T = 256
+    g, prog = lowered(Block(768, 12, T), torch.randn(T, 768), fuse_attention=True)
+    fams = [kl.FAMILY_NAMES[l.family] for l in prog.launches]
+    assert fams == ["row", "gemm", "attention", "gemm", "row", "gemm", "gemm"]
+    a = prog.launches[2].desc
+    assert (a.cfg[0], a.cfg[1], a.fparams[0]) == (kl.ATTN_MASK_CAUSAL, kl.ATTN_SCALE_MUL, 0.125)
+    assert tuple(a.gemm) == (12, T, T, 64) and a.n_refs == 4
+    # q, k, v are column blocks of the qkv buffer [T, 2304]; the output is the
+    # head-merged [T, 768] layout the projection reads
+    strides = [tuple(a.refs[j].strides[:3]) for j in range(4)]
+    assert strides == [(64, 2304, 1)] * 3 + [(64, 768, 1)]
+    assert [a.refs[j].offset - a.refs[0].offset for j in range(3)] == [0, 768, 1536]
+    # no [12, T, T] buffer is planned: the peak is now the MLP (residual,
+    # ln2 output and fc output live together), (768 + 768 + 3072) T floats
+    assert g.attrs["arena_bytes"] == 4 * 4608 * T
+    kl.Plan([l.desc for l in prog.launches])
+
+
+class _Attn(torch.nn.Module):
+    def __init__(self, mask=None, divide=False):
+        super().__init__()
+        self.divide = divide
+        if mask is not None:
+            self.register_buffer("mask", mask)
+        else:
+            self.mask = None
+
+    def forward(self, q, k, v):
+        s = q @ k.transpose(-2, -1)
+        s = s / 8.0 if self.divide else s * 0.125
+        if self.mask is not None:
+            s = s + self.mask
+        return F.softmax(s, dim=-1) @ v
+
+
+@pytest.mark.parametrize("d, mask, divide, want", [
+    (64, None, False, (kl.ATTN_MASK_NONE, kl.ATTN_SCALE_MUL, 4)),
+    (32, torch.randn(40, 40), True, (kl.ATTN_MASK_ADD, kl.ATTN_SCALE_DIV, 5)),
+    (64, torch.full((40, 40), float("-inf")).triu(1), False, (kl.ATTN_MASK_CAUSAL, kl.ATTN_SCALE_MUL, 4)),
+    (64, torch.full((40, 40), float("-inf")).triu(2), False, (kl.ATTN_MASK_ADD, kl.ATTN_SCALE_MUL, 5)),
+])
+def test_attention_modes(d, mask, divide, want):
+    xs = [torch.randn(3, 40, d) for _ in range(3)]
+    _, prog = lowered(_Attn(mask, divide), *xs, fuse_attention=True)
+    attn = [l.desc for l in prog.launches if l.family == kl.FAM_ATTN]
+    assert len(attn) == 1
+    assert (attn[0].cfg[0], attn[0].cfg[1], attn[0].n_refs) == want
+    kl.Plan([l.desc for l in prog.launches])
+
+
+def test_attention_needs_a_supported_head_dim():
+    xs = [torch.randn(2, 24, 16) for _ in range(3)]
+    _, prog = lowered(_Attn(), *xs, fuse_attention=True)
+    assert kl.FAM_ATTN not in [l.family for l in prog.launches]
+
+
+def test_attention_descriptor_checks():
+    xs = [torch.randn(2, 24, 64) for _ in range(3)]
+    _, prog = lowered(_Attn(), *xs, fuse_attention=True)
+    d = next(l.desc for l in prog.launches if l.family == kl.FAM_ATTN)
+    bad = kl.LaunchDesc.from_buffer_copy(d)
+    bad.refs[1].strides[2] = 2
+    with pytest.raises(NotImplementedError, match="unit head-dim stride"):
+        kl.Plan([bad])
+    bad = kl.LaunchDesc.from_buffer_copy(d)
+    bad.cfg[0] = 7
+    with pytest.raises(ValueError, match="mask or scale mode"):
+        kl.Plan([bad])
 
 
 def test_decode_uses_the_gemv_family():
