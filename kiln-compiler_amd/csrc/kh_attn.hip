@@ -62,7 +62,7 @@ struct AttnArgs {
 };
 
 template <int DH, int NW>
-__global__ __launch_bounds__(64 * NW) void attn_kernel(const AttnArgs a) {
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) void attn_kernel(const AttnArgs a) {
   constexpr int NT = DH / 32;  // 32-wide tiles of the head dimension in O^T
   constexpr int QS = DH / 2;   // head-dim elements per lane half (= MFMA steps of S^T)
   __shared__ float o_part[NW][kQB][DH + 4];
@@ -92,23 +92,45 @@ __global__ __launch_bounds__(64 * NW) void attn_kernel(const AttnArgs a) {
   if (a.mask_mode == KH_ATTN_MASK_CAUSAL) kend = min(a.tk, q0 + kQB);
   const int nkb = (kend + kKB - 1) / kKB;
 
-  const float *kbase = a.k + b * a.k_b + half * QS;
-  const float *vbase = a.v + b * a.v_b + col;
+  // Scores are kept in the base-2 domain: u = (s * scale + mask) * log2(e), so
+  // each exponential is one v_exp_f32 (exp2) and softmax(s) = 2^(u - max u) / sum.
+  constexpr float kLog2e = 1.4426950408889634f;
+  const float c_scale = a.scale_mode == KH_ATTN_SCALE_MUL   ? a.scale * kLog2e
+                        : a.scale_mode == KH_ATTN_SCALE_DIV ? kLog2e / a.scale
+                                                            : kLog2e;
+
+  // 32-bit element offsets from uniform per-head bases (the host checks
+  // that every operand spans < 2^31 elements), so loads use a scalar base
+  // plus one VGPR offset.
+  const float *kb_ptr = a.k + b * a.k_b;
+  const float *vb_ptr = a.v + b * a.v_b;
+  const uint32_t k_t = (uint32_t)a.k_t, v_t = (uint32_t)a.v_t;
   auto load_k = [&](int kb, float4 (&kf)[QS / 4]) {
-    const int key = min(kb * kKB + col, a.tk - 1);
-    const float *kp = kbase + (int64_t)key * a.k_t;
+    const uint32_t key = (uint32_t)min(kb * kKB + col, a.tk - 1);
+    const uint32_t off = key * k_t + half * QS;
 #pragma unroll
-    for (int j = 0; j < QS / 4; ++j) kf[j] = *reinterpret_cast<const float4 *>(kp + 4 * j);
+    for (int j = 0; j < QS / 4; ++j) kf[j] = *reinterpret_cast<const float4 *>(kb_ptr + off + 4 * j);
   };
-  // V^T operand of MFMA step r, tile t: V[key(r)][t*32 + col], key(r) the
-  // key held in accumulator register r of this lane half.
+  // V^T operand of MFMA step r, tile t: V[key(r)][t*32 + col], key(r) the key
+  // held in accumulator register r of this lane half (rows clamped on the
+  // last, partial block only).
+  const uint32_t v_lane = (uint32_t)(half * 4) * v_t + col;
   auto load_v = [&](int kb, float (&vf)[16 * NT]) {
+    const int key0 = kb * kKB;
+    if (key0 + kKB <= a.tk) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int key = min(kb * kKB + (r >> 2) * 8 + half * 4 + (r & 3), a.tk - 1);
-      const float *vp = vbase + (int64_t)key * a.v_t;
+      for (int r = 0; r < 16; ++r) {
+        const uint32_t off = v_lane + (uint32_t)(key0 + (r >> 2) * 8 + (r & 3)) * v_t;
 #pragma unroll
-      for (int t = 0; t < NT; ++t) vf[r * NT + t] = vp[t * 32];
+        for (int t = 0; t < NT; ++t) vf[r * NT + t] = vb_ptr[off + t * 32];
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const uint32_t key = (uint32_t)min(key0 + (r >> 2) * 8 + half * 4 + (r & 3), a.tk - 1);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) vf[r * NT + t] = vb_ptr[key * v_t + col + t * 32];
+      }
     }
   };
 
@@ -119,30 +141,26 @@ __global__ __launch_bounds__(64 * NW) void attn_kernel(const AttnArgs a) {
     for (int r = 0; r < 16; ++r) oacc[t][r] = 0.0f;
   float m_run = -INFINITY, l_run = 0.0f;
 
-  float4 kf[QS / 4], kn[QS / 4];
-  float vf[16 * NT], vn[16 * NT];
-  int kb = w;
-  if (kb < nkb) {
-    load_k(kb, kf);
+  // One key block: prefetch the next block's K into `kn`, then scores from
+  // `kc`, online softmax, and O^T += V^T P^T.
+  auto step = [&](int kb, float4 (&kc)[QS / 4]) {
+    // keep the scheduler from hoisting the next step's loads into this one
+    __builtin_amdgcn_sched_barrier(0);
+    float vf[16 * NT];
     load_v(kb, vf);
-  }
-  for (; kb < nkb; kb += NW) {
-    const int next = kb + NW;
-    if (next < nkb) {
-      load_k(next, kn);
-      load_v(next, vn);
-    }
-    // S^T block: 32 keys x 32 queries
     f32x16 s;
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[r] = 0.0f;
 #pragma unroll
     for (int j = 0; j < QS / 4; ++j) {
-      s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[j].x, qf[4 * j + 0], s, 0, 0, 0);
-      s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[j].y, qf[4 * j + 1], s, 0, 0, 0);
-      s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[j].z, qf[4 * j + 2], s, 0, 0, 0);
-      s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[j].w, qf[4 * j + 3], s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_32x32x2f32(kc[j].x, qf[4 * j + 0], s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_32x32x2f32(kc[j].y, qf[4 * j + 1], s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_32x32x2f32(kc[j].z, qf[4 * j + 2], s, 0, 0, 0);
+      s = __builtin_amdgcn_mfma_f32_32x32x2f32(kc[j].w, qf[4 * j + 3], s, 0, 0, 0);
     }
+    // K of this block is consumed: fetch the next block's into the same
+    // registers, hidden behind the softmax and the V MFMAs
+    if (kb + NW < nkb) load_k(kb + NW, kc);
     const int key0 = kb * kKB;
     const bool edge = key0 + kKB > a.tk || (a.mask_mode == KH_ATTN_MASK_CAUSAL && key0 + kKB - 1 > q0);
     float p[16];
@@ -150,48 +168,50 @@ __global__ __launch_bounds__(64 * NW) void attn_kernel(const AttnArgs a) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int key = key0 + (r >> 2) * 8 + half * 4 + (r & 3);
-      float x = s[r];
-      if (a.scale_mode == KH_ATTN_SCALE_MUL) x = x * a.scale;
-      else if (a.scale_mode == KH_ATTN_SCALE_DIV) x = x / a.scale;
+      float mk = 0.0f;
       if (a.mask_mode == KH_ATTN_MASK_ADD) {
-        const int kc = min(key, a.tk - 1), qc = min(qi, a.tq - 1);
-        x = x + a.mask[b * a.m_b + (int64_t)qc * a.m_q + (int64_t)kc * a.m_k];
+        const int kc2 = min(key, a.tk - 1), qc = min(qi, a.tq - 1);
+        mk = a.mask[b * a.m_b + (int64_t)qc * a.m_q + (int64_t)kc2 * a.m_k] * kLog2e;
       }
-      if (edge && (key >= a.tk || (a.mask_mode == KH_ATTN_MASK_CAUSAL && key > qi))) x = -INFINITY;
-      p[r] = x;
-      mx = fmaxf(mx, x);
+      float u = fmaf(s[r], c_scale, mk);
+      if (edge && (key >= a.tk || (a.mask_mode == KH_ATTN_MASK_CAUSAL && key > qi))) u = -INFINITY;
+      p[r] = u;
+      mx = fmaxf(mx, u);
     }
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     const float m_new = fmaxf(m_run, mx);
     // a row with no finite score so far keeps m = -inf; exponentials are then
     // taken against 0 so they stay 0 instead of becoming NaN
     const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-    const float alpha = expf(m_run - m_use);
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
     float sum = 0.0f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      p[r] = expf(p[r] - m_use);
+      p[r] = __builtin_amdgcn_exp2f(p[r] - m_use);
       sum += p[r];
     }
     sum += __shfl_xor(sum, 32);
     l_run = l_run * alpha + sum;
     m_run = m_new;
+    // the running maximum rarely moves after the first blocks: skip the
+    // rescale when it did not move for any query of the wave
+    if (!__all(alpha == 1.0f)) {
 #pragma unroll
-    for (int t = 0; t < NT; ++t) oacc[t] *= alpha;
+      for (int t = 0; t < NT; ++t) oacc[t] *= alpha;
+    }
     // O^T += V^T P^T, key order permuted to match the score registers
 #pragma unroll
     for (int r = 0; r < 16; ++r)
 #pragma unroll
-      for (int t = 0; t < NT; ++t) oacc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[r * NT + t], p[r], oacc[t], 0, 0, 0);
-    if (next < nkb) {
-#pragma unroll
-      for (int j = 0; j < QS / 4; ++j) kf[j] = kn[j];
-#pragma unroll
-      for (int j = 0; j < 16 * NT; ++j) vf[j] = vn[j];
-    }
-  }
+      for (int t = 0; t < NT; ++t)
+        oacc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[r * NT + t], p[r], oacc[t], 0, 0, 0);
+  };
 
-  // merge the NW key-split partials: o = sum_w e^(m_w - M) o_w / sum_w e^(m_w - M) l_w
+  float4 kf[QS / 4];
+  if (w < nkb) load_k(w, kf);
+  for (int kb = w; kb < nkb; kb += NW) step(kb, kf);
+
+  // merge the NW key-split partials: o = sum_w 2^(m_w - M) o_w / sum_w 2^(m_w - M) l_w
   if (half == 0) m_part[w][col] = m_run, l_part[w][col] = l_run;
 #pragma unroll
   for (int t = 0; t < NT; ++t)
@@ -210,7 +230,7 @@ __global__ __launch_bounds__(64 * NW) void attn_kernel(const AttnArgs a) {
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int u = 0; u < NW; ++u) {
-      const float e = expf(m_part[u][qr] - mu);
+      const float e = __builtin_amdgcn_exp2f(m_part[u][qr] - mu);   // m is in the base-2 domain
       l += l_part[u][qr] * e;
       acc.x += o_part[u][qr][d] * e, acc.y += o_part[u][qr][d + 1] * e;
       acc.z += o_part[u][qr][d + 2] * e, acc.w += o_part[u][qr][d + 3] * e;
@@ -238,6 +258,7 @@ class AttnOp final : public Op {
     hipLaunchKernelGGL((attn_kernel<D, W>), grid, dim3(64 * W), 0, stream, a);                      \
     return hipGetLastError();                                                                        \
   }
+    KH_ATTN_LAUNCH(64, 8)
     KH_ATTN_LAUNCH(64, 4)
     KH_ATTN_LAUNCH(64, 2)
     KH_ATTN_LAUNCH(64, 1)
@@ -289,6 +310,16 @@ std::unique_ptr<Op> make_attn(const kh_launch &L, std::string &err, bool &unsupp
       return nullptr;
     }
   }
+  for (int j = 0; j < 4; ++j) {
+    const kh_ref &r = L.refs[j];
+    const int64_t rows = j == 0 || j == 3 ? tq : tk;
+    const int64_t span = std::max<int64_t>(0, batch - 1) * r.strides[0] + std::max<int64_t>(0, rows - 1) * r.strides[1] + dh;
+    if (r.strides[0] < 0 || r.strides[1] < 0 || span >= (1ll << 31)) {
+      unsupported = true;
+      err = "attention: operands must span fewer than 2^31 elements with non-negative strides";
+      return nullptr;
+    }
+  }
   if (scale_mode == KH_ATTN_SCALE_DIV && L.fparams[0] == 0.0f) {
     err = "attention: division by a zero scale";
     return nullptr;
@@ -310,11 +341,13 @@ std::unique_ptr<Op> make_attn(const kh_launch &L, std::string &err, bool &unsupp
   if (nw <= 0) {
     const int64_t groups = batch * a.n_qblocks;
     const int64_t kblocks = (tk + kKB - 1) / kKB;
-    nw = groups >= 4ll * current_device().cus ? 1 : (groups >= 2ll * current_device().cus ? 2 : 4);
+    // four key-split waves per query block measured best from T = 128 to
+    // 2048 (more waves in flight, shorter critical path per workgroup)
+    nw = groups >= 16ll * current_device().cus ? 2 : 4;
     if (kblocks < nw) nw = kblocks >= 2 ? 2 : 1;
   }
-  if (nw != 1 && nw != 2 && nw != 4) {
-    err = "attention: waves per workgroup must be 1, 2 or 4";
+  if (nw != 1 && nw != 2 && nw != 4 && !(nw == 8 && dh == 64)) {
+    err = "attention: waves per workgroup must be 1, 2, 4 (or 8 for head dim 64)";
     return nullptr;
   }
   op->nw = nw;
