@@ -50,6 +50,12 @@ def parse():
     p.add_argument("--quick", action="store_true", help="headline, roofline and CPU baseline only")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-autotune", action="store_true")
+    p.add_argument("--traffic-probe", metavar="JSON",
+                   help="run only the dispatch sequence the rocprofv3 --pmc traffic passes count "
+                        "(a copy of known size, then every launch of the headline plan) and write its map to JSON")
+    p.add_argument("--traffic-report", nargs=3, metavar=("PROBE_JSON", "FETCH_DIR", "WRITE_DIR"),
+                   help="turn the FETCH_SIZE and WRITE_SIZE counter passes over --traffic-probe into the "
+                        "per-launch HBM traffic summary (no GPU needed)")
     return p.parse_args()
 
 
@@ -130,7 +136,7 @@ def headline(args):
     return compiled, model, x, ms, err
 
 
-def dominant_kernel_roofline(compiled, x):
+def dominant_kernel_roofline(compiled, x, T):
     """Roofline of the block's longest launch: algorithmic bytes or flops per
     launch / its average duration (HIP events over back-to-back launches on
     the stream the kernel runs on)."""
@@ -156,10 +162,145 @@ def dominant_kernel_roofline(compiled, x):
     else:
         achieved = launch.bytes / (avg_ms * 1e-3) / 1e9
         bound, peak, unit = "hbm", HBM_PEAK_GBS, "GB/s"
+    traffic = committed_traffic(T, launch)
     return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
-            "frac": round(achieved / peak, 4), "traffic": None,
+            "frac": round(achieved / peak, 4), "traffic": traffic,
+            "traffic_source": os.path.relpath(TRAFFIC_FILE.format(T=T), ROOT) if traffic else None,
             "kernel": name, "summary": launch.summary, "avg_us": round(avg_ms * 1e3, 2),
             "algorithmic": launch.flops or launch.bytes}, prof
+
+
+# -- HBM traffic (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE) ------------------------------------
+
+PROBE_REPS = 20
+COPY_BYTES = 256 * 2**20
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_block_T{T}.txt")
+
+
+def traffic_probe(args):
+    """The dispatch sequence the counter passes read: PROBE_REPS plain copies of
+    COPY_BYTES (the calibration kernel: it reads and writes exactly COPY_BYTES),
+    then for each launch of the headline block plan a one-element fill (the
+    group marker) followed by the launch PROBE_REPS times. A launch may issue
+    several kernels (split-K issues two), so groups are cut at the markers.
+    Writes the map from groups to launches as JSON."""
+    import torch
+
+    import kiln
+    from kiln.hip.runtime import current_stream_handle
+
+    T = args.tokens
+    model, x = make_block(T)
+    compiled = kiln.compile(model, (x,), device="cuda", autotune=not args.no_autotune)
+    exe = compiled._exe
+    inputs = exe._prepare((x,))
+    outputs = [torch.empty(s, device=x.device) for s in exe.output_shapes]
+    ins, outs = [t.data_ptr() for t in inputs], [t.data_ptr() for t in outputs]
+    exe.run_into(inputs, outputs)
+    src = torch.empty(COPY_BYTES // 4, device="cuda").normal_()
+    dst = torch.empty_like(src)
+    marker = torch.empty(1, device="cuda")
+    torch.cuda.synchronize()
+    for _ in range(PROBE_REPS):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    for i in range(len(exe.program.launches)):
+        marker.fill_(float(i))
+        for _ in range(PROBE_REPS):
+            exe.plan.run_one(i, ins, outs, current_stream_handle())
+        torch.cuda.synchronize()
+    info = {"tokens": T, "reps": PROBE_REPS, "copy_bytes": COPY_BYTES, "marker": "FillFunctor",
+            "launches": [{"name": l.name, "kernel": l.kernel, "summary": l.summary, "flops": l.flops,
+                          "bytes": l.bytes} for l in exe.program.launches]}
+    with open(args.traffic_probe, "w") as f:
+        json.dump(info, f, indent=1)
+    log(f"traffic probe: copy x{PROBE_REPS}, then {len(info['launches'])} marked launch groups x{PROBE_REPS}")
+
+
+def _counter_rows(path, counter):
+    """Per-dispatch values of one counter from a rocprofv3 csv output tree, in
+    dispatch order: [(kernel name, value)]."""
+    import csv
+    import glob
+
+    files = sorted(glob.glob(os.path.join(path, "**", "*counter_collection.csv"), recursive=True))
+    if not files:
+        raise SystemExit(f"no *counter_collection.csv under {path}")
+    per = {}
+    for fn in files:
+        with open(fn, newline="") as f:
+            for row in csv.DictReader(f):
+                if row.get("Counter_Name") != counter:
+                    continue
+                key = int(row["Dispatch_Id"])
+                name, val = per.get(key, (row["Kernel_Name"], 0.0))
+                per[key] = (name, val + float(row["Counter_Value"]))
+    return [per[k] for k in sorted(per)]
+
+
+def _probe_groups(rows, probe):
+    """Split the probe's dispatches: the copies right before the first marker,
+    then one group per launch between markers. Returns per-rep KiB lists."""
+    reps, n = probe["reps"], len(probe["launches"])
+    marks = [i for i, (name, _) in enumerate(rows) if probe["marker"] in name]
+    if len(marks) < n:
+        raise SystemExit(f"found {len(marks)} group markers, the probe issues {n}")
+    marks = marks[-n:]
+    copies = [v for _, v in rows[marks[0] - reps:marks[0]]]
+    groups = []
+    for g, start in enumerate(marks):
+        end = marks[g + 1] if g + 1 < n else len(rows)
+        grp = rows[start + 1:end]
+        if len(grp) % reps:
+            raise SystemExit(f"launch group {g} has {len(grp)} dispatches, not a multiple of {reps}")
+        per = len(grp) // reps
+        groups.append([sum(v for _, v in grp[r * per:(r + 1) * per]) for r in range(reps)])
+    return copies, groups
+
+
+def traffic_report(probe_json, fetch_dir, write_dir):
+    """Per-launch HBM bytes: each group's median counter value (KiB per launch,
+    summed over the kernels a launch issues) scaled by the copy calibration
+    (COPY_BYTES / the copy's median). FETCH_SIZE and WRITE_SIZE count L2
+    misses to the fabric, so a re-read served by the Infinity Cache counts."""
+    import statistics
+
+    with open(probe_json) as f:
+        probe = json.load(f)
+    launches = probe["launches"]
+    med = {}
+    for counter, path in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+        copies, groups = _probe_groups(_counter_rows(path, counter), probe)
+        med[counter] = [statistics.median(copies)] + [statistics.median(g) for g in groups]
+    copy_bytes = probe["copy_bytes"]
+    f_scale = copy_bytes / (med["FETCH_SIZE"][0] * 1024)
+    w_scale = copy_bytes / (med["WRITE_SIZE"][0] * 1024)
+    lines = [f"calibration copy {copy_bytes} B: FETCH_SIZE {med['FETCH_SIZE'][0]:.1f} KiB, "
+             f"WRITE_SIZE {med['WRITE_SIZE'][0]:.1f} KiB; scale fetch {f_scale:.4f}, write {w_scale:.4f}"]
+    for i, l in enumerate(launches):
+        fb = med["FETCH_SIZE"][1 + i] * 1024 * f_scale
+        wb = med["WRITE_SIZE"][1 + i] * 1024 * w_scale
+        lines.append(f"traffic {l['name']} fetch_bytes={fb:.0f} write_bytes={wb:.0f} hbm_bytes={fb + wb:.0f} "
+                     f"algorithmic_bytes={l['bytes']} ratio={(fb + wb) / max(l['bytes'], 1):.3f} "
+                     f"summary={l['summary']}")
+    print("\n".join(lines))
+
+
+def committed_traffic(T, launch):
+    """HBM bytes per launch of `launch` from the committed counter summary, if it
+    was measured for this very launch (same name and summary), else None."""
+    try:
+        with open(TRAFFIC_FILE.format(T=T)) as f:
+            text = f.read()
+    except OSError:
+        return None
+    for line in text.splitlines():
+        if not line.startswith(f"traffic {launch.name} "):
+            continue
+        fields = dict(kv.split("=", 1) for kv in line.split(" summary=")[0].split()[2:])
+        if line.split(" summary=", 1)[1].strip() == launch.summary:
+            return int(fields["hbm_bytes"])
+    return None
 
 
 def block_sweep(tokens, autotune):
@@ -306,6 +447,9 @@ def cpu_baseline(T):
 
 def main():
     args = parse()
+    if args.traffic_report:
+        traffic_report(*args.traffic_report)
+        return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); this build has no multi-GPU path",
               file=sys.stderr)
@@ -316,11 +460,14 @@ def main():
         sys.exit("bench.py needs an MI355X (no ROCm GPU visible)")
     from kiln.hip import lib as kl
 
+    if args.traffic_probe:
+        traffic_probe(args)
+        return
     torch.manual_seed(0)
     info = kl.device_info() if kl.load() else {}
     compiled, model, x, ms, err = headline(args)
     log(f"headline: block T={args.tokens}: {ms:.4f} ms/step over {args.steps} steps (max err {err:.2e})")
-    roofline, prof = dominant_kernel_roofline(compiled, x)
+    roofline, prof = dominant_kernel_roofline(compiled, x, args.tokens)
     log("per-launch ms: " + ", ".join(f"{n}={t:.4f}" for n, t in prof))
     extra = {}
     if not args.quick:
