@@ -133,7 +133,9 @@ typedef struct kh_pass {
  *        strides over (b, m, n). The tape starts with the accumulator in slot 0.
  *        cfg[1] = tile configuration id, cfg[2] = split-K (0: library picks),
  *        cfg[3] = precision.
- *   GEMV as GEMM with M = 1.
+ *   GEMV as GEMM with M = 1; cfg[1] = workgroup variant (0: library picks from
+ *        the shape; 1-3: 32/16/8 columns x 256 threads; 4-5: 32/16 columns x
+ *        1024 threads), cfg[2] = split-K (0: library picks).
  *   RED  shape = input shape; refs[0] = input, refs[1] = output, both with
  *        strides over the input shape (the output's reduced dims stride 0);
  *        cfg[0] = bitmask of reduced dims, cfg[1] = 1 for max else sum.

@@ -67,6 +67,7 @@ __device__ __forceinline__ void run_epilogue(const GemmArgs &a, int64_t b, int64
 // result does not depend on scheduling) and runs the epilogue.
 namespace {
 constexpr int kReduceThreads = 256;
+constexpr int kReduceGroup = 8;
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmArgs a) {
   const uint32_t n4 = (uint32_t)(a.N + 3) / 4;
   const uint64_t rows = (uint64_t)a.batch * a.M;
@@ -79,15 +80,27 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmArgs a) {
     const int valid = min(4, a.N - n);
     const float *p = a.ws_partial + row * a.N + n;
     Vec<4> s = splat4(0.0f);
-    for (int sp = 0; sp < a.splitk; ++sp, p += plane) {
-      if (vec) {
-        const float4 v = *reinterpret_cast<const float4 *>(p);
-        s.v[0] += v.x, s.v[1] += v.y, s.v[2] += v.z, s.v[3] += v.w;
-      } else {
+    // issue a group of split loads before the first add (one memory latency
+    // per group, not per split); the adds stay in split order
+    for (int sp0 = 0; sp0 < a.splitk; sp0 += kReduceGroup) {
+      float4 v[kReduceGroup];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (i < valid) s.v[i] += p[i];
+      for (int j = 0; j < kReduceGroup; ++j) {
+        v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (sp0 + j >= a.splitk) continue;
+        const float *src = p + (uint64_t)(sp0 + j) * plane;
+        if (vec) {
+          v[j] = *reinterpret_cast<const float4 *>(src);
+        } else {
+          if (0 < valid) v[j].x = src[0];
+          if (1 < valid) v[j].y = src[1];
+          if (2 < valid) v[j].z = src[2];
+          if (3 < valid) v[j].w = src[3];
+        }
       }
+#pragma unroll
+      for (int j = 0; j < kReduceGroup; ++j)
+        if (sp0 + j < a.splitk) s.v[0] += v[j].x, s.v[1] += v[j].y, s.v[2] += v[j].z, s.v[3] += v[j].w;
     }
     run_epilogue(a, (int64_t)(row / a.M), (int64_t)(row % a.M), n, valid, s);
   }

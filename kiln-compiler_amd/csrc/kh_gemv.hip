@@ -2,14 +2,26 @@
 // x[b, k] * W[b, k, n]).
 //
 // A GEMV moves every weight byte once and does 2 flops per 4 bytes, so it is
-// HBM-bound; MFMA tiles would waste 31/32 of their rows. Instead a workgroup
-// of 256 threads covers 64 columns: 16 lanes read 16 consecutive 128-bit
-// column quads of one weight row (1 KiB contiguous per k), 16 k-lanes walk
-// the K range four rows at a time so each thread has four loads in flight.
-// The 16 partial sums per column are combined through LDS in a fixed order.
-// When the column blocks cannot fill the GPU, K is split across workgroups:
-// each writes a dense partial row and splitk_reduce_kernel (shared with the
-// GEMM family) sums them in split order and applies the epilogue.
+// HBM-bound; at decode sizes (a few MB per launch) a launch lasts about one
+// memory latency plus the streaming time of the busiest CU, so the kernel is
+// shaped for memory-level parallelism and spread:
+//   * a workgroup of 256 or 1024 threads covers CQ column quads (4 * CQ
+//     columns, CQ = 8, 4 or 2, so a row segment is 128, 64 or 32 contiguous
+//     bytes) and threads / CQ k-lanes; each thread issues kRows 128-bit row
+//     loads (and the matching x values) before its first FMA;
+//   * CQ is the widest that still gives about half the CUs a workgroup, so
+//     the weight stream is spread over the chip rather than queued behind a
+//     few CUs; narrower segments than 64 bytes were measured slower (a wave's
+//     load then touches 64 cache lines). When even CQ = 4 leaves few column
+//     blocks (N small, K large) the workgroup grows to 1024 threads so each
+//     CU still has its whole share of rows in flight in one or two passes;
+//   * the k-lanes are reduced in a fixed tree (shuffles inside a wave, then the
+//     four waves through LDS) and the same workgroup runs the epilogue;
+//   * only when even CQ = 1 leaves too few workgroups for the rows (tiny N, huge
+//     K) is K split across workgroups; the splits' partials are then summed in
+//     split order by the split-K reduce kernel (shared with the GEMM family),
+//     which runs the epilogue. Cross-workgroup combining inside one launch was
+//     measured slower at these sizes (agent-scope fences across 8 XCDs).
 #include <algorithm>
 #include <cstring>
 #include <type_traits>
@@ -21,20 +33,31 @@
 namespace kh {
 namespace {
 
-constexpr int kCols = 64;  // columns per workgroup
+constexpr int kRows = 8;           // row loads in flight per thread
+constexpr int kTargetBlocks = 128;  // workgroups wanted before narrowing stops
 
-__global__ __launch_bounds__(256) void gemv_kernel(const GemmArgs a) {
-  __shared__ float4 part[16][16];
-  const int cq = threadIdx.x & 15, kl = threadIdx.x >> 4;
+__device__ __forceinline__ float4 add4(float4 a, float4 b) {
+  return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+}
+
+__device__ __forceinline__ float4 shfl_xor4(float4 v, int m) {
+  return make_float4(__shfl_xor(v.x, m, 64), __shfl_xor(v.y, m, 64), __shfl_xor(v.z, m, 64),
+                     __shfl_xor(v.w, m, 64));
+}
+
+template <int CQ, int THREADS>
+__global__ __launch_bounds__(THREADS) void gemv_kernel(const GemmArgs a) {
+  constexpr int KL = THREADS / CQ;  // k-lanes: rows one load instruction covers
+  constexpr int NW = THREADS / 64;
+  __shared__ float4 wave_part[NW][CQ];
+  const int tid = threadIdx.x;
+  const int cq = tid % CQ, kl = tid / CQ;
   const int nb = blockIdx.x, b = blockIdx.y, split = blockIdx.z;
-  const int n = nb * kCols + cq * 4;
+  const int n = nb * 4 * CQ + cq * 4;
   const int k_begin = split * a.k_per_split;
   const int k_end = min(a.K, k_begin + a.k_per_split);
   const float *x = a.A + (int64_t)b * a.sa_b;
   const float *W = a.B + (int64_t)b * a.sb_b;
-  // The vector/scalar choice is made once, outside the K loop, so the four
-  // row loads of an iteration carry no control flow between them and are all
-  // in flight together.
   auto walk = [&](auto vec_tag) {
     constexpr bool vec = decltype(vec_tag)::value;
     auto row = [&](int k) -> float4 {
@@ -51,50 +74,66 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemmArgs a) {
       }
     };
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    int k = k_begin + kl;
-    for (; k + 48 < k_end; k += 64) {
-      const float4 w0 = row(k), w1 = row(k + 16), w2 = row(k + 32), w3 = row(k + 48);
-      const float x0 = x[(int64_t)k * a.sa_k], x1 = x[(int64_t)(k + 16) * a.sa_k];
-      const float x2 = x[(int64_t)(k + 32) * a.sa_k], x3 = x[(int64_t)(k + 48) * a.sa_k];
-      acc.x = fmaf(x0, w0.x, acc.x), acc.y = fmaf(x0, w0.y, acc.y), acc.z = fmaf(x0, w0.z, acc.z), acc.w = fmaf(x0, w0.w, acc.w);
-      acc.x = fmaf(x1, w1.x, acc.x), acc.y = fmaf(x1, w1.y, acc.y), acc.z = fmaf(x1, w1.z, acc.z), acc.w = fmaf(x1, w1.w, acc.w);
-      acc.x = fmaf(x2, w2.x, acc.x), acc.y = fmaf(x2, w2.y, acc.y), acc.z = fmaf(x2, w2.z, acc.z), acc.w = fmaf(x2, w2.w, acc.w);
-      acc.x = fmaf(x3, w3.x, acc.x), acc.y = fmaf(x3, w3.y, acc.y), acc.z = fmaf(x3, w3.z, acc.z), acc.w = fmaf(x3, w3.w, acc.w);
-    }
-    for (; k < k_end; k += 16) {
-      const float4 w = row(k);
-      const float xv = x[(int64_t)k * a.sa_k];
-      acc.x = fmaf(xv, w.x, acc.x), acc.y = fmaf(xv, w.y, acc.y), acc.z = fmaf(xv, w.z, acc.z), acc.w = fmaf(xv, w.w, acc.w);
+    for (int k0 = k_begin + kl; k0 < k_end; k0 += KL * kRows) {
+      float4 w[kRows];
+      float xv[kRows];
+      // Rows past the end are clamped to the last row (an in-bounds load,
+      // issued with the others) and their products dropped by a select.
+#pragma unroll
+      for (int j = 0; j < kRows; ++j) {
+        const int k = min(k0 + j * KL, k_end - 1);
+        w[j] = row(k);
+        xv[j] = x[(int64_t)k * a.sa_k];
+      }
+#pragma unroll
+      for (int j = 0; j < kRows; ++j) {
+        const bool in = k0 + j * KL < k_end;
+        const float xs = in ? xv[j] : 0.0f;
+        const float4 ws = in ? w[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+        acc.x = fmaf(xs, ws.x, acc.x), acc.y = fmaf(xs, ws.y, acc.y);
+        acc.z = fmaf(xs, ws.z, acc.z), acc.w = fmaf(xs, ws.w, acc.w);
+      }
     }
     return acc;
   };
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
   if (n < a.N) acc = (a.b_vec && n + 3 < a.N) ? walk(std::true_type{}) : walk(std::false_type{});
-  part[kl][cq] = acc;
-  __syncthreads();
-  Vec<4> v = splat4(0.0f);
-  if (kl == 0) {
+  // fixed-order tree over the k-lanes of a wave (lane = CQ * k-lane + quad),
+  // then the waves in order
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const float4 p = part[i][cq];
-      v.v[0] += p.x, v.v[1] += p.y, v.v[2] += p.z, v.v[3] += p.w;
-    }
-  }
-  if (kl != 0 || n >= a.N) return;
+  for (int m = CQ; m < 64; m *= 2) acc = add4(acc, shfl_xor4(acc, m));
+  if ((tid & 63) < CQ) wave_part[tid >> 6][cq] = acc;
+  __syncthreads();
+  if (tid >= CQ || n >= a.N) return;
+  float4 s = wave_part[0][cq];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) s = add4(s, wave_part[w][cq]);
+  const int valid = min(4, a.N - n);
   if (a.splitk > 1) {
     // dense partial row [split][batch][N]; splitk_reduce_kernel finishes it
     float *dst = a.ws_partial + ((int64_t)split * a.batch + b) * a.N + n;
-    for (int i = 0; i < 4 && n + i < a.N; ++i) dst[i] = v.v[i];
+    if (valid > 0) dst[0] = s.x;
+    if (valid > 1) dst[1] = s.y;
+    if (valid > 2) dst[2] = s.z;
+    if (valid > 3) dst[3] = s.w;
     return;
   }
-  run_epilogue(a, b, 0, n, min(4, a.N - n), v);
+  Vec<4> out;
+  out.v[0] = s.x, out.v[1] = s.y, out.v[2] = s.z, out.v[3] = s.w;
+  run_epilogue(a, b, 0, n, valid, out);
 }
+
+// (column quads, threads) per workgroup by variant id (1..5); 0 = chosen
+// from the shape.
+constexpr int kVariants[][2] = {{0, 0}, {8, 256}, {4, 256}, {2, 256}, {8, 1024}, {4, 1024}};
+constexpr int kNumVariants = sizeof(kVariants) / sizeof(kVariants[0]);
 
 class GemvOp final : public Op {
  public:
   GemmArgs args{};
   dim3 grid;
   size_t n_partials = 0;
+  int quads = 8, threads = 256;
   bool b_vec_layout = false;
   uint32_t e_vec_candidates = 0;
 
@@ -112,7 +151,14 @@ class GemvOp final : public Op {
     a.ws_partial = partials;
     if (a.N == 0 || a.batch == 0) return hipSuccess;
     if (a.splitk > 1 && !partials) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(gemv_kernel, grid, dim3(256), 0, stream, a);
+    if (threads == 1024) {
+      if (quads == 8) hipLaunchKernelGGL((gemv_kernel<8, 1024>), grid, dim3(1024), 0, stream, a);
+      else hipLaunchKernelGGL((gemv_kernel<4, 1024>), grid, dim3(1024), 0, stream, a);
+    } else {
+      if (quads == 8) hipLaunchKernelGGL((gemv_kernel<8, 256>), grid, dim3(256), 0, stream, a);
+      else if (quads == 4) hipLaunchKernelGGL((gemv_kernel<4, 256>), grid, dim3(256), 0, stream, a);
+      else hipLaunchKernelGGL((gemv_kernel<2, 256>), grid, dim3(256), 0, stream, a);
+    }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.splitk == 1) return e;
     return launch_splitk_reduce(a, current_device().cus, stream);
@@ -145,17 +191,49 @@ std::unique_ptr<Op> make_gemv(const kh_launch &L, std::string &err, bool &unsupp
   a.sb_b = L.refs[1].strides[0], a.sb_k = L.refs[1].strides[1], a.sb_n = L.refs[1].strides[2];
   op->b_vec_layout = a.sb_n == 1 && L.refs[1].offset % 4 == 0 && a.sb_k % 4 == 0 && a.sb_b % 4 == 0;
   if (!fill_epilogue(L, a, op->e_vec_candidates, err)) return nullptr;
-  const int n_blocks = (int)std::max<int64_t>(1, (N + kCols - 1) / kCols);
-  int splitk = L.cfg[2];
-  if (splitk <= 0) {
-    const int64_t want = 2ll * current_device().cus;
-    splitk = (int)std::max<int64_t>(1, std::min<int64_t>(want / std::max<int64_t>(1, n_blocks * batch), K / 64));
+  // column quads per workgroup: the widest giving kTargetBlocks workgroups;
+  // if none does, 64-byte segments with 1024-thread workgroups
+  const int64_t b1 = std::max<int64_t>(1, batch);
+  const int variant = L.cfg[1];
+  if (variant < 0 || variant >= kNumVariants) {
+    err = "gemv: unknown variant " + std::to_string(variant);
+    return nullptr;
   }
-  const int64_t kper = std::max<int64_t>(16, ((K + splitk - 1) / splitk + 15) / 16 * 16);
-  splitk = (int)std::max<int64_t>(1, (K + kper - 1) / kper);
+  int quads = kVariants[variant][0], threads = kVariants[variant][1];
+  if (quads == 0) {
+    quads = 4, threads = 1024;
+    for (int q : {8, 4}) {
+      if ((N + 4 * q - 1) / (4 * q) * b1 >= kTargetBlocks) {
+        quads = q, threads = 256;
+        break;
+      }
+    }
+  }
+  const int64_t n_blocks = std::max<int64_t>(1, (N + 4 * quads - 1) / (4 * quads));
+  const int64_t k_lanes = threads / quads;
+  // split K (two kernels) only when the blocks are few and each thread would
+  // walk more than four passes of kRows rows
+  int64_t splitk = L.cfg[2];
+  if (splitk <= 0) {
+    splitk = 1;
+    const int64_t rows_per_thread = (K + k_lanes - 1) / k_lanes;
+    if (n_blocks * b1 < kTargetBlocks / 2 && rows_per_thread > 4 * kRows)
+      splitk = std::min<int64_t>((kTargetBlocks + n_blocks * b1 - 1) / (n_blocks * b1),
+                                 (rows_per_thread + 4 * kRows - 1) / (4 * kRows));
+  }
+  splitk = std::max<int64_t>(1, std::min<int64_t>(splitk, std::max<int64_t>(1, K / k_lanes)));
+  const int64_t kper = std::max<int64_t>(k_lanes, ((K + splitk - 1) / splitk + k_lanes - 1) / k_lanes * k_lanes);
+  splitk = std::max<int64_t>(1, (K + kper - 1) / kper);
+  if (n_blocks * b1 >= (1ll << 31) || b1 >= 65536) {
+    unsupported = true;
+    err = "gemv: too many column blocks";
+    return nullptr;
+  }
+  op->quads = quads;
+  op->threads = threads;
   a.k_per_split = (int)kper;
-  a.splitk = splitk;
-  op->grid = dim3((unsigned)n_blocks, (unsigned)std::max<int64_t>(batch, 1), (unsigned)splitk);
+  a.splitk = (int)splitk;
+  op->grid = dim3((unsigned)n_blocks, (unsigned)b1, (unsigned)splitk);
   if (splitk > 1) {
     op->n_partials = (size_t)splitk * batch * N;
   }

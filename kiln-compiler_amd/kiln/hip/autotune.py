@@ -28,6 +28,10 @@ from pathlib import Path
 MIN_GAIN = 1.03
 FINALISTS = 3
 SPLITS = (1, 2, 3, 4, 6, 8)
+# M = 1 (GEMV family): "tile" = workgroup variant (0 = from the shape; 1-3 =
+# 32/16/8 columns x 256 threads, 4-5 = 32/16 columns x 1024 threads), split-K
+# 0 = from the shape
+GEMV_CANDIDATES = [(v, 0) for v in range(6)] + [(0, s) for s in (2, 4)]
 
 # (BM, BN, BK, WM, WN, WK, MFMA) of the compiled configurations, by id; must
 # match the table in csrc/kh_gemm.hip (tests check it against kh_gemm_config).
@@ -100,6 +104,8 @@ def default_matmul_config(graph, kernel, cus=None) -> dict:
 
 
 def default_config_for(batch, m, n, k, cus=None) -> dict:
+    if m == 1:
+        return {"tile": 0, "splitk": 0}
     cus = cus or device_cus()
     best = None
     for tile in TILES:
@@ -117,6 +123,8 @@ def default_config_for(batch, m, n, k, cus=None) -> dict:
 
 
 def candidates(batch, m, n, k, cus=None) -> list:
+    if m == 1:
+        return [{"tile": v, "splitk": s} for v, s in GEMV_CANDIDATES if s == 0 or k // s >= 64]
     cus = cus or device_cus()
     out = []
     for tile in TILES:

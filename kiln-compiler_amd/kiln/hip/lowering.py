@@ -684,8 +684,11 @@ class _Lowerer:
         _encode(best[0], best[1], d, ref_offset=2)
         cfg = dict(self.matmul_config(self.g, k))
         if gemv:
-            cfg = {"tile": 0, "splitk": int(cfg.get("gemv_splitk", 0)), "precision": cfg.get("precision",
-                                                                                             self.precision)}
+            # GEMV family: "tile" picks the workgroup variant (0 = from the
+            # shape, 1-5), split-K 0 = from the shape
+            cfg = {"tile": int(cfg.get("tile", 0)) if 0 <= int(cfg.get("tile", 0)) <= 5 else 0,
+                   "splitk": int(cfg.get("gemv_splitk", cfg.get("splitk", 0))),
+                   "precision": cfg.get("precision", self.precision)}
         d.cfg[1] = int(cfg.get("tile", 0))
         d.cfg[2] = int(cfg.get("splitk", 1))
         d.cfg[3] = {"fp32": kl.PREC_FP32, "bf16": kl.PREC_BF16, "bf16x3": kl.PREC_BF16X3}[
@@ -695,8 +698,7 @@ class _Lowerer:
                       + len(outs) * math.prod(out_shape))
         epi = " ".join(nd.op for nd in k.nodes if nd is not mm)
         summary = f"{batch}x{m}x{n}x{kk}"
-        if not gemv:
-            summary += f" tile {d.cfg[1]} splitk {d.cfg[2]}"
+        summary += f" tile {d.cfg[1]} splitk {d.cfg[2]}"
         if epi:
             summary += f" epilogue: {epi}"
         self.add(d, k, summary, flops=flops, nbytes=nbytes)

@@ -6,8 +6,8 @@ Everything static is set up once:
   * the arena, one torch uint8 allocation (one hipMalloc) holding every
     intermediate at the memory plan's offsets;
   * the frozen weights, uploaded once;
-  * a workspace for split-K partial tiles and their counters (zero-filled
-    once; kernels leave the counters at zero after every launch);
+  * a workspace for split-K partial tiles (every split-K launch writes all
+    the partials it reads back, so it needs no initialisation);
   * the plan: every launch validated and prepared in C++ (kh_plan_create).
 
 A call either runs the plan directly (one ctypes call for all launches) or,

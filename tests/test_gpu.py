@@ -221,6 +221,31 @@ def test_every_gemm_tile_configuration(tile):
         np.testing.assert_allclose(out, ref, rtol=RTOL, atol=ATOL)
 
 
+@pytest.mark.parametrize("variant", range(6))
+def test_gemv_variants_and_ragged_sizes(variant):
+    # M = 1: every column-block width (0 = chosen from the shape), with and
+    # without a K split (two kernels, partials summed in split order); N not
+    # a multiple of 4 or of the block, K not a multiple of the k-lanes.
+    # Repeated launches (eager and graph replays) must agree bit for bit.
+    fn = lambda x, wt, b: x @ wt + b
+    for n, k in ((3072, 768), (133, 61), (1030, 999)):
+        x, wt, b = torch.randn(1, k), torch.randn(k, n) * 0.1, torch.randn(n)
+        ref = oracle.linear(x.numpy(), wt.numpy(), b.numpy())
+        for splitk, graphs in ((0, False), (3, False), (3, True)):
+            c = kiln.compile(fn, (x, wt, b), device="cuda", cuda_graphs=graphs,
+                             gpu_matmul_config=lambda *_: {"tile": variant, "splitk": splitk})
+            assert [l.family for l in c._exe.program.launches] == [4]
+            first = c(x, wt, b)
+            np.testing.assert_allclose(first.cpu().numpy(), ref, rtol=RTOL, atol=ATOL)
+            for _ in range(3):
+                assert torch.equal(c(x, wt, b), first)
+
+
+def test_batched_gemv_with_strided_weights():
+    # batch 3, M = 1, B read through a transposed view (no 128-bit column quads)
+    check(lambda a, b: torch.bmm(a, b.transpose(1, 2)) * 0.5, torch.randn(3, 1, 300), torch.randn(3, 70, 300))
+
+
 def test_strided_and_broadcast_gemm_operands():
     # A transposed (k-stride != 1), B a column slice, bias broadcast over rows
     a, b = torch.randn(40, 30), torch.randn(50, 70)
