@@ -2,19 +2,24 @@
 // CDNA4 matrix cores.
 //
 // Replaces the reference's tl.dot kernel with fused epilogue
-// (kiln/gpu/codegen.py:484-530) and its tile heuristic (552-598). MI355X design:
-//   * fp32 operands on v_mfma_f32_32x32x2_f32 / v_mfma_f32_16x16x4_f32 (full
-//     fp32 products, fp32 accumulation). Tiles are sized for wave64: a
-//     workgroup of WM x WN x WK waves computes a BM x BN tile; each wave owns a
-//     (BM/WM) x (BN/WN) sub-tile and, with WK > 1, a 1/WK share of every K
-//     step (the partial tiles are summed in LDS in a fixed order);
-//   * K advances in BK steps through two LDS buffers: the next step's global
-//     loads (128-bit along K for A, along N for B) are in flight while the
-//     matrix cores work on the current one;
-//   * the reduction order over K inside a step is permuted so each lane reads
-//     its A operand as 128-bit LDS vectors (a dot product is order-free; the
-//     same permutation is applied to A and B);
-//   * the epilogue stages the accumulator tile through LDS and runs the same
+// (kiln/gpu/codegen.py:484-530) and its tile heuristic (552-598). Two kernels
+// share the argument block, the epilogue tape and the split-K scheme:
+//   * gemm3_f32_kernel (configurations 0-7), the main path: fp32 operands on
+//     v_mfma_f32_16x16x4_f32, global memory copied straight into LDS
+//     (global_load_lds) through a three-stage ring two K steps ahead of the
+//     matrix cores, XOR/rotation-swizzled LDS chunks, four or eight waves per
+//     workgroup sized so that one to four workgroups share a CU; its design
+//     notes are at the kernel;
+//   * gemm_f32_kernel (configurations 8-14): register-staged loads into two
+//     LDS buffers, v_mfma_f32_32x32x2_f32 or 16x16x4, and optionally K split
+//     across the waves of a workgroup (WK > 1, summed in LDS in a fixed
+//     order) for skinny tiles; it also serves operands too large for the
+//     pipeline's 32-bit copy offsets.
+// Both:
+//   * permute the reduction order over K inside a step so each lane reads its
+//     A operand as 128-bit LDS vectors (a dot product is order-free; the same
+//     permutation is applied to A and B);
+//   * stage the accumulator tile through LDS for the epilogue and run the same
 //     instruction tape as the elementwise family on row-contiguous groups of
 //     4, so bias, GELU, residual, scale and mask operands are read with
 //     coalesced 128-bit loads and the output is written with 128-bit stores;
@@ -24,9 +29,10 @@
 //     kernel boundary is the only synchronisation (a per-tile device-scope
 //     counter would need an L2 write-back per workgroup across 8 XCDs), and
 //     the fixed summation order keeps the result independent of scheduling;
-//   * workgroup ids are remapped so each XCD (own L2) receives a contiguous
-//     block of tiles.
+//   * remap workgroup ids so each XCD (own L2) receives a contiguous block of
+//     tiles.
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 #include <type_traits>
 
@@ -314,34 +320,359 @@ __global__ __launch_bounds__(64 * WM * WN * WK) void gemm_f32_kernel(const GemmA
 }
 
 // ---------------------------------------------------------------------------
+// Pipelined variant: global memory is copied straight into LDS
+// (global_load_lds, 128-bit per lane for aligned row-major operands, 32-bit
+// for any other strides) through three LDS stages, two steps ahead of the
+// matrix cores, so no VGPRs hold data in flight and a load has two MFMA
+// phases to arrive.
+//   * K advances in steps of 32. Within a step, lane group g of an MFMA
+//     (lanes l / 16) owns K values 8g .. 8g+7 and MFMA j consumes value 8g + j
+//     in every group: each lane reads its A values as two 128-bit LDS vectors
+//     and its B values as one 32-bit read per MFMA, and B keeps its global
+//     [k][n] layout in LDS (no transpose);
+//   * LDS holds 16-byte chunks. A row r (32 floats = 8 chunks) puts chunk c at
+//     c ^ ((r ^ r/8) % 8); B row k of lane group g puts chunk c at
+//     (c + 4g) mod (BN/4). The 128-bit A reads and the per-group 32-bit B
+//     reads then hit distinct banks. A copy instruction writes 64 consecutive
+//     chunks, so each lane fetches the global chunk its LDS position holds;
+//   * each stage is its own LDS array and the loop is unrolled over the three
+//     stages, so the compiler sees which copies a read depends on; before a
+//     stage is read every wave waits for its own copies into it (vmcnt), then
+//     a barrier publishes them;
+//   * ragged edges: rows past M and columns past N are fetched from clamped,
+//     valid addresses (their results are never stored); K values past the
+//     end of the step range are fetched clamped and overwritten with zeros in
+//     LDS before the barrier;
+//   * the epilogue stages the accumulators through LDS per 16-row block and
+//     runs the tape on row-contiguous groups of 4 (coalesced 128-bit operand
+//     loads and stores).
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+__device__ __forceinline__ int swz_a(int r) { return (r ^ (r >> 3)) & 7; }
+
+// One wave-wide copy: lane l's VW floats at base + voff bytes go to LDS
+// byte address lds + l * 4 * VW (M0 holds the wave's LDS destination, `base`
+// is wave-uniform in SGPRs, `voff` a per-lane 32-bit byte offset). Issued as
+// inline assembly: the compiler's wait insertion would otherwise make every
+// LDS read wait for all copies in flight (it cannot tell the stages apart),
+// which would undo the two-step lead; the kernel waits for the copies it
+// needs itself.
+template <int VW>
+__device__ __forceinline__ void copy_to_lds(const float *base, uint32_t voff, uint32_t lds_addr) {
+  const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_addr);
+  if constexpr (VW == 4)
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds)
+                 : "memory", "m0");
+  else
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(base), "s"(lds)
+                 : "memory", "m0");
+}
+
+__device__ __forceinline__ const float *uniform_ptr(const float *p) {
+  const uint64_t v = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (const float *)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
+// vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Workgroup barrier for the copy pipeline: LDS writes of this wave complete,
+// then s_barrier. Unlike __syncthreads() it does not wait for outstanding
+// global loads (the copies of the step after next stay in flight); the
+// copies a stage depends on are waited for explicitly (wait_vmcnt) before it.
+__device__ __forceinline__ void stage_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt((3 << 14) | (7 << 4) | 15);  // lgkmcnt(0); vmcnt, expcnt unconstrained
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+template <int BM, int BN, int WM, int WN, int VW>
+__global__ __launch_bounds__(64 * WM * WN, 2) void gemm3_f32_kernel(const GemmArgs a) {
+  constexpr int MT = 16, BK = 32;
+  constexpr int kWaves = WM * WN, kThreads = 64 * kWaves;
+  constexpr int TM = BM / WM, TN = BN / WN;
+  constexpr int FM = TM / MT, FN = TN / MT;
+  constexpr int KG = 8;                 // K values per lane group per step
+  constexpr int B_CH = BN / 4;          // chunks per B row
+  constexpr int A_FLOATS = BM * BK, B_FLOATS = BK * BN, STAGE = A_FLOATS + B_FLOATS;
+  // copy instructions per wave per step: each covers 64 lanes x VW floats
+  constexpr int A_INSN = A_FLOATS / (64 * VW), B_INSN = B_FLOATS / (64 * VW);
+  constexpr int A_PER_WAVE = A_INSN / kWaves, B_PER_WAVE = B_INSN / kWaves;
+  constexpr int COPIES = A_PER_WAVE + B_PER_WAVE;
+  static_assert(VW == 4 || VW == 1, "copy width");
+  static_assert(TM % MT == 0 && TN % MT == 0, "wave tile must be a multiple of the MFMA tile");
+  static_assert(A_INSN % kWaves == 0 && B_INSN % kWaves == 0, "copy mapping");
+  static_assert(BN % 16 == 0 && B_CH >= 16, "B chunk rotation");
+  static_assert(COPIES < 64, "vmcnt");
+  using M = Mfma<MT>;
+  typedef typename M::acc_t acc_t;
+
+  __shared__ float4 st0[STAGE / 4], st1[STAGE / 4], st2[STAGE / 4];
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int wm = wave / WN, wn = wave % WN;
+  const int n_tiles = a.tiles_m * a.tiles_n;
+  const int tile = xcd_remap(blockIdx.x, n_tiles);
+  const int tm = tile / a.tiles_n, tn = tile % a.tiles_n;
+  const int bidx = blockIdx.y, split = blockIdx.z;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int k_begin = split * a.k_per_split;
+  const int k_end = min(a.K, k_begin + a.k_per_split);
+  const float *Ab = a.A + (int64_t)bidx * a.sa_b;
+  const float *Bb = a.B + (int64_t)bidx * a.sb_b;
+  const int n_steps = k_end > k_begin ? (k_end - k_begin + BK - 1) / BK : 0;
+
+  // Per-lane copy sources: byte offsets from the step's K origin (rows and
+  // columns clamped to valid ones), plus the K index each copy covers; the
+  // LDS destinations are wave-uniform.
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  uint32_t a_off0[A_PER_WAVE], b_off0[B_PER_WAVE];
+  int a_kk[A_PER_WAVE], b_kk[B_PER_WAVE], a_mn[A_PER_WAVE], b_mn[B_PER_WAVE];
+#pragma unroll
+  for (int i = 0; i < A_PER_WAVE; ++i) {
+    const int p = (wave * A_PER_WAVE + i) * 64 + lane;  // LDS position (units of VW floats)
+    int r, kk;
+    if constexpr (VW == 4) {
+      r = p / 8;
+      kk = ((p % 8) ^ swz_a(r)) * 4;
+    } else {
+      r = p / BK;
+      const int pc = (p % BK) / 4;
+      kk = ((pc ^ swz_a(r)) * 4) + (p & 3);
+    }
+    a_mn[i] = min(m0 + r, a.M - 1) * (int)a.sa_m;
+    a_kk[i] = kk;
+    a_off0[i] = (uint32_t)(a_mn[i] + kk * (int)a.sa_k) * 4u;
+  }
+#pragma unroll
+  for (int i = 0; i < B_PER_WAVE; ++i) {
+    const int p = (wave * B_PER_WAVE + i) * 64 + lane;
+    int k, nn;
+    if constexpr (VW == 4) {
+      k = p / B_CH;
+      const int g = k / KG;
+      nn = (((p % B_CH) - 4 * g + 4 * B_CH) % B_CH) * 4;
+    } else {
+      k = p / BN;
+      const int g = k / KG;
+      const int pc = (p % BN) / 4;
+      nn = (((pc - 4 * g + 4 * B_CH) % B_CH) * 4) + (p & 3);
+    }
+    b_mn[i] = min(n0 + nn, a.N - VW) * (int)a.sb_n;
+    b_kk[i] = k;
+    b_off0[i] = (uint32_t)(b_mn[i] + k * (int)a.sb_k) * 4u;
+  }
+  // issue the copies of step `step` into `stage`
+  auto issue = [&](int step, float4 *stage) {
+    const int k0 = k_begin + step * BK;
+    const float *abase = uniform_ptr(Ab + (int64_t)k0 * a.sa_k);
+    const float *bbase = uniform_ptr(Bb + (int64_t)k0 * a.sb_k);
+    const uint32_t lds = (uint32_t)(uintptr_t)(lds_void_t *)stage;
+    if (k0 + BK <= k_end) {
+#pragma unroll
+      for (int i = 0; i < A_PER_WAVE; ++i)
+        copy_to_lds<VW>(abase, a_off0[i], lds + ((wave_u * A_PER_WAVE + i) * 64 * VW) * 4);
+#pragma unroll
+      for (int i = 0; i < B_PER_WAVE; ++i)
+        copy_to_lds<VW>(bbase, b_off0[i], lds + (A_FLOATS + (wave_u * B_PER_WAVE + i) * 64 * VW) * 4);
+    } else {
+      // last, partial step: K indices clamped into the range (zeroed later)
+      const int kmax = k_end - k0;
+#pragma unroll
+      for (int i = 0; i < A_PER_WAVE; ++i)
+        copy_to_lds<VW>(abase, (uint32_t)(a_mn[i] + min(a_kk[i], kmax - VW) * (int)a.sa_k) * 4u,
+                        lds + ((wave_u * A_PER_WAVE + i) * 64 * VW) * 4);
+#pragma unroll
+      for (int i = 0; i < B_PER_WAVE; ++i)
+        copy_to_lds<VW>(bbase, (uint32_t)(b_mn[i] + min(b_kk[i], kmax - 1) * (int)a.sb_k) * 4u,
+                        lds + (A_FLOATS + (wave_u * B_PER_WAVE + i) * 64 * VW) * 4);
+    }
+  };
+  // after this thread's copies of `step` landed: zero what lies past k_end
+  auto zero_tail = [&](int step, float4 *stage) {
+    const int k0 = k_begin + step * BK;
+    if (k0 + BK <= k_end) return;
+    float *st = reinterpret_cast<float *>(stage);
+#pragma unroll
+    for (int i = 0; i < A_PER_WAVE; ++i) {
+      float *d = st + ((wave * A_PER_WAVE + i) * 64 + lane) * VW;
+#pragma unroll
+      for (int e = 0; e < VW; ++e)
+        if (k0 + a_kk[i] + e >= k_end) d[e] = 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < B_PER_WAVE; ++i) {
+      float *d = st + A_FLOATS + ((wave * B_PER_WAVE + i) * 64 + lane) * VW;
+      if (k0 + b_kk[i] >= k_end)
+#pragma unroll
+        for (int e = 0; e < VW; ++e) d[e] = 0.0f;
+    }
+  };
+
+  // per-lane LDS offsets of the MFMA fragments (loop invariant)
+  const int g = lane / MT, li = lane % MT;
+  int a_off[FM][2], b_off[FN];
+#pragma unroll
+  for (int fm = 0; fm < FM; ++fm) {
+    const int r = wm * TM + fm * MT + li;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) a_off[fm][h] = r * BK + (((2 * g + h) ^ swz_a(r)) * 4);
+  }
+#pragma unroll
+  for (int fn = 0; fn < FN; ++fn) {
+    const int n = wn * TN + fn * MT + li;
+    b_off[fn] = A_FLOATS + g * KG * BN + ((((n / 4) + 4 * g) % B_CH) * 4) + (n & 3);
+  }
+
+  acc_t acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < M::kRegs; ++r) acc[i][j][r] = 0.0f;
+
+  auto compute = [&](const float4 *stage) {
+    const float *st = reinterpret_cast<const float *>(stage);
+    float af[FM][KG], bf[FN][KG];
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const float4 v = *reinterpret_cast<const float4 *>(st + a_off[fm][h]);
+        af[fm][4 * h + 0] = v.x, af[fm][4 * h + 1] = v.y, af[fm][4 * h + 2] = v.z, af[fm][4 * h + 3] = v.w;
+      }
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+      for (int j = 0; j < KG; ++j) bf[fn][j] = st[b_off[fn] + j * BN];
+#pragma unroll
+    for (int j = 0; j < KG; ++j)
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) acc[fm][fn] = M::mma(af[fm][j], bf[fn][j], acc[fm][fn]);
+  };
+  // one step on stage `cur`: copies of step s+2 go into `nxt2`; afterwards the
+  // copies of step s+1 (into `nxt1`) must be visible to every wave
+  auto step = [&](int s, float4 *cur, float4 *nxt1, float4 *nxt2) {
+    if (s + 2 < n_steps) issue(s + 2, nxt2);
+    compute(cur);
+    if (s + 1 < n_steps) {
+      if (s + 2 < n_steps) wait_vmcnt<COPIES>();
+      else wait_vmcnt<0>();
+      zero_tail(s + 1, nxt1);
+    }
+    stage_barrier();
+  };
+
+  if (n_steps > 0) {
+    issue(0, st0);
+    if (n_steps > 1) {
+      issue(1, st1);
+      wait_vmcnt<COPIES>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    zero_tail(0, st0);
+    stage_barrier();
+    for (int s = 0; s < n_steps; s += 3) {
+      step(s, st0, st1, st2);
+      if (s + 1 >= n_steps) break;
+      step(s + 1, st1, st2, st0);
+      if (s + 2 >= n_steps) break;
+      step(s + 2, st2, st0, st1);
+    }
+  }
+
+  // Epilogue: the waves stage their accumulators through LDS one 16-row
+  // block (16 x TN per wave) at a time and read them back as row-contiguous
+  // groups of 4.
+  constexpr int CS = TN + 4;
+  static_assert(kWaves * MT * CS <= STAGE, "epilogue staging");
+  float *Cw = reinterpret_cast<float *>(st0) + wave * MT * CS;
+  const int row0 = m0 + wm * TM, col0 = n0 + wn * TN;
+  float *part = a.splitk > 1 ? a.ws_partial + ((int64_t)split * a.batch + bidx) * (int64_t)a.M * a.N : nullptr;
+  const bool vec = (a.N & 3) == 0;
+#pragma unroll
+  for (int fm = 0; fm < FM; ++fm) {
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+      for (int r = 0; r < M::kRegs; ++r) Cw[M::row(r, lane) * CS + fn * MT + li] = acc[fm][fn][r];
+    __syncthreads();
+#pragma unroll 1
+    for (int q = lane; q < MT * TN / 4; q += 64) {
+      const int r = q / (TN / 4), c = (q % (TN / 4)) * 4;
+      const int m = row0 + fm * MT + r, n = col0 + c;
+      if (m >= a.M || n >= a.N) continue;
+      const float4 p = *reinterpret_cast<const float4 *>(Cw + r * CS + c);
+      if (part) {
+        float *dst = part + (int64_t)m * a.N + n;
+        if (vec) {
+          *reinterpret_cast<float4 *>(dst) = p;
+        } else {
+          const float pv[4] = {p.x, p.y, p.z, p.w};
+          for (int i = 0; i < 4 && n + i < a.N; ++i) dst[i] = pv[i];
+        }
+      } else {
+        Vec<4> v;
+        v.v[0] = p.x, v.v[1] = p.y, v.v[2] = p.z, v.v[3] = p.w;
+        run_epilogue(a, bidx, m, n, min(4, a.N - n), v);
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Host side.
 
 struct TileCfg {
-  int bm, bn, bk, wm, wn, wk, mt;
+  int bm, bn, bk, wm, wn, wk, mt, kind;  // kind 1: register-staged loads; 3: LDS-copy pipeline
 };
 
+// Configurations by id. Ids 0-7: the copy pipeline (BK = 32, MFMA
+// 16x16x4; each has a 128-bit and a 32-bit copy variant, chosen at launch
+// from the operand layouts). Ids 8-14: register-staged loads, for skinny
+// tiles and K split across the waves of a workgroup.
+#define KH_GEMM3_CONFIGS(X) \
+  X(0, 64, 128, 2, 2)       \
+  X(1, 128, 64, 2, 2)       \
+  X(2, 64, 64, 2, 2)        \
+  X(3, 32, 128, 1, 4)       \
+  X(4, 32, 64, 2, 2)        \
+  X(5, 64, 96, 2, 2)        \
+  X(6, 128, 192, 2, 4)      \
+  X(7, 128, 128, 2, 4)
+
 #define KH_GEMM_CONFIGS(X)        \
-  X(0, 128, 128, 32, 2, 2, 1, 32) \
-  X(1, 128, 192, 32, 2, 2, 1, 32) \
-  X(2, 256, 128, 32, 2, 2, 1, 32) \
-  X(3, 64, 64, 32, 2, 2, 1, 32)   \
-  X(4, 64, 128, 32, 2, 2, 1, 32)  \
-  X(5, 128, 64, 32, 2, 2, 1, 32)  \
-  X(6, 32, 64, 32, 1, 2, 2, 32)   \
-  X(7, 32, 32, 32, 1, 1, 4, 32)   \
-  X(8, 64, 64, 32, 1, 1, 4, 32)   \
-  X(9, 32, 32, 32, 2, 2, 1, 16)   \
-  X(10, 16, 64, 32, 1, 4, 1, 16)  \
-  X(11, 64, 32, 32, 2, 2, 1, 16)  \
-  X(12, 128, 128, 32, 4, 2, 1, 32) \
-  X(13, 128, 192, 32, 4, 2, 1, 32) \
-  X(14, 256, 128, 32, 4, 2, 1, 32) \
-  X(15, 64, 128, 64, 2, 2, 1, 32)  \
-  X(16, 128, 64, 64, 2, 2, 1, 32)  \
-  X(17, 64, 64, 64, 2, 2, 1, 32)
+  X(8, 64, 64, 32, 2, 2, 1, 32)   \
+  X(9, 32, 64, 32, 1, 2, 2, 32)   \
+  X(10, 32, 32, 32, 1, 1, 4, 32)  \
+  X(11, 32, 32, 32, 2, 2, 1, 16)  \
+  X(12, 16, 64, 32, 1, 4, 1, 16)  \
+  X(13, 64, 32, 32, 2, 2, 1, 16)  \
+  X(14, 64, 64, 64, 2, 2, 1, 32)
+
+// the register-staged configuration a pipelined tile falls back to for
+// operands too large for 32-bit copy offsets
+constexpr int kFallbackConfig = 8;
 
 constexpr TileCfg kConfigs[] = {
-#define KH_CFG_ROW(id, bm, bn, bk, wm, wn, wk, mt) {bm, bn, bk, wm, wn, wk, mt},
+#define KH_CFG3_ROW(id, bm, bn, wm, wn) {bm, bn, 32, wm, wn, 1, 16, 3},
+    KH_GEMM3_CONFIGS(KH_CFG3_ROW)
+#undef KH_CFG3_ROW
+#define KH_CFG_ROW(id, bm, bn, bk, wm, wn, wk, mt) {bm, bn, bk, wm, wn, wk, mt, 1},
     KH_GEMM_CONFIGS(KH_CFG_ROW)
 #undef KH_CFG_ROW
 };
@@ -356,6 +687,15 @@ hipError_t launch_config(int id, const GemmArgs &a, dim3 grid, hipStream_t strea
     break;
     KH_GEMM_CONFIGS(KH_CFG_CASE)
 #undef KH_CFG_CASE
+#define KH_CFG3_CASE(cid, bm, bn, wm, wn)                                                                \
+  case cid:                                                                                              \
+    if (a.a_vec && a.b_vec)                                                                              \
+      hipLaunchKernelGGL((gemm3_f32_kernel<bm, bn, wm, wn, 4>), grid, dim3(64 * wm * wn), 0, stream, a); \
+    else                                                                                                 \
+      hipLaunchKernelGGL((gemm3_f32_kernel<bm, bn, wm, wn, 1>), grid, dim3(64 * wm * wn), 0, stream, a); \
+    break;
+    KH_GEMM3_CONFIGS(KH_CFG3_CASE)
+#undef KH_CFG3_CASE
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -472,12 +812,25 @@ std::unique_ptr<Op> make_gemm(const kh_launch &L, std::string &err, bool &unsupp
   op->a_vec_layout = a.sa_k == 1 && L.refs[0].offset % 4 == 0 && a.sa_m % 4 == 0 && a.sa_b % 4 == 0;
   op->b_vec_layout = a.sb_n == 1 && L.refs[1].offset % 4 == 0 && a.sb_k % 4 == 0 && a.sb_b % 4 == 0;
   if (!fill_epilogue(L, a, op->e_vec_candidates, err)) return nullptr;
-  a.tiles_m = (int)((M + t.bm - 1) / t.bm);
-  a.tiles_n = (int)((N + t.bn - 1) / t.bn);
+  int cfg_run = cfg;
+  if (t.kind == 3) {
+    // 128-bit copies never straddle the end of a row or of K
+    op->a_vec_layout = op->a_vec_layout && K % 4 == 0;
+    op->b_vec_layout = op->b_vec_layout && N % 4 == 0;
+    // per-lane copy offsets are 32-bit byte offsets: fall back to a general
+    // kernel for operands spanning 2^29 elements or more
+    const int64_t span_a = std::max<int64_t>(0, M - 1) * std::abs(a.sa_m) + std::max<int64_t>(0, K - 1) * std::abs(a.sa_k);
+    const int64_t span_b = std::max<int64_t>(0, K - 1) * std::abs(a.sb_k) + std::max<int64_t>(0, N - 1) * std::abs(a.sb_n);
+    if (span_a >= (1ll << 29) || span_b >= (1ll << 29) || a.sa_m < 0 || a.sa_k < 0 || a.sb_k < 0 || a.sb_n < 0)
+      cfg_run = kFallbackConfig;
+  }
+  const TileCfg &tr = kConfigs[cfg_run];
+  a.tiles_m = (int)((M + tr.bm - 1) / tr.bm);
+  a.tiles_n = (int)((N + tr.bn - 1) / tr.bn);
   int splitk = std::max(1, L.cfg[2]);
-  const int k_steps = (int)std::max<int64_t>(1, (K + t.bk - 1) / t.bk);
+  const int k_steps = (int)std::max<int64_t>(1, (K + tr.bk - 1) / tr.bk);
   splitk = std::min(splitk, k_steps);
-  a.k_per_split = ((k_steps + splitk - 1) / splitk) * t.bk;
+  a.k_per_split = ((k_steps + splitk - 1) / splitk) * tr.bk;
   splitk = (int)std::max<int64_t>(1, (K + a.k_per_split - 1) / std::max(1, a.k_per_split));
   if (K == 0) splitk = 1, a.k_per_split = 0;
   a.splitk = splitk;
@@ -487,7 +840,7 @@ std::unique_ptr<Op> make_gemm(const kh_launch &L, std::string &err, bool &unsupp
     err = "matmul: too many tiles";
     return nullptr;
   }
-  op->cfg = cfg;
+  op->cfg = cfg_run;
   op->grid = dim3((unsigned)n_tiles, (unsigned)batch, (unsigned)splitk);
   if (splitk > 1) {
     op->n_partials = (size_t)splitk * batch * M * N;

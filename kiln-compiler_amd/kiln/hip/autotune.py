@@ -35,26 +35,33 @@ GEMV_CANDIDATES = [(v, 0) for v in range(6)] + [(0, s) for s in (2, 4)]
 
 # (BM, BN, BK, WM, WN, WK, MFMA) of the compiled configurations, by id; must
 # match the table in csrc/kh_gemm.hip (tests check it against kh_gemm_config).
+# Ids 0-7 are the LDS-copy pipeline, 8-14 the register-staged kernel.
 TILES = {
-    0: (128, 128, 32, 2, 2, 1, 32),
-    1: (128, 192, 32, 2, 2, 1, 32),
-    2: (256, 128, 32, 2, 2, 1, 32),
-    3: (64, 64, 32, 2, 2, 1, 32),
-    4: (64, 128, 32, 2, 2, 1, 32),
-    5: (128, 64, 32, 2, 2, 1, 32),
-    6: (32, 64, 32, 1, 2, 2, 32),
-    7: (32, 32, 32, 1, 1, 4, 32),
-    8: (64, 64, 32, 1, 1, 4, 32),
-    9: (32, 32, 32, 2, 2, 1, 16),
-    10: (16, 64, 32, 1, 4, 1, 16),
-    11: (64, 32, 32, 2, 2, 1, 16),
-    12: (128, 128, 32, 4, 2, 1, 32),
-    13: (128, 192, 32, 4, 2, 1, 32),
-    14: (256, 128, 32, 4, 2, 1, 32),
-    15: (64, 128, 64, 2, 2, 1, 32),
-    16: (128, 64, 64, 2, 2, 1, 32),
-    17: (64, 64, 64, 2, 2, 1, 32),
+    0: (64, 128, 32, 2, 2, 1, 16),
+    1: (128, 64, 32, 2, 2, 1, 16),
+    2: (64, 64, 32, 2, 2, 1, 16),
+    3: (32, 128, 32, 1, 4, 1, 16),
+    4: (32, 64, 32, 2, 2, 1, 16),
+    5: (64, 96, 32, 2, 2, 1, 16),
+    6: (128, 192, 32, 2, 4, 1, 16),
+    7: (128, 128, 32, 2, 4, 1, 16),
+    8: (64, 64, 32, 2, 2, 1, 32),
+    9: (32, 64, 32, 1, 2, 2, 32),
+    10: (32, 32, 32, 1, 1, 4, 32),
+    11: (32, 32, 32, 2, 2, 1, 16),
+    12: (16, 64, 32, 1, 4, 1, 16),
+    13: (64, 32, 32, 2, 2, 1, 16),
+    14: (64, 64, 64, 2, 2, 1, 32),
 }
+# workgroups of each configuration one CU holds at once (LDS / VGPR bound,
+# from the compiler's resource report) and its measured main-loop efficiency
+# (fraction of the CU's fp32 MFMA rate), for the default heuristic only
+OCCUPANCY = {0: 2, 1: 2, 2: 3, 3: 2, 4: 4, 5: 2, 6: 1, 7: 1, 8: 4, 9: 4, 10: 4, 11: 5, 12: 5, 13: 4, 14: 2}
+EFFICIENCY = {0: 0.62, 1: 0.6, 2: 0.62, 3: 0.58, 4: 0.66, 5: 0.62, 6: 0.67, 7: 0.55,
+              8: 0.55, 9: 0.55, 10: 0.5, 11: 0.5, 12: 0.45, 13: 0.5, 14: 0.55}
+CU_MFLOP_PER_US = 0.614          # fp32 MFMA: 256 flop/clk/CU at 2.4 GHz
+ROUND_OVERHEAD_US = 8.0          # launch, prologue and epilogue of one round of workgroups
+REDUCE_US = 3.0                  # split-K reduce kernel launch
 DEFAULT_CUS = 256
 
 
@@ -81,15 +88,18 @@ def fits(tile, m, n, k) -> bool:
 
 
 def estimate(tile, splitk, batch, m, n, k, cus) -> float:
-    """Relative time model: rounds of workgroups over the CUs x per-tile work,
-    with a penalty for small (inefficient) tiles and for split-K traffic."""
-    bm, bn, bk, wm, wn, wk, mt = TILES[tile]
+    """Modelled microseconds: rounds of co-resident workgroups x a fixed
+    overhead, plus the MFMA time of the busiest CU (its workgroups share the
+    CU's matrix cores), plus the split-K reduce (partials through HBM)."""
+    bm, bn, bk = TILES[tile][:3]
     units = math.ceil(m / bm) * math.ceil(n / bn) * batch * splitk
-    rounds = math.ceil(units / cus)
+    rounds = math.ceil(units / (cus * OCCUPANCY[tile]))
     kper = math.ceil(k / splitk / bk) * bk
-    waves = wm * wn * wk
-    efficiency = min(1.0, (bm * bn) / (128 * 128)) ** 0.25 * (1.0 if waves == 4 else 0.9)
-    return rounds * bm * bn * kper / efficiency + (splitk > 1) * bm * bn * splitk * 8
+    per_cu = math.ceil(units / cus) * 2 * bm * bn * kper / 1e6 / CU_MFLOP_PER_US / EFFICIENCY[tile]
+    t = rounds * ROUND_OVERHEAD_US + per_cu
+    if splitk > 1:
+        t += REDUCE_US + batch * m * n * 4 * (splitk + 1) / 4e6
+    return t
 
 
 def default_matmul_config(graph, kernel, cus=None) -> dict:
@@ -118,7 +128,7 @@ def default_config_for(batch, m, n, k, cus=None) -> dict:
             if best is None or t < best[0]:
                 best = (t, tile, s)
     if best is None:
-        return {"tile": 9, "splitk": 1}
+        return {"tile": 11, "splitk": 1}
     return {"tile": best[1], "splitk": best[2]}
 
 

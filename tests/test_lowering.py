@@ -204,7 +204,7 @@ def test_unknown_precision_is_not_implemented():
 def test_split_k_workspace_is_reported():
     _, prog = lowered(lambda a, b: a @ b, torch.randn(128, 3072), torch.randn(3072, 768))
     d = kl.LaunchDesc.from_buffer_copy(prog.launches[0].desc)
-    d.cfg[1], d.cfg[2] = 3, 4          # 64x64 tiles, split-K 4
+    d.cfg[1], d.cfg[2] = 2, 4          # 64x64 tiles, split-K 4
     plan = kl.Plan([d])
     # dense fp32 partials [split][batch][M][N]; no counters
     assert plan.workspace_bytes == 4 * 128 * 768 * 4
