@@ -6,7 +6,7 @@
 // share the argument block, the epilogue tape and the split-K scheme:
 //   * gemm3_f32_kernel (configurations 0-7), the main path: fp32 operands on
 //     v_mfma_f32_16x16x4_f32, global memory copied straight into LDS
-//     (global_load_lds) through a three-stage ring two K steps ahead of the
+//     (global_load_lds) through a ring of LDS stages, two K steps ahead of the
 //     matrix cores, XOR/rotation-swizzled LDS chunks, four or eight waves per
 //     workgroup sized so that one to four workgroups share a CU; its design
 //     notes are at the kernel;
@@ -322,9 +322,10 @@ __global__ __launch_bounds__(64 * WM * WN * WK) void gemm_f32_kernel(const GemmA
 // ---------------------------------------------------------------------------
 // Pipelined variant: global memory is copied straight into LDS
 // (global_load_lds, 128-bit per lane for aligned row-major operands, 32-bit
-// for any other strides) through three LDS stages, two steps ahead of the
-// matrix cores, so no VGPRs hold data in flight and a load has two MFMA
-// phases to arrive.
+// for any other strides) through a ring of NS LDS stages, NS - 1 steps ahead
+// of the matrix cores, so no VGPRs hold data in flight and a load has NS - 1
+// MFMA phases to arrive. (Rings deeper than 3 were measured on the BASELINE
+// shapes and won nowhere, so every configuration uses NS = 3.)
 //   * K advances in steps of 32. Within a step, lane group g of an MFMA
 //     (lanes l / 16) owns K values 8g .. 8g+7 and MFMA j consumes value 8g + j
 //     in every group: each lane reads its A values as two 128-bit LDS vectors
@@ -394,7 +395,7 @@ __device__ __forceinline__ void stage_barrier() {
   asm volatile("" ::: "memory");
 }
 
-template <int BM, int BN, int WM, int WN, int VW>
+template <int BM, int BN, int WM, int WN, int NS, int VW>
 __global__ __launch_bounds__(64 * WM * WN, 2) void gemm3_f32_kernel(const GemmArgs a) {
   constexpr int MT = 16, BK = 32;
   constexpr int kWaves = WM * WN, kThreads = 64 * kWaves;
@@ -411,11 +412,11 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void gemm3_f32_kernel(const GemmAr
   static_assert(TM % MT == 0 && TN % MT == 0, "wave tile must be a multiple of the MFMA tile");
   static_assert(A_INSN % kWaves == 0 && B_INSN % kWaves == 0, "copy mapping");
   static_assert(BN % 16 == 0 && B_CH >= 16, "B chunk rotation");
-  static_assert(COPIES < 64, "vmcnt");
+  static_assert(NS >= 3 && (NS - 2) * COPIES < 64, "vmcnt");
   using M = Mfma<MT>;
   typedef typename M::acc_t acc_t;
 
-  __shared__ float4 st0[STAGE / 4], st1[STAGE / 4], st2[STAGE / 4];
+  __shared__ float4 ring[NS * STAGE / 4];
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
@@ -562,35 +563,35 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void gemm3_f32_kernel(const GemmAr
 #pragma unroll
         for (int fn = 0; fn < FN; ++fn) acc[fm][fn] = M::mma(af[fm][j], bf[fn][j], acc[fm][fn]);
   };
-  // one step on stage `cur`: copies of step s+2 go into `nxt2`; afterwards the
-  // copies of step s+1 (into `nxt1`) must be visible to every wave
-  auto step = [&](int s, float4 *cur, float4 *nxt1, float4 *nxt2) {
-    if (s + 2 < n_steps) issue(s + 2, nxt2);
-    compute(cur);
-    if (s + 1 < n_steps) {
-      if (s + 2 < n_steps) wait_vmcnt<COPIES>();
-      else wait_vmcnt<0>();
-      zero_tail(s + 1, nxt1);
+  // wait until this wave's copies of step `s` have landed, knowing that the
+  // copies of `later` further steps were issued after them
+  auto wait_step = [&](int later) {
+    switch (later) {
+      case 0: wait_vmcnt<0>(); break;
+      case 1: wait_vmcnt<COPIES>(); break;
+      case 2: wait_vmcnt<(NS > 3 ? 2 : 1) * COPIES>(); break;
+      case 3: wait_vmcnt<(NS > 4 ? 3 : 1) * COPIES>(); break;
+      default: wait_vmcnt<(NS > 5 ? 4 : 1) * COPIES>(); break;
     }
-    stage_barrier();
   };
+  static_assert(NS <= 6, "wait_step covers up to 4 later steps");
 
   if (n_steps > 0) {
-    issue(0, st0);
-    if (n_steps > 1) {
-      issue(1, st1);
-      wait_vmcnt<COPIES>();
-    } else {
-      wait_vmcnt<0>();
-    }
-    zero_tail(0, st0);
+    for (int p = 0; p < NS - 1 && p < n_steps; ++p) issue(p, ring + p * (STAGE / 4));
+    wait_step(min(NS - 2, n_steps - 1));
+    zero_tail(0, ring);
     stage_barrier();
-    for (int s = 0; s < n_steps; s += 3) {
-      step(s, st0, st1, st2);
-      if (s + 1 >= n_steps) break;
-      step(s + 1, st1, st2, st0);
-      if (s + 2 >= n_steps) break;
-      step(s + 2, st2, st0, st1);
+    int cur = 0, nxt = NS - 1;  // ring slots of step s and of step s + NS - 1
+    for (int s = 0; s < n_steps; ++s) {
+      if (s + NS - 1 < n_steps) issue(s + NS - 1, ring + nxt * (STAGE / 4));
+      compute(ring + cur * (STAGE / 4));
+      cur = cur + 1 == NS ? 0 : cur + 1;
+      nxt = nxt + 1 == NS ? 0 : nxt + 1;
+      if (s + 1 < n_steps) {
+        wait_step(min(NS - 2, n_steps - 2 - s));
+        zero_tail(s + 1, ring + cur * (STAGE / 4));
+      }
+      stage_barrier();
     }
   }
 
@@ -598,8 +599,8 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void gemm3_f32_kernel(const GemmAr
   // block (16 x TN per wave) at a time and read them back as row-contiguous
   // groups of 4.
   constexpr int CS = TN + 4;
-  static_assert(kWaves * MT * CS <= STAGE, "epilogue staging");
-  float *Cw = reinterpret_cast<float *>(st0) + wave * MT * CS;
+  static_assert(kWaves * MT * CS <= NS * STAGE, "epilogue staging");
+  float *Cw = reinterpret_cast<float *>(ring) + wave * MT * CS;
   const int row0 = m0 + wm * TM, col0 = n0 + wn * TN;
   float *part = a.splitk > 1 ? a.ws_partial + ((int64_t)split * a.batch + bidx) * (int64_t)a.M * a.N : nullptr;
   const bool vec = (a.N & 3) == 0;
@@ -638,26 +639,26 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void gemm3_f32_kernel(const GemmAr
 // Host side.
 
 struct TileCfg {
-  int bm, bn, bk, wm, wn, wk, mt, kind;  // kind 1: register-staged loads; 3: LDS-copy pipeline
+  int bm, bn, bk, wm, wn, wk, mt, kind, stages;  // kind 1: register-staged loads; 3: LDS-copy pipeline
 };
 
 // Configurations by id. Ids 0-7: the copy pipeline (BK = 32, MFMA
-// 16x16x4; each has a 128-bit and a 32-bit copy variant, chosen at launch
-// from the operand layouts). Ids 8-14: register-staged loads, for skinny
-// tiles and K split across the waves of a workgroup.
+// 16x16x4, NS LDS stages; each has a 128-bit and a 32-bit copy variant,
+// chosen at launch from the operand layouts). Ids 8-14: register-staged
+// loads, for skinny tiles and K split across the waves of a workgroup.
 #define KH_GEMM3_CONFIGS(X) \
-  X(0, 64, 128, 2, 2)       \
-  X(1, 128, 64, 2, 2)       \
-  X(2, 64, 64, 2, 2)        \
-  X(3, 32, 128, 1, 4)       \
-  X(4, 32, 64, 2, 2)        \
-  X(5, 64, 96, 2, 2)        \
-  X(6, 128, 192, 2, 4)      \
-  X(7, 128, 128, 2, 4)
+  X(0, 64, 128, 2, 2, 3)    \
+  X(1, 128, 64, 2, 2, 3)    \
+  X(2, 64, 64, 2, 2, 3)     \
+  X(3, 32, 128, 1, 4, 3)    \
+  X(4, 32, 64, 2, 2, 3)     \
+  X(5, 64, 96, 2, 2, 3)     \
+  X(6, 128, 192, 2, 4, 3)   \
+  X(7, 128, 128, 2, 4, 3)
 
 #define KH_GEMM_CONFIGS(X)        \
-  X(8, 64, 64, 32, 2, 2, 1, 32)   \
-  X(9, 32, 64, 32, 1, 2, 2, 32)   \
+  X(8, 64, 64, 32, 2, 2, 1, 32)  \
+  X(9, 32, 64, 32, 1, 2, 2, 32)  \
   X(10, 32, 32, 32, 1, 1, 4, 32)  \
   X(11, 32, 32, 32, 2, 2, 1, 16)  \
   X(12, 16, 64, 32, 1, 4, 1, 16)  \
@@ -669,10 +670,10 @@ struct TileCfg {
 constexpr int kFallbackConfig = 8;
 
 constexpr TileCfg kConfigs[] = {
-#define KH_CFG3_ROW(id, bm, bn, wm, wn) {bm, bn, 32, wm, wn, 1, 16, 3},
+#define KH_CFG3_ROW(id, bm, bn, wm, wn, ns) {bm, bn, 32, wm, wn, 1, 16, 3, ns},
     KH_GEMM3_CONFIGS(KH_CFG3_ROW)
 #undef KH_CFG3_ROW
-#define KH_CFG_ROW(id, bm, bn, bk, wm, wn, wk, mt) {bm, bn, bk, wm, wn, wk, mt, 1},
+#define KH_CFG_ROW(id, bm, bn, bk, wm, wn, wk, mt) {bm, bn, bk, wm, wn, wk, mt, 1, 2},
     KH_GEMM_CONFIGS(KH_CFG_ROW)
 #undef KH_CFG_ROW
 };
@@ -687,12 +688,12 @@ hipError_t launch_config(int id, const GemmArgs &a, dim3 grid, hipStream_t strea
     break;
     KH_GEMM_CONFIGS(KH_CFG_CASE)
 #undef KH_CFG_CASE
-#define KH_CFG3_CASE(cid, bm, bn, wm, wn)                                                                \
-  case cid:                                                                                              \
-    if (a.a_vec && a.b_vec)                                                                              \
-      hipLaunchKernelGGL((gemm3_f32_kernel<bm, bn, wm, wn, 4>), grid, dim3(64 * wm * wn), 0, stream, a); \
-    else                                                                                                 \
-      hipLaunchKernelGGL((gemm3_f32_kernel<bm, bn, wm, wn, 1>), grid, dim3(64 * wm * wn), 0, stream, a); \
+#define KH_CFG3_CASE(cid, bm, bn, wm, wn, ns)                                                                 \
+  case cid:                                                                                                  \
+    if (a.a_vec && a.b_vec)                                                                                  \
+      hipLaunchKernelGGL((gemm3_f32_kernel<bm, bn, wm, wn, ns, 4>), grid, dim3(64 * wm * wn), 0, stream, a); \
+    else                                                                                                     \
+      hipLaunchKernelGGL((gemm3_f32_kernel<bm, bn, wm, wn, ns, 1>), grid, dim3(64 * wm * wn), 0, stream, a); \
     break;
     KH_GEMM3_CONFIGS(KH_CFG3_CASE)
 #undef KH_CFG3_CASE

@@ -60,33 +60,6 @@ __device__ __forceinline__ void run_epilogue(const GemmArgs &a, int64_t b, int64
   exec_tape<kFastSlots>(a.insns, 0, a.n_insns, a.n_pre, f, load, store, [](const kh_insn &, const Vec<4> &) {});
 }
 
-// Run the epilogue tape for rows [m, m + valid) of output column (b, n): the
-// layout an MFMA accumulator leaves in a lane (4 consecutive rows of one
-// column). Operands broadcast along M (bias) are read once.
-__device__ __forceinline__ void run_epilogue_rows(const GemmArgs &a, int64_t b, int64_t m, int64_t n, int valid,
-                                                  const Vec<4> &acc) {
-  auto base = [&](int j) { return a.eptr[j] + b * a.estride[j][0] + n * a.estride[j][2]; };
-  auto load = [&](int j) -> Vec<4> {
-    const float *p = base(j);
-    const int64_t sm = a.estride[j][1];
-    if (sm == 0) return splat4(p[0]);
-    Vec<4> out;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) out.v[i] = i < valid ? p[(m + i) * sm] : 0.0f;
-    return out;
-  };
-  auto store = [&](int j, const Vec<4> &v) {
-    float *p = base(j);
-    const int64_t sm = a.estride[j][1];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (i < valid) p[(m + i) * sm] = v.v[i];
-  };
-  float f[kFastSlots * 4];
-  bank_set(f, 0, acc);
-  exec_tape<kFastSlots>(a.insns, 0, a.n_insns, a.n_pre, f, load, store, [](const kh_insn &, const Vec<4> &) {});
-}
-
 // Split-K, second kernel: partials are dense [split][batch][M][N] fp32 in the
 // workspace (written by the first kernel without any cross-workgroup
 // synchronisation; the kernel boundary makes them visible to every XCD).
