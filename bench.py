@@ -325,29 +325,57 @@ def block_sweep(tokens, autotune):
     return out
 
 
+GEMM_SHAPES = [(2048, 3072, 768), (128, 2304, 768), (128, 768, 768), (128, 3072, 768), (128, 768, 3072),
+               (1, 3072, 768)]
+
+
 def gemm_sweep(autotune):
+    """BASELINE's nn.Linear sweep (bias epilogue), fp32 and, reported
+    separately, the bf16-input / fp32-accumulate variant. TFLOP/s from GPU time
+    of a 20-call graph replay; eager torch beside each (bf16 with inputs
+    already cast, its best case). bf16 also reports the fraction of the
+    attainable bound min(bf16 peak, AI x 8 TB/s), AI from the algorithmic
+    bytes (fp32 X, bf16 W, fp32 bias and output)."""
     import torch
+    import torch.nn.functional as F
 
     import kiln
     from models.transformer import gpt2_init_
 
-    shapes = [(2048, 3072, 768), (128, 2304, 768), (128, 768, 768), (128, 3072, 768), (128, 768, 3072),
-              (1, 3072, 768)]
-    out = {}
-    for m, n, k in shapes:
+    out = {"fp32": {}, "bf16": {}}
+    for m, n, k in GEMM_SHAPES:
         torch.manual_seed(0)
         lin = gpt2_init_(torch.nn.Linear(k, n), seed=1).eval().cuda()
         x = torch.randn(m, k, device="cuda")
+        flops = 2 * m * n * k
         c = kiln.compile(lin, (x,), device="cuda", autotune=autotune, cuda_graphs=False)
         with torch.no_grad():
             torch.testing.assert_close(c(x), lin(x), rtol=1e-4, atol=1e-5)
             outs = [torch.empty(m, n, device="cuda")]
             kms = graph_ms(lambda: c._exe.run_into([x], outs))
             ems = graph_ms(lambda: lin(x))
-        flops = 2 * m * n * k
-        out[f"{m}x{n}x{k}"] = {"kiln_tflops": round(flops / kms / 1e9, 2), "torch_tflops": round(flops / ems / 1e9, 2),
-                               "kiln_us": round(kms * 1e3, 2)}
-        log(f"gemm {m}x{n}x{k}: kiln {flops / kms / 1e9:.1f} TFLOP/s, torch {flops / ems / 1e9:.1f}")
+        out["fp32"][f"{m}x{n}x{k}"] = {"kiln_tflops": round(flops / kms / 1e9, 2),
+                                       "torch_tflops": round(flops / ems / 1e9, 2), "kiln_us": round(kms * 1e3, 2),
+                                       "frac_of_fp32_peak": round(flops / kms / 1e9 / FP32_PEAK_TFLOPS, 3)}
+        log(f"gemm fp32 {m}x{n}x{k}: kiln {flops / kms / 1e9:.1f} TFLOP/s, torch {flops / ems / 1e9:.1f}")
+        cb = kiln.compile(lin, (x,), device="cuda", autotune=autotune, cuda_graphs=False, matmul_precision="bf16")
+        xb, wb, bb = x.bfloat16(), lin.weight.detach().bfloat16().contiguous(), lin.bias.detach().bfloat16()
+        with torch.no_grad():
+            ref = lin(x)
+            got = cb(x)
+            err = ((got - ref).abs().max() / ref.abs().max()).item()
+            assert err <= 2e-2, f"bf16 GEMM {m}x{n}x{k}: error {err:.2e} of the output scale"
+            bms = graph_ms(lambda: cb._exe.run_into([x], outs))
+            tms = graph_ms(lambda: F.linear(xb, wb, bb))
+        nbytes = 4 * m * k + 2 * k * n + 4 * n + 4 * m * n
+        attainable = min(BF16_PEAK_TFLOPS, flops / nbytes * HBM_PEAK_GBS / 1e3)
+        tf = flops / bms / 1e9
+        out["bf16"][f"{m}x{n}x{k}"] = {"kiln_tflops": round(tf, 2), "torch_tflops": round(flops / tms / 1e9, 2),
+                                       "kiln_us": round(bms * 1e3, 2), "error_of_scale": float(f"{err:.2e}"),
+                                       "attainable_tflops": round(attainable, 1),
+                                       "frac_of_attainable": round(tf / attainable, 3)}
+        log(f"gemm bf16 {m}x{n}x{k}: kiln {tf:.1f} TFLOP/s ({tf / attainable:.1%} of attainable "
+            f"{attainable:.0f}), torch-bf16 {flops / tms / 1e9:.1f}")
     return out
 
 

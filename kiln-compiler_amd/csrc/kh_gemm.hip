@@ -395,23 +395,39 @@ __device__ __forceinline__ void stage_barrier() {
   asm volatile("" ::: "memory");
 }
 
-template <int BM, int BN, int WM, int WN, int NS, int VW>
+// B rows of a bf16 stage are 32 K values = 64 bytes = 4 chunks; row n puts
+// chunk c at c ^ swz_b16(n), so the 16 rows one 128-bit fragment read
+// touches hit distinct banks.
+__device__ __forceinline__ int swz_b16(int n) { return ((n >> 1) ^ (n >> 3)) & 3; }
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// BF16B: B is a bf16 copy of a constant in [batch][N][K'] layout (K' = K
+// rounded up to 8, zero padded) and the products run on
+// v_mfma_f32_16x16x32_bf16 with A rounded to bf16 (round to nearest even) as
+// its fragments are read; accumulation stays fp32. In a 32-wide K step lane
+// group g holds K values 8g .. 8g+7 of A and of B - the same ownership as
+// the fp32 path, where MFMA j consumes value 8g + j.
+template <int BM, int BN, int WM, int WN, int NS, int VW, bool BF16B>
 __global__ __launch_bounds__(64 * WM * WN, 2) void gemm3_f32_kernel(const GemmArgs a) {
   constexpr int MT = 16, BK = 32;
   constexpr int kWaves = WM * WN, kThreads = 64 * kWaves;
   constexpr int TM = BM / WM, TN = BN / WN;
   constexpr int FM = TM / MT, FN = TN / MT;
   constexpr int KG = 8;                 // K values per lane group per step
-  constexpr int B_CH = BN / 4;          // chunks per B row
-  constexpr int A_FLOATS = BM * BK, B_FLOATS = BK * BN, STAGE = A_FLOATS + B_FLOATS;
+  constexpr int B_CH = BN / 4;          // chunks per fp32 B row
+  // stage sizes in 4-byte words (a bf16 B stage is BN rows of 64 bytes)
+  constexpr int A_FLOATS = BM * BK, B_FLOATS = BF16B ? BN * BK / 2 : BK * BN, STAGE = A_FLOATS + B_FLOATS;
+  // B copy width in 4-byte words per lane
+  constexpr int VB = BF16B ? 4 : VW;
   // copy instructions per wave per step: each covers 64 lanes x VW floats
-  constexpr int A_INSN = A_FLOATS / (64 * VW), B_INSN = B_FLOATS / (64 * VW);
+  constexpr int A_INSN = A_FLOATS / (64 * VW), B_INSN = B_FLOATS / (64 * VB);
   constexpr int A_PER_WAVE = A_INSN / kWaves, B_PER_WAVE = B_INSN / kWaves;
   constexpr int COPIES = A_PER_WAVE + B_PER_WAVE;
   static_assert(VW == 4 || VW == 1, "copy width");
   static_assert(TM % MT == 0 && TN % MT == 0, "wave tile must be a multiple of the MFMA tile");
   static_assert(A_INSN % kWaves == 0 && B_INSN % kWaves == 0, "copy mapping");
-  static_assert(BN % 16 == 0 && B_CH >= 16, "B chunk rotation");
+  static_assert(BF16B || (BN % 16 == 0 && B_CH >= 16), "B chunk rotation");
   static_assert(NS >= 3 && (NS - 2) * COPIES < 64, "vmcnt");
   using M = Mfma<MT>;
   typedef typename M::acc_t acc_t;
@@ -457,26 +473,37 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void gemm3_f32_kernel(const GemmAr
 #pragma unroll
   for (int i = 0; i < B_PER_WAVE; ++i) {
     const int p = (wave * B_PER_WAVE + i) * 64 + lane;
-    int k, nn;
-    if constexpr (VW == 4) {
-      k = p / B_CH;
-      const int g = k / KG;
-      nn = (((p % B_CH) - 4 * g + 4 * B_CH) % B_CH) * 4;
+    if constexpr (BF16B) {
+      // byte offsets into the bf16 copy: row n, chunk of 8 K values
+      const int n = p / 4;
+      const int kk = ((p % 4) ^ swz_b16(n)) * 8;
+      b_mn[i] = min(n0 + n, a.N - 1) * (int)a.sb_n;
+      b_kk[i] = kk;
+      b_off0[i] = (uint32_t)(b_mn[i] + kk) * 2u;
     } else {
-      k = p / BN;
-      const int g = k / KG;
-      const int pc = (p % BN) / 4;
-      nn = (((pc - 4 * g + 4 * B_CH) % B_CH) * 4) + (p & 3);
+      int k, nn;
+      if constexpr (VW == 4) {
+        k = p / B_CH;
+        const int g = k / KG;
+        nn = (((p % B_CH) - 4 * g + 4 * B_CH) % B_CH) * 4;
+      } else {
+        k = p / BN;
+        const int g = k / KG;
+        const int pc = (p % BN) / 4;
+        nn = (((pc - 4 * g + 4 * B_CH) % B_CH) * 4) + (p & 3);
+      }
+      b_mn[i] = min(n0 + nn, a.N - VW) * (int)a.sb_n;
+      b_kk[i] = k;
+      b_off0[i] = (uint32_t)(b_mn[i] + k * (int)a.sb_k) * 4u;
     }
-    b_mn[i] = min(n0 + nn, a.N - VW) * (int)a.sb_n;
-    b_kk[i] = k;
-    b_off0[i] = (uint32_t)(b_mn[i] + k * (int)a.sb_k) * 4u;
   }
   // issue the copies of step `step` into `stage`
   auto issue = [&](int step, float4 *stage) {
     const int k0 = k_begin + step * BK;
     const float *abase = uniform_ptr(Ab + (int64_t)k0 * a.sa_k);
-    const float *bbase = uniform_ptr(Bb + (int64_t)k0 * a.sb_k);
+    const float *bbase = BF16B ? uniform_ptr(reinterpret_cast<const float *>(
+                                     reinterpret_cast<const __bf16 *>(a.B) + (int64_t)bidx * a.sb_b + k0))
+                               : uniform_ptr(Bb + (int64_t)k0 * a.sb_k);
     const uint32_t lds = (uint32_t)(uintptr_t)(lds_void_t *)stage;
     if (k0 + BK <= k_end) {
 #pragma unroll
@@ -484,7 +511,7 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void gemm3_f32_kernel(const GemmAr
         copy_to_lds<VW>(abase, a_off0[i], lds + ((wave_u * A_PER_WAVE + i) * 64 * VW) * 4);
 #pragma unroll
       for (int i = 0; i < B_PER_WAVE; ++i)
-        copy_to_lds<VW>(bbase, b_off0[i], lds + (A_FLOATS + (wave_u * B_PER_WAVE + i) * 64 * VW) * 4);
+        copy_to_lds<VB>(bbase, b_off0[i], lds + (A_FLOATS + (wave_u * B_PER_WAVE + i) * 64 * VB) * 4);
     } else {
       // last, partial step: K indices clamped into the range (zeroed later)
       const int kmax = k_end - k0;
@@ -493,12 +520,18 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void gemm3_f32_kernel(const GemmAr
         copy_to_lds<VW>(abase, (uint32_t)(a_mn[i] + min(a_kk[i], kmax - VW) * (int)a.sa_k) * 4u,
                         lds + ((wave_u * A_PER_WAVE + i) * 64 * VW) * 4);
 #pragma unroll
-      for (int i = 0; i < B_PER_WAVE; ++i)
-        copy_to_lds<VW>(bbase, (uint32_t)(b_mn[i] + min(b_kk[i], kmax - 1) * (int)a.sb_k) * 4u,
-                        lds + (A_FLOATS + (wave_u * B_PER_WAVE + i) * 64 * VW) * 4);
+      for (int i = 0; i < B_PER_WAVE; ++i) {
+        uint32_t off;
+        if constexpr (BF16B)
+          off = (uint32_t)(b_mn[i] + min(b_kk[i], ((kmax - 1) / 8) * 8)) * 2u;
+        else
+          off = (uint32_t)(b_mn[i] + min(b_kk[i], kmax - 1) * (int)a.sb_k) * 4u;
+        copy_to_lds<VB>(bbase, off, lds + (A_FLOATS + (wave_u * B_PER_WAVE + i) * 64 * VB) * 4);
+      }
     }
   };
   // after this thread's copies of `step` landed: zero what lies past k_end
+  // (a bf16 chunk straddling k_end holds the copy's zero padding past K)
   auto zero_tail = [&](int step, float4 *stage) {
     const int k0 = k_begin + step * BK;
     if (k0 + BK <= k_end) return;
@@ -512,10 +545,10 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void gemm3_f32_kernel(const GemmAr
     }
 #pragma unroll
     for (int i = 0; i < B_PER_WAVE; ++i) {
-      float *d = st + A_FLOATS + ((wave * B_PER_WAVE + i) * 64 + lane) * VW;
+      float *d = st + A_FLOATS + ((wave * B_PER_WAVE + i) * 64 + lane) * VB;
       if (k0 + b_kk[i] >= k_end)
 #pragma unroll
-        for (int e = 0; e < VW; ++e) d[e] = 0.0f;
+        for (int e = 0; e < VB; ++e) d[e] = 0.0f;
     }
   };
 
@@ -531,7 +564,10 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void gemm3_f32_kernel(const GemmAr
 #pragma unroll
   for (int fn = 0; fn < FN; ++fn) {
     const int n = wn * TN + fn * MT + li;
-    b_off[fn] = A_FLOATS + g * KG * BN + ((((n / 4) + 4 * g) % B_CH) * 4) + (n & 3);
+    if constexpr (BF16B)
+      b_off[fn] = A_FLOATS + n * (BK / 2) + ((g ^ swz_b16(n)) * 4);  // word offset of 8 bf16
+    else
+      b_off[fn] = A_FLOATS + g * KG * BN + ((((n / 4) + 4 * g) % B_CH) * 4) + (n & 3);
   }
 
   acc_t acc[FM][FN];
@@ -544,7 +580,7 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void gemm3_f32_kernel(const GemmAr
 
   auto compute = [&](const float4 *stage) {
     const float *st = reinterpret_cast<const float *>(stage);
-    float af[FM][KG], bf[FN][KG];
+    float af[FM][KG];
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
@@ -552,16 +588,32 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void gemm3_f32_kernel(const GemmAr
         const float4 v = *reinterpret_cast<const float4 *>(st + a_off[fm][h]);
         af[fm][4 * h + 0] = v.x, af[fm][4 * h + 1] = v.y, af[fm][4 * h + 2] = v.z, af[fm][4 * h + 3] = v.w;
       }
-#pragma unroll
-    for (int fn = 0; fn < FN; ++fn)
-#pragma unroll
-      for (int j = 0; j < KG; ++j) bf[fn][j] = st[b_off[fn] + j * BN];
-#pragma unroll
-    for (int j = 0; j < KG; ++j)
+    if constexpr (BF16B) {
+      bf16x8 a8[FM], b8[FN];
 #pragma unroll
       for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
-        for (int fn = 0; fn < FN; ++fn) acc[fm][fn] = M::mma(af[fm][j], bf[fn][j], acc[fm][fn]);
+        for (int e = 0; e < 8; ++e) a8[fm][e] = (__bf16)af[fm][e];
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn) b8[fn] = *reinterpret_cast<const bf16x8 *>(st + b_off[fn]);
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn)
+          acc[fm][fn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a8[fm], b8[fn], acc[fm][fn], 0, 0, 0);
+    } else {
+      float bf[FN][KG];
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+        for (int j = 0; j < KG; ++j) bf[fn][j] = st[b_off[fn] + j * BN];
+#pragma unroll
+      for (int j = 0; j < KG; ++j)
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+          for (int fn = 0; fn < FN; ++fn) acc[fm][fn] = M::mma(af[fm][j], bf[fn][j], acc[fm][fn]);
+    }
   };
   // wait until this wave's copies of step `s` have landed, knowing that the
   // copies of `later` further steps were issued after them
@@ -639,7 +691,7 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void gemm3_f32_kernel(const GemmAr
 // Host side.
 
 struct TileCfg {
-  int bm, bn, bk, wm, wn, wk, mt, kind, stages;  // kind 1: register-staged loads; 3: LDS-copy pipeline
+  int bm, bn, bk, wm, wn, wk, mt, kind, stages, prec;  // kind 1: register-staged loads; 3: LDS-copy pipeline
 };
 
 // Configurations by id. Ids 0-7: the copy pipeline (BK = 32, MFMA
@@ -665,17 +717,30 @@ struct TileCfg {
   X(13, 64, 32, 32, 2, 2, 1, 16)  \
   X(14, 64, 64, 64, 2, 2, 1, 32)
 
+// bf16-input configurations of the copy pipeline (B is a bf16 copy of a
+// constant, A fp32 rounded to bf16 in the kernel)
+#define KH_GEMM3_BF16_CONFIGS(X) \
+  X(15, 128, 128, 2, 2, 3)       \
+  X(16, 64, 128, 2, 2, 4)        \
+  X(17, 128, 64, 2, 2, 4)        \
+  X(18, 64, 64, 2, 2, 4)         \
+  X(19, 32, 64, 2, 2, 4)         \
+  X(20, 128, 256, 2, 4, 3)
+
 // the register-staged configuration a pipelined tile falls back to for
 // operands too large for 32-bit copy offsets
 constexpr int kFallbackConfig = 8;
 
 constexpr TileCfg kConfigs[] = {
-#define KH_CFG3_ROW(id, bm, bn, wm, wn, ns) {bm, bn, 32, wm, wn, 1, 16, 3, ns},
+#define KH_CFG3_ROW(id, bm, bn, wm, wn, ns) {bm, bn, 32, wm, wn, 1, 16, 3, ns, KH_PREC_FP32},
     KH_GEMM3_CONFIGS(KH_CFG3_ROW)
 #undef KH_CFG3_ROW
-#define KH_CFG_ROW(id, bm, bn, bk, wm, wn, wk, mt) {bm, bn, bk, wm, wn, wk, mt, 1, 2},
+#define KH_CFG_ROW(id, bm, bn, bk, wm, wn, wk, mt) {bm, bn, bk, wm, wn, wk, mt, 1, 2, KH_PREC_FP32},
     KH_GEMM_CONFIGS(KH_CFG_ROW)
 #undef KH_CFG_ROW
+#define KH_CFGB_ROW(id, bm, bn, wm, wn, ns) {bm, bn, 32, wm, wn, 1, 16, 3, ns, KH_PREC_BF16},
+    KH_GEMM3_BF16_CONFIGS(KH_CFGB_ROW)
+#undef KH_CFGB_ROW
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
@@ -688,14 +753,24 @@ hipError_t launch_config(int id, const GemmArgs &a, dim3 grid, hipStream_t strea
     break;
     KH_GEMM_CONFIGS(KH_CFG_CASE)
 #undef KH_CFG_CASE
-#define KH_CFG3_CASE(cid, bm, bn, wm, wn, ns)                                                                 \
-  case cid:                                                                                                  \
-    if (a.a_vec && a.b_vec)                                                                                  \
-      hipLaunchKernelGGL((gemm3_f32_kernel<bm, bn, wm, wn, ns, 4>), grid, dim3(64 * wm * wn), 0, stream, a); \
-    else                                                                                                     \
-      hipLaunchKernelGGL((gemm3_f32_kernel<bm, bn, wm, wn, ns, 1>), grid, dim3(64 * wm * wn), 0, stream, a); \
+#define KH_CFG3_CASE(cid, bm, bn, wm, wn, ns)                                                                        \
+  case cid:                                                                                                         \
+    if (a.a_vec && a.b_vec)                                                                                         \
+      hipLaunchKernelGGL((gemm3_f32_kernel<bm, bn, wm, wn, ns, 4, false>), grid, dim3(64 * wm * wn), 0, stream, a); \
+    else                                                                                                            \
+      hipLaunchKernelGGL((gemm3_f32_kernel<bm, bn, wm, wn, ns, 1, false>), grid, dim3(64 * wm * wn), 0, stream, a); \
     break;
     KH_GEMM3_CONFIGS(KH_CFG3_CASE)
+#undef KH_CFG3_CASE
+#define KH_CFGB_CASE(cid, bm, bn, wm, wn, ns)                                                                      \
+  case cid:                                                                                                       \
+    if (a.a_vec)                                                                                                  \
+      hipLaunchKernelGGL((gemm3_f32_kernel<bm, bn, wm, wn, ns, 4, true>), grid, dim3(64 * wm * wn), 0, stream, a); \
+    else                                                                                                          \
+      hipLaunchKernelGGL((gemm3_f32_kernel<bm, bn, wm, wn, ns, 1, true>), grid, dim3(64 * wm * wn), 0, stream, a); \
+    break;
+    KH_GEMM3_BF16_CONFIGS(KH_CFGB_CASE)
+#undef KH_CFGB_CASE
 #undef KH_CFG3_CASE
     default: return hipErrorInvalidValue;
   }
@@ -740,7 +815,7 @@ int gemm_config_count() { return kNumConfigs; }
 bool gemm_config(int id, int32_t out8[8]) {
   if (id < 0 || id >= kNumConfigs) return false;
   const TileCfg &t = kConfigs[id];
-  const int32_t v[8] = {t.bm, t.bn, t.bk, t.wm, t.wn, t.wk, t.mt, KH_PREC_FP32};
+  const int32_t v[8] = {t.bm, t.bn, t.bk, t.wm, t.wn, t.wk, t.mt, t.prec};
   std::memcpy(out8, v, sizeof(v));
   return true;
 }
@@ -801,12 +876,16 @@ std::unique_ptr<Op> make_gemm(const kh_launch &L, std::string &err, bool &unsupp
     err = "matmul: unknown tile configuration " + std::to_string(cfg);
     return nullptr;
   }
-  if (L.cfg[3] != KH_PREC_FP32) {
+  if (L.cfg[3] != KH_PREC_FP32 && L.cfg[3] != KH_PREC_BF16) {
     unsupported = true;
     err = "matmul: precision not compiled into this library";
     return nullptr;
   }
   const TileCfg &t = kConfigs[cfg];
+  if (L.cfg[3] != t.prec) {
+    err = "matmul: tile configuration " + std::to_string(cfg) + " is for another precision";
+    return nullptr;
+  }
   a.batch = (int)batch, a.M = (int)M, a.N = (int)N, a.K = (int)K;
   a.sa_b = L.refs[0].strides[0], a.sa_m = L.refs[0].strides[1], a.sa_k = L.refs[0].strides[2];
   a.sb_b = L.refs[1].strides[0], a.sb_k = L.refs[1].strides[1], a.sb_n = L.refs[1].strides[2];
@@ -814,6 +893,16 @@ std::unique_ptr<Op> make_gemm(const kh_launch &L, std::string &err, bool &unsupp
   op->b_vec_layout = a.sb_n == 1 && L.refs[1].offset % 4 == 0 && a.sb_k % 4 == 0 && a.sb_b % 4 == 0;
   if (!fill_epilogue(L, a, op->e_vec_candidates, err)) return nullptr;
   int cfg_run = cfg;
+  if (t.prec == KH_PREC_BF16) {
+    // B must be the library-layout bf16 copy: [batch][N][K'] with K' a
+    // multiple of 8 (16-byte rows), unit K stride
+    const kh_ref &rb = L.refs[1];
+    if (a.sb_k != 1 || a.sb_n % 8 || a.sb_b % 8 || rb.offset % 8 || a.sb_n < K) {
+      err = "matmul: bf16 B operand must be [batch][N][K'] with K' a multiple of 8 and >= K";
+      return nullptr;
+    }
+    op->b_vec_layout = true;
+  }
   if (t.kind == 3) {
     // 128-bit copies never straddle the end of a row or of K
     op->a_vec_layout = op->a_vec_layout && K % 4 == 0;
@@ -822,8 +911,14 @@ std::unique_ptr<Op> make_gemm(const kh_launch &L, std::string &err, bool &unsupp
     // kernel for operands spanning 2^29 elements or more
     const int64_t span_a = std::max<int64_t>(0, M - 1) * std::abs(a.sa_m) + std::max<int64_t>(0, K - 1) * std::abs(a.sa_k);
     const int64_t span_b = std::max<int64_t>(0, K - 1) * std::abs(a.sb_k) + std::max<int64_t>(0, N - 1) * std::abs(a.sb_n);
-    if (span_a >= (1ll << 29) || span_b >= (1ll << 29) || a.sa_m < 0 || a.sa_k < 0 || a.sb_k < 0 || a.sb_n < 0)
+    if (span_a >= (1ll << 29) || span_b >= (1ll << 29) || a.sa_m < 0 || a.sa_k < 0 || a.sb_k < 0 || a.sb_n < 0) {
+      if (t.prec == KH_PREC_BF16) {
+        unsupported = true;
+        err = "matmul: bf16 operands spanning 2^29 elements or more";
+        return nullptr;
+      }
       cfg_run = kFallbackConfig;
+    }
   }
   const TileCfg &tr = kConfigs[cfg_run];
   a.tiles_m = (int)((M + tr.bm - 1) / tr.bm);

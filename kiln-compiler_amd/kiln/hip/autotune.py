@@ -52,13 +52,26 @@ TILES = {
     12: (16, 64, 32, 1, 4, 1, 16),
     13: (64, 32, 32, 2, 2, 1, 16),
     14: (64, 64, 64, 2, 2, 1, 32),
+    15: (128, 128, 32, 2, 2, 1, 16),
+    16: (64, 128, 32, 2, 2, 1, 16),
+    17: (128, 64, 32, 2, 2, 1, 16),
+    18: (64, 64, 32, 2, 2, 1, 16),
+    19: (32, 64, 32, 2, 2, 1, 16),
+    20: (128, 256, 32, 2, 4, 1, 16),
 }
+# input precision of each configuration: 0-14 fp32, 15-20 bf16 (A rounded in
+# the kernel, B a bf16 copy of a constant)
+PRECISION = {t: ("bf16" if t >= 15 else "fp32") for t in TILES}
 # workgroups of each configuration one CU holds at once (LDS / VGPR bound,
 # from the compiler's resource report) and its measured main-loop efficiency
 # (fraction of the CU's fp32 MFMA rate), for the default heuristic only
-OCCUPANCY = {0: 2, 1: 2, 2: 3, 3: 2, 4: 4, 5: 2, 6: 1, 7: 1, 8: 4, 9: 4, 10: 4, 11: 5, 12: 5, 13: 4, 14: 2}
+OCCUPANCY = {0: 2, 1: 2, 2: 3, 3: 2, 4: 4, 5: 2, 6: 1, 7: 1, 8: 4, 9: 4, 10: 4, 11: 5, 12: 5, 13: 4, 14: 2,
+             15: 2, 16: 2, 17: 1, 18: 3, 19: 4, 20: 1}
 EFFICIENCY = {0: 0.62, 1: 0.6, 2: 0.62, 3: 0.58, 4: 0.66, 5: 0.62, 6: 0.67, 7: 0.55,
-              8: 0.55, 9: 0.55, 10: 0.5, 11: 0.5, 12: 0.45, 13: 0.5, 14: 0.55}
+              8: 0.55, 9: 0.55, 10: 0.5, 11: 0.5, 12: 0.45, 13: 0.5, 14: 0.55,
+              15: 0.15, 16: 0.15, 17: 0.15, 18: 0.15, 19: 0.15, 20: 0.15}
+# MFMA rate of a CU relative to fp32, per precision
+RATE = {"fp32": 1.0, "bf16": 16.0}
 CU_MFLOP_PER_US = 0.614          # fp32 MFMA: 256 flop/clk/CU at 2.4 GHz
 ROUND_OVERHEAD_US = 8.0          # launch, prologue and epilogue of one round of workgroups
 REDUCE_US = 3.0                  # split-K reduce kernel launch
@@ -87,7 +100,7 @@ def fits(tile, m, n, k) -> bool:
     return bm <= max(16, p2(m)) and bn <= max(16, p2(n))
 
 
-def estimate(tile, splitk, batch, m, n, k, cus) -> float:
+def estimate(tile, splitk, batch, m, n, k, cus) -> float:  # noqa: C901
     """Modelled microseconds: rounds of co-resident workgroups x a fixed
     overhead, plus the MFMA time of the busiest CU (its workgroups share the
     CU's matrix cores), plus the split-K reduce (partials through HBM)."""
@@ -95,7 +108,8 @@ def estimate(tile, splitk, batch, m, n, k, cus) -> float:
     units = math.ceil(m / bm) * math.ceil(n / bn) * batch * splitk
     rounds = math.ceil(units / (cus * OCCUPANCY[tile]))
     kper = math.ceil(k / splitk / bk) * bk
-    per_cu = math.ceil(units / cus) * 2 * bm * bn * kper / 1e6 / CU_MFLOP_PER_US / EFFICIENCY[tile]
+    per_cu = (math.ceil(units / cus) * 2 * bm * bn * kper / 1e6 / CU_MFLOP_PER_US / EFFICIENCY[tile]
+              / RATE[PRECISION[tile]])
     t = rounds * ROUND_OVERHEAD_US + per_cu
     if splitk > 1:
         t += REDUCE_US + batch * m * n * 4 * (splitk + 1) / 4e6
@@ -113,13 +127,13 @@ def default_matmul_config(graph, kernel, cus=None) -> dict:
     return default_config_for(batch, m, n, k, cus)
 
 
-def default_config_for(batch, m, n, k, cus=None) -> dict:
-    if m == 1:
+def default_config_for(batch, m, n, k, cus=None, precision="fp32") -> dict:
+    if m == 1 and precision == "fp32":
         return {"tile": 0, "splitk": 0}
     cus = cus or device_cus()
     best = None
     for tile in TILES:
-        if not fits(tile, m, n, k):
+        if PRECISION[tile] != precision or not fits(tile, m, n, k):
             continue
         for s in SPLITS:
             if s > 1 and k // s < 128:
@@ -128,17 +142,17 @@ def default_config_for(batch, m, n, k, cus=None) -> dict:
             if best is None or t < best[0]:
                 best = (t, tile, s)
     if best is None:
-        return {"tile": 11, "splitk": 1}
+        return {"tile": 11 if precision == "fp32" else 19, "splitk": 1}
     return {"tile": best[1], "splitk": best[2]}
 
 
-def candidates(batch, m, n, k, cus=None) -> list:
-    if m == 1:
+def candidates(batch, m, n, k, cus=None, precision="fp32") -> list:
+    if m == 1 and precision == "fp32":
         return [{"tile": v, "splitk": s} for v, s in GEMV_CANDIDATES if s == 0 or k // s >= 64]
     cus = cus or device_cus()
     out = []
     for tile in TILES:
-        if not fits(tile, m, n, k):
+        if PRECISION[tile] != precision or not fits(tile, m, n, k):
             continue
         for s in SPLITS:
             if s > 1 and k // s < 64:
@@ -155,13 +169,15 @@ def cache_path() -> Path:
     return Path(base) / "hip_autotune.json"
 
 
-def _matmul_graph(batch, m, n, k):
+def _matmul_graph(batch, m, n, k, b_data=None):
+    """One-matmul graph; with `b_data` the B operand is a constant (the bf16
+    GEMM reads B as a bf16 copy of a constant)."""
     from kiln.ir import Graph, TensorType
 
     g = Graph("matmul")
     lead = (batch,) if batch > 1 else ()
     a = g.add_arg(TensorType((*lead, m, k)), "a")
-    b = g.add_arg(TensorType((*lead, k, n)), "b")
+    b = g.add_arg(TensorType((*lead, k, n)), "b") if b_data is None else g.constant(b_data, "b")
     g.results = [g.add_node("matmul", [a, b])]
     return g
 
@@ -206,7 +222,7 @@ class GPUAutotuner:
         key = f"{self.device_key()}|{self.precision}|{batch}x{m}x{n}x{k}"
         entry = self._cache.get(key)
         if not isinstance(entry, dict) or "config" not in entry:
-            entry = self.tune(batch, m, n, k, default_config_for(batch, m, n, k))
+            entry = self.tune(batch, m, n, k, default_config_for(batch, m, n, k, precision=self.precision))
             if entry["candidates"]:
                 self._cache[key] = entry
                 self._save()
@@ -216,12 +232,12 @@ class GPUAutotuner:
         self.log.append({"shape": (batch, m, n, k), "source": source, **entry})
         return dict(entry["config"])
 
-    def _compile(self, batch, m, n, k, config):
+    def _compile(self, batch, m, n, k, config, b_data=None):
         from kiln.api import Options, compile_graph
 
         opts = Options(device="cuda", cuda_graphs=False, matmul_precision=self.precision,
                        gpu_matmul_config=lambda *_: dict(config))
-        exe, _ = compile_graph(_matmul_graph(batch, m, n, k), opts)
+        exe, _ = compile_graph(_matmul_graph(batch, m, n, k, b_data), opts)
         return exe
 
     def tune(self, batch, m, n, k, default):
@@ -238,13 +254,16 @@ class GPUAutotuner:
         expected = (a.double() @ b.double()).float()
         tol = 1e-4 if self.precision == "fp32" else 2e-2
         scale = expected.abs().max().item() or 1.0
+        # the bf16 GEMM takes B as a constant (its bf16 copy is made at build time)
+        b_data = b.cpu().numpy() if self.precision == "bf16" else None
+        args = [a] if b_data is not None else [a, b]
         runs, seconds, rejected = {}, {}, []
-        configs = [default] + [c for c in candidates(batch, m, n, k) if c != default]
+        configs = [default] + [c for c in candidates(batch, m, n, k, precision=self.precision) if c != default]
         for cfg in configs:
             key = (cfg["tile"], cfg["splitk"])
             try:
-                exe = self._compile(batch, m, n, k, cfg)
-                (out,) = exe(a, b)
+                exe = self._compile(batch, m, n, k, cfg, b_data)
+                (out,) = exe(*args)
                 err = (out - expected).abs().max().item() / scale
                 if not err <= tol:
                     rejected.append(f"{cfg}: relative error {err:.1e}")
@@ -253,7 +272,7 @@ class GPUAutotuner:
                 rejected.append(f"{cfg}: {type(e).__name__}: {str(e).splitlines()[0][:80] if str(e) else ''}")
                 continue
             outs = [torch.empty_like(expected)]
-            runs[key] = lambda exe=exe, outs=outs: exe.run_into([a, b], outs)
+            runs[key] = lambda exe=exe, outs=outs: exe.run_into(args, outs)
             seconds[key] = kernel_seconds(runs[key], rounds=3)
         default_key = (default["tile"], default["splitk"])
         if not seconds:

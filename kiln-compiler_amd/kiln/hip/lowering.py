@@ -29,6 +29,7 @@ import hashlib
 import math
 from dataclasses import dataclass, field
 
+from kiln.hip import autotune, bf16
 from kiln.hip import lib as kl
 from kiln.ir import ops
 from kiln.ir.core import Graph, Kernel
@@ -60,6 +61,10 @@ class Program:
     launches: list = field(default_factory=list)
     consts: list = field(default_factory=list)   # const slot -> constant name
     precision: str = "fp32"
+    # constants made at build time from others: name -> (source constant,
+    # element offset, strides over (b, k, n), batch, K, N); today the bf16
+    # [batch][N][K'] copies of GEMM B operands (kiln/hip/bf16.py)
+    derived: dict = field(default_factory=dict)
 
     @property
     def source(self) -> str:
@@ -627,13 +632,21 @@ class _Lowerer:
                 r.strides[lead + i] = 0 if s == 1 and dims[lead + i] != 1 else st
             return r
 
-        gemv = m == 1
-        d = self.new_desc(kl.FAM_GEMV if gemv else kl.FAM_GEMM, "gemv" if gemv else "matmul", k, space3)
-        d.gemm[0], d.gemm[1], d.gemm[2], d.gemm[3] = batch, m, n, kk
         if a not in self.layouts or b not in self.layouts:
             raise NotImplementedError("HIP backend: matmul operand has no storage")
+        cfg = dict(self.matmul_config(self.g, k))
+        prec = cfg.get("precision", self.precision)
+        if prec == "bf16" and self.layouts[b].base[0] != "const":
+            # bf16 inputs need B as a build-time bf16 copy of a constant; a
+            # matmul on two activations stays on the fp32 path (more exact)
+            prec = "fp32"
+        gemv = m == 1 and prec == "fp32"
+        d = self.new_desc(kl.FAM_GEMV if gemv else kl.FAM_GEMM, "gemv" if gemv else "matmul", k, space3)
+        d.gemm[0], d.gemm[1], d.gemm[2], d.gemm[3] = batch, m, n, kk
         d.refs[0] = ref3(a, (batch, m, kk))
         d.refs[1] = ref3(b, (batch, kk, n))
+        if prec == "bf16":
+            d.refs[1] = self.bf16_weight(b, d.refs[1], batch, kk, n)
         externals = []
         for nd in k.nodes:
             if nd is mm:
@@ -682,7 +695,9 @@ class _Lowerer:
         if best is None:
             raise NotImplementedError("HIP backend: matmul epilogue needs more than 8 registers")
         _encode(best[0], best[1], d, ref_offset=2)
-        cfg = dict(self.matmul_config(self.g, k))
+        if not gemv and autotune.PRECISION.get(int(cfg.get("tile", -1))) != prec:
+            # a configuration of another precision (e.g. the fp32 fallback above)
+            cfg = {**cfg, **autotune.default_config_for(batch, m, n, kk, precision=prec)}
         if gemv:
             # GEMV family: "tile" picks the workgroup variant (0 = from the
             # shape, 1-5), split-K 0 = from the shape
@@ -691,17 +706,33 @@ class _Lowerer:
                    "precision": cfg.get("precision", self.precision)}
         d.cfg[1] = int(cfg.get("tile", 0))
         d.cfg[2] = int(cfg.get("splitk", 1))
-        d.cfg[3] = {"fp32": kl.PREC_FP32, "bf16": kl.PREC_BF16, "bf16x3": kl.PREC_BF16X3}[
-            cfg.get("precision", self.precision)]
+        d.cfg[3] = {"fp32": kl.PREC_FP32, "bf16": kl.PREC_BF16, "bf16x3": kl.PREC_BF16X3}[prec]
         flops = 2 * batch * m * n * kk
         nbytes = 4 * (math.prod(a.shape) + math.prod(b.shape) + sum(math.prod(v.shape) for v in externals)
                       + len(outs) * math.prod(out_shape))
         epi = " ".join(nd.op for nd in k.nodes if nd is not mm)
         summary = f"{batch}x{m}x{n}x{kk}"
         summary += f" tile {d.cfg[1]} splitk {d.cfg[2]}"
+        if prec != "fp32":
+            summary += f" {prec}"
         if epi:
             summary += f" epilogue: {epi}"
         self.add(d, k, summary, flops=flops, nbytes=nbytes)
+
+    def bf16_weight(self, b, ref, batch, kk, n):
+        """Ref of the bf16 [batch][N][K'] copy of constant view `b` (whose fp32
+        ref over (b, k, n) is `ref`); the copy is registered as a derived
+        constant and made when the executable is built."""
+        src = self.layouts[b].base[1]
+        strides = (int(ref.strides[0]), int(ref.strides[1]), int(ref.strides[2]))
+        name = f"{src}@bf16:{int(ref.offset)}:{strides[0]},{strides[1]},{strides[2]}:{batch}x{kk}x{n}"
+        self.program.derived[name] = (src, int(ref.offset), strides, batch, kk, n)
+        kp = bf16.padded_k(kk)
+        r = kl.Ref()
+        r.base, r.index = self.slot_of(("const", name))
+        r.offset = 0
+        r.strides[0], r.strides[1], r.strides[2] = (n * kp if batch > 1 else 0), 1, kp
+        return r
 
     # attention --------------------------------------------------------------------------------
 

@@ -27,6 +27,7 @@ from pathlib import Path
 import numpy as np
 import torch
 
+from kiln.hip import bf16
 from kiln.hip import lib as kl
 
 
@@ -131,7 +132,8 @@ class HIPExecutable:
         self.debug = debug
 
         self.plan = kl.Plan([l.desc for l in program.launches])
-        const_bytes = sum(int(constants[n].nbytes) for n in program.consts)
+        host_consts = [self._host_constant(program, constants, n) for n in program.consts]
+        const_bytes = sum(int(c.nbytes) for c in host_consts)
         out_bytes = sum(4 * int(np.prod(s)) for s in self.output_shapes)
         ws_bytes = self.plan.workspace_bytes
         check_memory(self.device, arena_bytes + const_bytes + out_bytes + ws_bytes,
@@ -139,8 +141,7 @@ class HIPExecutable:
                      f"workspace ({ws_bytes / 2**20:.1f} MiB) and outputs")
         self.arena = torch.empty(max(arena_bytes, 256), dtype=torch.uint8, device=self.device)
         self.workspace = torch.zeros(max(ws_bytes, 256), dtype=torch.uint8, device=self.device)
-        self.constants = [torch.from_numpy(np.ascontiguousarray(constants[n], np.float32)).to(self.device)
-                          for n in program.consts]
+        self.constants = [torch.from_numpy(c).to(self.device) for c in host_consts]
         self.arena_bytes = arena_bytes
         self.weight_bytes = const_bytes
         self.plan.bind([t.data_ptr() for t in self.constants], self.arena.data_ptr(),
@@ -149,6 +150,15 @@ class HIPExecutable:
             self.arena.view(torch.float32)[: self.arena.numel() // 4].fill_(float("nan"))
         self.use_cuda_graphs = bool(cuda_graphs)
         self.captured = False
+
+    @staticmethod
+    def _host_constant(program, constants, name):
+        """Host array of const slot `name`: the fp32 constant, or a copy the
+        lowering derived from one (bf16 GEMM weights, as int16 bit patterns)."""
+        if name in program.derived:
+            src, offset, strides, batch, k, n = program.derived[name]
+            return bf16.weight_copy(constants[src], offset, strides, batch, k, n).view(np.int16)
+        return np.ascontiguousarray(constants[name], np.float32)
 
     # -- launching ------------------------------------------------------------------
 

@@ -4,7 +4,7 @@ TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
 cpu_baseline leg of bench.py, as the checker. The product (kiln/) never
 imports it.
 
-  * ``kiln_oracle.c`` (via ``lib()``): float64 restatements of GELU, bias+GELU,
+  * ``kiln_oracle.c`` (via ``lib()``): bf16 rounding and float64 restatements of GELU, bias+GELU,
     LayerNorm, softmax, strided batched matmul, Linear + epilogue and the
     GPT-2 block, following the reference's op definitions and decompositions
     (file:line citations in the C source).
@@ -42,7 +42,8 @@ def lib():
         L.ko_matmul.argtypes = [f, i64, i64, i64, f, i64, i64, i64, i64, i64, i64, i64, f]
         L.ko_linear.argtypes = [f, f, f, f, i, i64, i64, i64, f]
         L.ko_block.argtypes = [f, i64, i64, i64] + [f] * 12 + [f]
-        for name in ("ko_gelu", "ko_bias_gelu", "ko_layernorm", "ko_softmax", "ko_matmul", "ko_linear", "ko_block"):
+        L.ko_bf16_round.argtypes = [f, i64, f]
+        for name in ("ko_bf16_round", "ko_gelu", "ko_bias_gelu", "ko_layernorm", "ko_softmax", "ko_matmul", "ko_linear", "ko_block"):
             getattr(L, name).restype = None
         _lib = L
     return _lib
@@ -54,6 +55,14 @@ def _f32(a):
 
 def _p(a):
     return None if a is None else a.ctypes.data
+
+
+def bf16_round(x):
+    """Nearest bfloat16 value of each element (ties to even), as float32."""
+    x = _f32(x)
+    out = np.empty_like(x)
+    lib().ko_bf16_round(_p(x), x.size, _p(out))
+    return out
 
 
 def gelu(x, approximate="none"):

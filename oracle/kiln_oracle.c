@@ -31,6 +31,32 @@ KO_API void ko_gelu(const float *x, int64_t n, int approximate, float *out) {
   for (int64_t i = 0; i < n; ++i) out[i] = (float)gelu(x[i], approximate);
 }
 
+/* Round to the nearest bfloat16 value, ties to even, computed arithmetically
+ * (not from the float's bits): the value is scaled by its bf16 quantum - 2^(e-7)
+ * for a normal value in [2^e, 2^(e+1)), 2^-133 below 2^-126 - and rint()
+ * (the default rounding mode, half to even) picks the neighbour. Results
+ * beyond the largest finite bf16 (0x7F7F, (2 - 2^-7) * 2^127) become inf.
+ * Follows the bf16 rounding of the GEMM variant the north star states
+ * (bf16 inputs, fp32 accumulation). */
+KO_API void ko_bf16_round(const float *x, int64_t n, float *out) {
+  const double max_bf16 = (2.0 - ldexp(1.0, -7)) * ldexp(1.0, 127);
+  for (int64_t i = 0; i < n; ++i) {
+    const double v = x[i];
+    if (isnan(v) || isinf(v) || v == 0.0) {
+      out[i] = x[i];
+      continue;
+    }
+    int e;
+    frexp(fabs(v), &e); /* |v| = f * 2^e, f in [0.5, 1): leading bit 2^(e-1) */
+    int qexp = (e - 1) - 7;
+    if (qexp < -133) qexp = -133;
+    const double q = ldexp(1.0, qexp);
+    double r = rint(v / q) * q;
+    if (fabs(r) > max_bf16) r = r > 0 ? INFINITY : -INFINITY;
+    out[i] = (float)r;
+  }
+}
+
 /* bias + GELU over rows: out[r][c] = gelu(x[r][c] + b[c]) (bench_gpu.py:149). */
 KO_API void ko_bias_gelu(const float *x, const float *b, int64_t rows, int64_t cols, int approximate, float *out) {
   for (int64_t r = 0; r < rows; ++r)

@@ -1,0 +1,139 @@
+"""Parity of the bf16-input GEMM variant (matmul_precision="bf16").
+
+The variant rounds both GEMM inputs to bf16 (round to nearest, ties to even:
+the weights once, when the executable is built, the activations in the
+kernel) and accumulates in fp32. Two checks, both written per test:
+  * the exact reference of that computation: the C oracle's bf16 rounding of
+    the inputs, then a float64 product. Only fp32 accumulation separates the
+    kernel from it: |out - ref| <= 1e-4 * max|ref| (1e-4 relative to the
+    output scale; a wrong rounding mode alone moves results by ~1e-3);
+  * eager PyTorch fp32, at the north star's stated tolerance for bf16-input
+    variants: rtol 2e-2, with atol 2e-2 * max|ref| for outputs near zero.
+"""
+
+import copy
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import kiln
+import oracle
+from kiln.hip import autotune
+from models.transformer import Block, gpt2_init_
+
+pytestmark = pytest.mark.gpu
+
+EXACT = 1e-4          # relative to the output scale, against the rounded-input reference
+# Through a chain of GEMMs the rounded-input reference is only approximate:
+# the kernel's fp32 activations differ from the float64 reference's by ~1e-7,
+# and an activation that close to a bf16 rounding boundary rounds to the other
+# neighbour (a 2^-8 relative step in that input). 1e-3 of the output scale
+# covers such flips and still fails a wrong rounding mode or a dropped term.
+CHAINED = 1e-3
+STATED = 2e-2         # against eager fp32
+
+
+def r16(a):
+    return oracle.bf16_round(np.asarray(a, np.float32)).astype(np.float64)
+
+
+def close_to_scale(out, ref, tol):
+    out, ref = np.asarray(out, np.float64), np.asarray(ref, np.float64)
+    scale = max(np.abs(ref).max(), 1e-30)
+    err = np.abs(out - ref).max() / scale
+    assert err <= tol, f"max error {err:.2e} of the output scale > {tol:.0e}"
+
+
+def stated(out, eager):
+    eager = np.asarray(eager, np.float64)
+    np.testing.assert_allclose(np.asarray(out, np.float64), eager, rtol=STATED,
+                               atol=STATED * np.abs(eager).max())
+
+
+@pytest.mark.parametrize("mnk", [(2048, 3072, 768), (128, 2304, 768), (128, 768, 768), (128, 3072, 768),
+                                 (128, 768, 3072), (1, 3072, 768)])
+def test_config_gemm_sweep_bf16(mnk):
+    m, n, k = mnk
+    torch.manual_seed(0)
+    lin = gpt2_init_(torch.nn.Linear(k, n), seed=1).eval()
+    x = torch.randn(m, k)
+    c = kiln.compile(lin, (x,), device="cuda", matmul_precision="bf16")
+    assert c.report.lowering["precision"] == "bf16"
+    out = c(x.cuda()).cpu().numpy()
+    w, b = lin.weight.detach().numpy(), lin.bias.detach().numpy()
+    ref = r16(x.numpy()) @ r16(w).T + b.astype(np.float64)
+    close_to_scale(out, ref, EXACT)
+    with torch.no_grad():
+        stated(out, lin(x).numpy())
+
+
+@pytest.mark.parametrize("tile", [t for t in sorted(autotune.TILES) if autotune.PRECISION[t] == "bf16"])
+def test_every_bf16_tile_configuration(tile):
+    # ragged sizes (K = 61: not a multiple of 4 or 8), then interior tiles with
+    # ragged edges; bias + residual epilogue; split-K 1 and 2
+    for m, n, k in ((77, 133, 61), (300, 452, 96)):
+        torch.manual_seed(tile)
+        w = torch.randn(n, k) * 0.1
+        b, r = torch.randn(n), torch.randn(m, n)
+        model = torch.nn.Linear(k, n)
+        with torch.no_grad():
+            model.weight.copy_(w)
+            model.bias.copy_(b)
+        fn = lambda x, r: model(x) + r
+        x = torch.randn(m, k)
+        ref = r16(x.numpy()) @ r16(w.numpy()).T + b.numpy().astype(np.float64) + r.numpy()
+        for splitk in (1, 2):
+            c = kiln.compile(fn, (x, r), device="cuda", matmul_precision="bf16",
+                             gpu_matmul_config=lambda *_: {"tile": tile, "splitk": splitk})
+            close_to_scale(c(x, r).cpu().numpy(), ref, EXACT)
+
+
+def test_batched_constant_operand():
+    class M(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.w = torch.nn.Parameter(torch.randn(3, 24, 56))
+
+        def forward(self, x):
+            return torch.matmul(x, self.w)
+
+    model = M().eval()
+    x = torch.randn(3, 40, 24)
+    c = kiln.compile(model, (x,), device="cuda", matmul_precision="bf16")
+    ref = np.matmul(r16(x.numpy()), r16(model.w.detach().numpy()))
+    close_to_scale(c(x).cpu().numpy(), ref, EXACT)
+
+
+def test_activation_product_stays_fp32():
+    a, b = torch.randn(64, 32), torch.randn(32, 48)
+    c = kiln.compile(lambda a, b: a @ b, (a, b), device="cuda", matmul_precision="bf16")
+    np.testing.assert_allclose(c(a, b).cpu().numpy(), (a.double() @ b.double()).numpy(), rtol=1e-4, atol=1e-5)
+
+
+def _bf16_reference_block(model):
+    """float64 copy of the block whose Linear layers see bf16-rounded inputs
+    and weights - the computation the bf16 variant performs."""
+    ref = copy.deepcopy(model).double()
+    for mod in ref.modules():
+        if isinstance(mod, torch.nn.Linear):
+            with torch.no_grad():
+                mod.weight.copy_(torch.from_numpy(r16(mod.weight.float().numpy())))
+            mod.register_forward_pre_hook(
+                lambda m, args: (torch.from_numpy(r16(args[0].float().numpy())),))
+    return ref
+
+
+@pytest.mark.parametrize("T", [128, 512])
+def test_gpt2_block_bf16(T):
+    torch.manual_seed(0)
+    model = gpt2_init_(Block(768, 12, T), seed=0).eval()
+    x = torch.randn(T, 768)
+    c = kiln.compile(model, (x,), device="cuda", matmul_precision="bf16")
+    out = c(x.cuda()).cpu().numpy()
+    with torch.no_grad():
+        ref = _bf16_reference_block(model)(x.double()).numpy()
+        eager = model(x).numpy()
+    close_to_scale(out, ref, CHAINED)
+    stated(out, eager)

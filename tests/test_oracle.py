@@ -169,3 +169,28 @@ def test_interpreter_ops_brute_force():
     assert mx.tolist() == [[1.0], [3.0]]
     assert tr.tolist() == [[1.0, 0.0], [-2.0, 3.0], [0.25, -1.0]]
     assert clip.tolist() == [[1.0, 0.5, 0.5], [0.5, 3.0, 0.5]]
+
+
+def test_bf16_round_matches_torch_and_known_answers():
+    # torch's float -> bfloat16 conversion (round to nearest, ties to even) is
+    # the library routine; the oracle computes the rounding arithmetically
+    rng = np.random.default_rng(7)
+    x = (rng.standard_normal(200_000) * 10.0 ** rng.integers(-44, 38, 200_000)).astype(np.float32)
+    want = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    np.testing.assert_array_equal(oracle.bf16_round(x), want)
+    one = np.float32(1.0)
+    cases = {
+        1 + 2.0 ** -8: 1.0,                  # tie -> even (1.0)
+        1 + 3 * 2.0 ** -8: 1 + 2.0 ** -6,    # tie -> even (mantissa ...10)
+        1 + 2.0 ** -8 + 2.0 ** -12: 1 + 2.0 ** -7,   # above the tie
+        -(1 + 2.0 ** -7): -(1 + 2.0 ** -7),  # exact
+        3.4e38: np.inf,                      # past the largest finite bf16
+        2.0 ** -133: 2.0 ** -133,            # smallest subnormal
+        2.0 ** -134: 0.0,                    # half of it: tie -> even (0)
+    }
+    got = oracle.bf16_round(np.array(list(cases), np.float32))
+    np.testing.assert_array_equal(got, np.array(list(cases.values()), np.float32))
+    special = oracle.bf16_round(np.array([np.nan, np.inf, -np.inf, -0.0], np.float32))
+    assert np.isnan(special[0]) and special[1] == np.inf and special[2] == -np.inf
+    assert special[3] == 0 and np.signbit(special[3])
+    assert oracle.bf16_round(np.array([one], np.float32))[0] == one
