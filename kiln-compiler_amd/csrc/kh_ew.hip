@@ -133,7 +133,7 @@ struct EwFastArgs {
   FastDiv div;
 };
 
-constexpr int kFastUnroll = 4;
+constexpr int kFastUnroll = 2;
 
 template <int OP, int ACT>
 __global__ __launch_bounds__(kEwThreads) void ew_fast_kernel(const EwFastArgs a) {
@@ -274,7 +274,10 @@ std::unique_ptr<Op> try_fast_ew(const kh_launch &L, EwOp &generic, int rank, int
   f.total4 = g.total_groups;
   f.div = make_fastdiv(f.inner4);
   const int64_t blocks = ((int64_t)f.total4 + kEwThreads * kFastUnroll - 1) / (kEwThreads * kFastUnroll);
-  fast->grid = (int)std::max<int64_t>(1, std::min<int64_t>(blocks, (int64_t)current_device().cus * 16));
+  // one pass over the data, no grid-stride loop: workgroups start and retire
+  // at different times, so reads, arithmetic and writes of different waves
+  // overlap (a capped grid moves every phase in lockstep)
+  fast->grid = (int)std::max<int64_t>(1, std::min<int64_t>(blocks, (int64_t)1 << 30));
   auto copy = std::make_unique<EwOp>(generic);
   fast->fallback = std::move(copy);
   return fast;
