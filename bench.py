@@ -44,8 +44,8 @@ def log(*a):
 def parse():
     p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=20)
-    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--tokens", type=int, default=2048)
     p.add_argument("--quick", action="store_true", help="headline, roofline and CPU baseline only")
     p.add_argument("--no-cpu-baseline", action="store_true")

@@ -341,9 +341,13 @@ std::unique_ptr<Op> make_attn(const kh_launch &L, std::string &err, bool &unsupp
   if (nw <= 0) {
     const int64_t groups = batch * a.n_qblocks;
     const int64_t kblocks = (tk + kKB - 1) / kKB;
-    // four key-split waves per query block measured best from T = 128 to
-    // 2048 (more waves in flight, shorter critical path per workgroup)
+    // key blocks an average query block visits (half of them under a causal mask)
+    const int64_t visited = mask_mode == KH_ATTN_MASK_CAUSAL ? (kblocks + 1) / 2 : kblocks;
+    // measured on the GPT-2 shapes (12 heads, T = 128 .. 2048): four waves per
+    // query block, eight once each wave still gets two or more key blocks and
+    // the grid is under three workgroups per CU (T = 1024 .. 1536: 20% faster)
     nw = groups >= 16ll * current_device().cus ? 2 : 4;
+    if (nw == 4 && visited >= 16 && groups < 3ll * current_device().cus && dh == 64) nw = 8;
     if (kblocks < nw) nw = kblocks >= 2 ? 2 : 1;
   }
   if (nw != 1 && nw != 2 && nw != 4 && !(nw == 8 && dh == 64)) {

@@ -1,0 +1,50 @@
+"""Regenerate the shipped tuning table (kiln/hip/tuned_configs.json).
+
+    python -m kiln.hip.tune_shipped [--out PATH]
+
+Runs the measured autotuner (kiln.hip.autotune.GPUAutotuner, no cache, no
+shipped table) on one MI355X for every GEMM shape of the GPT-2-small block at
+T = 128, 512, 1024 and 2048 tokens, the 12-layer stack and the BASELINE GEMM
+sweep, in fp32 and bf16, and writes the winners keyed like the on-disk cache
+(device|CUs|precision|BxMxNxK). The table is what makes a plan the same on
+every MI355X: compiled models look their shapes up there before measuring.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import sys
+
+from kiln.hip import autotune
+
+SHAPES = sorted({
+    # GPT-2 block: qkv, attention projection, MLP up, MLP down, at each token count
+    *((t, n, k) for t in (128, 512, 1024, 2048) for n, k in ((2304, 768), (768, 768), (3072, 768), (768, 3072))),
+    # BASELINE GEMM sweep (the M = 1 decode shape is a GEMV in fp32)
+    (2048, 3072, 768), (128, 2304, 768), (128, 768, 768), (128, 3072, 768), (128, 768, 3072), (1, 3072, 768),
+    (1, 2304, 768), (1, 768, 768), (1, 768, 3072),
+})
+
+
+def main(argv=None):
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--out", default=str(autotune.SHIPPED_PATH))
+    args = p.parse_args(argv)
+    table = {}
+    for precision in ("fp32", "bf16"):
+        tuner = autotune.GPUAutotuner(precision=precision, use_cache=False, use_shipped=False)
+        device = tuner.device_key()
+        for m, n, k in SHAPES:
+            entry = tuner.tune(1, m, n, k, autotune.default_config_for(1, m, n, k, precision=precision))
+            if entry["candidates"]:
+                table[f"{device}|{precision}|1x{m}x{n}x{k}"] = entry
+            print(f"{precision} {m}x{n}x{k}: {entry['config']} {entry['tflops']} TFLOP/s", flush=True)
+    with open(args.out, "w") as f:
+        json.dump(table, f, indent=1, sort_keys=True)
+        f.write("\n")
+    print(f"wrote {len(table)} entries to {args.out}")
+
+
+if __name__ == "__main__":
+    sys.exit(main())

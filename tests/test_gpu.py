@@ -174,6 +174,7 @@ def test_random_graphs(seed, fusion):
 def test_autotune_is_correct_and_cached(monkeypatch):
     from kiln.hip.autotune import GPUAutotuner
 
+    # a shape the shipped table does not hold, so the first compile measures
     model = torch.nn.Sequential(torch.nn.Linear(48, 64), torch.nn.GELU(approximate="tanh")).eval()
     x = torch.randn(20, 48)
     first = check(model, x, autotune=True)
@@ -182,6 +183,18 @@ def test_autotune_is_correct_and_cached(monkeypatch):
     monkeypatch.setattr(GPUAutotuner, "tune", lambda *a, **k: pytest.fail("cached shape re-tuned"))
     second = check(model, x, autotune=True)
     assert second.report.autotune[0]["source"] == "cache"
+
+
+def test_shipped_table_is_used_before_measuring(monkeypatch):
+    from kiln.hip.autotune import GPUAutotuner, shipped_configs
+
+    if not shipped_configs():
+        pytest.skip("no shipped tuning table in this tree")
+    monkeypatch.setattr(GPUAutotuner, "tune", lambda *a, **k: pytest.fail("shipped shape re-tuned"))
+    lin = gpt2_init_(torch.nn.Linear(768, 3072), seed=1).eval()
+    x = torch.randn(128, 768)
+    c = check(lin, x, autotune=True)
+    assert c.report.autotune[0]["source"] == "shipped"
 
 
 def test_graph_replays_with_new_inputs():

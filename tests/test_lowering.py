@@ -267,3 +267,16 @@ def test_autotune_cache_is_ignored_when_corrupt(tmp_path):
     autotune.cache_path().parent.mkdir(parents=True, exist_ok=True)
     autotune.cache_path().write_text("{not json")
     assert autotune.GPUAutotuner()._cache == {}
+
+
+def test_shipped_tuning_table_is_consistent():
+    table = autotune.shipped_configs()
+    for key, entry in table.items():
+        arch, cus, precision, shape = key.split("|")
+        b, m, n, k = map(int, shape.split("x"))
+        tile = entry["config"]["tile"]
+        if m == 1 and precision == "fp32":
+            assert 0 <= tile <= 5          # GEMV workgroup variants
+        else:
+            assert autotune.PRECISION[tile] == precision and (m == 1 or autotune.fits(tile, m, n, k))
+        assert arch.startswith("gfx950") and int(cus) > 0
