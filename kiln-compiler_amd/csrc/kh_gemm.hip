@@ -350,6 +350,12 @@ __global__ __launch_bounds__(64 * WM * WN * WK) void gemm_f32_kernel(const GemmA
 typedef __attribute__((address_space(3))) void lds_void_t;
 
 __device__ __forceinline__ int swz_a(int r) { return (r ^ (r >> 3)) & 7; }
+// A rows of CH 16-byte chunks (CH = 8 for 32 floats, 16 for 64)
+template <int CH>
+__device__ __forceinline__ int swz_rows(int r) {
+  if constexpr (CH == 8) return swz_a(r);
+  else return (r ^ (r >> 4)) & (CH - 1);
+}
 
 // One wave-wide copy: lane l's VW floats at base + voff bytes go to LDS
 // byte address lds + l * 4 * VW (M0 holds the wave's LDS destination, `base`
@@ -408,13 +414,15 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 // its fragments are read; accumulation stays fp32. In a 32-wide K step lane
 // group g holds K values 8g .. 8g+7 of A and of B - the same ownership as
 // the fp32 path, where MFMA j consumes value 8g + j.
-template <int BM, int BN, int WM, int WN, int NS, int VW, bool BF16B>
+template <int BM, int BN, int BK, int WM, int WN, int NS, int VW, bool BF16B>
 __global__ __launch_bounds__(64 * WM * WN, 2) void gemm3_f32_kernel(const GemmArgs a) {
-  constexpr int MT = 16, BK = 32;
+  constexpr int MT = 16;
   constexpr int kWaves = WM * WN, kThreads = 64 * kWaves;
   constexpr int TM = BM / WM, TN = BN / WN;
   constexpr int FM = TM / MT, FN = TN / MT;
-  constexpr int KG = 8;                 // K values per lane group per step
+  constexpr int KG = BK / 4;            // K values per lane group per step
+  constexpr int ACH = BK / 4;           // 16-byte chunks per A row
+  static_assert(BK == 32 || (BK == 64 && !BF16B), "K step");
   constexpr int B_CH = BN / 4;          // chunks per fp32 B row
   // stage sizes in 4-byte words (a bf16 B stage is BN rows of 64 bytes)
   constexpr int A_FLOATS = BM * BK, B_FLOATS = BF16B ? BN * BK / 2 : BK * BN, STAGE = A_FLOATS + B_FLOATS;
@@ -428,7 +436,7 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void gemm3_f32_kernel(const GemmAr
   static_assert(TM % MT == 0 && TN % MT == 0, "wave tile must be a multiple of the MFMA tile");
   static_assert(A_INSN % kWaves == 0 && B_INSN % kWaves == 0, "copy mapping");
   static_assert(BF16B || (BN % 16 == 0 && B_CH >= 16), "B chunk rotation");
-  static_assert(NS >= 3 && (NS - 2) * COPIES < 64, "vmcnt");
+  static_assert(NS >= 2 && (NS - 2) * COPIES < 64, "vmcnt");
   using M = Mfma<MT>;
   typedef typename M::acc_t acc_t;
 
@@ -459,12 +467,12 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void gemm3_f32_kernel(const GemmAr
     const int p = (wave * A_PER_WAVE + i) * 64 + lane;  // LDS position (units of VW floats)
     int r, kk;
     if constexpr (VW == 4) {
-      r = p / 8;
-      kk = ((p % 8) ^ swz_a(r)) * 4;
+      r = p / ACH;
+      kk = ((p % ACH) ^ swz_rows<ACH>(r)) * 4;
     } else {
       r = p / BK;
       const int pc = (p % BK) / 4;
-      kk = ((pc ^ swz_a(r)) * 4) + (p & 3);
+      kk = ((pc ^ swz_rows<ACH>(r)) * 4) + (p & 3);
     }
     a_mn[i] = min(m0 + r, a.M - 1) * (int)a.sa_m;
     a_kk[i] = kk;
@@ -554,12 +562,13 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void gemm3_f32_kernel(const GemmAr
 
   // per-lane LDS offsets of the MFMA fragments (loop invariant)
   const int g = lane / MT, li = lane % MT;
-  int a_off[FM][2], b_off[FN];
+  constexpr int AH = KG / 4;             // 128-bit A reads per fragment
+  int a_off[FM][AH], b_off[FN];
 #pragma unroll
   for (int fm = 0; fm < FM; ++fm) {
     const int r = wm * TM + fm * MT + li;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) a_off[fm][h] = r * BK + (((2 * g + h) ^ swz_a(r)) * 4);
+    for (int h = 0; h < AH; ++h) a_off[fm][h] = r * BK + (((AH * g + h) ^ swz_rows<ACH>(r)) * 4);
   }
 #pragma unroll
   for (int fn = 0; fn < FN; ++fn) {
@@ -584,7 +593,7 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void gemm3_f32_kernel(const GemmAr
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
+      for (int h = 0; h < AH; ++h) {
         const float4 v = *reinterpret_cast<const float4 *>(st + a_off[fm][h]);
         af[fm][4 * h + 0] = v.x, af[fm][4 * h + 1] = v.y, af[fm][4 * h + 2] = v.z, af[fm][4 * h + 3] = v.w;
       }
@@ -618,6 +627,10 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void gemm3_f32_kernel(const GemmAr
   // wait until this wave's copies of step `s` have landed, knowing that the
   // copies of `later` further steps were issued after them
   auto wait_step = [&](int later) {
+    if constexpr (NS == 2) {
+      wait_vmcnt<0>();
+      return;
+    }
     switch (later) {
       case 0: wait_vmcnt<0>(); break;
       case 1: wait_vmcnt<COPIES>(); break;
@@ -645,6 +658,41 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void gemm3_f32_kernel(const GemmAr
       }
       stage_barrier();
     }
+  }
+
+  // Direct epilogue (bias / activation / residual recognised on the host):
+  // straight from the accumulators, 4 consecutive rows of one column per
+  // lane and MFMA block; the bias element is read once per column.
+  if (a.direct && a.splitk == 1) {
+    const int col_base = n0 + wn * TN + li, row_base = m0 + wm * TM + 4 * g;
+    const float *bias = a.d_bias >= 0 ? a.eptr[a.d_bias] + (int64_t)bidx * a.estride[a.d_bias][0] : nullptr;
+    const float *res = a.d_res >= 0 ? a.eptr[a.d_res] + (int64_t)bidx * a.estride[a.d_res][0] : nullptr;
+    float *out = a.eptr[a.d_out] + (int64_t)bidx * a.estride[a.d_out][0];
+    const int64_t bn = bias ? a.estride[a.d_bias][2] : 0;
+    const int64_t rm = res ? a.estride[a.d_res][1] : 0, rn = res ? a.estride[a.d_res][2] : 0;
+    const int64_t om = a.estride[a.d_out][1], on = a.estride[a.d_out][2];
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) {
+      const int n = col_base + fn * MT;
+      if (n >= a.N) continue;
+      const float bv = bias ? bias[n * bn] : 0.0f;
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int m = row_base + fm * MT + i;
+          if (m >= a.M) continue;
+          float v = acc[fm][fn][i];
+          if (bias) v += bv;
+          if (res) v = res[m * rm + n * rn] + v;
+          if (a.d_act == KH_OP_GELU_TANH) v = op_gelu_tanh(v);
+          else if (a.d_act == KH_OP_GELU_ERF) v = op_gelu_erf(v);
+          else if (a.d_act == KH_OP_RELU) v = v != v ? v : fmaxf(v, 0.0f);
+          out[m * om + n * on] = v;
+        }
+      }
+    }
+    return;
   }
 
   // Epilogue: the waves stage their accumulators through LDS one 16-row
@@ -698,15 +746,15 @@ struct TileCfg {
 // 16x16x4, NS LDS stages; each has a 128-bit and a 32-bit copy variant,
 // chosen at launch from the operand layouts). Ids 8-14: register-staged
 // loads, for skinny tiles and K split across the waves of a workgroup.
-#define KH_GEMM3_CONFIGS(X) \
-  X(0, 64, 128, 2, 2, 3)    \
-  X(1, 128, 64, 2, 2, 3)    \
-  X(2, 64, 64, 2, 2, 3)     \
-  X(3, 32, 128, 1, 4, 3)    \
-  X(4, 32, 64, 2, 2, 3)     \
-  X(5, 64, 96, 2, 2, 3)     \
-  X(6, 128, 192, 2, 4, 3)   \
-  X(7, 128, 128, 2, 4, 3)
+#define KH_GEMM3_CONFIGS(X)  \
+  X(0, 64, 128, 32, 2, 2, 3) \
+  X(1, 128, 64, 32, 2, 2, 3) \
+  X(2, 64, 64, 32, 2, 2, 3)  \
+  X(3, 32, 128, 32, 1, 4, 3) \
+  X(4, 32, 64, 32, 2, 2, 3)  \
+  X(5, 64, 96, 32, 2, 2, 3)  \
+  X(6, 128, 192, 32, 2, 4, 3) \
+  X(7, 128, 128, 32, 2, 4, 3)
 
 #define KH_GEMM_CONFIGS(X)        \
   X(8, 64, 64, 32, 2, 2, 1, 32)  \
@@ -727,12 +775,21 @@ struct TileCfg {
   X(19, 32, 64, 2, 2, 4)         \
   X(20, 128, 256, 2, 4, 3)
 
+// copy pipeline with 64 K values per stage (half the barriers and fragment
+// reads per flop; two stages to stay within LDS)
+#define KH_GEMM3_DEEP_CONFIGS(X) \
+  X(21, 64, 64, 64, 2, 2, 2)     \
+  X(22, 64, 128, 64, 2, 2, 2)    \
+  X(23, 32, 64, 64, 2, 2, 3)     \
+  X(24, 128, 192, 64, 2, 4, 2)   \
+  X(25, 64, 96, 64, 2, 2, 2)
+
 // the register-staged configuration a pipelined tile falls back to for
 // operands too large for 32-bit copy offsets
 constexpr int kFallbackConfig = 8;
 
 constexpr TileCfg kConfigs[] = {
-#define KH_CFG3_ROW(id, bm, bn, wm, wn, ns) {bm, bn, 32, wm, wn, 1, 16, 3, ns, KH_PREC_FP32},
+#define KH_CFG3_ROW(id, bm, bn, bk, wm, wn, ns) {bm, bn, bk, wm, wn, 1, 16, 3, ns, KH_PREC_FP32},
     KH_GEMM3_CONFIGS(KH_CFG3_ROW)
 #undef KH_CFG3_ROW
 #define KH_CFG_ROW(id, bm, bn, bk, wm, wn, wk, mt) {bm, bn, bk, wm, wn, wk, mt, 1, 2, KH_PREC_FP32},
@@ -741,6 +798,9 @@ constexpr TileCfg kConfigs[] = {
 #define KH_CFGB_ROW(id, bm, bn, wm, wn, ns) {bm, bn, 32, wm, wn, 1, 16, 3, ns, KH_PREC_BF16},
     KH_GEMM3_BF16_CONFIGS(KH_CFGB_ROW)
 #undef KH_CFGB_ROW
+#define KH_CFG3_ROW(id, bm, bn, bk, wm, wn, ns) {bm, bn, bk, wm, wn, 1, 16, 3, ns, KH_PREC_FP32},
+    KH_GEMM3_DEEP_CONFIGS(KH_CFG3_ROW)
+#undef KH_CFG3_ROW
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
@@ -753,25 +813,27 @@ hipError_t launch_config(int id, const GemmArgs &a, dim3 grid, hipStream_t strea
     break;
     KH_GEMM_CONFIGS(KH_CFG_CASE)
 #undef KH_CFG_CASE
-#define KH_CFG3_CASE(cid, bm, bn, wm, wn, ns)                                                                        \
-  case cid:                                                                                                         \
-    if (a.a_vec && a.b_vec)                                                                                         \
-      hipLaunchKernelGGL((gemm3_f32_kernel<bm, bn, wm, wn, ns, 4, false>), grid, dim3(64 * wm * wn), 0, stream, a); \
-    else                                                                                                            \
-      hipLaunchKernelGGL((gemm3_f32_kernel<bm, bn, wm, wn, ns, 1, false>), grid, dim3(64 * wm * wn), 0, stream, a); \
+#define KH_CFG3_CASE(cid, bm, bn, bk, wm, wn, ns)                                                         \
+  case cid:                                                                                              \
+    if (a.a_vec && a.b_vec)                                                                              \
+      hipLaunchKernelGGL((gemm3_f32_kernel<bm, bn, bk, wm, wn, ns, 4, false>), grid, dim3(64 * wm * wn), 0, \
+                         stream, a);                                                                     \
+    else                                                                                                 \
+      hipLaunchKernelGGL((gemm3_f32_kernel<bm, bn, bk, wm, wn, ns, 1, false>), grid, dim3(64 * wm * wn), 0, \
+                         stream, a);                                                                     \
     break;
     KH_GEMM3_CONFIGS(KH_CFG3_CASE)
+    KH_GEMM3_DEEP_CONFIGS(KH_CFG3_CASE)
 #undef KH_CFG3_CASE
 #define KH_CFGB_CASE(cid, bm, bn, wm, wn, ns)                                                                      \
   case cid:                                                                                                       \
     if (a.a_vec)                                                                                                  \
-      hipLaunchKernelGGL((gemm3_f32_kernel<bm, bn, wm, wn, ns, 4, true>), grid, dim3(64 * wm * wn), 0, stream, a); \
+      hipLaunchKernelGGL((gemm3_f32_kernel<bm, bn, 32, wm, wn, ns, 4, true>), grid, dim3(64 * wm * wn), 0, stream, a); \
     else                                                                                                          \
-      hipLaunchKernelGGL((gemm3_f32_kernel<bm, bn, wm, wn, ns, 1, true>), grid, dim3(64 * wm * wn), 0, stream, a); \
+      hipLaunchKernelGGL((gemm3_f32_kernel<bm, bn, 32, wm, wn, ns, 1, true>), grid, dim3(64 * wm * wn), 0, stream, a); \
     break;
     KH_GEMM3_BF16_CONFIGS(KH_CFGB_CASE)
 #undef KH_CFGB_CASE
-#undef KH_CFG3_CASE
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -817,6 +879,67 @@ bool gemm_config(int id, int32_t out8[8]) {
   const TileCfg &t = kConfigs[id];
   const int32_t v[8] = {t.bm, t.bn, t.bk, t.wm, t.wn, t.wk, t.mt, t.prec};
   std::memcpy(out8, v, sizeof(v));
+  return true;
+}
+
+// Recognise an epilogue tape of the form out = act((acc [+ bias]) [+ res])
+// (bias broadcast along M, act one of GELU tanh / GELU erf / ReLU, applied
+// last and only without a residual) and fill the direct-epilogue fields. The
+// tape is evaluated symbolically; additions match in either operand order
+// (IEEE addition is commutative), so the direct path computes bit for bit
+// what the tape computes. Returns false for any other tape.
+bool match_direct_epilogue(const kh_launch &L, GemmArgs &a) {
+  enum { kAcc = 1, kBias = 2, kRes = 4, kAct = 8 };
+  int slot[KH_NREGS];     // expression per slot: bitmask of kAcc/kBias/kRes/kAct, or -1 for a raw load
+  int loaded[KH_NREGS];   // ref a slot holds when it is a raw load
+  for (int i = 0; i < KH_NREGS; ++i) slot[i] = -2, loaded[i] = -1;
+  slot[0] = kAcc;
+  int bias = -1, res = -1, out = -1, act = -1, stores = 0;
+  auto full = [&](int j) {  // an [M, N] operand (not broadcast along M or N)
+    return a.estride[j][1] != 0 && a.estride[j][2] != 0;
+  };
+  for (int pc = 0; pc < L.n_insns; ++pc) {
+    const kh_insn &in = a.insns[pc];
+    if (in.op == KH_OP_LOAD) {
+      if (in.dst >= KH_NREGS) return false;
+      slot[in.dst] = -1, loaded[in.dst] = in.a;
+      continue;
+    }
+    if (in.op == KH_OP_STORE) {
+      if (in.a >= KH_NREGS || ++stores > 1 || slot[in.a] < 0 || !full(in.dst)) return false;
+      out = in.dst;
+      const int e = slot[in.a];
+      if (!(e & kAcc)) return false;
+      continue;
+    }
+    if (in.dst >= KH_NREGS || in.a >= KH_NREGS) return false;
+    if (in.op == KH_OP_ADD) {
+      if (in.b >= KH_NREGS) return false;
+      int x = in.a, y = in.b;
+      if (slot[x] == -1) std::swap(x, y);         // x: the accumulator expression, y: a raw load
+      if (slot[x] < 0 || slot[y] != -1) return false;
+      const int j = loaded[y], e = slot[x];
+      if (e & kAct) return false;
+      if (e == kAcc && a.estride[j][1] == 0 && a.estride[j][2] != 0) {
+        if (bias >= 0) return false;
+        bias = j, slot[in.dst] = e | kBias;
+      } else if (!(e & kRes) && full(j)) {
+        res = j, slot[in.dst] = e | kRes;
+      } else {
+        return false;
+      }
+      continue;
+    }
+    if (in.op == KH_OP_GELU_TANH || in.op == KH_OP_GELU_ERF || in.op == KH_OP_RELU) {
+      const int e = slot[in.a];
+      if (e < 0 || (e & (kAct | kRes))) return false;
+      act = in.op, slot[in.dst] = e | kAct;
+      continue;
+    }
+    return false;
+  }
+  if (stores != 1) return false;
+  a.direct = 1, a.d_bias = bias, a.d_res = res, a.d_out = out, a.d_act = act;
   return true;
 }
 
@@ -892,6 +1015,8 @@ std::unique_ptr<Op> make_gemm(const kh_launch &L, std::string &err, bool &unsupp
   op->a_vec_layout = a.sa_k == 1 && L.refs[0].offset % 4 == 0 && a.sa_m % 4 == 0 && a.sa_b % 4 == 0;
   op->b_vec_layout = a.sb_n == 1 && L.refs[1].offset % 4 == 0 && a.sb_k % 4 == 0 && a.sb_b % 4 == 0;
   if (!fill_epilogue(L, a, op->e_vec_candidates, err)) return nullptr;
+  a.direct = 0, a.d_bias = a.d_res = a.d_out = a.d_act = -1;
+  match_direct_epilogue(L, a);
   int cfg_run = cfg;
   if (t.prec == KH_PREC_BF16) {
     // B must be the library-layout bf16 copy: [batch][N][K'] with K' a

@@ -23,6 +23,9 @@ struct GemmArgs {
   int64_t estride[KH_MAX_REFS][3];
   kh_insn insns[KH_MAX_INSNS];        // LOAD/STORE operands renumbered to epilogue slots
   float *ws_partial;
+  // direct epilogue (the host recognised the tape as out = act((acc [+ bias])
+  // [+ res])): epilogue operand indices, -1 when absent, and the activation
+  int32_t direct, d_bias, d_res, d_out, d_act;
 };
 
 // Run the epilogue tape for columns [n, n + valid) of output row (b, m);

@@ -39,7 +39,8 @@ GEMV_CANDIDATES = [(v, 0) for v in range(6)] + [(0, s) for s in (2, 4)]
 
 # (BM, BN, BK, WM, WN, WK, MFMA) of the compiled configurations, by id; must
 # match the table in csrc/kh_gemm.hip (tests check it against kh_gemm_config).
-# Ids 0-7 are the LDS-copy pipeline, 8-14 the register-staged kernel.
+# Ids 0-7 and 21-25 are the LDS-copy pipeline (21-25 with 64 K values per
+# stage), 8-14 the register-staged kernel, 15-20 the bf16-input pipeline.
 TILES = {
     0: (64, 128, 32, 2, 2, 1, 16),
     1: (128, 64, 32, 2, 2, 1, 16),
@@ -62,18 +63,24 @@ TILES = {
     18: (64, 64, 32, 2, 2, 1, 16),
     19: (32, 64, 32, 2, 2, 1, 16),
     20: (128, 256, 32, 2, 4, 1, 16),
+    21: (64, 64, 64, 2, 2, 1, 16),
+    22: (64, 128, 64, 2, 2, 1, 16),
+    23: (32, 64, 64, 2, 2, 1, 16),
+    24: (128, 192, 64, 2, 4, 1, 16),
+    25: (64, 96, 64, 2, 2, 1, 16),
 }
-# input precision of each configuration: 0-14 fp32, 15-20 bf16 (A rounded in
-# the kernel, B a bf16 copy of a constant)
-PRECISION = {t: ("bf16" if t >= 15 else "fp32") for t in TILES}
+# input precision of each configuration: 15-20 bf16 (A rounded in the kernel,
+# B a bf16 copy of a constant), the others fp32
+PRECISION = {t: ("bf16" if 15 <= t <= 20 else "fp32") for t in TILES}
 # workgroups of each configuration one CU holds at once (LDS / VGPR bound,
 # from the compiler's resource report) and its measured main-loop efficiency
 # (fraction of the CU's fp32 MFMA rate), for the default heuristic only
 OCCUPANCY = {0: 2, 1: 2, 2: 3, 3: 2, 4: 4, 5: 2, 6: 1, 7: 1, 8: 4, 9: 4, 10: 4, 11: 5, 12: 5, 13: 4, 14: 2,
-             15: 2, 16: 2, 17: 1, 18: 3, 19: 4, 20: 1}
+             15: 2, 16: 2, 17: 1, 18: 3, 19: 4, 20: 1, 21: 2, 22: 1, 23: 2, 24: 1, 25: 2}
 EFFICIENCY = {0: 0.62, 1: 0.6, 2: 0.62, 3: 0.58, 4: 0.66, 5: 0.62, 6: 0.67, 7: 0.55,
               8: 0.55, 9: 0.55, 10: 0.5, 11: 0.5, 12: 0.45, 13: 0.5, 14: 0.55,
-              15: 0.15, 16: 0.15, 17: 0.15, 18: 0.15, 19: 0.15, 20: 0.15}
+              15: 0.15, 16: 0.15, 17: 0.15, 18: 0.15, 19: 0.15, 20: 0.15,
+              21: 0.62, 22: 0.6, 23: 0.62, 24: 0.67, 25: 0.62}
 # MFMA rate of a CU relative to fp32, per precision
 RATE = {"fp32": 1.0, "bf16": 16.0}
 CU_MFLOP_PER_US = 0.614          # fp32 MFMA: 256 flop/clk/CU at 2.4 GHz
