@@ -21,15 +21,19 @@
 //     query block on the GPU;
 //   * the scores are computed transposed, S^T = K Q^T: an accumulator column
 //     is one query (lane % 32) and its 16 registers are 16 keys, so the
-//     softmax max/sum over keys is a per-lane loop plus one exchange with
-//     lane ^ 32. Each lane keeps its query's Q half-row (DH/2 floats) in
-//     registers for the whole kernel and reads K rows with 128-bit loads;
-//     the head dimension is split between the two lane halves (a dot product
-//     is order-free);
+//     softmax max/sum over keys is a per-lane loop plus one v_permlane32_swap
+//     between the lane halves. Each lane keeps its query's Q half-row (DH/2
+//     floats, pre-multiplied by scale * log2(e)) in registers for the whole
+//     kernel and reads K rows with 128-bit buffer loads; the head dimension
+//     is split between the two lane halves (a dot product is order-free);
 //   * O^T += V^T P^T consumes the probabilities straight from the score
 //     registers: MFMA step r takes, from each lane half, the key held in
 //     accumulator register r, so the V^T operand is read with the same key
 //     permutation and P never moves through LDS or across lanes;
+//   * software pipeline per wave: the score MFMAs of block j+1 are issued
+//     interleaved with the softmax VALU work of block j, then the P.V MFMAs of
+//     block j interleaved with the loads of later blocks (K two blocks ahead,
+//     V one), so the matrix cores keep working through the exponentials;
 //   * causal masks (the frozen upper-triangular -inf constant) are applied
 //     from indices: key blocks wholly above the diagonal are skipped and only
 //     the diagonal block is compared. Other additive masks are read from
@@ -39,6 +43,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <type_traits>
 
 #include "kh_common.hpp"
 #include "kh_internal.hpp"
@@ -50,6 +55,8 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kQB = 32;  // queries per workgroup
 constexpr int kKB = 32;  // keys per block
+// buffer resource word 3 for gfx9-family raw buffers: 32-bit data format
+constexpr int kBufferFlags = 0x00020000;
 
 struct AttnArgs {
   const float *q, *k, *v;
@@ -61,7 +68,15 @@ struct AttnArgs {
   float scale;
 };
 
-template <int DH, int NW>
+// Exchange between the two lane halves (lanes l and l ^ 32): returns
+// (x[l & 31], x[32 + (l & 31)]), the low half's value first in every lane,
+// so a combine of the two is the same in both halves. One v_permlane32_swap.
+__device__ __forceinline__ float2 halves(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+template <int DH, int NW, bool ADD>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) void attn_kernel(const AttnArgs a) {
   constexpr int NT = DH / 32;  // 32-wide tiles of the head dimension in O^T
   constexpr int QS = DH / 2;   // head-dim elements per lane half (= MFMA steps of S^T)
@@ -76,7 +91,14 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
   const int qi = q0 + col;
   const bool q_ok = qi < a.tq;
 
-  // this lane's Q half-row, kept for the whole kernel
+  // Scores are kept in the base-2 domain: u = (s * scale + mask) * log2(e), so
+  // each exponential is one v_exp_f32 (exp2) and softmax(s) = 2^(u - max u) / sum.
+  // The scale and log2(e) are folded into this lane's Q half-row, which is
+  // kept in registers for the whole kernel.
+  constexpr float kLog2e = 1.4426950408889634f;
+  const float c_scale = a.scale_mode == KH_ATTN_SCALE_MUL   ? a.scale * kLog2e
+                        : a.scale_mode == KH_ATTN_SCALE_DIV ? kLog2e / a.scale
+                                                            : kLog2e;
   float qf[QS];
   {
     const float *qp = a.q + b * a.q_b + (int64_t)min(qi, a.tq - 1) * a.q_t + half * QS;
@@ -84,70 +106,52 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     for (int j = 0; j < QS / 4; ++j) {
       float4 t = *reinterpret_cast<const float4 *>(qp + 4 * j);
       if (!q_ok) t = make_float4(0.f, 0.f, 0.f, 0.f);
-      qf[4 * j] = t.x, qf[4 * j + 1] = t.y, qf[4 * j + 2] = t.z, qf[4 * j + 3] = t.w;
+      qf[4 * j] = t.x * c_scale, qf[4 * j + 1] = t.y * c_scale;
+      qf[4 * j + 2] = t.z * c_scale, qf[4 * j + 3] = t.w * c_scale;
     }
   }
 
-  int kend = a.tk;
-  if (a.mask_mode == KH_ATTN_MASK_CAUSAL) kend = min(a.tk, q0 + kQB);
+  const bool causal = a.mask_mode == KH_ATTN_MASK_CAUSAL;
+  const int kend = causal ? min(a.tk, q0 + kQB) : a.tk;
   const int nkb = (kend + kKB - 1) / kKB;
+  // keys below `lim` are visible to this lane's query
+  const int lim = causal ? min(a.tk, qi + 1) : a.tk;
 
-  // Scores are kept in the base-2 domain: u = (s * scale + mask) * log2(e), so
-  // each exponential is one v_exp_f32 (exp2) and softmax(s) = 2^(u - max u) / sum.
-  constexpr float kLog2e = 1.4426950408889634f;
-  const float c_scale = a.scale_mode == KH_ATTN_SCALE_MUL   ? a.scale * kLog2e
-                        : a.scale_mode == KH_ATTN_SCALE_DIV ? kLog2e / a.scale
-                                                            : kLog2e;
-
-  // 32-bit element offsets from uniform per-head bases (the host checks
-  // that every operand spans < 2^31 elements), so loads use a scalar base
-  // plus one VGPR offset.
-  const float *kb_ptr = a.k + b * a.k_b;
-  const float *vb_ptr = a.v + b * a.v_b;
-  const uint32_t k_t = (uint32_t)a.k_t, v_t = (uint32_t)a.v_t;
+  // K and V are read with buffer loads: a per-head resource (base in SGPRs)
+  // plus a 32-bit byte offset per lane (the host checks that every operand
+  // spans < 2^30 elements) and the column step as an immediate. Key indices
+  // are clamped to the last key, so every load of a partial block stays
+  // inside the operand (and the resource's extent bounds it as well).
+  const uint32_t k_t4 = (uint32_t)a.k_t * 4, v_t4 = (uint32_t)a.v_t * 4;
+  const __amdgpu_buffer_rsrc_t k_res = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)(a.k + b * a.k_b), (short)0, (int)(((uint32_t)(a.tk - 1) * (uint32_t)a.k_t + DH) * 4), kBufferFlags);
+  const __amdgpu_buffer_rsrc_t v_res = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)(a.v + b * a.v_b), (short)0, (int)(((uint32_t)(a.tk - 1) * (uint32_t)a.v_t + DH) * 4), kBufferFlags);
+  const uint32_t k_last = (uint32_t)(a.tk - 1) * k_t4 + half * QS * 4;
+  const uint32_t v_last = (uint32_t)(a.tk - 1) * v_t4 + col * 4;
   auto load_k = [&](int kb, float4 (&kf)[QS / 4]) {
-    const uint32_t key = (uint32_t)min(kb * kKB + col, a.tk - 1);
-    const uint32_t off = key * k_t + half * QS;
+    const uint32_t off = min((uint32_t)(kb * kKB + col) * k_t4 + half * QS * 4, k_last);
 #pragma unroll
-    for (int j = 0; j < QS / 4; ++j) kf[j] = *reinterpret_cast<const float4 *>(kb_ptr + off + 4 * j);
-  };
-  // V^T operand of MFMA step r, tile t: V[key(r)][t*32 + col], key(r) the key
-  // held in accumulator register r of this lane half (rows clamped on the
-  // last, partial block only).
-  const uint32_t v_lane = (uint32_t)(half * 4) * v_t + col;
-  auto load_v = [&](int kb, float (&vf)[16 * NT]) {
-    const int key0 = kb * kKB;
-    if (key0 + kKB <= a.tk) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const uint32_t off = v_lane + (uint32_t)(key0 + (r >> 2) * 8 + (r & 3)) * v_t;
-#pragma unroll
-        for (int t = 0; t < NT; ++t) vf[r * NT + t] = vb_ptr[off + t * 32];
-      }
-    } else {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const uint32_t key = (uint32_t)min(key0 + (r >> 2) * 8 + half * 4 + (r & 3), a.tk - 1);
-#pragma unroll
-        for (int t = 0; t < NT; ++t) vf[r * NT + t] = vb_ptr[key * v_t + col + t * 32];
-      }
+    for (int j = 0; j < QS / 4; ++j) {
+      const auto x = __builtin_amdgcn_raw_buffer_load_b128(k_res, off + 16 * j, 0, 0);
+      kf[j] = make_float4(__uint_as_float(x[0]), __uint_as_float(x[1]), __uint_as_float(x[2]), __uint_as_float(x[3]));
     }
   };
-
-  f32x16 oacc[NT];
+  // V^T operand of MFMA step r, tile t: V[key(r)][t*32 + col], key(r) =
+  // key0 + (r/4)*8 + half*4 + r%4, the key held in accumulator register r of
+  // this lane half.
+  auto load_v = [&](int kb, float (&vf)[16 * NT]) {
+    const uint32_t base = (uint32_t)(kb * kKB + half * 4) * v_t4 + col * 4;
 #pragma unroll
-  for (int t = 0; t < NT; ++t)
+    for (int r = 0; r < 16; ++r) {
+      const uint32_t off = min(base + (uint32_t)((r >> 2) * 8 + (r & 3)) * v_t4, v_last);
 #pragma unroll
-    for (int r = 0; r < 16; ++r) oacc[t][r] = 0.0f;
-  float m_run = -INFINITY, l_run = 0.0f;
-
-  // One key block: prefetch the next block's K into `kn`, then scores from
-  // `kc`, online softmax, and O^T += V^T P^T.
-  auto step = [&](int kb, float4 (&kc)[QS / 4]) {
-    // keep the scheduler from hoisting the next step's loads into this one
-    __builtin_amdgcn_sched_barrier(0);
-    float vf[16 * NT];
-    load_v(kb, vf);
+      for (int t = 0; t < NT; ++t)
+        vf[r * NT + t] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(v_res, off + 128 * t, 0, 0));
+    }
+  };
+  // S^T block: register r of lane (col, half) = score of query col, key(r)
+  auto scores = [&](const float4 (&kc)[QS / 4]) {
     f32x16 s;
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[r] = 0.0f;
@@ -158,28 +162,37 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
       s = __builtin_amdgcn_mfma_f32_32x32x2f32(kc[j].z, qf[4 * j + 2], s, 0, 0, 0);
       s = __builtin_amdgcn_mfma_f32_32x32x2f32(kc[j].w, qf[4 * j + 3], s, 0, 0, 0);
     }
-    // K of this block is consumed: fetch the next block's into the same
-    // registers, hidden behind the softmax and the V MFMAs
-    if (kb + NW < nkb) load_k(kb + NW, kc);
-    const int key0 = kb * kKB;
-    const bool edge = key0 + kKB > a.tk || (a.mask_mode == KH_ATTN_MASK_CAUSAL && key0 + kKB - 1 > q0);
-    float p[16];
+    return s;
+  };
+
+  f32x16 oacc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) oacc[t][r] = 0.0f;
+  float m_run = -INFINITY, l_run = 0.0f;
+
+  // Online softmax of one score block, in place (scores become the
+  // unnormalised probabilities), with the running (max, sum) and O^T rescaled.
+  // Only a wave's last block can hold keys past the causal diagonal or past
+  // the last key (every earlier block lies wholly below both), so the mask
+  // is applied there alone.
+  auto softmax = [&](f32x16 &s, int kb, auto masked) {
+    const int room = lim - kb * kKB - half * 4;  // key(r) < lim  <=>  (r/4)*8 + r%4 < room
     float mx = -INFINITY;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int key = key0 + (r >> 2) * 8 + half * 4 + (r & 3);
-      float mk = 0.0f;
-      if (a.mask_mode == KH_ATTN_MASK_ADD) {
-        const int kc2 = min(key, a.tk - 1), qc = min(qi, a.tq - 1);
-        mk = a.mask[b * a.m_b + (int64_t)qc * a.m_q + (int64_t)kc2 * a.m_k] * kLog2e;
+      float u = s[r];
+      if (ADD) {
+        const int key = min(kb * kKB + half * 4 + (r >> 2) * 8 + (r & 3), a.tk - 1);
+        u = fmaf(a.mask[b * a.m_b + (int64_t)min(qi, a.tq - 1) * a.m_q + (int64_t)key * a.m_k], kLog2e, u);
       }
-      float u = fmaf(s[r], c_scale, mk);
-      if (edge && (key >= a.tk || (a.mask_mode == KH_ATTN_MASK_CAUSAL && key > qi))) u = -INFINITY;
-      p[r] = u;
+      if (decltype(masked)::value) u = (r >> 2) * 8 + (r & 3) < room ? u : -INFINITY;
+      s[r] = u;
       mx = fmaxf(mx, u);
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_run, mx);
+    const float2 mh = halves(mx);
+    const float m_new = fmaxf(m_run, fmaxf(mh.x, mh.y));
     // a row with no finite score so far keeps m = -inf; exponentials are then
     // taken against 0 so they stay 0 instead of becoming NaN
     const float m_use = m_new == -INFINITY ? 0.0f : m_new;
@@ -187,19 +200,17 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     float sum = 0.0f;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      p[r] = __builtin_amdgcn_exp2f(p[r] - m_use);
-      sum += p[r];
+      s[r] = __builtin_amdgcn_exp2f(s[r] - m_use);
+      sum += s[r];
     }
-    sum += __shfl_xor(sum, 32);
-    l_run = l_run * alpha + sum;
+    const float2 sh = halves(sum);
+    l_run = fmaf(l_run, alpha, sh.x + sh.y);
     m_run = m_new;
-    // the running maximum rarely moves after the first blocks: skip the
-    // rescale when it did not move for any query of the wave
-    if (!__all(alpha == 1.0f)) {
 #pragma unroll
-      for (int t = 0; t < NT; ++t) oacc[t] *= alpha;
-    }
-    // O^T += V^T P^T, key order permuted to match the score registers
+    for (int t = 0; t < NT; ++t) oacc[t] *= alpha;
+  };
+  // O^T += V^T P^T, key order permuted to match the score registers
+  auto pv = [&](const float (&vf)[16 * NT], const f32x16 &p) {
 #pragma unroll
     for (int r = 0; r < 16; ++r)
 #pragma unroll
@@ -207,9 +218,42 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
         oacc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[r * NT + t], p[r], oacc[t], 0, 0, 0);
   };
 
-  float4 kf[QS / 4];
-  if (w < nkb) load_k(w, kf);
-  for (int kb = w; kb < nkb; kb += NW) step(kb, kf);
+  // Software pipeline over this wave's key blocks (w, w + NW, ...): the score
+  // MFMAs of the next block are issued before the softmax of the current one,
+  // so the matrix cores work through the exponentials; K runs two blocks and
+  // V one block ahead of their use.
+  int kb = w;
+  if (kb < nkb) {
+    float4 kf[QS / 4];
+    float vf[16 * NT];
+    load_k(kb, kf);
+    load_v(kb, vf);
+    f32x16 s_cur = scores(kf);
+    load_k(min(kb + NW, nkb - 1), kf);
+    for (; kb + NW < nkb; kb += NW) {
+      const f32x16 s_nxt = scores(kf);
+      softmax(s_cur, kb, std::false_type{});
+      load_k(min(kb + 2 * NW, nkb - 1), kf);
+      pv(vf, s_cur);
+      load_v(kb + NW, vf);
+      s_cur = s_nxt;
+      // issue order: each score MFMA of the next block followed by softmax
+      // VALU work, then each P.V MFMA followed by a load and its addressing
+#pragma unroll
+      for (int i = 0; i < 32; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
+      }
+#pragma unroll
+      for (int i = 0; i < 32; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
+        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
+      }
+    }
+    softmax(s_cur, kb, std::true_type{});
+    pv(vf, s_cur);
+  }
 
   // merge the NW key-split partials: o = sum_w 2^(m_w - M) o_w / sum_w 2^(m_w - M) l_w
   if (half == 0) m_part[w][col] = m_run, l_part[w][col] = l_run;
@@ -255,7 +299,10 @@ class AttnOp final : public Op {
     if (a.batch == 0 || a.tq == 0) return hipSuccess;
 #define KH_ATTN_LAUNCH(D, W)                                                                         \
   if (dh == D && nw == W) {                                                                          \
-    hipLaunchKernelGGL((attn_kernel<D, W>), grid, dim3(64 * W), 0, stream, a);                      \
+    if (a.mask_mode == KH_ATTN_MASK_ADD)                                                             \
+      hipLaunchKernelGGL((attn_kernel<D, W, true>), grid, dim3(64 * W), 0, stream, a);              \
+    else                                                                                             \
+      hipLaunchKernelGGL((attn_kernel<D, W, false>), grid, dim3(64 * W), 0, stream, a);             \
     return hipGetLastError();                                                                        \
   }
     KH_ATTN_LAUNCH(64, 8)
@@ -314,9 +361,9 @@ std::unique_ptr<Op> make_attn(const kh_launch &L, std::string &err, bool &unsupp
     const kh_ref &r = L.refs[j];
     const int64_t rows = j == 0 || j == 3 ? tq : tk;
     const int64_t span = std::max<int64_t>(0, batch - 1) * r.strides[0] + std::max<int64_t>(0, rows - 1) * r.strides[1] + dh;
-    if (r.strides[0] < 0 || r.strides[1] < 0 || span >= (1ll << 31)) {
+    if (r.strides[0] < 0 || r.strides[1] < 0 || span >= (1ll << 30)) {
       unsupported = true;
-      err = "attention: operands must span fewer than 2^31 elements with non-negative strides";
+      err = "attention: operands must span fewer than 2^30 elements with non-negative strides";
       return nullptr;
     }
   }
