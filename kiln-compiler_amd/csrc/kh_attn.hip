@@ -83,7 +83,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
   __shared__ float o_part[NW][kQB][DH + 4];
   __shared__ float m_part[NW][kQB], l_part[NW][kQB];
 
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar loop control
   const int col = lane & 31, half = lane >> 5;
   const int b = blockIdx.x % a.batch;
   const int qb = a.n_qblocks - 1 - (int)(blockIdx.x / a.batch);
