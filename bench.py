@@ -428,6 +428,33 @@ def fused_ops():
             f"({nbytes / cold / 1e6:.0f} GB/s), eager {eager * 1e3:.2f} us")
         del xs, ys
         torch.cuda.empty_cache()
+    # the same kernels at 1.5 GiB of traffic per call (six times the Infinity
+    # Cache): HBM bandwidth against the 8 TB/s peak and against a plain
+    # device copy of the same bytes
+    scale = [
+        ("bias_gelu_65536x3072", work[0][1], (65536, 3072)),
+        ("layernorm_262144x768", ln, (262144, 768)),
+        ("softmax_48x2048x2048", work[2][1], (48, 2048, 2048)),
+    ]
+    for name, fn, shape in scale:
+        x = torch.randn(*shape, device="cuda")
+        nbytes = 2 * x.numel() * 4
+        c = kiln.compile(fn, (x,), device="cuda", cuda_graphs=False)
+        y = torch.empty_like(x)
+        c._exe.run_into([x], [y])
+        with torch.no_grad():
+            torch.testing.assert_close(y, fn(x), rtol=1e-4, atol=1e-5)
+            y.copy_(x)  # warm the copy path too
+            ms = events_ms(lambda: c._exe.run_into([x], [y]), 10)
+            copy = events_ms(lambda: y.copy_(x), 10)
+            eager = events_ms(lambda: fn(x), 10)
+        out[name] = {"kiln_us": round(ms * 1e3, 1), "copy_us": round(copy * 1e3, 1), "eager_us": round(eager * 1e3, 1),
+                     "gbs": round(nbytes / ms / 1e6, 1), "hbm_frac": round(nbytes / ms / 1e6 / HBM_PEAK_GBS, 3),
+                     "of_copy": round(copy / ms, 3), "bytes": nbytes}
+        log(f"{name}: {ms * 1e3:.1f} us ({nbytes / ms / 1e6:.0f} GB/s, {nbytes / ms / 1e6 / HBM_PEAK_GBS:.2f} of peak, "
+            f"{copy / ms:.2f} of a copy), eager {eager * 1e3:.1f} us")
+        del x, y, c
+        torch.cuda.empty_cache()
     return out
 
 
