@@ -379,6 +379,37 @@ def gemm_sweep(autotune):
     return out
 
 
+def linear_gelu(autotune):
+    """BASELINE's C1: nn.Linear(768, 3072) + bias + GELU at [128, 768], with
+    nn.GELU's default (erf) form and the tanh form the Block uses; GPU time of
+    a 20-call graph replay, eager torch beside each."""
+    import torch
+
+    import kiln
+    from models.transformer import gpt2_init_
+
+    m, k, n = 128, 768, 3072
+    flops = 2 * m * n * k
+    out = {}
+    for approx in ("none", "tanh"):
+        torch.manual_seed(0)
+        model = torch.nn.Sequential(gpt2_init_(torch.nn.Linear(k, n), seed=1),
+                                    torch.nn.GELU(approximate=approx)).eval().cuda()
+        x = torch.randn(m, k, device="cuda")
+        c = kiln.compile(model, (x,), device="cuda", autotune=autotune, cuda_graphs=False)
+        with torch.no_grad():
+            torch.testing.assert_close(c(x), model(x), rtol=1e-4, atol=1e-5)
+            outs = [torch.empty(m, n, device="cuda")]
+            kms = graph_ms(lambda: c._exe.run_into([x], outs))
+            ems = graph_ms(lambda: model(x))
+        name = f"linear_gelu_{'erf' if approx == 'none' else 'tanh'}_{m}x{k}x{n}"
+        out[name] = {"kiln_us": round(kms * 1e3, 2), "eager_us": round(ems * 1e3, 2),
+                     "kiln_tflops": round(flops / kms / 1e9, 2), "launches": c.report.lowering["launches"]}
+        log(f"{name}: kiln {kms * 1e3:.2f} us ({flops / kms / 1e9:.1f} TFLOP/s, "
+            f"{c.report.lowering['launches']} launch), eager {ems * 1e3:.2f} us")
+    return out
+
+
 def fused_ops():
     import torch
     import torch.nn.functional as F
@@ -528,6 +559,7 @@ def main():
     if not args.quick:
         extra["block"] = block_sweep([128, 512, 1024, 2048], not args.no_autotune)
         extra["gemm"] = gemm_sweep(not args.no_autotune)
+        extra["linear_gelu"] = linear_gelu(not args.no_autotune)
         extra["fused_ops"] = fused_ops()
         extra["stack"] = stack_bench(not args.no_autotune)
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.tokens)

@@ -135,7 +135,12 @@ typedef struct kh_pass {
  *        cfg[3] = precision.
  *   GEMV as GEMM with M = 1; cfg[1] = workgroup variant (0: library picks from
  *        the shape; 1-3: 32/16/8 columns x 256 threads; 4-5: 32/16 columns x
- *        1024 threads), cfg[2] = split-K (0: library picks).
+ *        1024 threads), cfg[2] = split-K (0: library picks). cfg[4] = 1:
+ *        LayerNorm prologue - refs[0] is the raw row x and the product uses
+ *        (x - mean) * rsqrt(var + eps) [* gamma] [+ beta], mean = sum(x) *
+ *        fparams[0], var = sum((x - mean)^2) * fparams[1], eps = fparams[2];
+ *        cfg[5] / cfg[6] = ref index (>= 2) of gamma / beta, unit stride over
+ *        K and stride 0 over M, or -1.
  *   RED  shape = input shape; refs[0] = input, refs[1] = output, both with
  *        strides over the input shape (the output's reduced dims stride 0);
  *        cfg[0] = bitmask of reduced dims, cfg[1] = 1 for max else sum.

@@ -26,6 +26,11 @@ struct GemmArgs {
   // direct epilogue (the host recognised the tape as out = act((acc [+ bias])
   // [+ res])): epilogue operand indices, -1 when absent, and the activation
   int32_t direct, d_bias, d_res, d_out, d_act;
+  // GEMV LayerNorm prologue: A is the raw row x and the kernel multiplies
+  // ((x - mean) * rstd [* gamma] [+ beta]); gamma / beta are epilogue operand
+  // indices (-1 when absent), c1 / c2 the 1/C factors of mean and variance
+  int32_t pro, pro_g, pro_b;
+  float pro_c1, pro_c2, pro_eps;
 };
 
 // Run the epilogue tape for columns [n, n + valid) of output row (b, m);

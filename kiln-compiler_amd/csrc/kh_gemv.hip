@@ -17,6 +17,11 @@
 //     CU still has its whole share of rows in flight in one or two passes;
 //   * the k-lanes are reduced in a fixed tree (shuffles inside a wave, then the
 //     four waves through LDS) and the same workgroup runs the epilogue;
+//   * a LayerNorm whose only consumer is the GEMV runs as its prologue (decode:
+//     the normalised row never goes through memory, one launch instead of
+//     two): every workgroup recomputes the row's mean and variance in one
+//     pass (sums shifted by the row's first value, one workgroup reduction)
+//     and normalises x as it loads it;
 //   * only when even CQ = 1 leaves too few workgroups for the rows (tiny N, huge
 //     K) is K split across workgroups; the splits' partials are then summed in
 //     split order by the split-K reduce kernel (shared with the GEMM family),
@@ -45,11 +50,28 @@ __device__ __forceinline__ float4 shfl_xor4(float4 v, int m) {
                      __shfl_xor(v.w, m, 64));
 }
 
-template <int CQ, int THREADS>
+// Sum of v over the workgroup, in a fixed order (wave tree, then the waves in
+// order); every thread gets the total. `red` holds NW entries.
+template <int NW>
+__device__ __forceinline__ float2 block_sum2(float2 v, float2 *red) {
+#pragma unroll
+  for (int m = 32; m >= 1; m /= 2) v.x += __shfl_xor(v.x, m, 64), v.y += __shfl_xor(v.y, m, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float2 s = red[0];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) s.x += red[w].x, s.y += red[w].y;
+  return s;
+}
+
+constexpr int kProCache = 4;  // x values per thread kept in registers by the prologue
+
+template <int CQ, int THREADS, bool PRO>
 __global__ __launch_bounds__(THREADS) void gemv_kernel(const GemmArgs a) {
   constexpr int KL = THREADS / CQ;  // k-lanes: rows one load instruction covers
   constexpr int NW = THREADS / 64;
   __shared__ float4 wave_part[NW][CQ];
+  __shared__ float2 red[NW];
   const int tid = threadIdx.x;
   const int cq = tid % CQ, kl = tid / CQ;
   const int nb = blockIdx.x, b = blockIdx.y, split = blockIdx.z;
@@ -58,6 +80,36 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const GemmArgs a) {
   const int k_end = min(a.K, k_begin + a.k_per_split);
   const float *x = a.A + (int64_t)b * a.sa_b;
   const float *W = a.B + (int64_t)b * a.sb_b;
+  // LayerNorm prologue: statistics of the whole row (every split needs them);
+  // an absent gamma / beta reads x[0] (stride 0) and is deselected
+  float mean = 0.0f, rstd = 1.0f;
+  const float *gam = x, *bet = x;
+  int g_st = 0, b_st = 0;
+  if constexpr (PRO) {
+    // one pass over the row, sums shifted by its first value c (so the
+    // variance does not cancel for rows far from zero):
+    //   mean = c + S1 / C,  var = (S2 - S1^2 / C) * c2,  S_p = sum (x - c)^p
+    const float c = x[0];
+    float xs[kProCache];
+#pragma unroll
+    for (int i = 0; i < kProCache; ++i) {
+      const int k = tid + i * THREADS;
+      xs[i] = k < a.K ? x[(int64_t)k * a.sa_k] - c : 0.0f;
+    }
+    float2 s = make_float2(0.0f, 0.0f);
+#pragma unroll
+    for (int i = 0; i < kProCache; ++i) s.x += xs[i], s.y = fmaf(xs[i], xs[i], s.y);
+    for (int k = tid + kProCache * THREADS; k < a.K; k += THREADS) {
+      const float d = x[(int64_t)k * a.sa_k] - c;
+      s.x += d, s.y = fmaf(d, d, s.y);
+    }
+    s = block_sum2<NW>(s, red);
+    const float m1 = s.x * a.pro_c1;
+    mean = c + m1;
+    rstd = rsqrtf(fmaxf(fmaf(-s.x, m1, s.y), 0.0f) * a.pro_c2 + a.pro_eps);
+    if (a.pro_g >= 0) gam = a.eptr[a.pro_g] + b * a.estride[a.pro_g][0], g_st = 1;
+    if (a.pro_b >= 0) bet = a.eptr[a.pro_b] + b * a.estride[a.pro_b][0], b_st = 1;
+  }
   auto walk = [&](auto vec_tag) {
     constexpr bool vec = decltype(vec_tag)::value;
     auto row = [&](int k) -> float4 {
@@ -76,19 +128,27 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const GemmArgs a) {
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int k0 = k_begin + kl; k0 < k_end; k0 += KL * kRows) {
       float4 w[kRows];
-      float xv[kRows];
+      float xv[kRows], gv[kRows], bv[kRows];
       // Rows past the end are clamped to the last row (an in-bounds load,
-      // issued with the others) and their products dropped by a select.
+      // issued with the others) and their products dropped by a select. All
+      // loads of the batch are issued before the first use of any of them.
 #pragma unroll
       for (int j = 0; j < kRows; ++j) {
         const int k = min(k0 + j * KL, k_end - 1);
         w[j] = row(k);
         xv[j] = x[(int64_t)k * a.sa_k];
+        if constexpr (PRO) gv[j] = gam[k * g_st], bv[j] = bet[k * b_st];
       }
 #pragma unroll
       for (int j = 0; j < kRows; ++j) {
         const bool in = k0 + j * KL < k_end;
-        const float xs = in ? xv[j] : 0.0f;
+        float xn = xv[j];
+        if constexpr (PRO) {
+          xn = (xn - mean) * rstd;
+          xn = g_st ? xn * gv[j] : xn;
+          xn = b_st ? xn + bv[j] : xn;
+        }
+        const float xs = in ? xn : 0.0f;
         const float4 ws = in ? w[j] : make_float4(0.f, 0.f, 0.f, 0.f);
         acc.x = fmaf(xs, ws.x, acc.x), acc.y = fmaf(xs, ws.y, acc.y);
         acc.z = fmaf(xs, ws.z, acc.z), acc.w = fmaf(xs, ws.w, acc.w);
@@ -151,19 +211,26 @@ class GemvOp final : public Op {
     a.ws_partial = partials;
     if (a.N == 0 || a.batch == 0) return hipSuccess;
     if (a.splitk > 1 && !partials) return hipErrorInvalidValue;
-    if (threads == 1024) {
-      if (quads == 8) hipLaunchKernelGGL((gemv_kernel<8, 1024>), grid, dim3(1024), 0, stream, a);
-      else hipLaunchKernelGGL((gemv_kernel<4, 1024>), grid, dim3(1024), 0, stream, a);
-    } else {
-      if (quads == 8) hipLaunchKernelGGL((gemv_kernel<8, 256>), grid, dim3(256), 0, stream, a);
-      else if (quads == 4) hipLaunchKernelGGL((gemv_kernel<4, 256>), grid, dim3(256), 0, stream, a);
-      else hipLaunchKernelGGL((gemv_kernel<2, 256>), grid, dim3(256), 0, stream, a);
-    }
+    if (a.pro) launch_variant(a, grid, stream, std::true_type{});
+    else launch_variant(a, grid, stream, std::false_type{});
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.splitk == 1) return e;
     return launch_splitk_reduce(a, current_device().cus, stream);
   }
   size_t partial_floats() const override { return n_partials; }
+
+  template <class P>
+  void launch_variant(const GemmArgs &a, dim3 g, hipStream_t stream, P) const {
+    constexpr bool pro = P::value;
+    if (threads == 1024) {
+      if (quads == 8) hipLaunchKernelGGL((gemv_kernel<8, 1024, pro>), g, dim3(1024), 0, stream, a);
+      else hipLaunchKernelGGL((gemv_kernel<4, 1024, pro>), g, dim3(1024), 0, stream, a);
+    } else {
+      if (quads == 8) hipLaunchKernelGGL((gemv_kernel<8, 256, pro>), g, dim3(256), 0, stream, a);
+      else if (quads == 4) hipLaunchKernelGGL((gemv_kernel<4, 256, pro>), g, dim3(256), 0, stream, a);
+      else hipLaunchKernelGGL((gemv_kernel<2, 256, pro>), g, dim3(256), 0, stream, a);
+    }
+  }
 };
 
 }  // namespace
@@ -191,6 +258,30 @@ std::unique_ptr<Op> make_gemv(const kh_launch &L, std::string &err, bool &unsupp
   a.sb_b = L.refs[1].strides[0], a.sb_k = L.refs[1].strides[1], a.sb_n = L.refs[1].strides[2];
   op->b_vec_layout = a.sb_n == 1 && L.refs[1].offset % 4 == 0 && a.sb_k % 4 == 0 && a.sb_b % 4 == 0;
   if (!fill_epilogue(L, a, op->e_vec_candidates, err)) return nullptr;
+  // LayerNorm prologue: cfg[4] = 1, cfg[5] / cfg[6] = ref index of gamma /
+  // beta (-1: none), fparams = {1/C, 1/C, eps}; gamma and beta are [K] rows
+  a.pro = L.cfg[4], a.pro_g = -1, a.pro_b = -1;
+  if (a.pro != 0 && a.pro != 1) {
+    err = "gemv: unknown prologue " + std::to_string(a.pro);
+    return nullptr;
+  }
+  if (a.pro) {
+    for (int w = 0; w < 2; ++w) {
+      const int r = L.cfg[5 + w];
+      if (r == -1) continue;
+      if (r < 2 || r >= L.n_refs) {
+        err = "gemv: prologue operand index out of range";
+        return nullptr;
+      }
+      const kh_ref &g = L.refs[r];
+      if (g.strides[1] != 0 || g.strides[2] != 1) {
+        err = "gemv: LayerNorm gamma / beta must be unit-stride rows over K";
+        return nullptr;
+      }
+      (w == 0 ? a.pro_g : a.pro_b) = r - 2;
+    }
+    a.pro_c1 = L.fparams[0], a.pro_c2 = L.fparams[1], a.pro_eps = L.fparams[2];
+  }
   // column quads per workgroup: the widest giving kTargetBlocks workgroups;
   // if none does, 64-byte segments with 1024-thread workgroups
   const int64_t b1 = std::max<int64_t>(1, batch);

@@ -184,6 +184,8 @@ class _Lowerer:
         self.matmul_config = matmul_config
         self.program = Program(precision=precision)
         self.const_slot = {}
+        self._cfg = {}
+        self.prologue = {}   # matmul kernel -> (x, gamma, beta, fparams) of a fused LayerNorm
 
     # operands ---------------------------------------------------------------------
 
@@ -634,16 +636,13 @@ class _Lowerer:
 
         if a not in self.layouts or b not in self.layouts:
             raise NotImplementedError("HIP backend: matmul operand has no storage")
-        cfg = dict(self.matmul_config(self.g, k))
-        prec = cfg.get("precision", self.precision)
-        if prec == "bf16" and self.layouts[b].base[0] != "const":
-            # bf16 inputs need B as a build-time bf16 copy of a constant; a
-            # matmul on two activations stays on the fp32 path (more exact)
-            prec = "fp32"
+        cfg, prec = self.matmul_choice(k)
         gemv = m == 1 and prec == "fp32"
+        pro = self.prologue.get(k) if gemv else None
+        a_src = pro[0] if pro else a   # the LayerNorm's input when the GEMV runs it as its prologue
         d = self.new_desc(kl.FAM_GEMV if gemv else kl.FAM_GEMM, "gemv" if gemv else "matmul", k, space3)
         d.gemm[0], d.gemm[1], d.gemm[2], d.gemm[3] = batch, m, n, kk
-        d.refs[0] = ref3(a, (batch, m, kk))
+        d.refs[0] = ref3(a_src, (batch, m, kk))
         d.refs[1] = ref3(b, (batch, kk, n))
         if prec == "bf16":
             d.refs[1] = self.bf16_weight(b, d.refs[1], batch, kk, n)
@@ -663,10 +662,20 @@ class _Lowerer:
         for v in outs:
             out_ref[v] = len(refs)
             refs.append(ref3(v, space3))
-        self._check_refs(refs + [None, None])
-        for j, r in enumerate(refs):
+        pro_refs = []
+        if pro:
+            x, gamma, beta, fparams = pro
+            d.cfg[4], d.cfg[5], d.cfg[6] = 1, -1, -1
+            for w, p in ((5, gamma), (6, beta)):
+                if p is not None:
+                    d.cfg[w] = 2 + len(refs) + len(pro_refs)
+                    pro_refs.append(ref3(p, (batch, m, kk)))
+            for i, f in enumerate(fparams):
+                d.fparams[i] = f
+        self._check_refs(refs + pro_refs + [None, None])
+        for j, r in enumerate(refs + pro_refs):
             d.refs[2 + j] = r
-        d.n_refs = 2 + len(refs)
+        d.n_refs = 2 + len(refs) + len(pro_refs)
 
         def build(eager):
             t = _Tape()
@@ -715,9 +724,92 @@ class _Lowerer:
         summary += f" tile {d.cfg[1]} splitk {d.cfg[2]}"
         if prec != "fp32":
             summary += f" {prec}"
+        if pro:
+            summary += " prologue: layernorm"
+            nbytes += 4 * kk * len(pro_refs)
         if epi:
             summary += f" epilogue: {epi}"
         self.add(d, k, summary, flops=flops, nbytes=nbytes)
+
+    def matmul_choice(self, k: Kernel):
+        """(configuration, precision) of matmul kernel k, asked once per kernel."""
+        if k not in self._cfg:
+            mm = next(n for n in k.nodes if n.op == "matmul")
+            cfg = dict(self.matmul_config(self.g, k))
+            prec = cfg.get("precision", self.precision)
+            if prec == "bf16" and self.layouts[mm.inputs[1]].base[0] != "const":
+                # bf16 inputs need B as a build-time bf16 copy of a constant; a
+                # matmul on two activations stays on the fp32 path (more exact)
+                prec = "fp32"
+            self._cfg[k] = (cfg, prec)
+        return self._cfg[k]
+
+    def _arena_range(self, v):
+        """Byte range [lo, hi) of v's storage in the arena, or None."""
+        lay = self.layouts.get(v)
+        if lay is None or lay.base[0] != "arena":
+            return None
+        buf = lay.base[1]
+        lo = buf.node.attrs.get("offset", 0)
+        return lo, lo + buf.type.nbytes
+
+    def find_ln_prologues(self):
+        """LayerNorm row kernels whose only consumer is the A operand of a
+        1-row fp32 matmul (decode: ln_1 -> qkv, ln_2 -> fc): the GEMV runs the
+        LayerNorm as its prologue and the row kernel is not launched. The
+        LayerNorm's input must stay intact until the GEMV, so no buffer that a
+        kernel from the LayerNorm up to the GEMV writes may overlap it."""
+        kernels = self.g.kernels
+        owner = {n: k for k in kernels for n in k.nodes}
+        results = set(self.g.results)
+        skip = set()
+        for i, k in enumerate(kernels):
+            if k.kind != "reduction":
+                continue
+            reds = [n for n in k.nodes if n.op.startswith("reduce_")]
+            if not reds or not all(is_row_reduction(n) for n in reds):
+                continue
+            members = set(k.nodes)
+            outs = kernel_outputs(self.g, k, self.users)
+            externals = []
+            for n in k.nodes:
+                for v in n.inputs:
+                    if (v.node not in members or v.node is None) and not self.is_imm(v) and v not in externals:
+                        externals.append(v)
+            variant, fparams, (has_g, has_b), ordered = self._row_pattern(k, reds, outs, externals)
+            if variant != kl.ROW_LAYERNORM or ordered is None:
+                continue
+            y, x = outs[0], ordered[0]
+            users = self.users.get(y, [])
+            if y in results or len(users) != 1 or users[0].op != "matmul":
+                continue
+            mm = users[0]
+            km = owner.get(mm)
+            if km is None or km.kind != "matmul" or mm.inputs[0] is not y or mm.inputs[1] is y:
+                continue
+            if y.type.rank != 2 or y.shape[0] != 1 or tuple(x.shape) != tuple(y.shape):
+                continue
+            if self._arena_range(y) is None and y not in self.layouts:
+                continue
+            _, prec = self.matmul_choice(km)
+            if prec != "fp32":
+                continue
+            j = kernels.index(km)
+            xr = self._arena_range(x)
+            if xr is not None:
+                clash = False
+                for kk in kernels[i:j + 1]:
+                    for v in kernel_outputs(self.g, kk, self.users):
+                        r = self._arena_range(v)
+                        if v is not y and r is not None and r[0] < xr[1] and xr[0] < r[1]:
+                            clash = True
+                if clash:
+                    continue
+            gamma = ordered[1] if has_g else None
+            beta = ordered[1 + has_g] if has_b else None
+            self.prologue[km] = (x, gamma, beta, list(fparams))
+            skip.add(k)
+        return skip
 
     def bf16_weight(self, b, ref, batch, kk, n):
         """Ref of the bf16 [batch][N][K'] copy of constant view `b` (whose fp32
@@ -781,7 +873,10 @@ class _Lowerer:
             for n in k.nodes:
                 if ops.kind(n.op) not in ("elementwise", "reduction", "matmul") and k.kind != "attention":
                     raise NotImplementedError(f"GPU backend: unexpected op '{n.op}' in a kernel")
+        fused = self.find_ln_prologues()
         for k in self.g.kernels:
+            if k in fused:
+                continue
             if k.kind == "attention":
                 self.lower_attention(k)
             elif k.kind == "matmul":

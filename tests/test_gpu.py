@@ -376,3 +376,20 @@ def test_config_stack_decode():
     sd = model.ln_f.state_dict()
     ref = oracle.layernorm(h, sd["weight"].numpy(), sd["bias"].numpy())
     np.testing.assert_allclose(c(x).cpu().numpy(), ref, rtol=1e-3, atol=1e-4)
+
+
+@pytest.mark.parametrize("k, n, affine, bias", [(768, 2304, True, True), (61, 37, True, False),
+                                               (64, 48, False, True), (3072, 768, True, True)])
+def test_layernorm_prologue_of_a_gemv(k, n, affine, bias):
+    """LayerNorm -> Linear at one row runs as one GEMV with the LayerNorm as
+    its prologue; checked against the oracle interpreter and eager torch."""
+    torch.manual_seed(0)
+    ln = torch.nn.LayerNorm(k, elementwise_affine=affine)
+    if affine:
+        with torch.no_grad():
+            ln.weight.copy_(1 + 0.1 * torch.randn(k))
+            ln.bias.copy_(0.1 * torch.randn(k))
+    model = torch.nn.Sequential(ln, torch.nn.Linear(k, n, bias=bias), torch.nn.GELU(approximate="tanh")).eval()
+    x = 3.0 + 2.0 * torch.randn(1, k)
+    c = check(model, x)
+    assert c.report.lowering["launches"] == 1 and c.report.lowering["families"] == {"gemv": 1}

@@ -123,7 +123,8 @@ def test_block_uses_one_attention_launch(T):
     model = gpt2_init_(Block(768, 12, T), seed=T).eval()
     x = torch.randn(T, 768, generator=torch.Generator().manual_seed(T + 1))
     c = kiln.compile(model, (x,), device="cuda")
-    assert c.report.lowering["launches"] == 7 and n_attention(c) == 1
+    # at T = 1 both LayerNorms run as the prologue of the qkv / fc GEMV
+    assert c.report.lowering["launches"] == (5 if T == 1 else 7) and n_attention(c) == 1
     # the scores never get arena memory: the peak is the MLP's (768 + 768 + 3072) T floats
     assert c.report.arena_bytes == 4 * 4608 * T
     params = {k: v.numpy() for k, v in model.state_dict().items()}

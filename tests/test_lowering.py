@@ -174,8 +174,44 @@ def test_bias_gelu_is_one_elementwise_launch_with_vector_operands():
 
 def test_stack_decode_plan():
     _, prog = lowered(Stack(12, 768, 12, 1), torch.randn(1, 768))
-    assert len(prog.launches) == 12 * 9 + 1
+    # ln_1 and ln_2 of every layer run as the prologue of the qkv / fc GEMV;
+    # the final LayerNorm feeds the output and stays a row kernel
+    assert len(prog.launches) == 12 * 7 + 1
+    assert sum("prologue: layernorm" in l.summary for l in prog.launches) == 24
+    assert kl.FAMILY_NAMES[prog.launches[-1].family] == "row"
     kl.Plan([l.desc for l in prog.launches])
+
+
+def _ln_linear(affine=True, bias=True):
+    ln = torch.nn.LayerNorm(64, elementwise_affine=affine)
+    lin = torch.nn.Linear(64, 48, bias=bias)
+    return torch.nn.Sequential(ln, lin).eval()
+
+
+@pytest.mark.parametrize("affine", [True, False])
+def test_layernorm_feeding_a_gemv_becomes_its_prologue(affine):
+    _, prog = lowered(_ln_linear(affine), torch.randn(1, 64))
+    assert [kl.FAMILY_NAMES[l.family] for l in prog.launches] == ["gemv"]
+    d = prog.launches[0].desc
+    assert d.cfg[4] == 1 and "prologue: layernorm" in prog.launches[0].summary
+    if affine:
+        assert 2 <= d.cfg[5] < d.n_refs and 2 <= d.cfg[6] < d.n_refs and d.cfg[5] != d.cfg[6]
+    else:
+        assert d.cfg[5] == -1 and d.cfg[6] == -1
+    assert list(d.fparams)[:3] == pytest.approx([1 / 64, 1 / 64, 1e-5])
+    kl.Plan([l.desc for l in prog.launches])
+
+
+def test_layernorm_is_not_fused_when_its_output_has_other_users():
+    ln, lin = torch.nn.LayerNorm(64), torch.nn.Linear(64, 48)
+    _, prog = lowered(lambda x: (lin(ln(x)), ln(x) * 2.0), torch.randn(1, 64))
+    assert "row" in [kl.FAMILY_NAMES[l.family] for l in prog.launches]
+    assert not any(l.desc.cfg[4] for l in prog.launches if l.family == kl.FAM_GEMV)
+
+
+def test_layernorm_is_not_fused_into_a_multi_row_gemm():
+    _, prog = lowered(_ln_linear(), torch.randn(4, 64))
+    assert [kl.FAMILY_NAMES[l.family] for l in prog.launches] == ["row", "gemm"]
 
 
 @pytest.mark.parametrize("mutate, err", [
