@@ -318,10 +318,20 @@ def block_sweep(tokens, autotune):
             e_ms = ms_per_call(lambda: model(x))
             c._exe.replay_only()
             replay_ms = min(events_ms(c._exe.replay_only, 20) for _ in range(5))
+        # allow_tf32 (three-pass bf16 GEMMs): reported beside, never the headline
+        ct = kiln.compile(model, (x,), device="cuda", autotune=autotune, allow_tf32=True)
+        with torch.no_grad():
+            ref64 = model.double()(x.double())
+            model.float()
+            tf_err = ((ct(x).double() - ref64).abs().max() / ref64.abs().max()).item()
+            assert tf_err <= 5e-5, f"block T={T} allow_tf32: error {tf_err:.2e} of the output scale"
+            tf_ms = ms_per_call(lambda: ct(x))
         out[str(T)] = {"kiln_ms": round(k_ms, 4), "eager_ms": round(e_ms, 4), "replay_ms": round(replay_ms, 4),
                        "speedup": round(e_ms / k_ms, 3), "tflops": round(block_flops(T) / k_ms / 1e9, 2),
-                       "arena_mib": round(c.report.arena_bytes / 2**20, 2)}
-        log(f"block T={T}: kiln {k_ms:.4f} ms (replay {replay_ms:.4f}), eager {e_ms:.4f} ms")
+                       "arena_mib": round(c.report.arena_bytes / 2**20, 2),
+                       "allow_tf32_ms": round(tf_ms, 4), "allow_tf32_error_of_scale": float(f"{tf_err:.2e}")}
+        log(f"block T={T}: kiln {k_ms:.4f} ms (replay {replay_ms:.4f}), eager {e_ms:.4f} ms, "
+            f"allow_tf32 {tf_ms:.4f} ms")
     return out
 
 
@@ -342,7 +352,7 @@ def gemm_sweep(autotune):
     import kiln
     from models.transformer import gpt2_init_
 
-    out = {"fp32": {}, "bf16": {}}
+    out = {"fp32": {}, "bf16": {}, "bf16x3": {}}
     for m, n, k in GEMM_SHAPES:
         torch.manual_seed(0)
         lin = gpt2_init_(torch.nn.Linear(k, n), seed=1).eval().cuda()
@@ -376,6 +386,19 @@ def gemm_sweep(autotune):
                                        "frac_of_attainable": round(tf / attainable, 3)}
         log(f"gemm bf16 {m}x{n}x{k}: kiln {tf:.1f} TFLOP/s ({tf / attainable:.1%} of attainable "
             f"{attainable:.0f}), torch-bf16 {flops / tms / 1e9:.1f}")
+        # allow_tf32: the three-pass bf16 GEMM (fp32-class error, see
+        # tests/test_gpu_bf16x3.py); error against float64 of the fp32 inputs
+        cx = kiln.compile(lin, (x,), device="cuda", autotune=autotune, cuda_graphs=False, allow_tf32=True)
+        with torch.no_grad():
+            ref64 = x.double() @ lin.weight.double().t() + lin.bias.double()
+            err = ((cx(x).double() - ref64).abs().max() / ref64.abs().max()).item()
+            assert err <= 5e-5, f"bf16x3 GEMM {m}x{n}x{k}: error {err:.2e} of the output scale"
+            xms = graph_ms(lambda: cx._exe.run_into([x], outs))
+        out["bf16x3"][f"{m}x{n}x{k}"] = {"kiln_tflops": round(flops / xms / 1e9, 2), "kiln_us": round(xms * 1e3, 2),
+                                         "error_of_scale": float(f"{err:.2e}"),
+                                         "vs_fp32": round(kms / xms, 3)}
+        log(f"gemm bf16x3 {m}x{n}x{k}: kiln {flops / xms / 1e9:.1f} TFLOP/s ({kms / xms:.2f}x the fp32 path), "
+            f"error {err:.1e} of the output scale")
     return out
 
 

@@ -414,7 +414,12 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 // its fragments are read; accumulation stays fp32. In a 32-wide K step lane
 // group g holds K values 8g .. 8g+7 of A and of B - the same ownership as
 // the fp32 path, where MFMA j consumes value 8g + j.
-template <int BM, int BN, int BK, int WM, int WN, int NS, int VW, bool BF16B>
+// X3 (with BF16B): three-pass bf16. B is [batch][N][2K'], row n holding
+// bf16(w) in [0, K') and bf16(w - bf16(w)) in [K', 2K'); A splits the same
+// way as its fragments are read, and a.b = a_lo.b_hi + a_hi.b_lo + a_hi.b_hi
+// (the a_lo.b_lo term, ~2^-16 of the product, is dropped). A stage holds the
+// B hi rows, then the B lo rows.
+template <int BM, int BN, int BK, int WM, int WN, int NS, int VW, bool BF16B, bool X3 = false>
 __global__ __launch_bounds__(64 * WM * WN, 2) void gemm3_f32_kernel(const GemmArgs a) {
   constexpr int MT = 16;
   constexpr int kWaves = WM * WN, kThreads = 64 * kWaves;
@@ -425,7 +430,10 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void gemm3_f32_kernel(const GemmAr
   static_assert(BK == 32 || (BK == 64 && !BF16B), "K step");
   constexpr int B_CH = BN / 4;          // chunks per fp32 B row
   // stage sizes in 4-byte words (a bf16 B stage is BN rows of 64 bytes)
-  constexpr int A_FLOATS = BM * BK, B_FLOATS = BF16B ? BN * BK / 2 : BK * BN, STAGE = A_FLOATS + B_FLOATS;
+  static_assert(BF16B || !X3, "three-pass bf16 needs the bf16 B layout");
+  constexpr int B_HALF = BN * BK / 2;   // words of one bf16 copy of a B stage
+  constexpr int A_FLOATS = BM * BK, B_FLOATS = BF16B ? B_HALF * (X3 ? 2 : 1) : BK * BN,
+                STAGE = A_FLOATS + B_FLOATS;
   // B copy width in 4-byte words per lane
   constexpr int VB = BF16B ? 4 : VW;
   // copy instructions per wave per step: each covers 64 lanes x VW floats
@@ -482,10 +490,13 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void gemm3_f32_kernel(const GemmAr
   for (int i = 0; i < B_PER_WAVE; ++i) {
     const int p = (wave * B_PER_WAVE + i) * 64 + lane;
     if constexpr (BF16B) {
-      // byte offsets into the bf16 copy: row n, chunk of 8 K values
-      const int n = p / 4;
-      const int kk = ((p % 4) ^ swz_b16(n)) * 8;
-      b_mn[i] = min(n0 + n, a.N - 1) * (int)a.sb_n;
+      // byte offsets into the bf16 copy: row n, chunk of 8 K values (three
+      // pass: positions past the hi rows read the row's lo half, K' further)
+      const int half = X3 ? p / (BN * 4) : 0;
+      const int pp = p - half * BN * 4;
+      const int n = pp / 4;
+      const int kk = ((pp % 4) ^ swz_b16(n)) * 8;
+      b_mn[i] = min(n0 + n, a.N - 1) * (int)a.sb_n + half * (int)(a.sb_n / 2);
       b_kk[i] = kk;
       b_off0[i] = (uint32_t)(b_mn[i] + kk) * 2u;
     } else {
@@ -597,7 +608,31 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void gemm3_f32_kernel(const GemmAr
         const float4 v = *reinterpret_cast<const float4 *>(st + a_off[fm][h]);
         af[fm][4 * h + 0] = v.x, af[fm][4 * h + 1] = v.y, af[fm][4 * h + 2] = v.z, af[fm][4 * h + 3] = v.w;
       }
-    if constexpr (BF16B) {
+    if constexpr (BF16B && X3) {
+      bf16x8 ah[FM], al[FM], bh[FN], bl[FN];
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          ah[fm][e] = (__bf16)af[fm][e];
+          // the difference is exact in fp32; a non-finite hi part keeps lo 0
+          const float hv = (float)ah[fm][e];
+          al[fm][e] = (__bf16)(__builtin_isfinite(hv) ? af[fm][e] - hv : 0.0f);
+        }
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn) {
+        bh[fn] = *reinterpret_cast<const bf16x8 *>(st + b_off[fn]);
+        bl[fn] = *reinterpret_cast<const bf16x8 *>(st + b_off[fn] + B_HALF);
+      }
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn) {
+          acc[fm][fn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[fm], bh[fn], acc[fm][fn], 0, 0, 0);
+          acc[fm][fn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[fm], bl[fn], acc[fm][fn], 0, 0, 0);
+          acc[fm][fn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[fm], bh[fn], acc[fm][fn], 0, 0, 0);
+        }
+    } else if constexpr (BF16B) {
       bf16x8 a8[FM], b8[FN];
 #pragma unroll
       for (int fm = 0; fm < FM; ++fm)
@@ -775,6 +810,15 @@ struct TileCfg {
   X(19, 32, 64, 2, 2, 4)         \
   X(20, 128, 256, 2, 4, 3)
 
+// three-pass bf16 (allow_tf32): the bf16 shapes with hi and lo B rows per stage
+#define KH_GEMM3_BF16X3_CONFIGS(X) \
+  X(26, 128, 128, 2, 2, 3)         \
+  X(27, 64, 128, 2, 2, 3)          \
+  X(28, 128, 64, 2, 2, 3)          \
+  X(29, 64, 64, 2, 2, 3)           \
+  X(30, 32, 64, 2, 2, 3)           \
+  X(31, 128, 256, 2, 4, 2)
+
 // copy pipeline with 64 K values per stage (half the barriers and fragment
 // reads per flop; two stages to stay within LDS)
 #define KH_GEMM3_DEEP_CONFIGS(X) \
@@ -801,6 +845,9 @@ constexpr TileCfg kConfigs[] = {
 #define KH_CFG3_ROW(id, bm, bn, bk, wm, wn, ns) {bm, bn, bk, wm, wn, 1, 16, 3, ns, KH_PREC_FP32},
     KH_GEMM3_DEEP_CONFIGS(KH_CFG3_ROW)
 #undef KH_CFG3_ROW
+#define KH_CFGX_ROW(id, bm, bn, wm, wn, ns) {bm, bn, 32, wm, wn, 1, 16, 3, ns, KH_PREC_BF16X3},
+    KH_GEMM3_BF16X3_CONFIGS(KH_CFGX_ROW)
+#undef KH_CFGX_ROW
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
@@ -834,6 +881,17 @@ hipError_t launch_config(int id, const GemmArgs &a, dim3 grid, hipStream_t strea
     break;
     KH_GEMM3_BF16_CONFIGS(KH_CFGB_CASE)
 #undef KH_CFGB_CASE
+#define KH_CFGX_CASE(cid, bm, bn, wm, wn, ns)                                                                        \
+  case cid:                                                                                                         \
+    if (a.a_vec)                                                                                                    \
+      hipLaunchKernelGGL((gemm3_f32_kernel<bm, bn, 32, wm, wn, ns, 4, true, true>), grid, dim3(64 * wm * wn), 0,    \
+                         stream, a);                                                                                \
+    else                                                                                                            \
+      hipLaunchKernelGGL((gemm3_f32_kernel<bm, bn, 32, wm, wn, ns, 1, true, true>), grid, dim3(64 * wm * wn), 0,    \
+                         stream, a);                                                                                \
+    break;
+    KH_GEMM3_BF16X3_CONFIGS(KH_CFGX_CASE)
+#undef KH_CFGX_CASE
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -999,7 +1057,7 @@ std::unique_ptr<Op> make_gemm(const kh_launch &L, std::string &err, bool &unsupp
     err = "matmul: unknown tile configuration " + std::to_string(cfg);
     return nullptr;
   }
-  if (L.cfg[3] != KH_PREC_FP32 && L.cfg[3] != KH_PREC_BF16) {
+  if (L.cfg[3] != KH_PREC_FP32 && L.cfg[3] != KH_PREC_BF16 && L.cfg[3] != KH_PREC_BF16X3) {
     unsupported = true;
     err = "matmul: precision not compiled into this library";
     return nullptr;
@@ -1028,6 +1086,15 @@ std::unique_ptr<Op> make_gemm(const kh_launch &L, std::string &err, bool &unsupp
     }
     op->b_vec_layout = true;
   }
+  if (t.prec == KH_PREC_BF16X3) {
+    // B must be the three-pass copy: [batch][N][2K'], hi then lo halves of K'
+    const kh_ref &rb = L.refs[1];
+    if (a.sb_k != 1 || a.sb_n % 16 || a.sb_b % 8 || rb.offset % 8 || a.sb_n / 2 < K) {
+      err = "matmul: bf16x3 B operand must be [batch][N][2K'] with K' a multiple of 8 and >= K";
+      return nullptr;
+    }
+    op->b_vec_layout = true;
+  }
   if (t.kind == 3) {
     // 128-bit copies never straddle the end of a row or of K
     op->a_vec_layout = op->a_vec_layout && K % 4 == 0;
@@ -1037,7 +1104,7 @@ std::unique_ptr<Op> make_gemm(const kh_launch &L, std::string &err, bool &unsupp
     const int64_t span_a = std::max<int64_t>(0, M - 1) * std::abs(a.sa_m) + std::max<int64_t>(0, K - 1) * std::abs(a.sa_k);
     const int64_t span_b = std::max<int64_t>(0, K - 1) * std::abs(a.sb_k) + std::max<int64_t>(0, N - 1) * std::abs(a.sb_n);
     if (span_a >= (1ll << 29) || span_b >= (1ll << 29) || a.sa_m < 0 || a.sa_k < 0 || a.sb_k < 0 || a.sb_n < 0) {
-      if (t.prec == KH_PREC_BF16) {
+      if (t.prec != KH_PREC_FP32) {
         unsupported = true;
         err = "matmul: bf16 operands spanning 2^29 elements or more";
         return nullptr;

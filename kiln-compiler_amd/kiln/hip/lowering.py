@@ -644,8 +644,8 @@ class _Lowerer:
         d.gemm[0], d.gemm[1], d.gemm[2], d.gemm[3] = batch, m, n, kk
         d.refs[0] = ref3(a_src, (batch, m, kk))
         d.refs[1] = ref3(b, (batch, kk, n))
-        if prec == "bf16":
-            d.refs[1] = self.bf16_weight(b, d.refs[1], batch, kk, n)
+        if prec in ("bf16", "bf16x3"):
+            d.refs[1] = self.bf16_weight(b, d.refs[1], batch, kk, n, split=prec == "bf16x3")
         externals = []
         for nd in k.nodes:
             if nd is mm:
@@ -737,7 +737,7 @@ class _Lowerer:
             mm = next(n for n in k.nodes if n.op == "matmul")
             cfg = dict(self.matmul_config(self.g, k))
             prec = cfg.get("precision", self.precision)
-            if prec == "bf16" and self.layouts[mm.inputs[1]].base[0] != "const":
+            if prec in ("bf16", "bf16x3") and self.layouts[mm.inputs[1]].base[0] != "const":
                 # bf16 inputs need B as a build-time bf16 copy of a constant; a
                 # matmul on two activations stays on the fp32 path (more exact)
                 prec = "fp32"
@@ -811,19 +811,21 @@ class _Lowerer:
             skip.add(k)
         return skip
 
-    def bf16_weight(self, b, ref, batch, kk, n):
+    def bf16_weight(self, b, ref, batch, kk, n, split=False):
         """Ref of the bf16 [batch][N][K'] copy of constant view `b` (whose fp32
-        ref over (b, k, n) is `ref`); the copy is registered as a derived
+        ref over (b, k, n) is `ref`), or with `split` the three-pass
+        [batch][N][2K'] hi/lo copy; the copy is registered as a derived
         constant and made when the executable is built."""
         src = self.layouts[b].base[1]
         strides = (int(ref.strides[0]), int(ref.strides[1]), int(ref.strides[2]))
-        name = f"{src}@bf16:{int(ref.offset)}:{strides[0]},{strides[1]},{strides[2]}:{batch}x{kk}x{n}"
+        kind = "bf16x3" if split else "bf16"
+        name = f"{src}@{kind}:{int(ref.offset)}:{strides[0]},{strides[1]},{strides[2]}:{batch}x{kk}x{n}"
         self.program.derived[name] = (src, int(ref.offset), strides, batch, kk, n)
-        kp = bf16.padded_k(kk)
+        row = bf16.padded_k(kk) * (2 if split else 1)
         r = kl.Ref()
         r.base, r.index = self.slot_of(("const", name))
         r.offset = 0
-        r.strides[0], r.strides[1], r.strides[2] = (n * kp if batch > 1 else 0), 1, kp
+        r.strides[0], r.strides[1], r.strides[2] = (n * row if batch > 1 else 0), 1, row
         return r
 
     # attention --------------------------------------------------------------------------------

@@ -157,7 +157,8 @@ class HIPExecutable:
         lowering derived from one (bf16 GEMM weights, as int16 bit patterns)."""
         if name in program.derived:
             src, offset, strides, batch, k, n = program.derived[name]
-            return bf16.weight_copy(constants[src], offset, strides, batch, k, n).view(np.int16)
+            copy = bf16.weight_copy_x3 if "@bf16x3:" in name else bf16.weight_copy
+            return copy(constants[src], offset, strides, batch, k, n).view(np.int16)
         return np.ascontiguousarray(constants[name], np.float32)
 
     # -- launching ------------------------------------------------------------------

@@ -32,7 +32,7 @@ def main(argv=None):
     p.add_argument("--out", default=str(autotune.SHIPPED_PATH))
     args = p.parse_args(argv)
     table = {}
-    for precision in ("fp32", "bf16"):
+    for precision in ("fp32", "bf16", "bf16x3"):
         tuner = autotune.GPUAutotuner(precision=precision, use_cache=False, use_shipped=False)
         device = tuner.device_key()
         for m, n, k in SHAPES:

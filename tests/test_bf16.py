@@ -93,3 +93,34 @@ def test_bf16_defaults_and_candidates_are_bf16_tiles():
         assert autotune.PRECISION[d["tile"]] == "bf16"
         assert all(autotune.PRECISION[c["tile"]] == "bf16"
                    for c in autotune.candidates(1, m, n, k, cus=256, precision="bf16"))
+
+
+def test_three_pass_weight_copy_layout_and_values():
+    rng = np.random.default_rng(3)
+    w = rng.standard_normal((2, 13, 11)).astype(np.float32)          # [batch, K, N], K not a multiple of 8
+    w[0, 0, 0], w[1, 2, 3] = np.inf, np.nan
+    out = bf16.weight_copy_x3(w, 0, (13 * 11, 11, 1), 2, 13, 11)
+    kp = bf16.padded_k(13)
+    assert out.shape == (2, 11, 2 * kp) and out.dtype == np.uint16
+    np.testing.assert_array_equal(out[:, :, :kp], bf16.weight_copy(w, 0, (13 * 11, 11, 1), 2, 13, 11))
+    assert not out[:, :, 13:kp].any() and not out[:, :, kp + 13:].any()
+    hi = bf16.bf16_value(out[:, :, :13]).transpose(0, 2, 1)
+    lo = bf16.bf16_value(out[:, :, kp:kp + 13]).transpose(0, 2, 1)
+    # the hi + lo split is checked against the C oracle's rounding
+    finite = np.isfinite(w)
+    np.testing.assert_array_equal(hi[finite], oracle.bf16_round(w)[finite])
+    np.testing.assert_array_equal(lo[finite], oracle.bf16_round((w - hi).astype(np.float32))[finite])
+    assert np.all(np.abs((hi[finite] + lo[finite]) - w[finite]) <= 2.0 ** -16 * np.abs(w[finite]))
+    assert hi[0, 0, 0] == np.inf and lo[0, 0, 0] == 0.0 and np.isnan(hi[1, 2, 3]) and lo[1, 2, 3] == 0.0
+
+
+def test_allow_tf32_lowers_to_the_three_pass_gemm():
+    lin = torch.nn.Linear(64, 40).eval()
+    g = import_exported(torch.export.export(lin, (torch.randn(32, 64),)).run_decompositions())
+    PassManager(build_passes(Options(device="cuda", allow_tf32=True))).run(g)
+    prog = lower_graph(g, precision="bf16x3")
+    (l,) = prog.launches
+    assert l.desc.cfg[3] == kl.PREC_BF16X3 and autotune.PRECISION[l.desc.cfg[1]] == "bf16x3"
+    (name,) = [n for n in prog.derived if "@bf16x3:" in n]
+    assert list(l.desc.refs[1].strides)[:3] == [0, 1, 2 * bf16.padded_k(64)]
+    kl.Plan([l.desc for l in prog.launches])
