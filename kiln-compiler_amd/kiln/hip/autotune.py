@@ -153,7 +153,7 @@ def default_config_for(batch, m, n, k, cus=None, precision="fp32") -> dict:
     cus = cus or device_cus()
     best = None
     for tile in TILES:
-        if PRECISION[tile] != precision or not fits(tile, m, n, k):
+        if tile in SPILLING or PRECISION[tile] != precision or not fits(tile, m, n, k):
             continue
         for s in SPLITS:
             if s > 1 and k // s < 128:
@@ -166,13 +166,18 @@ def default_config_for(batch, m, n, k, cus=None, precision="fp32") -> dict:
     return {"tile": best[1], "splitk": best[2]}
 
 
+# configurations the compiler builds with register spills (scratch), never
+# worth timing: 22 (64 x 128, 64-deep K steps)
+SPILLING = {22}
+
+
 def candidates(batch, m, n, k, cus=None, precision="fp32") -> list:
     if m == 1 and precision == "fp32":
         return [{"tile": v, "splitk": s} for v, s in GEMV_CANDIDATES if s == 0 or k // s >= 64]
     cus = cus or device_cus()
     out = []
     for tile in TILES:
-        if PRECISION[tile] != precision or not fits(tile, m, n, k):
+        if tile in SPILLING or PRECISION[tile] != precision or not fits(tile, m, n, k):
             continue
         for s in SPLITS:
             if s > 1 and k // s < 64:

@@ -316,3 +316,9 @@ def test_shipped_tuning_table_is_consistent():
         else:
             assert autotune.PRECISION[tile] == precision and (m == 1 or autotune.fits(tile, m, n, k))
         assert arch.startswith("gfx950") and int(cus) > 0
+
+
+def test_tuner_never_times_a_spilling_configuration():
+    for shape in ((1, 2048, 3072, 768), (1, 128, 768, 3072), (1, 300, 452, 96)):
+        assert not any(c["tile"] in autotune.SPILLING for c in autotune.candidates(*shape, cus=256))
+        assert autotune.default_config_for(*shape, cus=256)["tile"] not in autotune.SPILLING
