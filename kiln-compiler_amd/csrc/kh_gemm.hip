@@ -427,7 +427,7 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void gemm3_f32_kernel(const GemmAr
   constexpr int FM = TM / MT, FN = TN / MT;
   constexpr int KG = BK / 4;            // K values per lane group per step
   constexpr int ACH = BK / 4;           // 16-byte chunks per A row
-  static_assert(BK == 32 || (BK == 64 && !BF16B), "K step");
+  static_assert(BK == 32 || ((BK == 64 || BK == 128) && !BF16B), "K step");
   constexpr int B_CH = BN / 4;          // chunks per fp32 B row
   // stage sizes in 4-byte words (a bf16 B stage is BN rows of 64 bytes)
   static_assert(BF16B || !X3, "three-pass bf16 needs the bf16 B layout");
@@ -810,6 +810,12 @@ struct TileCfg {
   X(19, 32, 64, 2, 2, 4)         \
   X(20, 128, 256, 2, 4, 3)
 
+// 128-deep K steps for the smallest pipelined tile (M = 128 blocks: a quarter
+// of the 32-deep tile's barriers per K)
+#define KH_GEMM3_K128_CONFIGS(X) \
+  X(32, 32, 64, 128, 2, 2, 2)    \
+  X(33, 32, 64, 128, 2, 2, 3)
+
 // three-pass bf16 (allow_tf32): the bf16 shapes with hi and lo B rows per stage
 #define KH_GEMM3_BF16X3_CONFIGS(X) \
   X(26, 128, 128, 2, 2, 3)         \
@@ -848,6 +854,9 @@ constexpr TileCfg kConfigs[] = {
 #define KH_CFGX_ROW(id, bm, bn, wm, wn, ns) {bm, bn, 32, wm, wn, 1, 16, 3, ns, KH_PREC_BF16X3},
     KH_GEMM3_BF16X3_CONFIGS(KH_CFGX_ROW)
 #undef KH_CFGX_ROW
+#define KH_CFG3_ROW(id, bm, bn, bk, wm, wn, ns) {bm, bn, bk, wm, wn, 1, 16, 3, ns, KH_PREC_FP32},
+    KH_GEMM3_K128_CONFIGS(KH_CFG3_ROW)
+#undef KH_CFG3_ROW
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
@@ -871,6 +880,7 @@ hipError_t launch_config(int id, const GemmArgs &a, dim3 grid, hipStream_t strea
     break;
     KH_GEMM3_CONFIGS(KH_CFG3_CASE)
     KH_GEMM3_DEEP_CONFIGS(KH_CFG3_CASE)
+    KH_GEMM3_K128_CONFIGS(KH_CFG3_CASE)
 #undef KH_CFG3_CASE
 #define KH_CFGB_CASE(cid, bm, bn, wm, wn, ns)                                                                      \
   case cid:                                                                                                       \

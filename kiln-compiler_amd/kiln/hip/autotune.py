@@ -74,6 +74,8 @@ TILES = {
     29: (64, 64, 32, 2, 2, 1, 16),
     30: (32, 64, 32, 2, 2, 1, 16),
     31: (128, 256, 32, 2, 4, 1, 16),
+    32: (32, 64, 128, 2, 2, 1, 16),
+    33: (32, 64, 128, 2, 2, 1, 16),
 }
 # input precision of each configuration: 15-20 bf16 (A rounded in the kernel,
 # B a bf16 copy of a constant), 26-31 three-pass bf16 (allow_tf32: A and B
@@ -84,12 +86,12 @@ PRECISION = {t: ("bf16" if 15 <= t <= 20 else "bf16x3" if 26 <= t <= 31 else "fp
 # (fraction of the CU's fp32 MFMA rate), for the default heuristic only
 OCCUPANCY = {0: 2, 1: 2, 2: 3, 3: 2, 4: 4, 5: 2, 6: 1, 7: 1, 8: 4, 9: 4, 10: 4, 11: 5, 12: 5, 13: 4, 14: 2,
              15: 2, 16: 2, 17: 1, 18: 3, 19: 4, 20: 1, 21: 2, 22: 1, 23: 2, 24: 1, 25: 2,
-             26: 1, 27: 2, 28: 2, 29: 3, 30: 4, 31: 1}
+             26: 1, 27: 2, 28: 2, 29: 3, 30: 4, 31: 1, 32: 1, 33: 1}
 EFFICIENCY = {0: 0.62, 1: 0.6, 2: 0.62, 3: 0.58, 4: 0.66, 5: 0.62, 6: 0.67, 7: 0.55,
               8: 0.55, 9: 0.55, 10: 0.5, 11: 0.5, 12: 0.45, 13: 0.5, 14: 0.55,
               15: 0.15, 16: 0.15, 17: 0.15, 18: 0.15, 19: 0.15, 20: 0.15,
               21: 0.62, 22: 0.6, 23: 0.62, 24: 0.67, 25: 0.62,
-              26: 0.3, 27: 0.3, 28: 0.3, 29: 0.3, 30: 0.3, 31: 0.3}
+              26: 0.3, 27: 0.3, 28: 0.3, 29: 0.3, 30: 0.3, 31: 0.3, 32: 0.62, 33: 0.62}
 # MFMA rate of a CU relative to fp32, per precision
 RATE = {"fp32": 1.0, "bf16": 16.0, "bf16x3": 16.0 / 3}
 CU_MFLOP_PER_US = 0.614          # fp32 MFMA: 256 flop/clk/CU at 2.4 GHz
