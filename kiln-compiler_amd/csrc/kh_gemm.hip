@@ -401,19 +401,26 @@ __device__ __forceinline__ void stage_barrier() {
   asm volatile("" ::: "memory");
 }
 
-// B rows of a bf16 stage are 32 K values = 64 bytes = 4 chunks; row n puts
-// chunk c at c ^ swz_b16(n), so the 16 rows one 128-bit fragment read
-// touches hit distinct banks.
-__device__ __forceinline__ int swz_b16(int n) { return ((n >> 1) ^ (n >> 3)) & 3; }
+// B rows of a bf16 stage are BK K values = BK / 8 chunks of 16 bytes; row n
+// puts chunk c at c ^ swz_b16<CB>(n), so the 16 rows one 128-bit fragment
+// read touches hit distinct banks (64 banks of 4 bytes: 4, 2 or 1 rows of
+// 64, 128 or 256 bytes share a bank cycle).
+template <int CB>
+__device__ __forceinline__ int swz_b16(int n) {
+  if constexpr (CB == 4) return ((n >> 1) ^ (n >> 3)) & 3;
+  else if constexpr (CB == 8) return (n >> 1) & 7;
+  else return n & 15;
+}
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 // BF16B: B is a bf16 copy of a constant in [batch][N][K'] layout (K' = K
 // rounded up to 8, zero padded) and the products run on
 // v_mfma_f32_16x16x32_bf16 with A rounded to bf16 (round to nearest even) as
-// its fragments are read; accumulation stays fp32. In a 32-wide K step lane
-// group g holds K values 8g .. 8g+7 of A and of B - the same ownership as
-// the fp32 path, where MFMA j consumes value 8g + j.
+// its fragments are read; accumulation stays fp32. In a K step lane group g
+// holds K values KG.g .. KG.g + KG-1 of A and of B (KG = BK / 4) - the same
+// ownership as the fp32 path - and the step's BK / 32 MFMAs of one output
+// block take them 8 at a time.
 // X3 (with BF16B): three-pass bf16. B is [batch][N][2K'], row n holding
 // bf16(w) in [0, K') and bf16(w - bf16(w)) in [K', 2K'); A splits the same
 // way as its fragments are read, and a.b = a_lo.b_hi + a_hi.b_lo + a_hi.b_hi
@@ -427,7 +434,9 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void gemm3_f32_kernel(const GemmAr
   constexpr int FM = TM / MT, FN = TN / MT;
   constexpr int KG = BK / 4;            // K values per lane group per step
   constexpr int ACH = BK / 4;           // 16-byte chunks per A row
-  static_assert(BK == 32 || ((BK == 64 || BK == 128) && !BF16B), "K step");
+  static_assert(BK == 32 || BK == 64 || BK == 128, "K step");
+  constexpr int CB = BK / 8;            // 16-byte chunks per bf16 B row
+  constexpr int KB = BF16B ? BK / 32 : 1;  // bf16 MFMAs per output block per step
   constexpr int B_CH = BN / 4;          // chunks per fp32 B row
   // stage sizes in 4-byte words (a bf16 B stage is BN rows of 64 bytes)
   static_assert(BF16B || !X3, "three-pass bf16 needs the bf16 B layout");
@@ -492,10 +501,10 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void gemm3_f32_kernel(const GemmAr
     if constexpr (BF16B) {
       // byte offsets into the bf16 copy: row n, chunk of 8 K values (three
       // pass: positions past the hi rows read the row's lo half, K' further)
-      const int half = X3 ? p / (BN * 4) : 0;
-      const int pp = p - half * BN * 4;
-      const int n = pp / 4;
-      const int kk = ((pp % 4) ^ swz_b16(n)) * 8;
+      const int half = X3 ? p / (BN * CB) : 0;
+      const int pp = p - half * BN * CB;
+      const int n = pp / CB;
+      const int kk = ((pp % CB) ^ swz_b16<CB>(n)) * 8;
       b_mn[i] = min(n0 + n, a.N - 1) * (int)a.sb_n + half * (int)(a.sb_n / 2);
       b_kk[i] = kk;
       b_off0[i] = (uint32_t)(b_mn[i] + kk) * 2u;
@@ -574,7 +583,7 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void gemm3_f32_kernel(const GemmAr
   // per-lane LDS offsets of the MFMA fragments (loop invariant)
   const int g = lane / MT, li = lane % MT;
   constexpr int AH = KG / 4;             // 128-bit A reads per fragment
-  int a_off[FM][AH], b_off[FN];
+  int a_off[FM][AH], b_off[FN][KB];
 #pragma unroll
   for (int fm = 0; fm < FM; ++fm) {
     const int r = wm * TM + fm * MT + li;
@@ -584,10 +593,13 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void gemm3_f32_kernel(const GemmAr
 #pragma unroll
   for (int fn = 0; fn < FN; ++fn) {
     const int n = wn * TN + fn * MT + li;
-    if constexpr (BF16B)
-      b_off[fn] = A_FLOATS + n * (BK / 2) + ((g ^ swz_b16(n)) * 4);  // word offset of 8 bf16
-    else
-      b_off[fn] = A_FLOATS + g * KG * BN + ((((n / 4) + 4 * g) % B_CH) * 4) + (n & 3);
+    if constexpr (BF16B) {
+#pragma unroll
+      for (int j = 0; j < KB; ++j)  // word offset of the 8 bf16 K values KG.g + 8j ..
+        b_off[fn][j] = A_FLOATS + n * (BK / 2) + (((KB * g + j) ^ swz_b16<CB>(n)) * 4);
+    } else {
+      b_off[fn][0] = A_FLOATS + g * KG * BN + ((((n / 4) + 4 * g) % B_CH) * 4) + (n & 3);
+    }
   }
 
   acc_t acc[FM][FN];
@@ -609,48 +621,54 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void gemm3_f32_kernel(const GemmAr
         af[fm][4 * h + 0] = v.x, af[fm][4 * h + 1] = v.y, af[fm][4 * h + 2] = v.z, af[fm][4 * h + 3] = v.w;
       }
     if constexpr (BF16B && X3) {
-      bf16x8 ah[FM], al[FM], bh[FN], bl[FN];
 #pragma unroll
-      for (int fm = 0; fm < FM; ++fm)
+      for (int j = 0; j < KB; ++j) {
+        bf16x8 ah[FM], al[FM], bh[FN], bl[FN];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          ah[fm][e] = (__bf16)af[fm][e];
-          // the difference is exact in fp32; a non-finite hi part keeps lo 0
-          const float hv = (float)ah[fm][e];
-          al[fm][e] = (__bf16)(__builtin_isfinite(hv) ? af[fm][e] - hv : 0.0f);
-        }
+        for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
-      for (int fn = 0; fn < FN; ++fn) {
-        bh[fn] = *reinterpret_cast<const bf16x8 *>(st + b_off[fn]);
-        bl[fn] = *reinterpret_cast<const bf16x8 *>(st + b_off[fn] + B_HALF);
-      }
-#pragma unroll
-      for (int fm = 0; fm < FM; ++fm)
+          for (int e = 0; e < 8; ++e) {
+            ah[fm][e] = (__bf16)af[fm][8 * j + e];
+            // the difference is exact in fp32; a non-finite hi part keeps lo 0
+            const float hv = (float)ah[fm][e];
+            al[fm][e] = (__bf16)(__builtin_isfinite(hv) ? af[fm][8 * j + e] - hv : 0.0f);
+          }
 #pragma unroll
         for (int fn = 0; fn < FN; ++fn) {
-          acc[fm][fn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[fm], bh[fn], acc[fm][fn], 0, 0, 0);
-          acc[fm][fn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[fm], bl[fn], acc[fm][fn], 0, 0, 0);
-          acc[fm][fn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[fm], bh[fn], acc[fm][fn], 0, 0, 0);
+          bh[fn] = *reinterpret_cast<const bf16x8 *>(st + b_off[fn][j]);
+          bl[fn] = *reinterpret_cast<const bf16x8 *>(st + b_off[fn][j] + B_HALF);
         }
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+          for (int fn = 0; fn < FN; ++fn) {
+            acc[fm][fn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[fm], bh[fn], acc[fm][fn], 0, 0, 0);
+            acc[fm][fn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[fm], bl[fn], acc[fm][fn], 0, 0, 0);
+            acc[fm][fn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[fm], bh[fn], acc[fm][fn], 0, 0, 0);
+          }
+      }
     } else if constexpr (BF16B) {
-      bf16x8 a8[FM], b8[FN];
 #pragma unroll
-      for (int fm = 0; fm < FM; ++fm)
+      for (int j = 0; j < KB; ++j) {
+        bf16x8 a8[FM], b8[FN];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) a8[fm][e] = (__bf16)af[fm][e];
+        for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
-      for (int fn = 0; fn < FN; ++fn) b8[fn] = *reinterpret_cast<const bf16x8 *>(st + b_off[fn]);
+          for (int e = 0; e < 8; ++e) a8[fm][e] = (__bf16)af[fm][8 * j + e];
 #pragma unroll
-      for (int fm = 0; fm < FM; ++fm)
+        for (int fn = 0; fn < FN; ++fn) b8[fn] = *reinterpret_cast<const bf16x8 *>(st + b_off[fn][j]);
 #pragma unroll
-        for (int fn = 0; fn < FN; ++fn)
-          acc[fm][fn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a8[fm], b8[fn], acc[fm][fn], 0, 0, 0);
+        for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+          for (int fn = 0; fn < FN; ++fn)
+            acc[fm][fn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a8[fm], b8[fn], acc[fm][fn], 0, 0, 0);
+      }
     } else {
       float bf[FN][KG];
 #pragma unroll
       for (int fn = 0; fn < FN; ++fn)
 #pragma unroll
-        for (int j = 0; j < KG; ++j) bf[fn][j] = st[b_off[fn] + j * BN];
+        for (int j = 0; j < KG; ++j) bf[fn][j] = st[b_off[fn][0] + j * BN];
 #pragma unroll
       for (int j = 0; j < KG; ++j)
 #pragma unroll
@@ -816,6 +834,25 @@ struct TileCfg {
   X(32, 32, 64, 128, 2, 2, 2)    \
   X(33, 32, 64, 128, 2, 2, 3)
 
+// bf16-input configurations with 64- and 128-deep K steps (two or four bf16
+// MFMAs per output block between barriers instead of one)
+#define KH_GEMM3_BF16_DEEP_CONFIGS(X) \
+  X(34, 128, 128, 64, 2, 2, 2)        \
+  X(35, 64, 128, 64, 2, 2, 2)         \
+  X(36, 128, 64, 64, 2, 2, 2)         \
+  X(37, 64, 64, 64, 2, 2, 3)          \
+  X(38, 32, 64, 64, 2, 2, 3)          \
+  X(39, 128, 256, 64, 2, 4, 2)        \
+  X(40, 32, 64, 128, 2, 2, 2)         \
+  X(41, 64, 64, 128, 2, 2, 2)
+
+// three-pass bf16 with 64-deep K steps
+#define KH_GEMM3_BF16X3_DEEP_CONFIGS(X) \
+  X(42, 128, 128, 64, 2, 2, 2)          \
+  X(43, 64, 128, 64, 2, 2, 2)           \
+  X(44, 64, 64, 64, 2, 2, 2)            \
+  X(45, 32, 64, 64, 2, 2, 3)
+
 // three-pass bf16 (allow_tf32): the bf16 shapes with hi and lo B rows per stage
 #define KH_GEMM3_BF16X3_CONFIGS(X) \
   X(26, 128, 128, 2, 2, 3)         \
@@ -857,6 +894,12 @@ constexpr TileCfg kConfigs[] = {
 #define KH_CFG3_ROW(id, bm, bn, bk, wm, wn, ns) {bm, bn, bk, wm, wn, 1, 16, 3, ns, KH_PREC_FP32},
     KH_GEMM3_K128_CONFIGS(KH_CFG3_ROW)
 #undef KH_CFG3_ROW
+#define KH_CFGBD_ROW(id, bm, bn, bk, wm, wn, ns) {bm, bn, bk, wm, wn, 1, 16, 3, ns, KH_PREC_BF16},
+    KH_GEMM3_BF16_DEEP_CONFIGS(KH_CFGBD_ROW)
+#undef KH_CFGBD_ROW
+#define KH_CFGXD_ROW(id, bm, bn, bk, wm, wn, ns) {bm, bn, bk, wm, wn, 1, 16, 3, ns, KH_PREC_BF16X3},
+    KH_GEMM3_BF16X3_DEEP_CONFIGS(KH_CFGXD_ROW)
+#undef KH_CFGXD_ROW
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
@@ -902,6 +945,22 @@ hipError_t launch_config(int id, const GemmArgs &a, dim3 grid, hipStream_t strea
     break;
     KH_GEMM3_BF16X3_CONFIGS(KH_CFGX_CASE)
 #undef KH_CFGX_CASE
+#define KH_CFGD_CASE(cid, bm, bn, bk, wm, wn, ns, x3)                                                          \
+  case cid:                                                                                                  \
+    if (a.a_vec)                                                                                             \
+      hipLaunchKernelGGL((gemm3_f32_kernel<bm, bn, bk, wm, wn, ns, 4, true, x3>), grid, dim3(64 * wm * wn), 0, \
+                         stream, a);                                                                         \
+    else                                                                                                     \
+      hipLaunchKernelGGL((gemm3_f32_kernel<bm, bn, bk, wm, wn, ns, 1, true, x3>), grid, dim3(64 * wm * wn), 0, \
+                         stream, a);                                                                         \
+    break;
+#define KH_CFGBD_CASE(cid, bm, bn, bk, wm, wn, ns) KH_CFGD_CASE(cid, bm, bn, bk, wm, wn, ns, false)
+#define KH_CFGXD_CASE(cid, bm, bn, bk, wm, wn, ns) KH_CFGD_CASE(cid, bm, bn, bk, wm, wn, ns, true)
+    KH_GEMM3_BF16_DEEP_CONFIGS(KH_CFGBD_CASE)
+    KH_GEMM3_BF16X3_DEEP_CONFIGS(KH_CFGXD_CASE)
+#undef KH_CFGBD_CASE
+#undef KH_CFGXD_CASE
+#undef KH_CFGD_CASE
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

@@ -30,9 +30,14 @@ SHAPES = sorted({
 def main(argv=None):
     p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     p.add_argument("--out", default=str(autotune.SHIPPED_PATH))
+    p.add_argument("--precision", nargs="+", choices=("fp32", "bf16", "bf16x3"), default=None,
+                   help="re-tune only these precisions and keep the table's other entries")
     args = p.parse_args(argv)
     table = {}
-    for precision in ("fp32", "bf16", "bf16x3"):
+    if args.precision:
+        keep = autotune.shipped_configs()
+        table = {k: v for k, v in keep.items() if k.split("|")[-2] not in args.precision}
+    for precision in args.precision or ("fp32", "bf16", "bf16x3"):
         tuner = autotune.GPUAutotuner(precision=precision, use_cache=False, use_shipped=False)
         device = tuner.device_key()
         for m, n, k in SHAPES:
