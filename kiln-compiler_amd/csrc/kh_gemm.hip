@@ -32,6 +32,7 @@
 //   * remap workgroup ids so each XCD (own L2) receives a contiguous block of
 //     tiles.
 #include <algorithm>
+#include <cmath>
 #include <cstdlib>
 #include <cstring>
 #include <type_traits>
@@ -75,6 +76,20 @@ __device__ __forceinline__ int xcd_remap(int id, int n) {
   return (id % kXcd) * (n / kXcd) + id / kXcd;
 }
 
+// Tile coordinates of workgroup `id`: the XCD remap, then the tile range
+// walked `group_m` tile rows at a time, column-major inside a group, so the
+// workgroups one XCD holds at once share a few A row panels and a narrow band
+// of B column panels (both stay in that XCD's 4 MB L2). group_m = 1 is
+// row-major order.
+__device__ __forceinline__ void tile_coords(int id, const GemmArgs &a, int &tm, int &tn) {
+  const int tile = xcd_remap(id, a.tiles_m * a.tiles_n);
+  const int span = a.group_m * a.tiles_n;
+  const int g = tile / span, r = tile - g * span;
+  const int rows = min(a.group_m, a.tiles_m - g * a.group_m);
+  tm = g * a.group_m + r % rows;
+  tn = r / rows;
+}
+
 template <int BM, int BN, int BK, int WM, int WN, int WK, int MT>
 __global__ __launch_bounds__(64 * WM * WN * WK) void gemm_f32_kernel(const GemmArgs a) {
   constexpr int kThreads = 64 * WM * WN * WK;
@@ -108,9 +123,8 @@ __global__ __launch_bounds__(64 * WM * WN * WK) void gemm_f32_kernel(const GemmA
   const int wk = wave / (WM * WN);
   const int wm = (wave % (WM * WN)) / WN;
   const int wn = wave % WN;
-  const int n_tiles = a.tiles_m * a.tiles_n;
-  const int tile = xcd_remap(blockIdx.x, n_tiles);
-  const int tm = tile / a.tiles_n, tn = tile % a.tiles_n;
+  int tm, tn;
+  tile_coords(blockIdx.x, a, tm, tn);
   const int bidx = blockIdx.y, split = blockIdx.z;
   const int m0 = tm * BM, n0 = tn * BN;
   const int k_begin = split * a.k_per_split;
@@ -462,9 +476,8 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void gemm3_f32_kernel(const GemmAr
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int wm = wave / WN, wn = wave % WN;
-  const int n_tiles = a.tiles_m * a.tiles_n;
-  const int tile = xcd_remap(blockIdx.x, n_tiles);
-  const int tm = tile / a.tiles_n, tn = tile % a.tiles_n;
+  int tm, tn;
+  tile_coords(blockIdx.x, a, tm, tn);
   const int bidx = blockIdx.y, split = blockIdx.z;
   const int m0 = tm * BM, n0 = tn * BN;
   const int k_begin = split * a.k_per_split;
@@ -903,6 +916,26 @@ constexpr TileCfg kConfigs[] = {
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
+// Tile rows per group of the tile order (tile_coords). An XCD (32 CUs) holds
+// about R = 32 x (workgroups per CU) tiles at once; walking g tile rows
+// column-major, they cover g x BM rows of A and R / g x BN columns of B, whose
+// panels sum to the least L2 footprint at g = sqrt(R x BN / BM). Workgroups
+// per CU are estimated from the LDS a workgroup holds (at most 4). Measured
+// on the GPT-2 block's shapes against row-major order (interleaved, warm
+// GPU): 2048x3072x768 on the 32x64 tile 5% faster, the others within 1%.
+int tile_group(const TileCfg &t, int tiles_m) {
+  const int lds = t.kind == 3 ? 4 * t.stages * (t.bm * t.bk + (t.prec == KH_PREC_FP32 ? t.bk * t.bn
+                                                                 : t.bn * t.bk / 2 * (t.prec == KH_PREC_BF16X3 ? 2 : 1)))
+                              : 8 * (t.bm * (t.bk + 4) + t.bn * (t.bk + 2));
+  const int per_cu = std::max(1, std::min(4, 163840 / std::max(1, lds)));
+  const double ideal = std::sqrt(32.0 * per_cu * t.bn / t.bm);
+  int g = 1;
+  while (g * 2 <= tiles_m && g * 2 <= 64 && std::abs(std::log2(g * 2.0) - std::log2(ideal)) <
+                                                 std::abs(std::log2((double)g) - std::log2(ideal)))
+    g *= 2;
+  return g;
+}
+
 hipError_t launch_config(int id, const GemmArgs &a, dim3 grid, hipStream_t stream) {
   switch (id) {
 #define KH_CFG_CASE(cid, bm, bn, bk, wm, wn, wk, mt)                                                          \
@@ -1197,6 +1230,7 @@ std::unique_ptr<Op> make_gemm(const kh_launch &L, std::string &err, bool &unsupp
     err = "matmul: too many tiles";
     return nullptr;
   }
+  a.group_m = tile_group(tr, a.tiles_m);
   op->cfg = cfg_run;
   op->grid = dim3((unsigned)n_tiles, (unsigned)batch, (unsigned)splitk);
   if (splitk > 1) {

@@ -16,7 +16,7 @@ struct GemmArgs {
   const float *B;
   int64_t sb_b, sb_k, sb_n;
   int32_t a_vec, b_vec;
-  int32_t tiles_m, tiles_n, splitk, k_per_split;
+  int32_t tiles_m, tiles_n, splitk, k_per_split, group_m;
   int32_t n_refs, n_insns, n_pre;
   uint32_t e_vec_mask, e_bcast_mask;
   float *eptr[KH_MAX_REFS];           // epilogue operand j = descriptor ref j + 2
