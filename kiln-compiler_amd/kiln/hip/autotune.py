@@ -39,8 +39,8 @@ GEMV_CANDIDATES = [(v, 0) for v in range(6)] + [(0, s) for s in (2, 4)]
 
 # (BM, BN, BK, WM, WN, WK, MFMA) of the compiled configurations, by id; must
 # match the table in csrc/kh_gemm.hip (tests check it against kh_gemm_config).
-# Ids 0-7, 21-25 and 32-33 are the LDS-copy pipeline (21-25 with 64 K values
-# per stage, 32-33 with 128), 8-14 the register-staged kernel, 15-20 and 34-41
+# Ids 0-7, 21-25, 32-33 and 46 are the LDS-copy pipeline (21-25 with 64 K
+# values per stage, 32-33 with 128), 8-14 the register-staged kernel, 15-20 and 34-41
 # the bf16-input pipeline (34-41 with 64 or 128 K values per stage), 26-31 and
 # 42-45 the three-pass bf16 pipeline.
 TILES = {
@@ -90,6 +90,7 @@ TILES = {
     43: (64, 128, 64, 2, 2, 1, 16),
     44: (64, 64, 64, 2, 2, 1, 16),
     45: (32, 64, 64, 2, 2, 1, 16),
+    46: (32, 96, 32, 2, 2, 1, 16),
 }
 # input precision of each configuration: 15-20 and 34-41 bf16 (A rounded in
 # the kernel, B a bf16 copy of a constant), 26-31 and 42-45 three-pass bf16
@@ -103,14 +104,14 @@ PRECISION = {t: ("bf16" if 15 <= t <= 20 or 34 <= t <= 41 else "bf16x3" if 26 <=
 OCCUPANCY = {0: 2, 1: 2, 2: 3, 3: 2, 4: 4, 5: 2, 6: 1, 7: 1, 8: 4, 9: 4, 10: 4, 11: 5, 12: 5, 13: 4, 14: 2,
              15: 2, 16: 2, 17: 1, 18: 3, 19: 4, 20: 1, 21: 2, 22: 1, 23: 2, 24: 1, 25: 2,
              26: 1, 27: 2, 28: 2, 29: 3, 30: 4, 31: 1, 32: 1, 33: 1,
-             34: 1, 35: 2, 36: 2, 37: 2, 38: 3, 39: 1, 40: 2, 41: 1, 42: 1, 43: 1, 44: 2, 45: 2}
+             34: 1, 35: 2, 36: 2, 37: 2, 38: 3, 39: 1, 40: 2, 41: 1, 42: 1, 43: 1, 44: 2, 45: 2, 46: 3}
 EFFICIENCY = {0: 0.62, 1: 0.6, 2: 0.62, 3: 0.58, 4: 0.66, 5: 0.62, 6: 0.67, 7: 0.55,
               8: 0.55, 9: 0.55, 10: 0.5, 11: 0.5, 12: 0.45, 13: 0.5, 14: 0.55,
               15: 0.15, 16: 0.15, 17: 0.15, 18: 0.15, 19: 0.15, 20: 0.15,
               21: 0.62, 22: 0.6, 23: 0.62, 24: 0.67, 25: 0.62,
               26: 0.3, 27: 0.3, 28: 0.3, 29: 0.3, 30: 0.3, 31: 0.3, 32: 0.62, 33: 0.62,
               34: 0.2, 35: 0.2, 36: 0.2, 37: 0.2, 38: 0.2, 39: 0.2, 40: 0.2, 41: 0.2,
-              42: 0.35, 43: 0.35, 44: 0.35, 45: 0.35}
+              42: 0.35, 43: 0.35, 44: 0.35, 45: 0.35, 46: 0.62}
 # MFMA rate of a CU relative to fp32, per precision
 RATE = {"fp32": 1.0, "bf16": 16.0, "bf16x3": 16.0 / 3}
 CU_MFLOP_PER_US = 0.614          # fp32 MFMA: 256 flop/clk/CU at 2.4 GHz
