@@ -183,6 +183,111 @@ __global__ __launch_bounds__(THREADS) void gemv_kernel(const GemmArgs a) {
   run_epilogue(a, b, 0, n, valid, out);
 }
 
+// K-contiguous GEMV: W is [batch][N][K] (each output column's weights are one
+// contiguous row, the nn.Linear layout, kept as a copy of the frozen constant
+// for M = 1 plans). A workgroup owns 4 adjacent output columns and its NW
+// waves split K: lane l of wave w reads float4 q = w*64 + l + i*64*NW (i < R)
+// of x and of the 4 weight rows, so one wave load is 1 KiB of one row. Every
+// load of a pass - 4R weight vectors and R of x (and gamma / beta) - is
+// issued before the first FMA, and with the LayerNorm prologue before the row
+// statistics are computed, so a launch costs about one memory latency plus
+// the streaming time of its bytes. Partial dot products are summed in a
+// fixed order: lanes by the DPP tree, then the waves in index order.
+constexpr int kNkCols = 4;
+constexpr int kNkMaxWaves = 8;
+
+// Sum over the workgroup's nw waves in wave order; every thread gets it.
+__device__ __forceinline__ float nk_block_sum(float v, float *red, int wave, int nw) {
+  v = wave_sum(v);
+  __syncthreads();  // `red` may still be read from a previous reduction
+  if ((threadIdx.x & 63) == 0) red[wave] = v;
+  __syncthreads();
+  float s = red[0];
+  for (int w = 1; w < nw; ++w) s += red[w];
+  return s;
+}
+
+template <int R, bool PRO>
+__global__ __launch_bounds__(64 * kNkMaxWaves) void gemv_nk_kernel(const GemmArgs a) {
+  __shared__ float red[kNkMaxWaves];
+  __shared__ float part[kNkMaxWaves][kNkCols];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int n0 = blockIdx.x * kNkCols, b = blockIdx.y;
+  const int K4 = a.K >> 2, step = 64 * nw;
+  const float4 *x4 = reinterpret_cast<const float4 *>(a.A + (int64_t)b * a.sa_b);
+  const float4 *w4[kNkCols];
+#pragma unroll
+  for (int c = 0; c < kNkCols; ++c)
+    w4[c] = reinterpret_cast<const float4 *>(a.B + (int64_t)b * a.sb_b + (int64_t)min(n0 + c, a.N - 1) * a.sb_n);
+  float p[kNkCols] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int base = wave * 64 + lane; base - lane < K4; base += R * step) {
+    float4 wv[kNkCols][R], xv[R], gv[R], bv[R];
+    bool in[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      const int q = base + i * step;
+      in[i] = q < K4;
+      const int qc = in[i] ? q : K4 - 1;  // clamped: an in-bounds load, product dropped
+#pragma unroll
+      for (int c = 0; c < kNkCols; ++c) wv[c][i] = w4[c][qc];
+      xv[i] = x4[qc];
+      if constexpr (PRO) {
+        gv[i] = a.pro_g >= 0 ? reinterpret_cast<const float4 *>(a.eptr[a.pro_g] + (int64_t)b * a.estride[a.pro_g][0])[qc]
+                             : make_float4(1.f, 1.f, 1.f, 1.f);
+        bv[i] = a.pro_b >= 0 ? reinterpret_cast<const float4 *>(a.eptr[a.pro_b] + (int64_t)b * a.estride[a.pro_b][0])[qc]
+                             : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+    if constexpr (PRO) {
+      // the whole row is in this pass (the host guarantees K4 <= R * 64 * NW):
+      // mean, then the variance of the centred values
+      float s = 0.0f;
+#pragma unroll
+      for (int i = 0; i < R; ++i)
+        if (in[i]) s += (xv[i].x + xv[i].y) + (xv[i].z + xv[i].w);
+      const float mean = nk_block_sum(s, red, wave, nw) * a.pro_c1;
+      float s2 = 0.0f;
+#pragma unroll
+      for (int i = 0; i < R; ++i) {
+        xv[i] = make_float4(xv[i].x - mean, xv[i].y - mean, xv[i].z - mean, xv[i].w - mean);
+        if (in[i]) s2 += (xv[i].x * xv[i].x + xv[i].y * xv[i].y) + (xv[i].z * xv[i].z + xv[i].w * xv[i].w);
+      }
+      const float rstd = rsqrtf(nk_block_sum(s2, red, wave, nw) * a.pro_c2 + a.pro_eps);
+#pragma unroll
+      for (int i = 0; i < R; ++i) {
+        xv[i].x = xv[i].x * rstd * gv[i].x + bv[i].x, xv[i].y = xv[i].y * rstd * gv[i].y + bv[i].y;
+        xv[i].z = xv[i].z * rstd * gv[i].z + bv[i].z, xv[i].w = xv[i].w * rstd * gv[i].w + bv[i].w;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      if (!in[i]) continue;
+#pragma unroll
+      for (int c = 0; c < kNkCols; ++c) {
+        float t = p[c];
+        t = fmaf(xv[i].x, wv[c][i].x, t), t = fmaf(xv[i].y, wv[c][i].y, t);
+        t = fmaf(xv[i].z, wv[c][i].z, t), t = fmaf(xv[i].w, wv[c][i].w, t);
+        p[c] = t;
+      }
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < kNkCols; ++c) p[c] = wave_sum(p[c]);
+  if (lane == 0)
+#pragma unroll
+    for (int c = 0; c < kNkCols; ++c) part[wave][c] = p[c];
+  __syncthreads();
+  if (threadIdx.x != 0 || n0 >= a.N) return;
+  Vec<4> out;
+#pragma unroll
+  for (int c = 0; c < kNkCols; ++c) {
+    float v = part[0][c];
+    for (int w = 1; w < nw; ++w) v += part[w][c];
+    out.v[c] = v;
+  }
+  run_epilogue(a, b, 0, n0, min(kNkCols, a.N - n0), out);
+}
+
 // (column quads, threads) per workgroup by variant id (1..5); 0 = chosen
 // from the shape.
 constexpr int kVariants[][2] = {{0, 0}, {8, 256}, {4, 256}, {2, 256}, {8, 1024}, {4, 1024}};
@@ -196,6 +301,10 @@ class GemvOp final : public Op {
   int quads = 8, threads = 256;
   bool b_vec_layout = false;
   uint32_t e_vec_candidates = 0;
+  // K-contiguous kernel: chosen at plan creation (nk_r > 0), taken at launch
+  // when the operands it reads as float4 are 16-byte aligned
+  int nk_r = 0, nk_waves = 1;
+  dim3 nk_grid;
 
   hipError_t launch(float *const *ptrs, uint32_t *counters, float *partials, hipStream_t stream) override {
     GemmArgs a = args;
@@ -210,6 +319,12 @@ class GemvOp final : public Op {
     }
     a.ws_partial = partials;
     if (a.N == 0 || a.batch == 0) return hipSuccess;
+    if (nk_r > 0 && aligned16(ptrs[0]) && aligned16(ptrs[1]) && (a.pro_g < 0 || aligned16(a.eptr[a.pro_g])) &&
+        (a.pro_b < 0 || aligned16(a.eptr[a.pro_b]))) {
+      a.splitk = 1;
+      launch_nk(a, stream);
+      return hipGetLastError();
+    }
     if (a.splitk > 1 && !partials) return hipErrorInvalidValue;
     if (a.pro) launch_variant(a, grid, stream, std::true_type{});
     else launch_variant(a, grid, stream, std::false_type{});
@@ -218,6 +333,24 @@ class GemvOp final : public Op {
     return launch_splitk_reduce(a, current_device().cus, stream);
   }
   size_t partial_floats() const override { return n_partials; }
+
+  static bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+  void launch_nk(const GemmArgs &a, hipStream_t stream) const {
+    const dim3 block(64 * nk_waves);
+#define KH_NK_CASE(R)                                                                                   \
+  case R:                                                                                               \
+    if (a.pro) hipLaunchKernelGGL((gemv_nk_kernel<R, true>), nk_grid, block, 0, stream, a);            \
+    else hipLaunchKernelGGL((gemv_nk_kernel<R, false>), nk_grid, block, 0, stream, a);                 \
+    break;
+    switch (nk_r) {
+      KH_NK_CASE(1)
+      KH_NK_CASE(2)
+      KH_NK_CASE(3)
+      KH_NK_CASE(4)
+    }
+#undef KH_NK_CASE
+  }
 
   template <class P>
   void launch_variant(const GemmArgs &a, dim3 g, hipStream_t stream, P) const {
@@ -319,6 +452,33 @@ std::unique_ptr<Op> make_gemv(const kh_launch &L, std::string &err, bool &unsupp
     unsupported = true;
     err = "gemv: too many column blocks";
     return nullptr;
+  }
+  // K-contiguous layout ([batch][N][K] weights, unit-stride x, K a multiple
+  // of 4, gamma / beta unit-stride): float4 loads per lane; R float4 per lane
+  // and wave, NW = ceil(K/4 / 64R) waves, the (R, NW) with the fewest idle
+  // lanes. A LayerNorm prologue needs the whole row in one pass.
+  const bool nk_layout = a.sb_k == 1 && a.sb_n >= K && a.sb_n % 4 == 0 && a.sb_b % 4 == 0 &&
+                         L.refs[1].offset % 4 == 0 && a.sa_k == 1 && a.sa_b % 4 == 0 && L.refs[0].offset % 4 == 0 &&
+                         K % 4 == 0 && K > 0 && (N + kNkCols - 1) / kNkCols < (1ll << 31);
+  bool nk_pro_ok = true;
+  if (a.pro)
+    for (int r : {L.cfg[5], L.cfg[6]})
+      if (r >= 0 && (L.refs[r].offset % 4 != 0 || L.refs[r].strides[0] % 4 != 0)) nk_pro_ok = false;
+  if (nk_layout && nk_pro_ok) {
+    const int64_t k4 = K / 4;
+    int best_r = 0, best_w = 0;
+    int64_t best_waste = -1;
+    for (int r : {3, 4, 2, 1}) {
+      const int64_t w = (k4 + 64 * r - 1) / (64 * r);
+      if (w > kNkMaxWaves) continue;
+      const int64_t waste = 64 * r * w - k4;
+      if (best_waste < 0 || waste < best_waste) best_r = r, best_w = (int)w, best_waste = waste;
+    }
+    if (best_r == 0 && !a.pro) best_r = 4, best_w = kNkMaxWaves;  // several passes over K
+    if (best_r > 0) {
+      op->nk_r = best_r, op->nk_waves = best_w;
+      op->nk_grid = dim3((unsigned)((N + kNkCols - 1) / kNkCols), (unsigned)b1, 1);
+    }
   }
   op->quads = quads;
   op->threads = threads;

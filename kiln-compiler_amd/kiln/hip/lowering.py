@@ -646,6 +646,8 @@ class _Lowerer:
         d.refs[1] = ref3(b, (batch, kk, n))
         if prec in ("bf16", "bf16x3"):
             d.refs[1] = self.bf16_weight(b, d.refs[1], batch, kk, n, split=prec == "bf16x3")
+        elif gemv and self.layouts[b].base[0] == "const" and kk % 4 == 0:
+            d.refs[1] = self.nk_weight(b, d.refs[1], batch, kk, n)
         externals = []
         for nd in k.nodes:
             if nd is mm:
@@ -810,6 +812,22 @@ class _Lowerer:
             self.prologue[km] = (x, gamma, beta, list(fparams))
             skip.add(k)
         return skip
+
+    def nk_weight(self, b, ref, batch, kk, n):
+        """Ref of an fp32 [batch][N][K] copy of constant view `b` (fp32 ref
+        `ref` over (b, k, n)) for the GEMV family: each output column's
+        weights become one contiguous row, which the K-contiguous GEMV kernel
+        reads 1 KiB per wave load. Registered as a derived constant, made when
+        the executable is built."""
+        src = self.layouts[b].base[1]
+        strides = (int(ref.strides[0]), int(ref.strides[1]), int(ref.strides[2]))
+        name = f"{src}@nk:{int(ref.offset)}:{strides[0]},{strides[1]},{strides[2]}:{batch}x{kk}x{n}"
+        self.program.derived[name] = (src, int(ref.offset), strides, batch, kk, n)
+        r = kl.Ref()
+        r.base, r.index = self.slot_of(("const", name))
+        r.offset = 0
+        r.strides[0], r.strides[1], r.strides[2] = (n * kk if batch > 1 else 0), 1, kk
+        return r
 
     def bf16_weight(self, b, ref, batch, kk, n, split=False):
         """Ref of the bf16 [batch][N][K'] copy of constant view `b` (whose fp32

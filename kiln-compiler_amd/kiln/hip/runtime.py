@@ -117,6 +117,17 @@ def kernel_seconds(fn, repeats=20, rounds=5):
     return best
 
 
+def nk_copy(data: np.ndarray, offset: int, strides, batch: int, k: int, n: int) -> np.ndarray:
+    """The fp32 [batch][N][K] copy (values unchanged, K contiguous) of the
+    [batch, K, N] view (element offset, strides over (b, k, n)) of a constant:
+    the layout of the K-contiguous GEMV kernel."""
+    flat = np.ascontiguousarray(data, dtype=np.float32).reshape(-1)
+    sb, sk, sn = (int(s) for s in strides)
+    idx = (offset + np.arange(batch)[:, None, None] * sb + np.arange(n)[None, :, None] * sn
+           + np.arange(k)[None, None, :] * sk)
+    return np.ascontiguousarray(flat[idx])
+
+
 class HIPExecutable:
     """Runs one compiled graph on an MI355X. Not reentrant."""
 
@@ -154,9 +165,12 @@ class HIPExecutable:
     @staticmethod
     def _host_constant(program, constants, name):
         """Host array of const slot `name`: the fp32 constant, or a copy the
-        lowering derived from one (bf16 GEMM weights, as int16 bit patterns)."""
+        lowering derived from one (bf16 GEMM weights, as int16 bit patterns;
+        fp32 [batch][N][K] GEMV weights)."""
         if name in program.derived:
             src, offset, strides, batch, k, n = program.derived[name]
+            if "@nk:" in name:
+                return nk_copy(constants[src], offset, strides, batch, k, n)
             copy = bf16.weight_copy_x3 if "@bf16x3:" in name else bf16.weight_copy
             return copy(constants[src], offset, strides, batch, k, n).view(np.int16)
         return np.ascontiguousarray(constants[name], np.float32)

@@ -27,12 +27,30 @@ SHAPES = sorted({
 })
 
 
+def warm_up(seconds=1.0):
+    """Run large products until the GPU's clocks are up, so the first shape
+    is not timed on a cold GPU."""
+    import time
+
+    import torch
+
+    from kiln.hip.runtime import device
+
+    x = torch.randn(8192, 8192, device=device())
+    end = time.perf_counter() + seconds
+    while time.perf_counter() < end:
+        for _ in range(10):
+            x @ x
+        torch.cuda.synchronize()
+
+
 def main(argv=None):
     p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     p.add_argument("--out", default=str(autotune.SHIPPED_PATH))
     p.add_argument("--precision", nargs="+", choices=("fp32", "bf16", "bf16x3"), default=None,
                    help="re-tune only these precisions and keep the table's other entries")
     args = p.parse_args(argv)
+    warm_up()
     table = {}
     if args.precision:
         keep = autotune.shipped_configs()

@@ -256,6 +256,38 @@ def test_gemv_variants_and_ragged_sizes(variant):
                 assert torch.equal(c(x, wt, b), first)
 
 
+class _BatchedConstant(torch.nn.Module):
+    def __init__(self, batch, k, n):
+        super().__init__()
+        self.w = torch.nn.Parameter(torch.randn(batch, k, n) * 0.1)
+
+    def forward(self, x):
+        return torch.matmul(x, self.w) * 0.5
+
+
+@pytest.mark.parametrize("k, n, batch", [(768, 2304, 1), (3072, 768, 1), (9000, 70, 1), (64, 130, 3), (12, 5, 1)])
+def test_k_contiguous_gemv(k, n, batch):
+    # M = 1 with a constant weight: the weight is read as a [batch][N][K] copy
+    # by the K-contiguous kernel (one pass of R float4 per lane; several
+    # passes beyond K = 8192; N not a multiple of 4; batched constants);
+    # eager and graph-replayed launches agree bit for bit
+    torch.manual_seed(k + n)
+    if batch == 1:
+        model = torch.nn.Sequential(torch.nn.Linear(k, n), torch.nn.GELU(approximate="tanh")).eval()
+        x = torch.randn(1, k)
+    else:
+        model = _BatchedConstant(batch, k, n).eval()
+        x = torch.randn(batch, 1, k)
+    c = check(model, x)
+    assert c.report.lowering["families"] == {"gemv": 1}
+    assert any("@nk:" in name for name in c._exe.program.derived)
+    first = c(x)
+    for graphs in (False, True):
+        c2 = kiln.compile(model, (x,), device="cuda", cuda_graphs=graphs)
+        for _ in range(3):
+            assert torch.equal(c2(x), first)
+
+
 def test_batched_gemv_with_strided_weights():
     # batch 3, M = 1, B read through a transposed view (no 128-bit column quads)
     check(lambda a, b: torch.bmm(a, b.transpose(1, 2)) * 0.5, torch.randn(3, 1, 300), torch.randn(3, 70, 300))

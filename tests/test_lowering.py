@@ -146,6 +146,26 @@ def test_decode_uses_the_gemv_family():
     assert [l.family for l in prog.launches] == [kl.FAM_GEMV]
 
 
+def test_gemv_weights_are_k_contiguous_copies():
+    # a constant GEMV weight is read as a derived [N][K] copy (the nn.Linear
+    # layout) holding exactly the frozen W^T's values; K not a multiple of 4
+    # keeps the [K][N] constant
+    from kiln.hip.runtime import HIPExecutable, nk_copy
+
+    lin = torch.nn.Linear(768, 300)
+    g, prog = lowered(lin, torch.randn(1, 768))
+    (name,) = [n for n in prog.derived if "@nk:" in n]
+    d = prog.launches[0].desc
+    assert (d.refs[1].strides[1], d.refs[1].strides[2]) == (1, 768)
+    src, offset, strides, batch, k, n = prog.derived[name]
+    copy = nk_copy(g.constants[src], offset, strides, batch, k, n)
+    assert copy.shape == (1, 300, 768) and copy.flags.c_contiguous
+    np.testing.assert_array_equal(copy[0], lin.weight.detach().numpy())
+    assert HIPExecutable._host_constant(prog, g.constants, name).shape == (1, 300, 768)
+    _, prog = lowered(torch.nn.Linear(37, 30), torch.randn(1, 37))
+    assert not prog.derived
+
+
 def test_long_rows_are_chunked_and_short_rows_fast():
     _, prog = lowered(torch.nn.LayerNorm(10000), torch.randn(2, 10000))
     assert "(chunked)" in prog.launches[0].summary
