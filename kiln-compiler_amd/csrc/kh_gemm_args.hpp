@@ -125,5 +125,8 @@ inline hipError_t launch_splitk_reduce(const GemmArgs &a, int cus, hipStream_t s
 
 // Host: validate the epilogue refs/tape of a matmul descriptor into `a`.
 bool fill_epilogue(const kh_launch &L, GemmArgs &a, uint32_t &vec_candidates, std::string &err);
+// Recognise the tape out = act((acc [+ bias]) [+ res]) and fill the direct
+// epilogue fields (a.direct = 1); false (fields untouched) for any other tape.
+bool match_direct_epilogue(const kh_launch &L, GemmArgs &a);
 
 }  // namespace kh

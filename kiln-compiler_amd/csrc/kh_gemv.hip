@@ -219,6 +219,18 @@ __global__ __launch_bounds__(64 * kNkMaxWaves) void gemv_nk_kernel(const GemmArg
 #pragma unroll
   for (int c = 0; c < kNkCols; ++c)
     w4[c] = reinterpret_cast<const float4 *>(a.B + (int64_t)b * a.sb_b + (int64_t)min(n0 + c, a.N - 1) * a.sb_n);
+  // direct epilogue (bias / residual / activation recognised on the host):
+  // the thread that finishes the 4 columns loads their operands up front, so
+  // they arrive with the weights rather than after the reduction
+  float pre_b[kNkCols] = {0.0f, 0.0f, 0.0f, 0.0f}, pre_r[kNkCols] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (a.direct && threadIdx.x == 0) {
+#pragma unroll
+    for (int c = 0; c < kNkCols; ++c) {
+      const int64_t n = min(n0 + c, a.N - 1);
+      if (a.d_bias >= 0) pre_b[c] = a.eptr[a.d_bias][b * a.estride[a.d_bias][0] + n * a.estride[a.d_bias][2]];
+      if (a.d_res >= 0) pre_r[c] = a.eptr[a.d_res][b * a.estride[a.d_res][0] + n * a.estride[a.d_res][2]];
+    }
+  }
   float p[kNkCols] = {0.0f, 0.0f, 0.0f, 0.0f};
   for (int base = wave * 64 + lane; base - lane < K4; base += R * step) {
     float4 wv[kNkCols][R], xv[R], gv[R], bv[R];
@@ -285,7 +297,24 @@ __global__ __launch_bounds__(64 * kNkMaxWaves) void gemv_nk_kernel(const GemmArg
     for (int w = 1; w < nw; ++w) v += part[w][c];
     out.v[c] = v;
   }
-  run_epilogue(a, b, 0, n0, min(kNkCols, a.N - n0), out);
+  const int valid = min(kNkCols, a.N - n0);
+  if (a.direct) {
+    // the tape's operations in its order: (acc + bias), then res + that, then act
+    float *o = a.eptr[a.d_out] + b * a.estride[a.d_out][0];
+#pragma unroll
+    for (int c = 0; c < kNkCols; ++c) {
+      if (c >= valid) break;
+      float v = out.v[c];
+      if (a.d_bias >= 0) v += pre_b[c];
+      if (a.d_res >= 0) v = pre_r[c] + v;
+      if (a.d_act == KH_OP_GELU_TANH) v = op_gelu_tanh(v);
+      else if (a.d_act == KH_OP_GELU_ERF) v = op_gelu_erf(v);
+      else if (a.d_act == KH_OP_RELU) v = v != v ? v : fmaxf(v, 0.0f);
+      o[(int64_t)(n0 + c) * a.estride[a.d_out][2]] = v;
+    }
+    return;
+  }
+  run_epilogue(a, b, 0, n0, valid, out);
 }
 
 // (column quads, threads) per workgroup by variant id (1..5); 0 = chosen
@@ -391,6 +420,8 @@ std::unique_ptr<Op> make_gemv(const kh_launch &L, std::string &err, bool &unsupp
   a.sb_b = L.refs[1].strides[0], a.sb_k = L.refs[1].strides[1], a.sb_n = L.refs[1].strides[2];
   op->b_vec_layout = a.sb_n == 1 && L.refs[1].offset % 4 == 0 && a.sb_k % 4 == 0 && a.sb_b % 4 == 0;
   if (!fill_epilogue(L, a, op->e_vec_candidates, err)) return nullptr;
+  a.direct = 0, a.d_bias = a.d_res = a.d_out = a.d_act = -1;
+  match_direct_epilogue(L, a);
   // LayerNorm prologue: cfg[4] = 1, cfg[5] / cfg[6] = ref index of gamma /
   // beta (-1: none), fparams = {1/C, 1/C, eps}; gamma and beta are [K] rows
   a.pro = L.cfg[4], a.pro_g = -1, a.pro_b = -1;
