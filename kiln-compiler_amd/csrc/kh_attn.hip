@@ -39,7 +39,9 @@
 //     the diagonal block is compared. Other additive masks are read from
 //     memory;
 //   * workgroups are issued longest-first (causal rows near the end of the
-//     sequence have the most key blocks).
+//     sequence have the most key blocks);
+//   * decode shapes (at most 4 queries over at most 64 keys) run a separate
+//     kernel with one wave per query row (attn_rows_kernel).
 #include <algorithm>
 #include <cmath>
 #include <cstring>
@@ -285,10 +287,65 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
   }
 }
 
+// Few-query attention (decode shapes: Tq <= kRowsMaxQ queries over at most
+// kRowsMaxK keys): one wave per (head, query), lane d holding head dimension
+// d (lanes DH.. idle for DH = 32). Each chunk of kRowKeys keys has its K and
+// V rows (and mask values) loaded before the first dot product; a score is
+// one wave sum. The online softmax is the one of attn_kernel: base-2 domain,
+// u = (s * scale + mask) * log2(e), and a row with no finite score so far
+// takes its exponentials against 0, so a fully masked row ends as 0 / 0 =
+// NaN (as in eager) and a NaN or +inf score turns the row NaN.
+constexpr int kRowsMaxQ = 4;
+constexpr int kRowsMaxK = 64;
+constexpr int kRowKeys = 8;
+
+template <int DH, bool ADD>
+__global__ __launch_bounds__(256) void attn_rows_kernel(const AttnArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= a.batch * a.tq) return;  // whole waves; the kernel has no barrier
+  const int b = row / a.tq, qi = row % a.tq;
+  const bool on = lane < DH;
+  const int d = on ? lane : 0;
+  constexpr float kLog2e = 1.4426950408889634f;
+  const float c_scale = a.scale_mode == KH_ATTN_SCALE_MUL   ? a.scale * kLog2e
+                        : a.scale_mode == KH_ATTN_SCALE_DIV ? kLog2e / a.scale
+                                                            : kLog2e;
+  const float qv = on ? a.q[b * a.q_b + (int64_t)qi * a.q_t + d] * c_scale : 0.0f;
+  const int lim = a.mask_mode == KH_ATTN_MASK_CAUSAL ? min(a.tk, qi + 1) : a.tk;
+  const float *kp = a.k + b * a.k_b + d, *vp = a.v + b * a.v_b + d;
+  float m = -INFINITY, l = 0.0f, acc = 0.0f;
+  for (int j0 = 0; j0 < lim; j0 += kRowKeys) {
+    float kv[kRowKeys], vv[kRowKeys], mv[kRowKeys];
+#pragma unroll
+    for (int c = 0; c < kRowKeys; ++c) {
+      const int j = min(j0 + c, lim - 1);  // clamped: an in-bounds load, the key is dropped below
+      kv[c] = kp[(int64_t)j * a.k_t];
+      vv[c] = vp[(int64_t)j * a.v_t];
+      if (ADD) mv[c] = a.mask[b * a.m_b + (int64_t)qi * a.m_q + (int64_t)j * a.m_k];
+    }
+#pragma unroll
+    for (int c = 0; c < kRowKeys; ++c) {
+      if (j0 + c >= lim) break;
+      float u = wave_sum(qv * kv[c]);
+      if (ADD) u = fmaf(mv[c], kLog2e, u);
+      const float m_new = fmaxf(m, u);
+      const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+      const float alpha = __builtin_amdgcn_exp2f(m - m_use);
+      const float p = __builtin_amdgcn_exp2f(u - m_use);
+      l = fmaf(l, alpha, p);
+      acc = fmaf(acc, alpha, p * vv[c]);
+      m = m_new;
+    }
+  }
+  if (on) a.o[b * a.o_b + (int64_t)qi * a.o_t + d] = acc / l;
+}
+
 class AttnOp final : public Op {
  public:
   AttnArgs args{};
   int dh = 64, nw = 4;
+  bool rows = false;  // few-query kernel
   dim3 grid;
 
   hipError_t launch(float *const *ptrs, uint32_t *, float *, hipStream_t stream) override {
@@ -298,6 +355,15 @@ class AttnOp final : public Op {
     for (int j = 0; j < 4; ++j)
       if (reinterpret_cast<uintptr_t>(ptrs[j]) & 15) return hipErrorInvalidValue;
     if (a.batch == 0 || a.tq == 0) return hipSuccess;
+    if (rows) {
+      const dim3 g((unsigned)((a.batch * a.tq + 3) / 4));
+      const bool add = a.mask_mode == KH_ATTN_MASK_ADD;
+      if (dh == 64 && add) hipLaunchKernelGGL((attn_rows_kernel<64, true>), g, dim3(256), 0, stream, a);
+      else if (dh == 64) hipLaunchKernelGGL((attn_rows_kernel<64, false>), g, dim3(256), 0, stream, a);
+      else if (add) hipLaunchKernelGGL((attn_rows_kernel<32, true>), g, dim3(256), 0, stream, a);
+      else hipLaunchKernelGGL((attn_rows_kernel<32, false>), g, dim3(256), 0, stream, a);
+      return hipGetLastError();
+    }
 #define KH_ATTN_LAUNCH(D, W)                                                                         \
   if (dh == D && nw == W) {                                                                          \
     if (a.mask_mode == KH_ATTN_MASK_ADD)                                                             \
@@ -403,6 +469,8 @@ std::unique_ptr<Op> make_attn(const kh_launch &L, std::string &err, bool &unsupp
     return nullptr;
   }
   op->nw = nw;
+  // decode shapes (a few queries, a few keys): one wave per query row
+  op->rows = tq <= kRowsMaxQ && tk <= kRowsMaxK && L.cfg[2] <= 0 && batch * tq < (1ll << 31);
   const int64_t n_groups = batch * (int64_t)a.n_qblocks;
   if (n_groups >= (1ll << 31)) {
     unsupported = true;

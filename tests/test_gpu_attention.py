@@ -81,6 +81,25 @@ def test_no_mask_cross_attention(tq, tk):
     compare(Attn(None, scale=0.125), *qkv(2, tq, tk, 64, seed=tq + tk))
 
 
+@pytest.mark.parametrize("tq, tk", [(1, 1), (1, 40), (3, 9), (4, 64), (2, 65)])
+@pytest.mark.parametrize("d", [32, 64])
+@pytest.mark.parametrize("masked", [False, True])
+def test_few_query_rows(tq, tk, d, masked):
+    # decode shapes (up to 4 queries over up to 64 keys) run one wave per query
+    # row; (2, 65) is just past that and runs the MFMA kernel. The additive
+    # mask has -inf entries and, with several queries, one fully masked row
+    # (NaN, as in eager)
+    mask = None
+    if masked:
+        g = torch.Generator().manual_seed(tq * 100 + tk)
+        mask = torch.randn(tq, tk, generator=g)
+        mask[torch.rand(tq, tk, generator=g) < 0.3] = float("-inf")
+        mask[:, 0] = 0.0
+        if tq > 1:
+            mask[1, :] = float("-inf")
+    compare(Attn(mask, scale=8.0, divide=True, merge=False), *qkv(3, tq, tk, d, seed=tq + tk + d))
+
+
 def test_divided_scale_and_no_head_merge():
     c = compare(Attn(None, scale=8.0, divide=True, merge=False), *qkv(4, 70, 70, 64, seed=3))
     assert "scores / 8" in c._exe.program.source
