@@ -207,18 +207,50 @@ __device__ __forceinline__ float nk_block_sum(float v, float *red, int wave, int
   return s;
 }
 
-template <int R, bool PRO>
+// One K value of a weight chunk (4 fp32 or 8 bf16 values in a uint4).
+template <bool BF16>
+__device__ __forceinline__ float nk_weight(const uint4 &w, int e) {
+  const uint32_t word = e / (BF16 ? 2 : 1) == 0 ? w.x : e / (BF16 ? 2 : 1) == 1 ? w.y
+                        : e / (BF16 ? 2 : 1) == 2 ? w.z : w.w;
+  if constexpr (BF16) return __uint_as_float(e & 1 ? word & 0xffff0000u : word << 16);
+  else return __uint_as_float(word);
+}
+
+// BF16: the weights are the bf16 [batch][N][K] copy, a unit is 8 K values
+// (one 16-byte chunk), x is rounded to bf16 (round to nearest even) at the
+// product - the arithmetic of the bf16 GEMM (exact products, fp32 sums).
+template <int R, bool PRO, bool BF16>
 __global__ __launch_bounds__(64 * kNkMaxWaves) void gemv_nk_kernel(const GemmArgs a) {
+  constexpr int KV = BF16 ? 8 : 4;  // K values per lane and unit
   __shared__ float red[kNkMaxWaves];
   __shared__ float part[kNkMaxWaves][kNkCols];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
   const int n0 = blockIdx.x * kNkCols, b = blockIdx.y;
-  const int K4 = a.K >> 2, step = 64 * nw;
-  const float4 *x4 = reinterpret_cast<const float4 *>(a.A + (int64_t)b * a.sa_b);
-  const float4 *w4[kNkCols];
+  const int U = a.K / KV, step = 64 * nw;  // the host checks K % KV == 0
+  const float *xrow = a.A + (int64_t)b * a.sa_b;
+  const float *grow = PRO && a.pro_g >= 0 ? a.eptr[a.pro_g] + (int64_t)b * a.estride[a.pro_g][0] : nullptr;
+  const float *brow = PRO && a.pro_b >= 0 ? a.eptr[a.pro_b] + (int64_t)b * a.estride[a.pro_b][0] : nullptr;
+  const uint4 *w16[kNkCols];
 #pragma unroll
-  for (int c = 0; c < kNkCols; ++c)
-    w4[c] = reinterpret_cast<const float4 *>(a.B + (int64_t)b * a.sb_b + (int64_t)min(n0 + c, a.N - 1) * a.sb_n);
+  for (int c = 0; c < kNkCols; ++c) {
+    const int64_t off = (int64_t)b * a.sb_b + (int64_t)min(n0 + c, a.N - 1) * a.sb_n;
+    w16[c] = BF16 ? reinterpret_cast<const uint4 *>(reinterpret_cast<const __bf16 *>(a.B) + off)
+                  : reinterpret_cast<const uint4 *>(a.B + off);
+  }
+  // KV consecutive floats of a row at unit u: 128-bit loads when the rows
+  // are 16-byte aligned (a_vec, set at launch), else scalar loads
+  auto load_row = [&](const float *row, int u, float (&dst)[KV]) {
+    if (a.a_vec) {
+#pragma unroll
+      for (int h = 0; h < KV / 4; ++h) {
+        const float4 t = reinterpret_cast<const float4 *>(row)[u * (KV / 4) + h];
+        dst[4 * h] = t.x, dst[4 * h + 1] = t.y, dst[4 * h + 2] = t.z, dst[4 * h + 3] = t.w;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < KV; ++e) dst[e] = row[u * KV + e];
+    }
+  };
   // direct epilogue (bias / residual / activation recognised on the host):
   // the thread that finishes the 4 columns loads their operands up front, so
   // they arrive with the weights rather than after the reduction
@@ -232,44 +264,51 @@ __global__ __launch_bounds__(64 * kNkMaxWaves) void gemv_nk_kernel(const GemmArg
     }
   }
   float p[kNkCols] = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int base = wave * 64 + lane; base - lane < K4; base += R * step) {
-    float4 wv[kNkCols][R], xv[R], gv[R], bv[R];
+  for (int base = wave * 64 + lane; base - lane < U; base += R * step) {
+    uint4 wv[kNkCols][R];
+    float xv[R][KV], gv[R][KV], bv[R][KV];
     bool in[R];
 #pragma unroll
     for (int i = 0; i < R; ++i) {
-      const int q = base + i * step;
-      in[i] = q < K4;
-      const int qc = in[i] ? q : K4 - 1;  // clamped: an in-bounds load, product dropped
+      const int u = base + i * step;
+      in[i] = u < U;
+      const int uc = in[i] ? u : U - 1;  // clamped: an in-bounds load, product dropped
 #pragma unroll
-      for (int c = 0; c < kNkCols; ++c) wv[c][i] = w4[c][qc];
-      xv[i] = x4[qc];
+      for (int c = 0; c < kNkCols; ++c) wv[c][i] = w16[c][uc];
+      load_row(xrow, uc, xv[i]);
       if constexpr (PRO) {
-        gv[i] = a.pro_g >= 0 ? reinterpret_cast<const float4 *>(a.eptr[a.pro_g] + (int64_t)b * a.estride[a.pro_g][0])[qc]
-                             : make_float4(1.f, 1.f, 1.f, 1.f);
-        bv[i] = a.pro_b >= 0 ? reinterpret_cast<const float4 *>(a.eptr[a.pro_b] + (int64_t)b * a.estride[a.pro_b][0])[qc]
-                             : make_float4(0.f, 0.f, 0.f, 0.f);
+        if (grow) load_row(grow, uc, gv[i]);
+        if (brow) load_row(brow, uc, bv[i]);
       }
     }
     if constexpr (PRO) {
-      // the whole row is in this pass (the host guarantees K4 <= R * 64 * NW):
+      // the whole row is in this pass (the host guarantees U <= R * 64 * NW):
       // mean, then the variance of the centred values
       float s = 0.0f;
 #pragma unroll
       for (int i = 0; i < R; ++i)
-        if (in[i]) s += (xv[i].x + xv[i].y) + (xv[i].z + xv[i].w);
+        if (in[i])
+#pragma unroll
+          for (int e = 0; e < KV; ++e) s += xv[i][e];
       const float mean = nk_block_sum(s, red, wave, nw) * a.pro_c1;
       float s2 = 0.0f;
 #pragma unroll
-      for (int i = 0; i < R; ++i) {
-        xv[i] = make_float4(xv[i].x - mean, xv[i].y - mean, xv[i].z - mean, xv[i].w - mean);
-        if (in[i]) s2 += (xv[i].x * xv[i].x + xv[i].y * xv[i].y) + (xv[i].z * xv[i].z + xv[i].w * xv[i].w);
-      }
+      for (int i = 0; i < R; ++i)
+#pragma unroll
+        for (int e = 0; e < KV; ++e) {
+          xv[i][e] -= mean;
+          if (in[i]) s2 = fmaf(xv[i][e], xv[i][e], s2);
+        }
       const float rstd = rsqrtf(nk_block_sum(s2, red, wave, nw) * a.pro_c2 + a.pro_eps);
 #pragma unroll
-      for (int i = 0; i < R; ++i) {
-        xv[i].x = xv[i].x * rstd * gv[i].x + bv[i].x, xv[i].y = xv[i].y * rstd * gv[i].y + bv[i].y;
-        xv[i].z = xv[i].z * rstd * gv[i].z + bv[i].z, xv[i].w = xv[i].w * rstd * gv[i].w + bv[i].w;
-      }
+      for (int i = 0; i < R; ++i)
+#pragma unroll
+        for (int e = 0; e < KV; ++e) {
+          float y = xv[i][e] * rstd;
+          if (grow) y *= gv[i][e];
+          if (brow) y += bv[i][e];
+          xv[i][e] = y;
+        }
     }
 #pragma unroll
     for (int i = 0; i < R; ++i) {
@@ -277,8 +316,11 @@ __global__ __launch_bounds__(64 * kNkMaxWaves) void gemv_nk_kernel(const GemmArg
 #pragma unroll
       for (int c = 0; c < kNkCols; ++c) {
         float t = p[c];
-        t = fmaf(xv[i].x, wv[c][i].x, t), t = fmaf(xv[i].y, wv[c][i].y, t);
-        t = fmaf(xv[i].z, wv[c][i].z, t), t = fmaf(xv[i].w, wv[c][i].w, t);
+#pragma unroll
+        for (int e = 0; e < KV; ++e) {
+          const float xe = BF16 ? (float)(__bf16)xv[i][e] : xv[i][e];
+          t = fmaf(xe, nk_weight<BF16>(wv[c][i], e), t);
+        }
         p[c] = t;
       }
     }
@@ -333,6 +375,7 @@ class GemvOp final : public Op {
   // K-contiguous kernel: chosen at plan creation (nk_r > 0), taken at launch
   // when the operands it reads as float4 are 16-byte aligned
   int nk_r = 0, nk_waves = 1;
+  bool bf16 = false;  // weights are the bf16 [batch][N][K] copy (K-contiguous kernel only)
   dim3 nk_grid;
 
   hipError_t launch(float *const *ptrs, uint32_t *counters, float *partials, hipStream_t stream) override {
@@ -348,9 +391,11 @@ class GemvOp final : public Op {
     }
     a.ws_partial = partials;
     if (a.N == 0 || a.batch == 0) return hipSuccess;
-    if (nk_r > 0 && aligned16(ptrs[0]) && aligned16(ptrs[1]) && (a.pro_g < 0 || aligned16(a.eptr[a.pro_g])) &&
-        (a.pro_b < 0 || aligned16(a.eptr[a.pro_b]))) {
+    if (nk_r > 0 && (bf16 || aligned16(ptrs[1]))) {
       a.splitk = 1;
+      a.a_vec = aligned16(ptrs[0]) && (a.pro_g < 0 || aligned16(a.eptr[a.pro_g])) &&
+                (a.pro_b < 0 || aligned16(a.eptr[a.pro_b]));
+      if (bf16 && !aligned16(ptrs[1])) return hipErrorInvalidValue;
       launch_nk(a, stream);
       return hipGetLastError();
     }
@@ -369,8 +414,10 @@ class GemvOp final : public Op {
     const dim3 block(64 * nk_waves);
 #define KH_NK_CASE(R)                                                                                   \
   case R:                                                                                               \
-    if (a.pro) hipLaunchKernelGGL((gemv_nk_kernel<R, true>), nk_grid, block, 0, stream, a);            \
-    else hipLaunchKernelGGL((gemv_nk_kernel<R, false>), nk_grid, block, 0, stream, a);                 \
+    if (bf16 && a.pro) hipLaunchKernelGGL((gemv_nk_kernel<R, true, true>), nk_grid, block, 0, stream, a); \
+    else if (bf16) hipLaunchKernelGGL((gemv_nk_kernel<R, false, true>), nk_grid, block, 0, stream, a);   \
+    else if (a.pro) hipLaunchKernelGGL((gemv_nk_kernel<R, true, false>), nk_grid, block, 0, stream, a);  \
+    else hipLaunchKernelGGL((gemv_nk_kernel<R, false, false>), nk_grid, block, 0, stream, a);            \
     break;
     switch (nk_r) {
       KH_NK_CASE(1)
@@ -422,6 +469,12 @@ std::unique_ptr<Op> make_gemv(const kh_launch &L, std::string &err, bool &unsupp
   if (!fill_epilogue(L, a, op->e_vec_candidates, err)) return nullptr;
   a.direct = 0, a.d_bias = a.d_res = a.d_out = a.d_act = -1;
   match_direct_epilogue(L, a);
+  if (L.cfg[3] != KH_PREC_FP32 && L.cfg[3] != KH_PREC_BF16) {
+    unsupported = true;
+    err = "gemv: precision must be fp32 or bf16";
+    return nullptr;
+  }
+  op->bf16 = L.cfg[3] == KH_PREC_BF16;
   // LayerNorm prologue: cfg[4] = 1, cfg[5] / cfg[6] = ref index of gamma /
   // beta (-1: none), fparams = {1/C, 1/C, eps}; gamma and beta are [K] rows
   a.pro = L.cfg[4], a.pro_g = -1, a.pro_b = -1;
@@ -488,15 +541,22 @@ std::unique_ptr<Op> make_gemv(const kh_launch &L, std::string &err, bool &unsupp
   // of 4, gamma / beta unit-stride): float4 loads per lane; R float4 per lane
   // and wave, NW = ceil(K/4 / 64R) waves, the (R, NW) with the fewest idle
   // lanes. A LayerNorm prologue needs the whole row in one pass.
-  const bool nk_layout = a.sb_k == 1 && a.sb_n >= K && a.sb_n % 4 == 0 && a.sb_b % 4 == 0 &&
-                         L.refs[1].offset % 4 == 0 && a.sa_k == 1 && a.sa_b % 4 == 0 && L.refs[0].offset % 4 == 0 &&
-                         K % 4 == 0 && K > 0 && (N + kNkCols - 1) / kNkCols < (1ll << 31);
+  const int kv = op->bf16 ? 8 : 4;  // K values per 16-byte weight chunk
+  const bool nk_layout = a.sb_k == 1 && a.sb_n >= K && a.sb_n % kv == 0 && a.sb_b % kv == 0 &&
+                         L.refs[1].offset % kv == 0 && a.sa_k == 1 && a.sa_b % 4 == 0 &&
+                         L.refs[0].offset % 4 == 0 && K % kv == 0 && K > 0 &&
+                         (N + kNkCols - 1) / kNkCols < (1ll << 31);
   bool nk_pro_ok = true;
   if (a.pro)
     for (int r : {L.cfg[5], L.cfg[6]})
       if (r >= 0 && (L.refs[r].offset % 4 != 0 || L.refs[r].strides[0] % 4 != 0)) nk_pro_ok = false;
+  if (op->bf16 && !(nk_layout && nk_pro_ok)) {
+    err = "gemv: bf16 weights must be a [batch][N][K] copy with K a multiple of 8 and unit-stride, "
+          "16-byte aligned x (and LayerNorm gamma / beta) rows";
+    return nullptr;
+  }
   if (nk_layout && nk_pro_ok) {
-    const int64_t k4 = K / 4;
+    const int64_t k4 = K / kv;
     int best_r = 0, best_w = 0;
     int64_t best_waste = -1;
     for (int r : {3, 4, 2, 1}) {
@@ -506,6 +566,11 @@ std::unique_ptr<Op> make_gemv(const kh_launch &L, std::string &err, bool &unsupp
       if (best_waste < 0 || waste < best_waste) best_r = r, best_w = (int)w, best_waste = waste;
     }
     if (best_r == 0 && !a.pro) best_r = 4, best_w = kNkMaxWaves;  // several passes over K
+    if (best_r == 0 && op->bf16) {
+      unsupported = true;
+      err = "gemv: a bf16 LayerNorm prologue needs the row in one pass (K <= 16384)";
+      return nullptr;
+    }
     if (best_r > 0) {
       op->nk_r = best_r, op->nk_waves = best_w;
       op->nk_grid = dim3((unsigned)((N + kNkCols - 1) / kNkCols), (unsigned)b1, 1);

@@ -623,11 +623,14 @@ class _Lowerer:
         outs = kernel_outputs(self.g, k, self.users)
         space3 = (batch, m, n)
 
-        def ref3(v, dims):
-            """Strides of v over a 3-d space named by `dims` (v's own dims right-aligned)."""
+        def ref3(v, dims, register=True):
+            """Strides of v over a 3-d space named by `dims` (v's own dims
+            right-aligned). register=False describes a constant that is only
+            read through a derived copy, so it gets no slot (and is not
+            uploaded)."""
             lay = self.layouts[v]
             r = kl.Ref()
-            r.base, r.index = self.slot_of(lay.base)
+            r.base, r.index = self.slot_of(lay.base) if register else (kl.BASE_CONST, -1)
             r.offset = self.element_offset(v)
             lead = 3 - len(lay.shape)
             for i, (s, st) in enumerate(zip(lay.shape, lay.strides)):
@@ -637,13 +640,14 @@ class _Lowerer:
         if a not in self.layouts or b not in self.layouts:
             raise NotImplementedError("HIP backend: matmul operand has no storage")
         cfg, prec = self.matmul_choice(k)
-        gemv = m == 1 and prec == "fp32"
+        gemv = self.is_gemv(k)
         pro = self.prologue.get(k) if gemv else None
         a_src = pro[0] if pro else a   # the LayerNorm's input when the GEMV runs it as its prologue
         d = self.new_desc(kl.FAM_GEMV if gemv else kl.FAM_GEMM, "gemv" if gemv else "matmul", k, space3)
         d.gemm[0], d.gemm[1], d.gemm[2], d.gemm[3] = batch, m, n, kk
         d.refs[0] = ref3(a_src, (batch, m, kk))
-        d.refs[1] = ref3(b, (batch, kk, n))
+        derived_b = prec in ("bf16", "bf16x3") or (gemv and self.layouts[b].base[0] == "const" and kk % 4 == 0)
+        d.refs[1] = ref3(b, (batch, kk, n), register=not derived_b)
         if prec in ("bf16", "bf16x3"):
             d.refs[1] = self.bf16_weight(b, d.refs[1], batch, kk, n, split=prec == "bf16x3")
         elif gemv and self.layouts[b].base[0] == "const" and kk % 4 == 0:
@@ -710,8 +714,8 @@ class _Lowerer:
             # a configuration of another precision (e.g. the fp32 fallback above)
             cfg = {**cfg, **autotune.default_config_for(batch, m, n, kk, precision=prec)}
         if gemv:
-            # GEMV family: "tile" picks the workgroup variant (0 = from the
-            # shape, 1-5), split-K 0 = from the shape
+            # GEMV family: "tile" picks the workgroup variant of the [K][N]
+            # kernel (0 = from the shape, 1-5), split-K 0 = from the shape
             cfg = {"tile": int(cfg.get("tile", 0)) if 0 <= int(cfg.get("tile", 0)) <= 5 else 0,
                    "splitk": int(cfg.get("gemv_splitk", cfg.get("splitk", 0))),
                    "precision": cfg.get("precision", self.precision)}
@@ -732,6 +736,20 @@ class _Lowerer:
         if epi:
             summary += f" epilogue: {epi}"
         self.add(d, k, summary, flops=flops, nbytes=nbytes)
+
+    def is_gemv(self, k: Kernel) -> bool:
+        """A one-row matmul runs on the GEMV family: in fp32 always, in bf16
+        when B is a constant (read as its bf16 [batch][N][K] copy) and K is a
+        multiple of 8 (whole 16-byte weight chunks); other bf16 / bf16x3
+        one-row products run on the GEMM tiles."""
+        mm = next(n for n in k.nodes if n.op == "matmul")
+        a, b = mm.inputs
+        if a.shape[-2] != 1:
+            return False
+        _, prec = self.matmul_choice(k)
+        if prec == "fp32":
+            return True
+        return prec == "bf16" and self.layouts[b].base[0] == "const" and a.shape[-1] % 8 == 0
 
     def matmul_choice(self, k: Kernel):
         """(configuration, precision) of matmul kernel k, asked once per kernel."""
@@ -793,8 +811,7 @@ class _Lowerer:
                 continue
             if self._arena_range(y) is None and y not in self.layouts:
                 continue
-            _, prec = self.matmul_choice(km)
-            if prec != "fp32":
+            if not self.is_gemv(km):
                 continue
             j = kernels.index(km)
             xr = self._arena_range(x)

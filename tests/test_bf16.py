@@ -61,11 +61,20 @@ def test_linear_lowers_to_the_bf16_gemm_with_a_weight_copy():
     assert (b.offset, b.strides[0], b.strides[1], b.strides[2]) == (0, 0, 1, 64)   # K' = 64
     src, offset, strides, batch, k, n = prog.derived[name]
     assert (batch, k, n) == (1, 61, 133) and strides[2] == 1 and strides[1] == 133
+    # the fp32 original is read only through the copy: it is not uploaded
+    assert src not in prog.consts
 
 
 def test_bf16_decode_and_activation_products():
-    # M = 1 runs on the bf16 GEMM (the GEMV family is fp32 only)
+    # M = 1 with a constant weight and K a multiple of 8 runs on the GEMV
+    # family over the bf16 [N][K] copy; K = 61 (partial 16-byte chunks) on the
+    # bf16 GEMM tiles
     _, prog = lowered(torch.nn.Linear(768, 3072), torch.randn(1, 768))
+    d = prog.launches[0].desc
+    assert prog.launches[0].family == kl.FAM_GEMV and d.cfg[3] == kl.PREC_BF16
+    assert (d.refs[1].base, d.refs[1].strides[1], d.refs[1].strides[2]) == (kl.BASE_CONST, 1, 768)
+    kl.Plan([d])
+    _, prog = lowered(torch.nn.Linear(61, 30), torch.randn(1, 61))
     assert prog.launches[0].family == kl.FAM_GEMM and prog.launches[0].desc.cfg[3] == kl.PREC_BF16
     # a product of two activations has no constant to copy: it stays fp32
     _, prog = lowered(lambda a, b: a @ b, torch.randn(64, 32), torch.randn(32, 48))

@@ -90,6 +90,32 @@ def test_every_bf16_tile_configuration(tile):
             close_to_scale(c(x, r).cpu().numpy(), ref, EXACT)
 
 
+@pytest.mark.parametrize("k, n, ln", [(768, 2304, True), (3072, 768, False), (64, 130, False), (16, 5, True)])
+def test_bf16_gemv(k, n, ln):
+    # one-row products with a constant weight run on the K-contiguous GEMV over
+    # the bf16 [N][K] copy (x rounded to bf16, fp32 sums), with and without a
+    # LayerNorm prologue (normalised in fp32, then rounded: CHAINED covers an
+    # activation that lands on the other side of a bf16 rounding boundary)
+    torch.manual_seed(k + n)
+    lin = gpt2_init_(torch.nn.Linear(k, n), seed=k).eval()
+    layers = [torch.nn.LayerNorm(k)] if ln else []
+    model = torch.nn.Sequential(*layers, lin).eval()
+    x = 1.0 + torch.randn(1, k)
+    c = kiln.compile(model, (x,), device="cuda", matmul_precision="bf16")
+    assert c.report.lowering["families"] == {"gemv": 1} and c.report.lowering["precision"] == "bf16"
+    out = c(x.cuda()).cpu().numpy()
+    xa = x.numpy().astype(np.float64)
+    if ln:
+        xa = (xa - xa.mean(-1, keepdims=True)) / np.sqrt(xa.var(-1, keepdims=True) + 1e-5)
+    w, b = lin.weight.detach().numpy(), lin.bias.detach().numpy()
+    ref = r16(xa) @ r16(w).T + b.astype(np.float64)
+    close_to_scale(out, ref, CHAINED if ln else EXACT)
+    with torch.no_grad():
+        stated(out, model(x).numpy())
+    for _ in range(2):
+        assert np.array_equal(c(x.cuda()).cpu().numpy(), out)
+
+
 def test_batched_constant_operand():
     class M(torch.nn.Module):
         def __init__(self):

@@ -162,6 +162,8 @@ def test_gemv_weights_are_k_contiguous_copies():
     assert copy.shape == (1, 300, 768) and copy.flags.c_contiguous
     np.testing.assert_array_equal(copy[0], lin.weight.detach().numpy())
     assert HIPExecutable._host_constant(prog, g.constants, name).shape == (1, 300, 768)
+    # the frozen W^T itself is read only through the copy: it gets no slot
+    assert name in prog.consts and src not in prog.consts
     _, prog = lowered(torch.nn.Linear(37, 30), torch.randn(1, 37))
     assert not prog.derived
 
