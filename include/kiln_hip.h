@@ -75,6 +75,8 @@ enum { KH_ROW_GENERIC = 0, KH_ROW_LAYERNORM = 1, KH_ROW_SOFTMAX = 2 };
 
 /* GEMM precisions */
 enum { KH_PREC_FP32 = 0, KH_PREC_BF16 = 1, KH_PREC_BF16X3 = 2 };
+/* GEMV prologues (kh_launch.cfg[4] of a KH_FAM_GEMV launch) */
+enum { KH_GEMV_PRO_NONE = 0, KH_GEMV_PRO_LAYERNORM = 1, KH_GEMV_PRO_ATTN = 2 };
 
 /*
  * Tape: a straight-line program over KH_NREGS slots, each slot holding the
@@ -140,7 +142,14 @@ typedef struct kh_pass {
  *        (x - mean) * rsqrt(var + eps) [* gamma] [+ beta], mean = sum(x) *
  *        fparams[0], var = sum((x - mean)^2) * fparams[1], eps = fparams[2];
  *        cfg[5] / cfg[6] = ref index (>= 2) of gamma / beta, unit stride over
- *        K and stride 0 over M, or -1.
+ *        K and stride 0 over M, or -1. cfg[4] = 2: attention prologue (decode:
+ *        the head-merged output of one query's attention is the row x) -
+ *        refs[0] is not read; refs[cfg[5]], +1, +2 = Q, K, V over (head,
+ *        token, d) as in ATTN (+3: an additive mask over (head, query, key));
+ *        cfg[0] = head dim (32 or 64, K = heads * head dim), cfg[7] = keys
+ *        (1..64), cfg[6] = mask mode + 4 * scale mode, fparams[0] = scale;
+ *        x[h * dh + d] = softmax_j(scaled q_h . k_jh [+ mask]) . v_jh[d].
+ *        Needs the K-contiguous weight layout (B unit stride over K).
  *   RED  shape = input shape; refs[0] = input, refs[1] = output, both with
  *        strides over the input shape (the output's reduced dims stride 0);
  *        cfg[0] = bitmask of reduced dims, cfg[1] = 1 for max else sum.

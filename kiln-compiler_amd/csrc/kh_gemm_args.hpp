@@ -31,6 +31,11 @@ struct GemmArgs {
   // indices (-1 when absent), c1 / c2 the 1/C factors of mean and variance
   int32_t pro, pro_g, pro_b;
   float pro_c1, pro_c2, pro_eps;
+  // GEMV attention prologue (pro == 2): epilogue operand index of Q (K and V
+  // follow), of the additive mask (-1: none), keys, head dim, mask and scale
+  // modes, scale
+  int32_t att_q, att_mask, att_tk, att_dh, att_mask_mode, att_scale_mode;
+  float att_scale;
 };
 
 // Run the epilogue tape for columns [n, n + valid) of output row (b, m);

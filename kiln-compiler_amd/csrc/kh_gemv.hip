@@ -216,10 +216,93 @@ __device__ __forceinline__ float nk_weight(const uint4 &w, int e) {
   else return __uint_as_float(word);
 }
 
+// Attention prologue: x values k0 .. k0 + KV - 1 (k0 = u * KV) of the
+// head-merged attention output of one query, x[h * dh + d] = softmax_j(s_j) .
+// v_jh[d] with s_j = q_h . k_jh scaled (+ mask). The dh / KV lanes that share
+// a head hold its dims k0 % dh .. + KV - 1 and sum their partial dot products
+// by xor shuffles, so every lane of the group has s_j; the online softmax is
+// attn_kernel's (base 2, exponentials against 0 while no score is finite).
+template <int KV, int R>
+__device__ __forceinline__ void nk_attention(const GemmArgs &a, const int (&u)[R], float (&x)[R][KV]) {
+  constexpr float kLog2e = 1.4426950408889634f;
+  constexpr int kChunk = 2;  // keys per round of loads (all R units' rows issued together)
+  const int group = a.att_dh / KV;  // lanes per head
+  const float c_scale = a.att_scale_mode == KH_ATTN_SCALE_MUL   ? a.att_scale * kLog2e
+                        : a.att_scale_mode == KH_ATTN_SCALE_DIV ? kLog2e / a.att_scale
+                                                                : kLog2e;
+  const int qi = a.att_q, ki = a.att_q + 1, vi = a.att_q + 2;
+  int h[R], d0[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) h[i] = u[i] * KV / a.att_dh, d0[i] = u[i] * KV - h[i] * a.att_dh;
+  auto row = [&](int j, int i, int t) {  // operand j's (head h[i], token t) row at dim d0[i]
+    return a.eptr[j] + (int64_t)h[i] * a.estride[j][0] + (int64_t)t * a.estride[j][1] + d0[i];
+  };
+  auto load = [&](const float *p, float (&dst)[KV]) {
+    if (a.a_vec) {
+#pragma unroll
+      for (int e = 0; e < KV; e += 4) {
+        const float4 t = *reinterpret_cast<const float4 *>(p + e);
+        dst[e] = t.x, dst[e + 1] = t.y, dst[e + 2] = t.z, dst[e + 3] = t.w;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < KV; ++e) dst[e] = p[e];
+    }
+  };
+  const int lim = a.att_mask_mode == KH_ATTN_MASK_CAUSAL ? 1 : a.att_tk;  // the query is token 0
+  float q[R][KV], m[R], l[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    load(row(qi, i, 0), q[i]);
+    m[i] = -INFINITY, l[i] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < KV; ++e) x[i][e] = 0.0f;  // the running sum of p v
+  }
+  for (int j0 = 0; j0 < lim; j0 += kChunk) {
+    float kv[R][kChunk][KV], vv[R][kChunk][KV], mk[R][kChunk];
+#pragma unroll
+    for (int i = 0; i < R; ++i)
+#pragma unroll
+      for (int c = 0; c < kChunk; ++c) {
+        const int j = min(j0 + c, lim - 1);  // clamped: an in-bounds load, the key is dropped below
+        load(row(ki, i, j), kv[i][c]);
+        load(row(vi, i, j), vv[i][c]);
+        mk[i][c] = a.att_mask >= 0 ? a.eptr[a.att_mask][(int64_t)h[i] * a.estride[a.att_mask][0] +
+                                                         (int64_t)j * a.estride[a.att_mask][2]]
+                                   : 0.0f;
+      }
+#pragma unroll
+    for (int c = 0; c < kChunk; ++c) {
+      if (j0 + c >= lim) break;
+#pragma unroll
+      for (int i = 0; i < R; ++i) {
+        float t = 0.0f;
+#pragma unroll
+        for (int e = 0; e < KV; ++e) t = fmaf(q[i][e] * c_scale, kv[i][c][e], t);
+        for (int s = 1; s < group; s <<= 1) t += __shfl_xor(t, s, 64);
+        if (a.att_mask >= 0) t = fmaf(mk[i][c], kLog2e, t);
+        const float m_new = fmaxf(m[i], t);
+        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+        const float alpha = __builtin_amdgcn_exp2f(m[i] - m_use);
+        const float p = __builtin_amdgcn_exp2f(t - m_use);
+        l[i] = fmaf(l[i], alpha, p);
+#pragma unroll
+        for (int e = 0; e < KV; ++e) x[i][e] = fmaf(x[i][e], alpha, p * vv[i][c][e]);
+        m[i] = m_new;
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < R; ++i)
+#pragma unroll
+    for (int e = 0; e < KV; ++e) x[i][e] /= l[i];
+}
+
 // BF16: the weights are the bf16 [batch][N][K] copy, a unit is 8 K values
 // (one 16-byte chunk), x is rounded to bf16 (round to nearest even) at the
 // product - the arithmetic of the bf16 GEMM (exact products, fp32 sums).
-template <int R, bool PRO, bool BF16>
+// PRO: 0 none, 1 LayerNorm prologue, 2 attention prologue.
+template <int R, int PRO, bool BF16>
 __global__ __launch_bounds__(64 * kNkMaxWaves) void gemv_nk_kernel(const GemmArgs a) {
   constexpr int KV = BF16 ? 8 : 4;  // K values per lane and unit
   __shared__ float red[kNkMaxWaves];
@@ -228,8 +311,8 @@ __global__ __launch_bounds__(64 * kNkMaxWaves) void gemv_nk_kernel(const GemmArg
   const int n0 = blockIdx.x * kNkCols, b = blockIdx.y;
   const int U = a.K / KV, step = 64 * nw;  // the host checks K % KV == 0
   const float *xrow = a.A + (int64_t)b * a.sa_b;
-  const float *grow = PRO && a.pro_g >= 0 ? a.eptr[a.pro_g] + (int64_t)b * a.estride[a.pro_g][0] : nullptr;
-  const float *brow = PRO && a.pro_b >= 0 ? a.eptr[a.pro_b] + (int64_t)b * a.estride[a.pro_b][0] : nullptr;
+  const float *grow = PRO == 1 && a.pro_g >= 0 ? a.eptr[a.pro_g] + (int64_t)b * a.estride[a.pro_g][0] : nullptr;
+  const float *brow = PRO == 1 && a.pro_b >= 0 ? a.eptr[a.pro_b] + (int64_t)b * a.estride[a.pro_b][0] : nullptr;
   const uint4 *w16[kNkCols];
 #pragma unroll
   for (int c = 0; c < kNkCols; ++c) {
@@ -275,13 +358,19 @@ __global__ __launch_bounds__(64 * kNkMaxWaves) void gemv_nk_kernel(const GemmArg
       const int uc = in[i] ? u : U - 1;  // clamped: an in-bounds load, product dropped
 #pragma unroll
       for (int c = 0; c < kNkCols; ++c) wv[c][i] = w16[c][uc];
-      load_row(xrow, uc, xv[i]);
-      if constexpr (PRO) {
+      if constexpr (PRO != 2) load_row(xrow, uc, xv[i]);
+      if constexpr (PRO == 1) {
         if (grow) load_row(grow, uc, gv[i]);
         if (brow) load_row(brow, uc, bv[i]);
       }
     }
-    if constexpr (PRO) {
+    if constexpr (PRO == 2) {
+      int us[R];
+#pragma unroll
+      for (int i = 0; i < R; ++i) us[i] = min(base + i * step, U - 1);
+      nk_attention<KV, R>(a, us, xv);
+    }
+    if constexpr (PRO == 1) {
       // the whole row is in this pass (the host guarantees U <= R * 64 * NW):
       // mean, then the variance of the centred values
       float s = 0.0f;
@@ -376,6 +465,7 @@ class GemvOp final : public Op {
   // when the operands it reads as float4 are 16-byte aligned
   int nk_r = 0, nk_waves = 1;
   bool bf16 = false;  // weights are the bf16 [batch][N][K] copy (K-contiguous kernel only)
+  bool att_vec = false;  // attention prologue rows keep 16-byte alignment (strides and offsets)
   dim3 nk_grid;
 
   hipError_t launch(float *const *ptrs, uint32_t *counters, float *partials, hipStream_t stream) override {
@@ -391,16 +481,21 @@ class GemvOp final : public Op {
     }
     a.ws_partial = partials;
     if (a.N == 0 || a.batch == 0) return hipSuccess;
-    if (nk_r > 0 && (bf16 || aligned16(ptrs[1]))) {
+    // bf16 weights and the attention prologue exist only on the K-contiguous kernel
+    if (nk_r > 0 && (bf16 || a.pro == 2 || aligned16(ptrs[1]))) {
       a.splitk = 1;
-      a.a_vec = aligned16(ptrs[0]) && (a.pro_g < 0 || aligned16(a.eptr[a.pro_g])) &&
-                (a.pro_b < 0 || aligned16(a.eptr[a.pro_b]));
-      if (bf16 && !aligned16(ptrs[1])) return hipErrorInvalidValue;
+      if (a.pro == 2)
+        a.a_vec = att_vec && aligned16(a.eptr[a.att_q]) && aligned16(a.eptr[a.att_q + 1]) &&
+                  aligned16(a.eptr[a.att_q + 2]);
+      else
+        a.a_vec = aligned16(ptrs[0]) && (a.pro_g < 0 || aligned16(a.eptr[a.pro_g])) &&
+                  (a.pro_b < 0 || aligned16(a.eptr[a.pro_b]));
+      if ((bf16 || a.pro == 2) && !aligned16(ptrs[1])) return hipErrorInvalidValue;
       launch_nk(a, stream);
       return hipGetLastError();
     }
     if (a.splitk > 1 && !partials) return hipErrorInvalidValue;
-    if (a.pro) launch_variant(a, grid, stream, std::true_type{});
+    if (a.pro == KH_GEMV_PRO_LAYERNORM) launch_variant(a, grid, stream, std::true_type{});
     else launch_variant(a, grid, stream, std::false_type{});
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.splitk == 1) return e;
@@ -412,20 +507,29 @@ class GemvOp final : public Op {
 
   void launch_nk(const GemmArgs &a, hipStream_t stream) const {
     const dim3 block(64 * nk_waves);
-#define KH_NK_CASE(R)                                                                                   \
-  case R:                                                                                               \
-    if (bf16 && a.pro) hipLaunchKernelGGL((gemv_nk_kernel<R, true, true>), nk_grid, block, 0, stream, a); \
-    else if (bf16) hipLaunchKernelGGL((gemv_nk_kernel<R, false, true>), nk_grid, block, 0, stream, a);   \
-    else if (a.pro) hipLaunchKernelGGL((gemv_nk_kernel<R, true, false>), nk_grid, block, 0, stream, a);  \
-    else hipLaunchKernelGGL((gemv_nk_kernel<R, false, false>), nk_grid, block, 0, stream, a);            \
+#define KH_NK_PRO(R, P)                                                                             \
+  if (a.pro == P) {                                                                                 \
+    if (bf16) hipLaunchKernelGGL((gemv_nk_kernel<R, P, true>), nk_grid, block, 0, stream, a);        \
+    else hipLaunchKernelGGL((gemv_nk_kernel<R, P, false>), nk_grid, block, 0, stream, a);            \
+  }
+#define KH_NK_CASE(R) \
+  case R:             \
+    KH_NK_PRO(R, 0)   \
+    KH_NK_PRO(R, 1)   \
+    KH_NK_PRO(R, 2)   \
     break;
+    // R = 4 has no attention-prologue variant (its registers would spill)
     switch (nk_r) {
       KH_NK_CASE(1)
       KH_NK_CASE(2)
       KH_NK_CASE(3)
-      KH_NK_CASE(4)
+      case 4:
+        KH_NK_PRO(4, 0)
+        KH_NK_PRO(4, 1)
+        break;
     }
 #undef KH_NK_CASE
+#undef KH_NK_PRO
   }
 
   template <class P>
@@ -477,12 +581,38 @@ std::unique_ptr<Op> make_gemv(const kh_launch &L, std::string &err, bool &unsupp
   op->bf16 = L.cfg[3] == KH_PREC_BF16;
   // LayerNorm prologue: cfg[4] = 1, cfg[5] / cfg[6] = ref index of gamma /
   // beta (-1: none), fparams = {1/C, 1/C, eps}; gamma and beta are [K] rows
-  a.pro = L.cfg[4], a.pro_g = -1, a.pro_b = -1;
-  if (a.pro != 0 && a.pro != 1) {
+  a.pro = L.cfg[4], a.pro_g = -1, a.pro_b = -1, a.att_q = -1, a.att_mask = -1;
+  if (a.pro != KH_GEMV_PRO_NONE && a.pro != KH_GEMV_PRO_LAYERNORM && a.pro != KH_GEMV_PRO_ATTN) {
     err = "gemv: unknown prologue " + std::to_string(a.pro);
     return nullptr;
   }
-  if (a.pro) {
+  if (a.pro == KH_GEMV_PRO_ATTN) {
+    // attention prologue: Q, K, V (+ mask) refs from cfg[5]; one query
+    const int r = L.cfg[5], mask_mode = L.cfg[6] & 3, scale_mode = L.cfg[6] >> 2, dh = L.cfg[0], tk = L.cfg[7];
+    const int n_att = mask_mode == KH_ATTN_MASK_ADD ? 4 : 3;
+    if (r < 2 || r + n_att > L.n_refs) {
+      err = "gemv: attention prologue operand index out of range";
+      return nullptr;
+    }
+    if (mask_mode > KH_ATTN_MASK_ADD || scale_mode > KH_ATTN_SCALE_DIV || (dh != 32 && dh != 64) || K % dh ||
+        tk < 1 || tk > 64 || batch != 1 || (scale_mode == KH_ATTN_SCALE_DIV && L.fparams[0] == 0.0f)) {
+      err = "gemv: attention prologue needs one query, 1..64 keys, head dim 32 or 64 dividing K, batch 1";
+      return nullptr;
+    }
+    op->att_vec = true;
+    for (int j = 0; j < 3; ++j) {
+      const kh_ref &q = L.refs[r + j];
+      if (q.strides[2] != 1 || q.strides[0] < 0 || q.strides[1] < 0) {
+        err = "gemv: attention prologue Q / K / V need unit head-dim stride";
+        return nullptr;
+      }
+      op->att_vec = op->att_vec && q.offset % 4 == 0 && q.strides[0] % 4 == 0 && q.strides[1] % 4 == 0;
+    }
+    a.att_q = r - 2, a.att_mask = mask_mode == KH_ATTN_MASK_ADD ? r + 1 : -1;
+    a.att_tk = tk, a.att_dh = dh, a.att_mask_mode = mask_mode, a.att_scale_mode = scale_mode;
+    a.att_scale = L.fparams[0];
+  }
+  if (a.pro == KH_GEMV_PRO_LAYERNORM) {
     for (int w = 0; w < 2; ++w) {
       const int r = L.cfg[5 + w];
       if (r == -1) continue;
@@ -547,9 +677,13 @@ std::unique_ptr<Op> make_gemv(const kh_launch &L, std::string &err, bool &unsupp
                          L.refs[0].offset % 4 == 0 && K % kv == 0 && K > 0 &&
                          (N + kNkCols - 1) / kNkCols < (1ll << 31);
   bool nk_pro_ok = true;
-  if (a.pro)
+  if (a.pro == KH_GEMV_PRO_LAYERNORM)
     for (int r : {L.cfg[5], L.cfg[6]})
       if (r >= 0 && (L.refs[r].offset % 4 != 0 || L.refs[r].strides[0] % 4 != 0)) nk_pro_ok = false;
+  if (a.pro == KH_GEMV_PRO_ATTN && !nk_layout) {
+    err = "gemv: an attention prologue needs the K-contiguous weight layout";
+    return nullptr;
+  }
   if (op->bf16 && !(nk_layout && nk_pro_ok)) {
     err = "gemv: bf16 weights must be a [batch][N][K] copy with K a multiple of 8 and unit-stride, "
           "16-byte aligned x (and LayerNorm gamma / beta) rows";
@@ -560,12 +694,14 @@ std::unique_ptr<Op> make_gemv(const kh_launch &L, std::string &err, bool &unsupp
     int best_r = 0, best_w = 0;
     int64_t best_waste = -1;
     for (int r : {3, 4, 2, 1}) {
+      if (r == 4 && a.pro == KH_GEMV_PRO_ATTN) continue;
       const int64_t w = (k4 + 64 * r - 1) / (64 * r);
       if (w > kNkMaxWaves) continue;
       const int64_t waste = 64 * r * w - k4;
       if (best_waste < 0 || waste < best_waste) best_r = r, best_w = (int)w, best_waste = waste;
     }
-    if (best_r == 0 && !a.pro) best_r = 4, best_w = kNkMaxWaves;  // several passes over K
+    if (best_r == 0 && a.pro != KH_GEMV_PRO_LAYERNORM)  // several passes over K
+      best_r = a.pro == KH_GEMV_PRO_ATTN ? 3 : 4, best_w = kNkMaxWaves;
     if (best_r == 0 && op->bf16) {
       unsupported = true;
       err = "gemv: a bf16 LayerNorm prologue needs the row in one pass (K <= 16384)";

@@ -24,6 +24,7 @@ OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP, ERR_NO_DEVICE, ERR_CAPACITY = range(6
 BASE_INPUT, BASE_OUTPUT, BASE_CONST, BASE_ARENA, BASE_WORKSPACE = range(5)
 FAM_EW, FAM_ROW, FAM_GEMM, FAM_GEMV, FAM_RED, FAM_ATTN = 1, 2, 3, 4, 5, 6
 ATTN_MASK_NONE, ATTN_MASK_CAUSAL, ATTN_MASK_ADD = 0, 1, 2
+GEMV_PRO_NONE, GEMV_PRO_LAYERNORM, GEMV_PRO_ATTN = 0, 1, 2
 ATTN_SCALE_NONE, ATTN_SCALE_MUL, ATTN_SCALE_DIV = 0, 1, 2
 ROW_GENERIC, ROW_LAYERNORM, ROW_SOFTMAX = 0, 1, 2
 PREC_FP32, PREC_BF16, PREC_BF16X3 = 0, 1, 2

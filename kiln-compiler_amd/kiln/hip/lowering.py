@@ -186,6 +186,7 @@ class _Lowerer:
         self.const_slot = {}
         self._cfg = {}
         self.prologue = {}   # matmul kernel -> (x, gamma, beta, fparams) of a fused LayerNorm
+        self.attn_prologue = {}  # GEMV kernel -> (attention match, strides, mask mode, (heads, tk, dh))
 
     # operands ---------------------------------------------------------------------
 
@@ -669,6 +670,9 @@ class _Lowerer:
             out_ref[v] = len(refs)
             refs.append(ref3(v, space3))
         pro_refs = []
+        attn_work = None
+        if gemv and k in self.attn_prologue:
+            pro_refs, *attn_work = self.attn_prologue_refs(d, k, 2 + len(refs))
         if pro:
             x, gamma, beta, fparams = pro
             d.cfg[4], d.cfg[5], d.cfg[6] = 1, -1, -1
@@ -733,6 +737,10 @@ class _Lowerer:
         if pro:
             summary += " prologue: layernorm"
             nbytes += 4 * kk * len(pro_refs)
+        if attn_work:
+            summary += " prologue: attention"
+            flops += attn_work[0]
+            nbytes += attn_work[1] - 4 * kk
         if epi:
             summary += f" epilogue: {epi}"
         self.add(d, k, summary, flops=flops, nbytes=nbytes)
@@ -846,6 +854,94 @@ class _Lowerer:
         r.strides[0], r.strides[1], r.strides[2] = (n * kk if batch > 1 else 0), 1, kk
         return r
 
+    def find_attn_prologues(self):
+        """Decode-shaped attention (one query over at most 64 keys, head dim
+        32 or 64) whose head-merged output is only the A operand of the next
+        kernel, a GEMV (decode: attention -> c_proj): the GEMV computes each
+        head's attention output for the K values it loads and the attention
+        kernel is not launched. The GEMV's outputs must not overlap q, k, v or
+        the mask (its workgroups write while others still read them)."""
+        from kiln.hip.attention import causal_or_none, match_kernel, operand_strides
+
+        kernels = self.g.kernels
+        results = set(self.g.results)
+        skip = set()
+        for i, k in enumerate(kernels[:-1]):
+            km = kernels[i + 1]
+            if k.kind != "attention" or km.kind != "matmul" or km in self.prologue or not self.is_gemv(km):
+                continue
+            m = match_kernel(self.g, k)
+            strides = operand_strides(m, self.layouts) if m is not None else None
+            if strides is None:
+                continue
+            heads, tq, dh = m.q.shape
+            tk = m.v.shape[1]
+            mm = next(n for n in km.nodes if n.op == "matmul")
+            a, b = mm.inputs
+            kk = a.shape[-1]
+            if tq != 1 or tk > 64 or dh not in (32, 64) or a.shape[-2] != 1 or kk != heads * dh:
+                continue
+            if self.layouts[b].base[0] != "const" or kk % (8 if self.matmul_choice(km)[1] == "bf16" else 4):
+                continue
+            # the attention's values feed only the GEMV kernel, directly or
+            # through views (no graph result)
+            members = set(k.nodes) | set(km.nodes)
+
+            def feeds_only_gemv(v, depth=0):
+                if v in results or depth > 8:
+                    return False
+                return all(u in members or (ops.kind(u.op) == "view" and feeds_only_gemv(u.out, depth + 1))
+                           for u in self.users.get(v, []))
+
+            if not all(feeds_only_gemv(n.out) for n in k.nodes):
+                continue
+            # A is the head-merged attention output: same storage, k = head * dh + d
+            la, lr = self.layouts.get(a), self.layouts.get(m.result)
+            if la is None or lr is None or la.base != lr.base or self.element_offset(a) != self.element_offset(m.result):
+                continue
+            if la.strides[-1] != 1 or tuple(strides[3][1][i] for i in (0, 2)) != (dh, 1):
+                continue
+            mode = kl.ATTN_MASK_NONE
+            if m.mask is not None:
+                mode = causal_or_none(self.g, m.mask, heads, tq, tk)
+                if mode is None:
+                    mode = kl.ATTN_MASK_ADD
+            reads = [m.q, m.k, m.v] + ([m.mask] if mode == kl.ATTN_MASK_ADD else [])
+            outs = kernel_outputs(self.g, km, self.users)
+            clash = False
+            for v in outs:
+                r = self._arena_range(v)
+                for w in reads:
+                    rw = self._arena_range(w)
+                    if r is not None and rw is not None and r[0] < rw[1] and rw[0] < r[1]:
+                        clash = True
+            if clash:
+                continue
+            self.attn_prologue[km] = (m, strides, mode, (heads, tk, dh))
+            skip.add(k)
+        return skip
+
+    def attn_prologue_refs(self, d, km, first_ref):
+        """Fill GEMV descriptor `d` for the attention prologue of `km`; its q,
+        k, v (and mask) refs start at descriptor ref `first_ref`. Returns the
+        refs and (flops, bytes) of the attention."""
+        m, strides, mode, (heads, tk, dh) = self.attn_prologue[km]
+        refs = []
+        for v, (_, st) in zip((m.q, m.k, m.v), strides[:3]):
+            r = kl.Ref()
+            r.base, r.index = self.slot_of(self.layouts[v].base)
+            r.offset = self.element_offset(v)
+            for i in range(3):
+                r.strides[i] = st[i]
+            refs.append(r)
+        if mode == kl.ATTN_MASK_ADD:
+            refs.append(self.ref(m.mask, (heads, 1, tk)))
+        d.cfg[0], d.cfg[4], d.cfg[5] = dh, kl.GEMV_PRO_ATTN, first_ref
+        d.cfg[6], d.cfg[7] = mode + 4 * m.scale_mode, tk
+        d.fparams[0] = m.scale
+        pairs = 1 if mode == kl.ATTN_MASK_CAUSAL else tk
+        return refs, 4 * heads * pairs * dh, 4 * heads * dh * (2 + 2 * tk)
+
     def bf16_weight(self, b, ref, batch, kk, n, split=False):
         """Ref of the bf16 [batch][N][K'] copy of constant view `b` (whose fp32
         ref over (b, k, n) is `ref`), or with `split` the three-pass
@@ -910,7 +1006,7 @@ class _Lowerer:
             for n in k.nodes:
                 if ops.kind(n.op) not in ("elementwise", "reduction", "matmul") and k.kind != "attention":
                     raise NotImplementedError(f"GPU backend: unexpected op '{n.op}' in a kernel")
-        fused = self.find_ln_prologues()
+        fused = self.find_ln_prologues() | self.find_attn_prologues()
         for k in self.g.kernels:
             if k in fused:
                 continue

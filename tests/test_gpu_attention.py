@@ -100,6 +100,50 @@ def test_few_query_rows(tq, tk, d, masked):
     compare(Attn(mask, scale=8.0, divide=True, merge=False), *qkv(3, tq, tk, d, seed=tq + tk + d))
 
 
+class AttnProj(torch.nn.Module):
+    """One query's attention over tk keys, heads merged, then a Linear (decode)."""
+
+    def __init__(self, heads, d, mask=None, divide=False):
+        super().__init__()
+        self.attn = Attn(mask, scale=8.0 if divide else 0.125, divide=divide)
+        self.proj = torch.nn.Linear(heads * d, 48)
+
+    def forward(self, q, k, v):
+        return self.proj(self.attn(q, k, v))
+
+
+@pytest.mark.parametrize("tk, d, masked, prec", [(1, 64, False, "fp32"), (40, 64, True, "fp32"),
+                                                 (9, 32, False, "fp32"), (64, 64, True, "bf16"),
+                                                 (7, 32, True, "bf16"), (65, 64, False, "fp32")])
+def test_decode_attention_as_gemv_prologue(tk, d, masked, prec):
+    # one query over at most 64 keys feeding a GEMV: the GEMV computes the
+    # attention for the K values it loads and no attention kernel runs
+    # (65 keys: past that, the attention launch stays)
+    heads = 4
+    mask = None
+    if masked:
+        g = torch.Generator().manual_seed(tk)
+        mask = torch.randn(1, tk, generator=g)
+        mask[torch.rand(1, tk, generator=g) < 0.3] = float("-inf")
+        mask[:, 0] = 0.0
+    model = AttnProj(heads, d, mask, divide=tk % 2 == 1).eval()
+    q, k, v = qkv(heads, 1, tk, d, seed=tk + d)
+    fused = tk <= 64
+    if prec == "fp32":
+        c = compare(model, q, k, v, fused=0 if fused else 1)
+    else:
+        c = kiln.compile(model, (q, k, v), device="cuda", matmul_precision=prec)
+        assert n_attention(c) == 0
+        with torch.no_grad():
+            eager = model(q, k, v)
+        got = c(q, k, v).cpu()
+        torch.testing.assert_close(got, eager, rtol=2e-2, atol=2e-2 * eager.abs().max().item())
+    assert ("prologue: attention" in c._exe.program.source) == fused
+    first = c(q, k, v)
+    for _ in range(2):
+        assert torch.equal(c(q, k, v), first)
+
+
 def test_divided_scale_and_no_head_merge():
     c = compare(Attn(None, scale=8.0, divide=True, merge=False), *qkv(4, 70, 70, 64, seed=3))
     assert "scores / 8" in c._exe.program.source
@@ -143,7 +187,8 @@ def test_block_uses_one_attention_launch(T):
     x = torch.randn(T, 768, generator=torch.Generator().manual_seed(T + 1))
     c = kiln.compile(model, (x,), device="cuda")
     # at T = 1 both LayerNorms run as the prologue of the qkv / fc GEMV
-    assert c.report.lowering["launches"] == (5 if T == 1 else 7) and n_attention(c) == 1
+    # at T = 1 the attention runs as the prologue of the c_proj GEMV
+    assert (c.report.lowering["launches"], n_attention(c)) == ((4, 0) if T == 1 else (7, 1))
     # the scores never get arena memory: the peak is the MLP's (768 + 768 + 3072) T floats
     assert c.report.arena_bytes == 4 * 4608 * T
     params = {k: v.numpy() for k, v in model.state_dict().items()}

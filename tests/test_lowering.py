@@ -204,6 +204,21 @@ def test_stack_decode_plan():
     kl.Plan([l.desc for l in prog.launches])
 
 
+def test_decode_attention_runs_as_the_projection_prologue():
+    _, prog = lowered(Block(768, 12, 1), torch.randn(1, 768), fuse_attention=True)
+    # ln_1 -> qkv, attention -> c_proj, ln_2 -> fc, proj: four GEMVs
+    assert [kl.FAMILY_NAMES[l.family] for l in prog.launches] == ["gemv"] * 4
+    assert "prologue: attention" in prog.launches[1].summary
+    d = prog.launches[1].desc
+    assert (d.cfg[0], d.cfg[4], d.cfg[7]) == (64, kl.GEMV_PRO_ATTN, 1)
+    kl.Plan([l.desc for l in prog.launches])
+    for field, value in ((7, 65), (0, 48), (5, 1)):
+        bad = kl.LaunchDesc.from_buffer_copy(d)
+        bad.cfg[field] = value
+        with pytest.raises(ValueError, match="attention prologue"):
+            kl.Plan([bad])
+
+
 def _ln_linear(affine=True, bias=True):
     ln = torch.nn.LayerNorm(64, elementwise_affine=affine)
     lin = torch.nn.Linear(64, 48, bias=bias)
