@@ -135,9 +135,12 @@ typedef struct kh_pass {
  *        strides over (b, m, n). The tape starts with the accumulator in slot 0.
  *        cfg[1] = tile configuration id, cfg[2] = split-K (0: library picks),
  *        cfg[3] = precision.
- *   GEMV as GEMM with M = 1; cfg[1] = workgroup variant (0: library picks from
- *        the shape; 1-3: 32/16/8 columns x 256 threads; 4-5: 32/16 columns x
- *        1024 threads), cfg[2] = split-K (0: library picks). cfg[4] = 1:
+ *   GEMV as GEMM with M = 1; cfg[1] = workgroup variant of the [K][N] kernel
+ *        (0: library picks from the shape; 1-3: 32/16/8 columns x 256 threads;
+ *        4-5: 32/16 columns x 1024 threads), cfg[2] = split-K (0: library
+ *        picks). B with unit K stride ([batch][N][K], K a multiple of 4) runs
+ *        the K-contiguous kernel; cfg[3] = KH_PREC_BF16 reads B as bf16
+ *        [batch][N][K] (K a multiple of 8) and rounds x to bf16. cfg[4] = 1:
  *        LayerNorm prologue - refs[0] is the raw row x and the product uses
  *        (x - mean) * rsqrt(var + eps) [* gamma] [+ beta], mean = sum(x) *
  *        fparams[0], var = sum((x - mean)^2) * fparams[1], eps = fparams[2];
