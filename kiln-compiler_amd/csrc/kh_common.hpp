@@ -59,6 +59,14 @@ __device__ __forceinline__ float op_gelu_erf(float x) {
   return 0.5f * x * (1.0f + erff(x * 0.7071067811865476f));
 }
 
+// 128-bit store marked non-temporal (streamed past the caches): for
+// outputs of memory-bound kernels
+__device__ __forceinline__ void store_stream(float *p, float x, float y, float z, float w) {
+  typedef float f32x4_t __attribute__((ext_vector_type(4)));
+  const f32x4_t v = {x, y, z, w};
+  __builtin_nontemporal_store(v, reinterpret_cast<f32x4_t *>(p));
+}
+
 __device__ __forceinline__ float nan_max(float a, float b) {
   return (a != a) ? a : ((b != b) ? b : fmaxf(a, b));
 }

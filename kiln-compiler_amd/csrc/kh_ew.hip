@@ -181,7 +181,7 @@ __global__ __launch_bounds__(kEwThreads) void ew_fast_kernel(const EwFastArgs a)
         if (ACT == kActRelu) x = x != x ? x : fmaxf(x, 0.0f);
         v[i] = x;
       }
-      *reinterpret_cast<float4 *>(a.out + (int64_t)row[u] * a.out_os + col[u]) = make_float4(v[0], v[1], v[2], v[3]);
+      store_stream(a.out + (int64_t)row[u] * a.out_os + col[u], v[0], v[1], v[2], v[3]);
     }
   }
 }

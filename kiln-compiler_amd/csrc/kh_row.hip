@@ -81,7 +81,7 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const LnArgs a) {
           const float4 b = *reinterpret_cast<const float4 *>(a.beta + c);
           y.x += b.x, y.y += b.y, y.z += b.z, y.w += b.w;
         }
-        *reinterpret_cast<float4 *>(o + c) = y;
+        store_stream(o + c, y.x, y.y, y.z, y.w);
       }
     }
   }
@@ -142,7 +142,7 @@ __global__ __launch_bounds__(256) void softmax_kernel(const SmxArgs a) {
     for (int i = 0; i < NV; ++i) {
       const uint32_t c = (i * 64 + lane) * 4;
       if (c < a.inner)
-        *reinterpret_cast<float4 *>(o + c) = make_float4(v[i].x * r, v[i].y * r, v[i].z * r, v[i].w * r);
+        store_stream(o + c, v[i].x * r, v[i].y * r, v[i].z * r, v[i].w * r);
     }
   }
 }
