@@ -207,6 +207,14 @@ __device__ __forceinline__ float nk_block_sum(float v, float *red, int wave, int
   return s;
 }
 
+// 128-bit load marked non-temporal: each weight byte is read once per call,
+// so the weights should not displace the activations in the caches.
+__device__ __forceinline__ uint4 load_stream(const uint4 *p) {
+  typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+  const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // One K value of a weight chunk (4 fp32 or 8 bf16 values in a uint4).
 template <bool BF16>
 __device__ __forceinline__ float nk_weight(const uint4 &w, int e) {
@@ -357,7 +365,7 @@ __global__ __launch_bounds__(64 * kNkMaxWaves) void gemv_nk_kernel(const GemmArg
       in[i] = u < U;
       const int uc = in[i] ? u : U - 1;  // clamped: an in-bounds load, product dropped
 #pragma unroll
-      for (int c = 0; c < kNkCols; ++c) wv[c][i] = w16[c][uc];
+      for (int c = 0; c < kNkCols; ++c) wv[c][i] = load_stream(w16[c] + uc);
       if constexpr (PRO != 2) load_row(xrow, uc, xv[i]);
       if constexpr (PRO == 1) {
         if (grow) load_row(grow, uc, gv[i]);
