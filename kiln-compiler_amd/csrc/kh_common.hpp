@@ -59,6 +59,13 @@ __device__ __forceinline__ float op_gelu_erf(float x) {
   return 0.5f * x * (1.0f + erff(x * 0.7071067811865476f));
 }
 
+// 128-bit load marked non-temporal
+__device__ __forceinline__ float4 load_stream4(const float *p) {
+  typedef float f32x4_t __attribute__((ext_vector_type(4)));
+  const f32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t *>(p));
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+
 // 128-bit store marked non-temporal (streamed past the caches): for
 // outputs of memory-bound kernels
 __device__ __forceinline__ void store_stream(float *p, float x, float y, float z, float w) {

@@ -107,7 +107,10 @@ struct SmxArgs {
 // the whole range |v - m| < 88 of normal results, below 1e-6 where
 // |v - m| < 8); the quotient is a product with the row's reciprocal sum (one
 // IEEE division per row).
-template <int NV>
+// NTL: the input is read with non-temporal loads, for inputs larger than the
+// 256 MB Infinity Cache (streamed once: 303 -> 292 us at 1.5 GiB per call);
+// smaller inputs keep cached loads (a re-read input stays in the cache).
+template <int NV, bool NTL>
 __global__ __launch_bounds__(256) void softmax_kernel(const SmxArgs a) {
   const int lane = threadIdx.x & 63;
   const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -119,7 +122,7 @@ __global__ __launch_bounds__(256) void softmax_kernel(const SmxArgs a) {
     for (int i = 0; i < NV; ++i) {
       const uint32_t c = (i * 64 + lane) * 4;
       if (c < a.inner) {
-        v[i] = *reinterpret_cast<const float4 *>(x + c);
+        v[i] = NTL ? load_stream4(x + c) : *reinterpret_cast<const float4 *>(x + c);
         if (a.pre == 1) v[i].x *= a.scale, v[i].y *= a.scale, v[i].z *= a.scale, v[i].w *= a.scale;
         if (a.pre == 2) v[i].x /= a.scale, v[i].y /= a.scale, v[i].z /= a.scale, v[i].w /= a.scale;
         m = nan_max(m, nan_max(nan_max(v[i].x, v[i].y), nan_max(v[i].z, v[i].w)));
@@ -307,6 +310,8 @@ class LayerNormOp final : public Op {
   }
 };
 
+constexpr int64_t kStreamBytes = 256ll << 20;  // the Infinity Cache
+
 class SoftmaxOp final : public Op {
  public:
   SmxArgs args{};
@@ -317,7 +322,11 @@ class SoftmaxOp final : public Op {
     a.x = ptrs[x_ref];
     a.out = ptrs[out_ref];
     if (a.rows == 0) return hipSuccess;
-    KH_NV_SWITCH(nv, hipLaunchKernelGGL((softmax_kernel<kNV>), dim3(grid), dim3(256), 0, stream, a));
+    if ((int64_t)a.rows * a.inner * 4 >= kStreamBytes) {
+      KH_NV_SWITCH(nv, hipLaunchKernelGGL((softmax_kernel<kNV, true>), dim3(grid), dim3(256), 0, stream, a));
+    } else {
+      KH_NV_SWITCH(nv, hipLaunchKernelGGL((softmax_kernel<kNV, false>), dim3(grid), dim3(256), 0, stream, a));
+    }
     return hipGetLastError();
   }
 };
