@@ -42,7 +42,9 @@ struct LnArgs {
 // One row per wave and no grid-stride loop: the grid covers every row, so
 // workgroups start and retire at different times and one wave's reductions
 // overlap other waves' loads and stores.
-template <int NV>
+// NTL: non-temporal input loads, for inputs larger than the Infinity Cache
+// (as in softmax_kernel).
+template <int NV, bool NTL>
 __global__ __launch_bounds__(256) void layernorm_kernel(const LnArgs a) {
   const int lane = threadIdx.x & 63;
   const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -53,7 +55,9 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const LnArgs a) {
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const uint32_t c = (i * 64 + lane) * 4;
-      v[i] = c < a.inner ? *reinterpret_cast<const float4 *>(x + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+      v[i] = c >= a.inner ? make_float4(0.f, 0.f, 0.f, 0.f)
+             : NTL        ? load_stream4(x + c)
+                          : *reinterpret_cast<const float4 *>(x + c);
       s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
     }
     const float mean = wave_sum(s) * a.inv_n1;
@@ -293,6 +297,8 @@ int pick_nv(int64_t inner) {
     default: { constexpr int kNV = 16; __VA_ARGS__; } break;    \
   }
 
+constexpr int64_t kStreamBytes = 256ll << 20;  // the Infinity Cache
+
 class LayerNormOp final : public Op {
  public:
   LnArgs args{};
@@ -305,12 +311,14 @@ class LayerNormOp final : public Op {
     a.beta = b_ref >= 0 ? ptrs[b_ref] : nullptr;
     a.out = ptrs[out_ref];
     if (a.rows == 0) return hipSuccess;
-    KH_NV_SWITCH(nv, hipLaunchKernelGGL((layernorm_kernel<kNV>), dim3(grid), dim3(256), 0, stream, a));
+    if ((int64_t)a.rows * a.inner * 4 >= kStreamBytes) {
+      KH_NV_SWITCH(nv, hipLaunchKernelGGL((layernorm_kernel<kNV, true>), dim3(grid), dim3(256), 0, stream, a));
+    } else {
+      KH_NV_SWITCH(nv, hipLaunchKernelGGL((layernorm_kernel<kNV, false>), dim3(grid), dim3(256), 0, stream, a));
+    }
     return hipGetLastError();
   }
 };
-
-constexpr int64_t kStreamBytes = 256ll << 20;  // the Infinity Cache
 
 class SoftmaxOp final : public Op {
  public:
