@@ -348,7 +348,7 @@ class AttnOp final : public Op {
   bool rows = false;  // few-query kernel
   dim3 grid;
 
-  hipError_t launch(float *const *ptrs, uint32_t *, float *, hipStream_t stream) override {
+  hipError_t launch(float *const *ptrs, float *, hipStream_t stream) override {
     AttnArgs a = args;
     a.q = ptrs[0], a.k = ptrs[1], a.v = ptrs[2], a.o = ptrs[3];
     a.mask = a.mask_mode == KH_ATTN_MASK_ADD ? ptrs[4] : nullptr;

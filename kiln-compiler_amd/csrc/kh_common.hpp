@@ -98,13 +98,15 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// NaN-propagating at every step (v_max_f32 alone returns the non-NaN operand),
+// so a NaN held by any lane reaches all lanes, like max over the row.
 __device__ __forceinline__ float wave_max(float v) {
-  v = fmaxf(v, dpp<0xB1>(v));
-  v = fmaxf(v, dpp<0x4E>(v));
-  v = fmaxf(v, dpp<0x141>(v));
-  v = fmaxf(v, dpp<0x140>(v));
-  v = fmaxf(v, __shfl_xor(v, 16, kWave));
-  v = fmaxf(v, __shfl_xor(v, 32, kWave));
+  v = nan_max(v, dpp<0xB1>(v));
+  v = nan_max(v, dpp<0x4E>(v));
+  v = nan_max(v, dpp<0x141>(v));
+  v = nan_max(v, dpp<0x140>(v));
+  v = nan_max(v, __shfl_xor(v, 16, kWave));
+  v = nan_max(v, __shfl_xor(v, 32, kWave));
   return v;
 }
 

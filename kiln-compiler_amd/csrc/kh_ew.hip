@@ -100,7 +100,7 @@ class EwOp final : public Op {
   uint32_t vec_candidates = 0;  // refs whose layout allows 128-bit access
   int grid = 1;
 
-  hipError_t launch(float *const *ptrs, uint32_t *, float *, hipStream_t stream) override {
+  hipError_t launch(float *const *ptrs, float *, hipStream_t stream) override {
     EwArgs a = args;
     a.vec_mask = 0;
     for (int j = 0; j < a.n_refs; ++j) {
@@ -190,7 +190,7 @@ class EwFastOp final : public Op {
  public:
   EwFastArgs args{};
   int op = kFastAdd, act = kActNone, ra = 0, rb = -1, ro = 0, grid = 1;
-  hipError_t launch(float *const *ptrs, uint32_t *, float *, hipStream_t stream) override {
+  hipError_t launch(float *const *ptrs, float *, hipStream_t stream) override {
     EwFastArgs x = args;
     x.a = ptrs[ra];
     x.b = rb >= 0 ? ptrs[rb] : nullptr;
@@ -198,7 +198,7 @@ class EwFastOp final : public Op {
     for (int j : {ra, rb, ro})
       if (j >= 0 && (reinterpret_cast<uintptr_t>(ptrs[j]) & 15) != 0 &&
           !(j == ra && x.a_bc) && !(j == rb && x.b_bc))
-        return fallback->launch(ptrs, nullptr, nullptr, stream);  // unaligned buffer: tape path
+        return fallback->launch(ptrs, nullptr, stream);  // unaligned buffer: tape path
     if (x.total4 == 0) return hipSuccess;
 #define KH_FAST_CASE(O, A) \
   if (op == O && act == A) hipLaunchKernelGGL((ew_fast_kernel<O, A>), dim3(grid), dim3(kEwThreads), 0, stream, x);

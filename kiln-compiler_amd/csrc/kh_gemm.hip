@@ -1017,7 +1017,7 @@ class GemmOp final : public Op {
   bool a_vec_layout = false, b_vec_layout = false;
   uint32_t e_vec_candidates = 0;
 
-  hipError_t launch(float *const *ptrs, uint32_t *counters, float *partials, hipStream_t stream) override {
+  hipError_t launch(float *const *ptrs, float *partials, hipStream_t stream) override {
     GemmArgs a = args;
     a.A = ptrs[0];
     a.B = ptrs[1];

@@ -476,7 +476,7 @@ class GemvOp final : public Op {
   bool att_vec = false;  // attention prologue rows keep 16-byte alignment (strides and offsets)
   dim3 nk_grid;
 
-  hipError_t launch(float *const *ptrs, uint32_t *counters, float *partials, hipStream_t stream) override {
+  hipError_t launch(float *const *ptrs, float *partials, hipStream_t stream) override {
     GemmArgs a = args;
     a.A = ptrs[0];
     a.B = ptrs[1];

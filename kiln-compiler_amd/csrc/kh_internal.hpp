@@ -25,11 +25,10 @@ class Op {
  public:
   virtual ~Op() = default;
   // ptrs[j] = device address of element 0 of ref j (slot pointer + offset).
-  // counters: this op's own zero-initialised uint32 counters (kernels leave
-  // them at zero), partials: scratch shared by every op of the plan (ops run
-  // one after another on one stream). Either may be null if not requested.
-  virtual hipError_t launch(float *const *ptrs, uint32_t *counters, float *partials, hipStream_t stream) = 0;
-  virtual size_t counter_count() const { return 0; }
+  // partials: scratch of at least partial_floats() floats shared by every op
+  // of the plan (ops run one after another on one stream); null when the op
+  // asks for none. Every op writes all the partials it reads back.
+  virtual hipError_t launch(float *const *ptrs, float *partials, hipStream_t stream) = 0;
   virtual size_t partial_floats() const { return 0; }
 };
 

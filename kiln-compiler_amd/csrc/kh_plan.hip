@@ -109,13 +109,11 @@ bool check_tape(const kh_launch &L, int begin, int end, bool allow_row_ops, Tape
 
 }  // namespace kh
 
-// Workspace layout: [counters of op 0 | counters of op 1 | ... | shared partials],
-// counters 4-byte, partials 256-byte aligned.
+// The workspace holds the split-K partials, shared by every launch of the
+// plan in turn (launches run one after another on one stream).
 struct kh_plan {
   std::vector<kh_launch> desc;
   std::vector<std::unique_ptr<kh::Op>> ops;
-  std::vector<size_t> counter_offset;  // uint32 index of each op's counters
-  size_t partial_offset = 0;           // byte offset of the shared partial area
   size_t ws_needed = 0;
   std::vector<void *> consts;
   void *arena = nullptr;
@@ -174,14 +172,8 @@ int run_range(kh_plan *p, int begin, int end, void *const *inputs, int n_in, voi
   for (int i = begin; i < end; ++i) {
     const int rc = resolve(p, i, inputs, n_in, outputs, n_out, ptrs);
     if (rc != KH_OK) return rc;
-    uint32_t *counters = nullptr;
-    float *partials = nullptr;
-    if (p->workspace) {
-      if (p->ops[i]->counter_count()) counters = static_cast<uint32_t *>(p->workspace) + p->counter_offset[i];
-      if (p->ops[i]->partial_floats())
-        partials = reinterpret_cast<float *>(static_cast<char *>(p->workspace) + p->partial_offset);
-    }
-    const hipError_t e = p->ops[i]->launch(ptrs, counters, partials, stream);
+    float *partials = p->ops[i]->partial_floats() ? static_cast<float *>(p->workspace) : nullptr;
+    const hipError_t e = p->ops[i]->launch(ptrs, partials, stream);
     if (e != hipSuccess) return kh::hip_fail(e, p->desc[i].name);
   }
   return KH_OK;
@@ -271,14 +263,9 @@ int kh_plan_create(const kh_launch *launches, int n_launches, kh_plan **out) {
     }
     p->ops.push_back(std::move(op));
   }
-  size_t counters = 0, partials = 0;
-  for (auto &op : p->ops) {
-    p->counter_offset.push_back(counters);
-    counters += op->counter_count();
-    partials = std::max(partials, op->partial_floats());
-  }
-  p->partial_offset = (counters * sizeof(uint32_t) + 255) / 256 * 256;
-  p->ws_needed = partials ? p->partial_offset + partials * sizeof(float) : counters * sizeof(uint32_t);
+  size_t partials = 0;
+  for (auto &op : p->ops) partials = std::max(partials, op->partial_floats());
+  p->ws_needed = partials * sizeof(float);
   *out = p.release();
   return KH_OK;
 }

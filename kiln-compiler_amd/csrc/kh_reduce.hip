@@ -84,7 +84,7 @@ class RedOp final : public Op {
   RedArgs args{};
   bool per_block = false;
   int grid = 1;
-  hipError_t launch(float *const *ptrs, uint32_t *, float *, hipStream_t stream) override {
+  hipError_t launch(float *const *ptrs, float *, hipStream_t stream) override {
     RedArgs a = args;
     a.x = ptrs[0];
     a.out = ptrs[1];

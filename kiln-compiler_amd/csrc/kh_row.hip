@@ -304,7 +304,7 @@ class LayerNormOp final : public Op {
   LnArgs args{};
   int x_ref = 0, g_ref = -1, b_ref = -1, out_ref = 0;
   int nv = 1, grid = 1;
-  hipError_t launch(float *const *ptrs, uint32_t *, float *, hipStream_t stream) override {
+  hipError_t launch(float *const *ptrs, float *, hipStream_t stream) override {
     LnArgs a = args;
     a.x = ptrs[x_ref];
     a.gamma = g_ref >= 0 ? ptrs[g_ref] : nullptr;
@@ -325,7 +325,7 @@ class SoftmaxOp final : public Op {
   SmxArgs args{};
   int x_ref = 0, out_ref = 1;
   int nv = 1, grid = 1;
-  hipError_t launch(float *const *ptrs, uint32_t *, float *, hipStream_t stream) override {
+  hipError_t launch(float *const *ptrs, float *, hipStream_t stream) override {
     SmxArgs a = args;
     a.x = ptrs[x_ref];
     a.out = ptrs[out_ref];
@@ -344,7 +344,7 @@ class RowOp final : public Op {
   RowArgs args{};
   uint32_t vec_candidates = 0;
   int threads = 256, grid = 1, slots = kFastSlots;
-  hipError_t launch(float *const *ptrs, uint32_t *, float *, hipStream_t stream) override {
+  hipError_t launch(float *const *ptrs, float *, hipStream_t stream) override {
     RowArgs a = args;
     a.vec_mask = 0;
     for (int j = 0; j < a.n_refs; ++j) {

@@ -171,6 +171,24 @@ def test_random_graphs(seed, fusion):
         np.testing.assert_allclose(out.cpu().numpy(), ref, rtol=RTOL, atol=ATOL)
 
 
+@pytest.mark.parametrize("dim, shape, nan_at", [(-1, (4, 200), (1, 37)), (-1, (3, 5000), (2, 4099)),
+                                                 (0, (3000, 5), (1234, 3)), (0, (7, 6), (5, 2))],
+                         ids=["row", "chunked row", "column, workgroup tree", "column, per thread"])
+def test_max_reductions_propagate_nan(dim, shape, nan_at):
+    # One NaN held by a lane other than 0 must reach the result through every
+    # cross-lane step (the row kernel's RMAX and both reduce kernels), as in
+    # the oracle (np.max) and eager torch.amax.
+    x = torch.randn(*shape)
+    x[nan_at] = float("nan")
+    fn = lambda t: t.amax(dim, keepdim=True) + 0.0 * t
+    graph = imported(fn, (x,))
+    (ref,) = interp.run(graph, x.numpy())
+    out = kiln.compile(fn, (x,), device="cuda")(x).cpu()
+    np.testing.assert_allclose(out.numpy(), ref, rtol=RTOL, atol=ATOL, equal_nan=True)
+    torch.testing.assert_close(out, fn(x), rtol=RTOL, atol=ATOL, equal_nan=True)
+    assert torch.isnan(out).sum() == (shape[1] if dim == -1 else shape[0])
+
+
 def test_autotune_is_correct_and_cached(monkeypatch):
     from kiln.hip.autotune import GPUAutotuner
 
