@@ -204,13 +204,30 @@ int kh_plan_create(const kh_launch *launches, int n_launches, kh_plan **out);
 /* Workspace bytes the plan needs (dense split-K partials, reused by every
  * launch in turn); the caller allocates it and passes it to kh_plan_bind. Its
  * contents need no initialisation: each split-K launch writes all the partials
- * it reads back. */
+ * it reads back. kh_plan_bind accepts workspace = NULL with 0 bytes (no
+ * workspace bound): kh_plan_run then fails with KH_ERR_CAPACITY on a plan that
+ * needs one, and kh_plan_run_noalloc runs it. */
 int kh_plan_workspace_bytes(const kh_plan *plan, size_t *bytes);
 int kh_plan_bind(kh_plan *plan, void *const *consts, int n_consts, void *arena, void *workspace,
                  size_t workspace_bytes);
 /* Run every launch in order on `stream` (GPUExecutable._run, runtime.py:164-179). */
 int kh_plan_run(kh_plan *plan, void *const *inputs, int n_inputs, void *const *outputs, int n_outputs,
                 void *stream);
+/*
+ * kh_plan_run without a caller workspace. No counterpart in the reference: it
+ * is for callers that cannot allocate device memory (code under hipGraph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). The split-K
+ * partials go to a device array of KH_NOALLOC_WORKSPACE_BYTES that the library
+ * holds on each GPU it runs on until the process ends; the call allocates
+ * nothing. The plan is bound as for kh_plan_run (constants and arena; its
+ * workspace argument may be NULL with 0 bytes). Returns KH_ERR_CAPACITY when
+ * kh_plan_workspace_bytes exceeds KH_NOALLOC_WORKSPACE_BYTES. Every call on one
+ * GPU shares that GPU's array and the array keeps the last call's contents:
+ * calls that overlap on one GPU (other streams, other threads) race.
+ */
+#define KH_NOALLOC_WORKSPACE_BYTES (16u << 20)
+int kh_plan_run_noalloc(kh_plan *plan, void *const *inputs, int n_inputs, void *const *outputs, int n_outputs,
+                        void *stream);
 /* Run one launch (per-kernel profiling). */
 int kh_plan_run_one(kh_plan *plan, int index, void *const *inputs, int n_inputs, void *const *outputs,
                     int n_outputs, void *stream);

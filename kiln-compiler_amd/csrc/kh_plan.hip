@@ -12,12 +12,20 @@
 #include <algorithm>
 #include <cstring>
 #include <memory>
+#include <mutex>
 #include <string>
 #include <vector>
 
 #include "kh_common.hpp"
 #include "kh_internal.hpp"
 #include "kiln_hip.h"
+
+// Split-K partials of kh_plan_run_noalloc. Each GPU the library runs on holds
+// its own copy of this array, at its own address, until the process ends. In
+// host code `scratch` names a host-side stand-in, not device memory: kernels
+// and copies get the device address that hipGetSymbolAddress returns for the
+// current device, kept in kh::g_scratch (resolved once per device).
+static __device__ __align__(256) unsigned char scratch[KH_NOALLOC_WORKSPACE_BYTES];
 
 namespace kh {
 namespace {
@@ -33,6 +41,25 @@ int fail(int code, const std::string &msg) {
 
 int hip_fail(hipError_t e, const char *what) {
   return fail(KH_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch[kMaxDevices] = {};
+
+// Device address of `scratch` on `device`, which must be the current device.
+int scratch_address(int device, void **out) {
+  if (device < 0 || device >= kMaxDevices) return fail(KH_ERR_INVALID, "device index beyond the scratch table");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[device]) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    if (p == nullptr) return fail(KH_ERR_HIP, "hipGetSymbolAddress(scratch) returned a null address");
+    g_scratch[device] = p;
+  }
+  *out = g_scratch[device];
+  return KH_OK;
 }
 
 }  // namespace
@@ -165,14 +192,19 @@ int resolve(const kh_plan *p, int i, void *const *inputs, int n_in, void *const 
   return KH_OK;
 }
 
+// Run launches [begin, end) with `workspace` (at least p->ws_needed bytes)
+// holding the split-K partials.
 int run_range(kh_plan *p, int begin, int end, void *const *inputs, int n_in, void *const *outputs, int n_out,
-              hipStream_t stream) {
+              hipStream_t stream, void *workspace) {
   if (!p->bound) return fail(KH_ERR_INVALID, "plan is not bound (call kh_plan_bind)");
+  if (p->ws_needed && !workspace)
+    return fail(KH_ERR_CAPACITY, "plan needs a workspace of " + std::to_string(p->ws_needed) +
+                                     " bytes: bind one (kh_plan_bind) or run it with kh_plan_run_noalloc");
   float *ptrs[KH_MAX_REFS];
   for (int i = begin; i < end; ++i) {
     const int rc = resolve(p, i, inputs, n_in, outputs, n_out, ptrs);
     if (rc != KH_OK) return rc;
-    float *partials = p->ops[i]->partial_floats() ? static_cast<float *>(p->workspace) : nullptr;
+    float *partials = p->ops[i]->partial_floats() ? static_cast<float *>(workspace) : nullptr;
     const hipError_t e = p->ops[i]->launch(ptrs, partials, stream);
     if (e != hipSuccess) return kh::hip_fail(e, p->desc[i].name);
   }
@@ -214,7 +246,8 @@ int kh_init(int device) {
   kh::g_device.lds_bytes = (int)prop.maxSharedMemoryPerMultiProcessor;
   std::snprintf(kh::g_device.arch, sizeof(kh::g_device.arch), "%s", prop.gcnArchName);
   kh::g_device_ready = true;
-  return KH_OK;
+  void *ws = nullptr;
+  return kh::scratch_address(device, &ws);  // once per device, with that device current
 }
 
 int kh_device_info(int *cus, int *lds_bytes, char *arch, int arch_len) {
@@ -279,10 +312,11 @@ int kh_plan_workspace_bytes(const kh_plan *plan, size_t *bytes) {
 int kh_plan_bind(kh_plan *plan, void *const *consts, int n_consts, void *arena, void *workspace,
                  size_t workspace_bytes) {
   if (!plan || n_consts < 0 || (n_consts > 0 && !consts)) return fail(KH_ERR_INVALID, "bad arguments");
-  if (workspace_bytes < plan->ws_needed)
+  const bool none = workspace == nullptr && workspace_bytes == 0;  // kh_plan_run_noalloc callers
+  if (!none && workspace_bytes < plan->ws_needed)
     return fail(KH_ERR_CAPACITY, "workspace of " + std::to_string(workspace_bytes) + " bytes, plan needs " +
                                      std::to_string(plan->ws_needed));
-  if (plan->ws_needed && !workspace) return fail(KH_ERR_INVALID, "plan needs a workspace");
+  if (!none && plan->ws_needed && !workspace) return fail(KH_ERR_INVALID, "plan needs a workspace");
   plan->consts.assign(consts, consts + n_consts);
   plan->arena = arena;
   plan->workspace = workspace;
@@ -295,13 +329,31 @@ int kh_plan_run(kh_plan *plan, void *const *inputs, int n_inputs, void *const *o
                 void *stream) {
   if (!plan) return fail(KH_ERR_INVALID, "null plan");
   return run_range(plan, 0, (int)plan->ops.size(), inputs, n_inputs, outputs, n_outputs,
-                   static_cast<hipStream_t>(stream));
+                   static_cast<hipStream_t>(stream), plan->workspace);
+}
+
+int kh_plan_run_noalloc(kh_plan *plan, void *const *inputs, int n_inputs, void *const *outputs, int n_outputs,
+                        void *stream) {
+  if (!plan) return fail(KH_ERR_INVALID, "null plan");
+  if (plan->ws_needed > KH_NOALLOC_WORKSPACE_BYTES)
+    return fail(KH_ERR_CAPACITY, "plan needs a workspace of " + std::to_string(plan->ws_needed) +
+                                     " bytes, more than kh_plan_run_noalloc's " +
+                                     std::to_string((size_t)KH_NOALLOC_WORKSPACE_BYTES));
+  int device = 0;
+  const hipError_t e = hipGetDevice(&device);
+  if (e != hipSuccess) return kh::hip_fail(e, "hipGetDevice");
+  void *ws = nullptr;
+  const int rc = kh::scratch_address(device, &ws);
+  if (rc != KH_OK) return rc;
+  return run_range(plan, 0, (int)plan->ops.size(), inputs, n_inputs, outputs, n_outputs,
+                   static_cast<hipStream_t>(stream), ws);
 }
 
 int kh_plan_run_one(kh_plan *plan, int index, void *const *inputs, int n_inputs, void *const *outputs,
                     int n_outputs, void *stream) {
   if (!plan || index < 0 || index >= (int)plan->ops.size()) return fail(KH_ERR_INVALID, "bad launch index");
-  return run_range(plan, index, index + 1, inputs, n_inputs, outputs, n_outputs, static_cast<hipStream_t>(stream));
+  return run_range(plan, index, index + 1, inputs, n_inputs, outputs, n_outputs, static_cast<hipStream_t>(stream),
+                   plan->workspace);
 }
 
 int kh_plan_capture(kh_plan *plan, void *const *inputs, int n_inputs, void *const *outputs, int n_outputs) {
@@ -319,7 +371,8 @@ int kh_plan_capture(kh_plan *plan, void *const *inputs, int n_inputs, void *cons
     return kh::hip_fail(e, "hipStreamCreateWithFlags");
   if ((e = hipStreamBeginCapture(plan->capture_stream, hipStreamCaptureModeThreadLocal)) != hipSuccess)
     return kh::hip_fail(e, "hipStreamBeginCapture");
-  const int rc = run_range(plan, 0, (int)plan->ops.size(), inputs, n_inputs, outputs, n_outputs, plan->capture_stream);
+  const int rc = run_range(plan, 0, (int)plan->ops.size(), inputs, n_inputs, outputs, n_outputs, plan->capture_stream,
+                           plan->workspace);
   hipGraph_t g = nullptr;
   e = hipStreamEndCapture(plan->capture_stream, &g);
   if (rc != KH_OK) {

@@ -28,6 +28,7 @@ GEMV_PRO_NONE, GEMV_PRO_LAYERNORM, GEMV_PRO_ATTN = 0, 1, 2
 ATTN_SCALE_NONE, ATTN_SCALE_MUL, ATTN_SCALE_DIV = 0, 1, 2
 ROW_GENERIC, ROW_LAYERNORM, ROW_SOFTMAX = 0, 1, 2
 PREC_FP32, PREC_BF16, PREC_BF16X3 = 0, 1, 2
+NOALLOC_WORKSPACE_BYTES = 16 << 20   # KH_NOALLOC_WORKSPACE_BYTES: kh_plan_run_noalloc's device array
 
 OPCODES = ["mov", "add", "sub", "mul", "div", "max", "min", "neg", "relu", "exp", "tanh", "sigmoid",
            "erf", "gelu_tanh", "gelu_erf", "rsqrt", "sqrt", "rsum", "rmax", "load", "store"]
@@ -98,6 +99,7 @@ def load():
         "kh_plan_workspace_bytes": (ip, [vp, ctypes.POINTER(ctypes.c_size_t)]),
         "kh_plan_bind": (ip, [vp, ctypes.POINTER(vp), ip, vp, vp, ctypes.c_size_t]),
         "kh_plan_run": (ip, [vp, ctypes.POINTER(vp), ip, ctypes.POINTER(vp), ip, vp]),
+        "kh_plan_run_noalloc": (ip, [vp, ctypes.POINTER(vp), ip, ctypes.POINTER(vp), ip, vp]),
         "kh_plan_run_one": (ip, [vp, ip, ctypes.POINTER(vp), ip, ctypes.POINTER(vp), ip, vp]),
         "kh_plan_capture": (ip, [vp, ctypes.POINTER(vp), ip, ctypes.POINTER(vp), ip]),
         "kh_plan_replay": (ip, [vp, vp]),
@@ -118,7 +120,8 @@ def load():
 
 
 EXPORTED = ("kh_version", "kh_abi_sizes", "kh_last_error", "kh_init", "kh_device_info", "kh_gemm_config_count", "kh_gemm_config",
-            "kh_plan_create", "kh_plan_workspace_bytes", "kh_plan_bind", "kh_plan_run", "kh_plan_run_one",
+            "kh_plan_create", "kh_plan_workspace_bytes", "kh_plan_bind", "kh_plan_run", "kh_plan_run_noalloc",
+            "kh_plan_run_one",
             "kh_plan_capture", "kh_plan_replay", "kh_plan_destroy")
 
 
