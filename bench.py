@@ -9,13 +9,17 @@ a step is one call as a user makes it (copy input in, one hipGraph replay of
 the 11-launch plan, clone output out). `value` = ms per step, averaged over
 exactly K steps between synchronisations, after W warm-up steps.
 
-Also reported (outside the timed steps): block latency at 128/512/1024/2048
-tokens with eager PyTorch beside it, the GEMM sweep in TFLOP/s, the fused
+Also reported (outside the timed steps, and run before them so the timed
+steps see a GPU whose clocks are up): block latency at 128/512/1024/2048
+tokens with eager PyTorch and torch.compile(mode="reduce-overhead") beside it
+and the per-call memory of each, the GEMM sweep in TFLOP/s, the fused
 memory-bound ops in GB/s (hot = same buffers, as the reference times them;
 cold = buffers rotated over > 512 MiB so the 256 MiB Infinity Cache cannot
 hold them), the 12-layer stack, the roofline of the block's dominant kernel,
-and the CPU baseline: the C oracle (float64, one thread) timed on this host
-on one block at the headline size.
+and the CPU baseline: eager PyTorch CPU fp32 running the headline block on
+this host at one thread and at all the cores the process may use (best of 3,
+the reference's bench_block.py method), with the C oracle (float64, one
+thread) as a separately labelled line.
 """
 
 from __future__ import annotations
@@ -52,6 +56,7 @@ def parse():
     p.add_argument("--quick", action="store_true", help="headline, roofline and CPU baseline only")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-autotune", action="store_true")
+    p.add_argument("--no-inductor", action="store_true", help="skip the torch.compile column of the block sweep")
     p.add_argument("--traffic-probe", metavar="JSON",
                    help="run only the dispatch sequence the rocprofv3 --pmc traffic passes count "
                         "(a copy of known size, then every launch of the headline plan) and write its map to JSON")
@@ -93,6 +98,36 @@ def ms_per_call(fn, rounds=5, min_time=0.05):
     one = events_ms(fn, 1)
     calls = max(1, int(min_time * 1e3 / max(one, 1e-3)))
     return min(events_ms(fn, calls) for _ in range(rounds))
+
+
+def peak_mib(fn, *xs):
+    """MiB allocated by one call beyond what was allocated before it (the
+    reference's per-call peak, benchmarks/bench_gpu.py:91-102)."""
+    import torch
+
+    with torch.no_grad():
+        fn(*xs)
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats()
+        base = torch.cuda.memory_allocated()
+        fn(*xs)
+        torch.cuda.synchronize()
+    return (torch.cuda.max_memory_allocated() - base) / 2**20
+
+
+def inductor_ms(fn, x, mode):
+    """ms per call of torch.compile(fn, mode=mode) (Inductor's Triton kernels;
+    "reduce-overhead" replays them as a graph), or None when it cannot run."""
+    import torch
+
+    try:
+        compiled = torch.compile(fn, mode=mode)
+        with torch.no_grad():
+            torch.testing.assert_close(compiled(x), fn(x), rtol=1e-3, atol=1e-4)
+            return ms_per_call(lambda: compiled(x))
+    except Exception as err:  # noqa: BLE001 - a missing or failing compiler only drops the column
+        log(f"  torch.compile unavailable: {str(err).splitlines()[0][:120]}")
+        return None
 
 
 # -- workloads ------------------------------------------------------------------------------
@@ -305,7 +340,12 @@ def committed_traffic(T, launch):
     return None
 
 
-def block_sweep(tokens, autotune):
+def block_sweep(tokens, autotune, inductor=True):
+    """Per T: kiln end to end (copy in, replay, clone out) against eager
+    PyTorch-ROCm and torch.compile(mode="reduce-overhead"), and memory per
+    call as the reference reports it (benchmarks/bench_gpu.py:163-195): kiln =
+    its planned arena + what a call allocates, eager = what a call allocates
+    (weights excluded on both sides)."""
     import torch
 
     import kiln
@@ -320,6 +360,9 @@ def block_sweep(tokens, autotune):
             e_ms = ms_per_call(lambda: model(x))
             c._exe.replay_only()
             replay_ms = min(events_ms(c._exe.replay_only, 20) for _ in range(5))
+        kiln_mib = c.report.arena_bytes / 2**20 + peak_mib(c, x)
+        eager_mib = peak_mib(model, x)
+        ind_ms = inductor_ms(model, x, "reduce-overhead") if inductor else None
         # allow_tf32 (three-pass bf16 GEMMs): reported beside, never the headline
         ct = kiln.compile(model, (x,), device="cuda", autotune=autotune, allow_tf32=True)
         with torch.no_grad():
@@ -329,11 +372,14 @@ def block_sweep(tokens, autotune):
             assert tf_err <= 5e-5, f"block T={T} allow_tf32: error {tf_err:.2e} of the output scale"
             tf_ms = ms_per_call(lambda: ct(x))
         out[str(T)] = {"kiln_ms": round(k_ms, 4), "eager_ms": round(e_ms, 4), "replay_ms": round(replay_ms, 4),
+                       "inductor_ms": round(ind_ms, 4) if ind_ms else None,
                        "speedup": round(e_ms / k_ms, 3), "tflops": round(block_flops(T) / k_ms / 1e9, 2),
                        "arena_mib": round(c.report.arena_bytes / 2**20, 2),
+                       "kiln_mib": round(kiln_mib, 2), "eager_mib": round(eager_mib, 2),
                        "allow_tf32_ms": round(tf_ms, 4), "allow_tf32_error_of_scale": float(f"{tf_err:.2e}")}
         log(f"block T={T}: kiln {k_ms:.4f} ms (replay {replay_ms:.4f}), eager {e_ms:.4f} ms, "
-            f"allow_tf32 {tf_ms:.4f} ms")
+            f"inductor {ind_ms if ind_ms else float('nan'):.4f} ms, allow_tf32 {tf_ms:.4f} ms, "
+            f"MiB kiln {kiln_mib:.1f} / eager {eager_mib:.1f}")
     return out
 
 
@@ -537,23 +583,83 @@ def stack_bench(autotune):
     return out
 
 
-def cpu_baseline(T):
-    """The C oracle (float64, single thread) on one block at the headline size."""
-    import numpy as np
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_ms_per_call(fn, x, min_time=1.0):
+    """The reference's CPU timing (benchmarks/bench_block.py:41-54): one
+    warm-up call, as many calls as fit in min_time / 3, then the best of 3
+    rounds of that many calls."""
     import torch
 
-    import oracle
+    with torch.no_grad():
+        fn(x)
+        start, calls = time.perf_counter(), 0
+        while time.perf_counter() - start < min_time / 3:
+            fn(x)
+            calls += 1
+        calls = max(calls, 1)
+        best = float("inf")
+        for _ in range(3):
+            start = time.perf_counter()
+            for _ in range(calls):
+                fn(x)
+            best = min(best, (time.perf_counter() - start) / calls)
+    return best * 1e3
+
+
+def cpu_baseline(T, oracle_line=True):
+    """Eager PyTorch CPU fp32 on the headline block (same weights and input as
+    the GPU run) at 1 thread (the reference's convention,
+    benchmarks/bench_block.py:61) and at every core this process may use
+    (capped by OMP_NUM_THREADS, the box's CPU share). The reference's own CPU
+    path (MLIR -> LLVM JIT) cannot be built here: no MLIR bindings, an empty
+    LLVM pin, a network-only build script. The C oracle (float64, one thread)
+    is timed once as a separately labelled line."""
+    import torch
+
     from models.transformer import Block, gpt2_init_
 
+    torch.manual_seed(0)
     model = gpt2_init_(Block(768, 12, T), seed=0).eval()
-    x = torch.randn(T, 768, generator=torch.Generator().manual_seed(1)).numpy()
-    params = {k: v.numpy() for k, v in model.state_dict().items()}
-    oracle.lib()
-    t0 = time.perf_counter()
-    oracle.block(x, params, 12)
-    dt = time.perf_counter() - t0
-    return {"value": round(dt * 1e3, 1), "unit": "ms", "cores": 1, "kind": "port",
-            "sample": f"one full GPT-2 block forward at T={T} by oracle/kiln_oracle.c (float64, 1 thread)"}
+    x = torch.randn(T, 768, generator=torch.Generator().manual_seed(1))
+    cores = len(os.sched_getaffinity(0))
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        cores = min(cores, int(os.environ["OMP_NUM_THREADS"]))
+    before = torch.get_num_threads()
+    try:
+        torch.set_num_threads(1)
+        one = cpu_ms_per_call(model, x)
+        torch.set_num_threads(cores)
+        many = cpu_ms_per_call(model, x)
+    finally:
+        torch.set_num_threads(before)
+    log(f"cpu baseline: eager PyTorch CPU fp32 block T={T}: {one:.1f} ms at 1 thread, {many:.1f} ms at {cores}")
+    out = {"value": round(many, 2), "unit": "ms", "cores": cores, "kind": "port",
+           "impl": "eager PyTorch CPU fp32 (torch " + torch.__version__ + ")",
+           "cpu_model": cpu_model(),
+           "sample": f"one full GPT-2-small block forward at T={T} (the headline workload, same seeded weights and "
+                     f"input), best of 3 rounds after calibration (reference benchmarks/bench_block.py:41-54)",
+           "single_thread": {"value": round(one, 2), "unit": "ms", "cores": 1},
+           "reference_cpu_path": "unavailable: MLIR Python bindings absent, LLVM pin empty, network-only build"}
+    if oracle_line:
+        import oracle
+
+        params = {k: v.numpy() for k, v in model.state_dict().items()}
+        oracle.lib()
+        t0 = time.perf_counter()
+        oracle.block(x.numpy(), params, 12)
+        out["oracle_port"] = {"value": round((time.perf_counter() - t0) * 1e3, 1), "unit": "ms", "cores": 1,
+                              "impl": "oracle/kiln_oracle.c, float64 naive loops (the parity checker)"}
+    return out
 
 
 def main():
@@ -576,17 +682,18 @@ def main():
         return
     torch.manual_seed(0)
     info = kl.device_info() if kl.load() else {}
-    compiled, model, x, ms, err = headline(args)
-    log(f"headline: block T={args.tokens}: {ms:.4f} ms/step over {args.steps} steps (max err {err:.2e})")
-    roofline, prof = dominant_kernel_roofline(compiled, x, args.tokens)
-    log("per-launch ms: " + ", ".join(f"{n}={t:.4f}" for n, t in prof))
     extra = {}
     if not args.quick:
-        extra["block"] = block_sweep([128, 512, 1024, 2048], not args.no_autotune)
+        # untimed sections first: the headline's timed steps then run on a warm GPU
+        extra["block"] = block_sweep([128, 512, 1024, 2048], not args.no_autotune, not args.no_inductor)
         extra["gemm"] = gemm_sweep(not args.no_autotune)
         extra["linear_gelu"] = linear_gelu(not args.no_autotune)
         extra["fused_ops"] = fused_ops()
         extra["stack"] = stack_bench(not args.no_autotune)
+    compiled, model, x, ms, err = headline(args)
+    log(f"headline: block T={args.tokens}: {ms:.4f} ms/step over {args.steps} steps (max err {err:.2e})")
+    roofline, prof = dominant_kernel_roofline(compiled, x, args.tokens)
+    log("per-launch ms: " + ", ".join(f"{n}={t:.4f}" for n, t in prof))
     cpu = None if args.no_cpu_baseline else cpu_baseline(args.tokens)
     line = {
         "metric": "GPT-2 block latency ms @128-2048 tok; GEMM TFLOP/s; fused-op GB/s (1 GPU)",
