@@ -1,28 +1,29 @@
-"""Kiln graph IR: an SSA dataflow graph over statically shaped f32 tensors.
+"""The graph IR this build compiles: SSA values over static-shape f32 tensors.
 
-Contract-compatible counterpart of the reference IR (kiln/ir/core.py:28-239):
-the same classes, fields and query/mutation methods, because every pass and
-the HIP backend's lowering consume exactly these objects.
+A ``Graph`` is an ordered list of ``Node``s. Every node yields exactly one
+``Value``; graph arguments are Values without a node. Nothing in the IR says
+how a tensor is laid out: buffer assignment later records ``buffer``,
+``offset`` and ``strides`` as node attributes, and fusion records ``kernel``
+(the name of the ``Kernel`` the node belongs to), so one text form (printer /
+parser) shows the graph at every stage.
 
-  * Every node produces one value; values are immutable and carry no layout.
-  * Layout (strides, aliasing) is decided late, by buffer assignment.
-  * Passes annotate nodes with attributes (``kernel``, ``buffer``, ``offset``,
-    ``strides``), so one printer/parser covers every stage.
+The interface is Kiln's (class, field and method names of the reference's
+kiln/ir/core.py:28-239), because the passes, the text form and the HIP
+lowering are all written against it; the implementation is this build's own.
 """
 
 from __future__ import annotations
 
+from collections import defaultdict
 from dataclasses import dataclass, field
 from math import prod
+from typing import NamedTuple
 
 import numpy as np
 
-ELEMENT_BYTES = 4  # every Kiln tensor is f32
 
-
-@dataclass(frozen=True)
-class TensorType:
-    """Static shape + element type (reference: kiln/ir/core.py:28-46)."""
+class TensorType(NamedTuple):
+    """Static shape and element type (only "f32" is produced)."""
 
     shape: tuple
     dtype: str = "f32"
@@ -37,37 +38,31 @@ class TensorType:
 
     @property
     def nbytes(self) -> int:
-        return self.numel * ELEMENT_BYTES
+        return 4 * self.numel
 
-    def __str__(self):
-        return "%s[%s]" % (self.dtype, ", ".join(str(d) for d in self.shape))
+    def __str__(self) -> str:
+        return self.dtype + "[" + ", ".join(map(str, self.shape)) + "]"
 
 
 class Value:
-    """An SSA value: a graph argument (``node is None``) or a node's result."""
+    """An SSA value. ``node`` is the producer (None for a graph argument);
+    ``name`` is kept for arguments and used as a printing hint."""
 
     __slots__ = ("type", "node", "name")
 
-    def __init__(self, type: TensorType, node=None, name=None):
-        self.type = type
-        self.node = node
-        self.name = name
+    def __init__(self, type: TensorType, node: "Node | None" = None, name: str | None = None):
+        self.type, self.node, self.name = type, node, name
 
-    @property
-    def shape(self):
-        return self.type.shape
+    shape = property(lambda self: self.type.shape)
+    is_arg = property(lambda self: self.node is None)
 
-    @property
-    def is_arg(self) -> bool:
-        return self.node is None
-
-    def __repr__(self):
-        src = "arg" if self.node is None else self.node.op
-        return f"<Value {self.name or '?'}: {self.type} from {src}>"
+    def __repr__(self) -> str:
+        made_by = "arg" if self.node is None else self.node.op
+        return f"<Value {self.name or '?'}: {self.type} from {made_by}>"
 
 
 class Node:
-    """One operation; owns its single result ``out``."""
+    """One operation; ``out`` is the Value it defines."""
 
     __slots__ = ("op", "inputs", "attrs", "out")
 
@@ -77,14 +72,14 @@ class Node:
         self.attrs = dict(attrs)
         self.out = Value(out_type, self)
 
-    def __repr__(self):
+    def __repr__(self) -> str:
         return f"<Node {self.op} -> {self.out.type}>"
 
 
 @dataclass(eq=False)
 class Kernel:
-    """A fusion group compiled into one device program (kind: elementwise |
-    reduction | matmul | copy)."""
+    """A fusion group, compiled as one device program. ``kind`` is
+    elementwise, reduction, matmul or copy."""
 
     name: str
     kind: str
@@ -93,160 +88,172 @@ class Kernel:
 
 
 class Graph:
-    """The whole program: arguments, nodes in program order, results,
-    kernel partition and constant data (reference: kiln/ir/core.py:95-214)."""
+    """Arguments (``args`` with per-argument ``arg_attrs``; ``param = name``
+    marks a weight whose data is in ``constants``), ``nodes`` in program
+    order, ``results``, graph ``attrs`` (``arena_bytes`` after planning), the
+    ``kernels`` partition and the named constant arrays."""
 
     def __init__(self, name: str = "forward"):
         self.name = name
-        self.args: list = []
-        self.arg_attrs: list = []
-        self.nodes: list = []
-        self.results: list = []
-        self.attrs: dict = {}
-        self.kernels: list = []
-        self.constants: dict = {}
+        self.args = []
+        self.arg_attrs = []
+        self.nodes = []
+        self.results = []
+        self.attrs = {}
+        self.kernels = []
+        self.constants = {}
 
-    # construction ---------------------------------------------------------
+    # -- building -------------------------------------------------------------------
 
     def add_arg(self, type: TensorType, name: str, **attrs) -> Value:
-        v = Value(type, None, name)
-        self.args.append(v)
-        self.arg_attrs.append(dict(attrs))
-        return v
+        arg = Value(type, None, name)
+        self.args.append(arg)
+        self.arg_attrs.append(attrs)
+        return arg
 
-    def add_node(self, op, inputs, attrs=None, out_type=None, index=None) -> Value:
-        """Append (or insert at ``index``) a node; infers the type if not given."""
-        from kiln.ir.ops import infer_type
-
-        attrs = dict(attrs or {})
+    def add_node(self, op: str, inputs, attrs=None, out_type=None, index=None) -> Value:
+        """New node defining a new value; the type is inferred from the op
+        table unless given. ``index`` inserts it before that position."""
+        inputs = list(inputs)
+        attrs = {} if attrs is None else dict(attrs)
         if out_type is None:
+            from kiln.ir.ops import infer_type
+
             out_type = infer_type(op, [v.type for v in inputs], attrs)
         node = Node(op, inputs, attrs, out_type)
-        if index is None:
-            self.nodes.append(node)
-        else:
-            self.nodes.insert(index, node)
+        self.nodes.insert(len(self.nodes) if index is None else index, node)
         return node.out
 
     def constant(self, array, name: str, index=None) -> Value:
-        """A named tensor constant; its data goes to ``self.constants`` under a
-        unique name (``name``, ``name_1``, ...)."""
+        """A tensor constant. Its data is stored under ``name``, or under
+        ``name_<k>`` with the smallest k that is still free."""
         data = np.ascontiguousarray(array, dtype=np.float32)
-        unique, n = name, 0
-        while unique in self.constants:
-            n += 1
-            unique = f"{name}_{n}"
-        self.constants[unique] = data
-        return self.add_node("const", [], {"name": unique}, TensorType(tuple(data.shape)), index)
+        key, k = name, 0
+        while key in self.constants:
+            k += 1
+            key = f"{name}_{k}"
+        self.constants[key] = data
+        return self.add_node("const", [], {"name": key}, TensorType(tuple(data.shape)), index)
 
     def scalar(self, value: float, index=None) -> Value:
         return self.add_node("const", [], {"value": float(value)}, TensorType(()), index)
 
-    # queries ----------------------------------------------------------------
+    # -- questions ------------------------------------------------------------------
 
     def users(self) -> dict:
-        """Value -> nodes that read it, in program order."""
-        out: dict = {}
-        for n in self.nodes:
-            for v in n.inputs:
-                out.setdefault(v, []).append(n)
-        return out
+        """{value: [nodes reading it, in program order]}; a node that reads a
+        value twice is listed twice."""
+        readers = defaultdict(list)
+        for node in self.nodes:
+            for v in node.inputs:
+                readers[v].append(node)
+        return dict(readers)
 
     def is_const(self, v: Value) -> bool:
         return v.node is not None and v.node.op == "const"
 
     def is_scalar_const(self, v: Value) -> bool:
-        return self.is_const(v) and v.type.rank == 0
+        return self.is_const(v) and not v.type.shape
 
-    def const_data(self, v: Value):
-        node = v.node
-        assert node is not None and node.op == "const", v
-        if "value" in node.attrs:
-            return np.asarray(node.attrs["value"], dtype=np.float32)
-        return self.constants[node.attrs["name"]]
+    def const_data(self, v: Value) -> np.ndarray:
+        if not self.is_const(v):
+            raise ValueError(f"{v} is not a constant")
+        attrs = v.node.attrs
+        if "value" in attrs:
+            return np.asarray(attrs["value"], dtype=np.float32)
+        return self.constants[attrs["name"]]
 
     def kernel_of(self, node: Node):
-        name = node.attrs.get("kernel")
-        return next((k for k in self.kernels if k.name == name), None)
+        wanted = node.attrs.get("kernel")
+        for kernel in self.kernels:
+            if kernel.name == wanted:
+                return kernel
+        return None
 
-    # mutation ----------------------------------------------------------------
+    # -- rewriting ------------------------------------------------------------------
 
     def replace_all_uses(self, old: Value, new: Value):
-        for n in self.nodes:
-            if any(v is old for v in n.inputs):
-                n.inputs = [new if v is old else v for v in n.inputs]
-        self.results = [new if v is old else v for v in self.results]
+        for node in self.nodes:
+            if old in node.inputs:
+                node.inputs = [new if v is old else v for v in node.inputs]
+        if old in self.results:
+            self.results = [new if v is old else v for v in self.results]
 
     def remove_dead(self) -> int:
-        """Drop nodes that no result depends on, and constant data nobody names.
-        Returns the number of nodes removed."""
-        needed = set(self.results)
-        keep = []
-        for n in reversed(self.nodes):
-            if n.out in needed:
-                keep.append(n)
-                needed.update(n.inputs)
-        removed = len(self.nodes) - len(keep)
-        keep.reverse()
-        self.nodes = keep
-        names = {n.attrs["name"] for n in keep if n.op == "const" and "name" in n.attrs}
-        names.update(a["param"] for a in self.arg_attrs if "param" in a)
-        self.constants = {k: d for k, d in self.constants.items() if k in names}
-        return removed
+        """Delete nodes no result depends on, then constant arrays that no
+        const node or param argument names. Returns the nodes deleted."""
+        live = set()
+        pending = [v for v in self.results if v.node is not None]
+        while pending:
+            node = pending.pop().node
+            if node in live:
+                continue
+            live.add(node)
+            pending.extend(v for v in node.inputs if v.node is not None and v.node not in live)
+        before = len(self.nodes)
+        self.nodes = [n for n in self.nodes if n in live]
+        named = {n.attrs["name"] for n in self.nodes if n.op == "const" and "name" in n.attrs}
+        named.update(a["param"] for a in self.arg_attrs if "param" in a)
+        for key in [k for k in self.constants if k not in named]:
+            del self.constants[key]
+        return before - len(self.nodes)
 
     def toposort(self):
-        """Stable topological re-ordering of ``nodes`` (iterative DFS)."""
-        members = set(self.nodes)
-        done, order = set(), []
+        """Order nodes so every operand's producer comes first. Stable: a node
+        keeps its place unless a producer listed after it must move ahead, in
+        which case that producer (and its own late producers, recursively, in
+        operand order) is emitted right before the first node that needs it."""
+        position = {n: i for i, n in enumerate(self.nodes)}
+        placed, order = set(), []
         for root in self.nodes:
-            if root in done:
-                continue
-            stack = [(root, iter(root.inputs))]
-            done.add(root)
+            # explicit stack of (node, index of the next operand to look at)
+            stack = [[root, 0]]
             while stack:
-                node, it = stack[-1]
-                pushed = False
-                for v in it:
-                    p = v.node
-                    if p is not None and p in members and p not in done:
-                        done.add(p)
-                        stack.append((p, iter(p.inputs)))
-                        pushed = True
-                        break
-                if not pushed:
+                frame = stack[-1]
+                node, i = frame
+                if node in placed:
                     stack.pop()
-                    order.append(node)
+                    continue
+                if i < len(node.inputs):
+                    frame[1] += 1
+                    producer = node.inputs[i].node
+                    if producer is not None and producer in position and producer not in placed:
+                        stack.append([producer, 0])
+                    continue
+                placed.add(node)
+                order.append(node)
+                stack.pop()
         self.nodes = order
 
-    def __str__(self):
+    def __str__(self) -> str:
         from kiln.ir.printer import print_graph
 
         return print_graph(self)
 
 
 def verify(graph: Graph):
-    """SSA dominance, known ops, const data present, types equal inference
-    (reference: kiln/ir/core.py:217-239). Raises ValueError."""
+    """Raise ValueError unless the graph is well formed: every op is known,
+    every operand is defined before its use, const nodes have their data,
+    node types agree with the op table and every result is defined."""
     from kiln.ir.ops import OPS, infer_type
 
-    defined = set(graph.args)
-    for n in graph.nodes:
-        if n.op not in OPS:
-            raise ValueError(f"unknown op '{n.op}'")
-        for v in n.inputs:
-            if v not in defined:
-                raise ValueError(f"{n.op}: operand used before definition: {v}")
-        if n.op == "const":
-            if "value" in n.attrs:
-                if n.out.type.rank != 0:
-                    raise ValueError("const with 'value' must be a scalar (f32[])")
-            elif n.attrs.get("name") not in graph.constants:
-                raise ValueError(f"const refers to missing data '{n.attrs.get('name')}'")
-        else:
-            want = infer_type(n.op, [v.type for v in n.inputs], n.attrs)
-            if want != n.out.type:
-                raise ValueError(f"{n.op}: type {n.out.type} does not match inferred {want}")
-        defined.add(n.out)
+    seen = set(graph.args)
+    for node in graph.nodes:
+        if node.op not in OPS:
+            raise ValueError(f"unknown op '{node.op}'")
+        missing = [v for v in node.inputs if v not in seen]
+        if missing:
+            raise ValueError(f"{node.op}: operand used before definition: {missing[0]}")
+        if node.op != "const":
+            inferred = infer_type(node.op, [v.type for v in node.inputs], node.attrs)
+            if inferred != node.out.type:
+                raise ValueError(f"{node.op}: type {node.out.type} does not match inferred {inferred}")
+        elif "value" in node.attrs:
+            if node.out.type.shape:
+                raise ValueError("const with 'value' must be a scalar (f32[])")
+        elif node.attrs.get("name") not in graph.constants:
+            raise ValueError(f"const refers to missing data '{node.attrs.get('name')}'")
+        seen.add(node.out)
     for v in graph.results:
-        if v not in defined:
+        if v not in seen:
             raise ValueError(f"result {v} is not defined in the graph")

@@ -1,15 +1,25 @@
-"""Parser for the textual Kiln IR printed by kiln/ir/printer.py.
+"""Reader for the text form that kiln/ir/printer.py writes (Kiln's grammar,
+the reference's kiln/ir/parser.py:17-234)::
 
-Accepts the reference's grammar (kiln/ir/parser.py:17-234). Constants or
-``param`` arguments written without data get deterministic data derived from
-their name, N(0, 1) * 0.1 drawn from ``numpy.random.default_rng(crc32(name))``
-(the same rule as the reference's parser.py:225-227, so hand-written IR
-compiles to the same numbers in both).
+    graph   := 'graph' @name '(' [arg {',' arg}] ')' '->' '(' [type {',' type}] ')'
+               ['attributes' attrs] '{' {kernel} {node} 'return' [%v {',' %v}] '}'
+    arg     := %name ':' type [attrs]
+    kernel  := 'kernel' @name kind [attrs]
+    node    := %name '=' op [%v {',' %v}] [attrs] ':' type
+    type    := dtype '[' [int {',' int}] ']'
+    attrs   := '{' [key '=' value {',' key '=' value}] '}'
+
+``//`` starts a comment. A ``param`` argument or named ``const`` whose data
+is not supplied gets N(0, 1) * 0.1 data drawn from
+``numpy.random.default_rng(zlib.crc32(name))``: the rule Kiln's own parser
+uses (reference parser.py:225-227), so hand-written IR holds the same numbers
+in both.
+
+This reader is a character scanner feeding a recursive-descent parser.
 """
 
 from __future__ import annotations
 
-import re
 import zlib
 
 import numpy as np
@@ -21,195 +31,269 @@ class ParseError(ValueError):
     pass
 
 
-_LEX = re.compile(r"""
-    (?P<ws>\s+) | (?P<comment>//[^\n]*)
-  | (?P<value>%[A-Za-z0-9_.]+) | (?P<symbol>@[A-Za-z0-9_.]+)
-  | (?P<string>"(?:[^"\\]|\\.)*")
-  | (?P<number>[-+]?(?:\d+\.\d*(?:[eE][-+]?\d+)?|\d+[eE][-+]?\d+|\d+|inf|nan)(?![A-Za-z_]))
-  | (?P<arrow>->) | (?P<ident>[A-Za-z_][A-Za-z0-9_.]*) | (?P<punct>[{}()\[\],:=])
-""", re.VERBOSE)
-
-
-def _lex(text):
-    toks, pos, line = [], 0, 1
-    while pos < len(text):
-        m = _LEX.match(text, pos)
-        if m is None:
-            raise ParseError(f"line {line}: unexpected character {text[pos]!r}")
-        kind = m.lastgroup
-        if kind not in ("ws", "comment"):
-            toks.append((kind, m.group(), line))
-        line += m.group().count("\n")
-        pos = m.end()
-    toks.append(("eof", None, line))
-    return toks
-
-
 def fake_data(name: str, shape) -> np.ndarray:
     rng = np.random.default_rng(zlib.crc32(name.encode()))
     return rng.standard_normal(shape).astype(np.float32) * 0.1
 
 
-class _Reader:
-    def __init__(self, text):
-        self.toks = _lex(text)
-        self.pos = 0
+_PUNCT = set("{}()[],:=")
+_NAME_CHARS = set("abcdefghijklmnopqrstuvwxyzABCDEFGHIJKLMNOPQRSTUVWXYZ0123456789_.")
 
-    @property
-    def tok(self):
-        return self.toks[self.pos]
 
-    def take(self):
-        t = self.toks[self.pos]
-        self.pos += 1
-        return t
+class _Token:
+    __slots__ = ("kind", "text", "line")
 
-    def need(self, text=None, kind=None):
-        k, v, line = self.take()
-        if (text is not None and v != text) or (kind is not None and k != kind):
-            raise ParseError(f"line {line}: expected {text if text is not None else kind!r}, got {v!r}")
-        return v
+    def __init__(self, kind, text, line):
+        self.kind, self.text, self.line = kind, text, line
 
-    def maybe(self, text):
-        if self.tok[1] == text:
-            self.pos += 1
+
+def _scan(text: str) -> list:
+    """Tokens: value (%x), symbol (@x), string, number, ident, '->' and the
+    single punctuation characters; ends with an 'eof' token."""
+    out, i, line, n = [], 0, 1, len(text)
+    while i < n:
+        c = text[i]
+        if c == "\n":
+            line += 1
+            i += 1
+        elif c.isspace():
+            i += 1
+        elif text.startswith("//", i):
+            while i < n and text[i] != "\n":
+                i += 1
+        elif c in "%@":
+            j = i + 1
+            while j < n and text[j] in _NAME_CHARS:
+                j += 1
+            if j == i + 1:
+                raise ParseError(f"line {line}: '{c}' without a name")
+            out.append(_Token("value" if c == "%" else "symbol", text[i:j], line))
+            i = j
+        elif c == '"':
+            j = i + 1
+            while j < n and text[j] != '"':
+                j += 2 if text[j] == "\\" else 1
+            if j >= n:
+                raise ParseError(f"line {line}: unterminated string")
+            out.append(_Token("string", text[i:j + 1], line))
+            i = j + 1
+        elif text.startswith("->", i):
+            out.append(_Token("arrow", "->", line))
+            i += 2
+        elif c in _PUNCT:
+            out.append(_Token("punct", c, line))
+            i += 1
+        elif c.isdigit() or c in "+-" or c.isalpha() or c == "_":
+            j = i + 1
+            while j < n and (text[j] in _NAME_CHARS or (text[j] in "+-" and text[j - 1] in "eE")):
+                j += 1
+            word = text[i:j]
+            out.append(_Token(_classify(word, line), word, line))
+            i = j
+        else:
+            raise ParseError(f"line {line}: unexpected character {c!r}")
+    out.append(_Token("eof", None, line))
+    return out
+
+
+def _classify(word: str, line: int) -> str:
+    body = word.lstrip("+-")
+    if body in ("inf", "nan"):
+        return "number"
+    if body[:1].isdigit():
+        try:
+            float(word)
+        except ValueError:
+            raise ParseError(f"line {line}: bad number {word!r}") from None
+        return "number"
+    if word[0] in "+-":
+        raise ParseError(f"line {line}: unexpected {word!r}")
+    return "ident"
+
+
+def _number(word: str):
+    body = word.lstrip("+-")
+    if body.isdigit():
+        return int(word)
+    return float(word)
+
+
+class _Parser:
+    def __init__(self, text: str):
+        self.tokens = _scan(text)
+        self.i = 0
+
+    # -- token helpers ------------------------------------------------------------------
+
+    def peek(self) -> _Token:
+        return self.tokens[self.i]
+
+    def next(self) -> _Token:
+        tok = self.tokens[self.i]
+        self.i += 1
+        return tok
+
+    def fail(self, what, tok=None):
+        tok = tok or self.peek()
+        raise ParseError(f"line {tok.line}: expected {what}, got {tok.text!r}")
+
+    def expect(self, text):
+        tok = self.next()
+        if tok.text != text or tok.kind == "string":
+            self.fail(repr(text), tok)
+        return tok
+
+    def expect_kind(self, kind):
+        tok = self.next()
+        if tok.kind != kind:
+            self.fail(kind, tok)
+        return tok.text
+
+    def accept(self, text) -> bool:
+        tok = self.peek()
+        if tok.text == text and tok.kind in ("punct", "arrow", "ident"):
+            self.i += 1
             return True
         return False
 
-    def comma_list(self, close, item):
+    def sequence(self, close, item) -> list:
+        """item {',' item} close (possibly empty)."""
         items = []
-        if self.maybe(close):
+        if self.accept(close):
             return items
-        while True:
+        items.append(item())
+        while not self.accept(close):
+            self.expect(",")
             items.append(item())
-            if self.maybe(close):
-                return items
-            self.need(",")
+        return items
 
-    # attributes / types ---------------------------------------------------------
+    # -- pieces ---------------------------------------------------------------------------
 
-    def value_attr(self):
-        k, v, line = self.take()
-        if k == "number":
-            is_float = any(c in v for c in ".eEn") or v.lstrip("+-") == "inf"
-            return float(v) if is_float else int(v)
-        if k == "string":
-            return bytes(v[1:-1], "utf-8").decode("unicode_escape")
-        if k == "ident" and v in ("true", "false"):
-            return v == "true"
-        if v == "[":
-            return self.comma_list("]", self.value_attr)
-        if v == "{":
-            self.pos -= 1
-            return self.attr_dict()
-        raise ParseError(f"line {line}: bad attribute value {v!r}")
-
-    def attr_dict(self):
-        if self.tok[1] != "{":
-            return {}
-        self.take()
-        out = {}
-
-        def entry():
-            key = self.need(kind="ident")
-            self.need("=")
-            out[key] = self.value_attr()
-
-        self.comma_list("}", entry)
-        return out
-
-    def tensor_type(self):
-        dtype = self.need(kind="ident")
-        self.need("[")
-        dims = self.comma_list("]", lambda: int(self.need(kind="number")))
+    def type(self) -> TensorType:
+        dtype = self.expect_kind("ident")
+        self.expect("[")
+        dims = self.sequence("]", lambda: int(self.expect_kind("number")))
         return TensorType(tuple(dims), dtype)
 
-    # graph --------------------------------------------------------------------------
+    def attr_value(self):
+        tok = self.next()
+        if tok.kind == "number":
+            return _number(tok.text)
+        if tok.kind == "string":
+            return tok.text[1:-1].encode("utf-8").decode("unicode_escape")
+        if tok.kind == "ident" and tok.text in ("true", "false"):
+            return tok.text == "true"
+        if tok.text == "[":
+            return self.sequence("]", self.attr_value)
+        if tok.text == "{":
+            self.i -= 1
+            return self.attrs()
+        self.fail("an attribute value", tok)
+
+    def attrs(self) -> dict:
+        out = {}
+        if not self.accept("{"):
+            return out
+
+        def entry():
+            key = self.expect_kind("ident")
+            self.expect("=")
+            out[key] = self.attr_value()
+
+        self.sequence("}", entry)
+        return out
+
+    def operand(self, names):
+        tok = self.next()
+        if tok.kind != "value":
+            self.fail("a value", tok)
+        if tok.text not in names:
+            raise ParseError(f"line {tok.line}: use of undefined value {tok.text}")
+        return names[tok.text]
+
+    def operands(self, names) -> list:
+        found = []
+        if self.peek().kind == "value":
+            found.append(self.operand(names))
+            while self.accept(","):
+                found.append(self.operand(names))
+        return found
+
+    # -- the graph ---------------------------------------------------------------------------
 
     def graph(self) -> Graph:
-        self.need("graph")
-        g = Graph(self.need(kind="symbol")[1:])
-        env = {}
+        self.expect("graph")
+        graph = Graph(self.expect_kind("symbol")[1:])
+        names = {}
 
-        def arg():
-            vname = self.need(kind="value")
-            self.need(":")
-            t = self.tensor_type()
-            at = self.attr_dict()
-            env[vname] = g.add_arg(t, at.get("param", vname[1:]), **at)
+        def argument():
+            label = self.expect_kind("value")
+            self.expect(":")
+            t = self.type()
+            attrs = self.attrs()
+            names[label] = graph.add_arg(t, attrs.get("param", label[1:]), **attrs)
 
-        self.need("(")
-        self.comma_list(")", arg)
-        self.need("->")
-        self.need("(")
-        self.comma_list(")", self.tensor_type)
-        if self.maybe("attributes"):
-            g.attrs = self.attr_dict()
-        self.need("{")
-        while True:
-            k, v, line = self.tok
-            if v == "kernel":
-                self.take()
-                kname = self.need(kind="symbol")[1:]
-                kkind = self.need(kind="ident")
-                g.kernels.append(Kernel(kname, kkind, [], self.attr_dict()))
-            elif v == "return":
-                self.take()
-                res = []
-                if self.tok[0] == "value":
-                    res.append(self.lookup(env))
-                    while self.maybe(","):
-                        res.append(self.lookup(env))
-                g.results = res
-                self.need("}")
-                break
-            elif k == "value":
-                self.node(g, env)
-            else:
-                raise ParseError(f"line {line}: unexpected {v!r}")
+        self.expect("(")
+        self.sequence(")", argument)
+        self.expect("->")
+        self.expect("(")
+        result_types = self.sequence(")", self.type)
+        if self.accept("attributes"):
+            graph.attrs = self.attrs()
+        self.expect("{")
+        while self.peek().text == "kernel":
+            self.next()
+            kname = self.expect_kind("symbol")[1:]
+            kkind = self.expect_kind("ident")
+            graph.kernels.append(Kernel(kname, kkind, [], self.attrs()))
+        while self.peek().kind == "value":
+            self.node(graph, names)
+        tok = self.peek()
+        if tok.text != "return":
+            self.fail("a node or 'return'", tok)
+        self.next()
+        graph.results = self.operands(names)
+        self.expect("}")
+        if self.peek().kind != "eof":
+            self.fail("end of input")
+        if [v.type for v in graph.results] != result_types:
+            raise ParseError(f"graph @{graph.name}: declared result types {[str(t) for t in result_types]} "
+                             f"differ from the returned values")
+        self._attach(graph)
+        return graph
 
-        by_name = {k.name: k for k in g.kernels}
-        for n in g.nodes:
-            kname = n.attrs.get("kernel")
-            if kname is not None:
-                if kname not in by_name:
-                    raise ParseError(f"node refers to undeclared kernel @{kname}")
-                by_name[kname].nodes.append(n)
-        for a, at in zip(g.args, g.arg_attrs):
-            if "param" in at and at["param"] not in g.constants:
-                g.constants[at["param"]] = fake_data(at["param"], a.shape)
-        return g
+    def node(self, graph, names):
+        label = self.expect_kind("value")
+        self.expect("=")
+        op = self.expect_kind("ident")
+        inputs = self.operands(names)
+        attrs = self.attrs()
+        self.expect(":")
+        node = Node(op, inputs, attrs, self.type())
+        graph.nodes.append(node)
+        names[label] = node.out
 
-    def lookup(self, env):
-        k, v, line = self.take()
-        if k != "value":
-            raise ParseError(f"line {line}: expected a value, got {v!r}")
-        if v not in env:
-            raise ParseError(f"line {line}: use of undefined value {v}")
-        return env[v]
-
-    def node(self, g, env):
-        vname = self.need(kind="value")
-        self.need("=")
-        op = self.need(kind="ident")
-        operands = []
-        if self.tok[0] == "value":
-            operands.append(self.lookup(env))
-            while self.maybe(","):
-                operands.append(self.lookup(env))
-        attrs = self.attr_dict()
-        self.need(":")
-        t = self.tensor_type()
-        node = Node(op, operands, attrs, t)
-        g.nodes.append(node)
-        if op == "const" and "name" in attrs and attrs["name"] not in g.constants:
-            g.constants[attrs["name"]] = fake_data(attrs["name"], t.shape)
-        env[vname] = node.out
+    @staticmethod
+    def _attach(graph):
+        """Give kernels their nodes and missing data its name-seeded values."""
+        kernels = {k.name: k for k in graph.kernels}
+        for node in graph.nodes:
+            if "kernel" in node.attrs:
+                owner = kernels.get(node.attrs["kernel"])
+                if owner is None:
+                    raise ParseError(f"node refers to undeclared kernel @{node.attrs['kernel']}")
+                owner.nodes.append(node)
+            if node.op == "const" and "name" in node.attrs and node.attrs["name"] not in graph.constants:
+                graph.constants[node.attrs["name"]] = fake_data(node.attrs["name"], node.out.type.shape)
+        for arg, attrs in zip(graph.args, graph.arg_attrs):
+            if "param" in attrs and attrs["param"] not in graph.constants:
+                graph.constants[attrs["param"]] = fake_data(attrs["param"], arg.type.shape)
 
 
 def parse(text: str) -> Graph:
+    """Parse and verify one graph."""
     from kiln.ir.core import verify
 
-    g = _Reader(text).graph()
-    verify(g)
-    return g
+    graph = _Parser(text).graph()
+    verify(graph)
+    return graph

@@ -1,13 +1,15 @@
-"""Weight freezing and constant folding (reference: kiln/passes/freeze.py:25-75).
+"""Freezing and constant folding (Kiln's passes, the reference's
+kiln/passes/freeze.py:25-75).
 
-Freezing turns ``param`` arguments into named constants. Folding then
-evaluates every node whose operands are all constants. For ``nn.Linear`` that
-folds ``W.t()`` into a constant ``"<name>.transpose"`` stored as [K, N] with N
-contiguous: the B layout the HIP GEMM streams without a transposing load (the
-frozen weight is prepacked once at compile time).
-
-A fold that would *grow* data (e.g. expanding a scalar to a matrix) is refused:
-a broadcast is a free stride-0 view, materialising it costs HBM bandwidth.
+``FreezeParameters`` turns every ``param`` argument into a named ``const``
+node (placed at the top of the graph, in argument order) and drops the
+argument. ``ConstantFold`` then evaluates, front to back, every node whose
+operands are all constants. A tensor result becomes the constant
+``"<first named operand>.<op>"`` (so ``nn.Linear``'s ``W.t()`` becomes
+``"fc.weight.transpose"``, stored [K, N] with N contiguous: the B layout the
+HIP GEMM streams), a scalar result a scalar const. A fold whose result would
+hold more elements than its largest operand is skipped: a broadcast costs
+nothing as a stride-0 view and HBM bandwidth once materialised.
 """
 
 from __future__ import annotations
@@ -21,40 +23,45 @@ class FreezeParameters(Pass):
     name = "freeze"
 
     def run(self, g: Graph):
-        frozen = 0
-        args, attrs = [], []
-        for a, at in zip(g.args, g.arg_attrs):
-            if "param" not in at:
-                args.append(a)
-                attrs.append(at)
-                continue
-            c = g.add_node("const", [], {"name": at["param"]}, a.type, index=frozen)
-            g.replace_all_uses(a, c)
-            frozen += 1
-        g.args, g.arg_attrs = args, attrs
-        return {"frozen": frozen} if frozen else None
+        keep = [(a, attrs) for a, attrs in zip(g.args, g.arg_attrs) if "param" not in attrs]
+        frozen = [(a, attrs["param"]) for a, attrs in zip(g.args, g.arg_attrs) if "param" in attrs]
+        for position, (arg, pname) in enumerate(frozen):
+            const = g.add_node("const", [], {"name": pname}, arg.type, index=position)
+            g.replace_all_uses(arg, const)
+        g.args = [a for a, _ in keep]
+        g.arg_attrs = [attrs for _, attrs in keep]
+        return {"frozen": len(frozen)} if frozen else None
 
 
 class ConstantFold(Pass):
     name = "const-fold"
 
+    @staticmethod
+    def _foldable(g: Graph, node) -> bool:
+        if node.op == "const" or not node.inputs:
+            return False
+        if not all(g.is_const(v) for v in node.inputs):
+            return False
+        largest = max(1, *(v.type.numel for v in node.inputs))
+        return node.out.type.numel <= largest
+
     def run(self, g: Graph):
-        folded = nbytes = 0
-        for n in list(g.nodes):
-            if n.op == "const" or not n.inputs or not all(g.is_const(v) for v in n.inputs):
+        folded, new_bytes, i = 0, 0, 0
+        while i < len(g.nodes):
+            node = g.nodes[i]
+            if not self._foldable(g, node):
+                i += 1
                 continue
-            if n.out.type.numel > max(max(v.type.numel for v in n.inputs), 1):
-                continue
-            data = ops.evaluate(n.op, [g.const_data(v) for v in n.inputs], n.attrs)
-            at = g.nodes.index(n)
-            if n.out.type.rank == 0:
-                new = g.scalar(float(data), index=at)
+            data = ops.evaluate(node.op, [g.const_data(v) for v in node.inputs], node.attrs)
+            del g.nodes[i]
+            if node.out.type.rank == 0:
+                value = g.scalar(float(data), index=i)
             else:
-                stem = next((v.node.attrs["name"] for v in n.inputs if "name" in v.node.attrs), "folded")
-                new = g.constant(data, f"{stem}.{n.op}", index=at)
-                nbytes += data.nbytes
-            g.replace_all_uses(n.out, new)
-            g.nodes.remove(n)
+                stems = [v.node.attrs["name"] for v in node.inputs if "name" in v.node.attrs]
+                value = g.constant(data, f"{stems[0] if stems else 'folded'}.{node.op}", index=i)
+                new_bytes += data.nbytes
+            g.replace_all_uses(node.out, value)
             folded += 1
+            i += 1
         g.remove_dead()
-        return {"folded": folded, "bytes": nbytes} if folded else None
+        return {"folded": folded, "bytes": new_bytes} if folded else None

@@ -1,10 +1,18 @@
-"""Pass infrastructure (contract of the reference's kiln/passes/manager.py:11-41):
-``Pass.run(graph) -> stats | None`` and a ``PassManager`` that times each pass,
-records its statistics, verifies the IR after it and can dump the IR."""
+"""Pass driver.
+
+A pass is an object with a ``name`` and ``run(graph)`` that rewrites the graph
+in place and may return a dict of statistics (Kiln's pass interface, the
+reference's kiln/passes/manager.py:11-41). ``PassManager`` runs a list of
+them, keeping one ``PassRecord`` per execution; ``timings`` (seconds summed
+per pass name) and ``stats`` (the latest non-empty statistics per name) are
+views of that history, which is what ``Report`` shows.
+"""
 
 from __future__ import annotations
 
+import sys
 import time
+from dataclasses import dataclass
 
 from kiln.ir.core import Graph, verify
 
@@ -13,27 +21,43 @@ class Pass:
     name = "pass"
 
     def run(self, graph: Graph):
-        """Transform ``graph`` in place; may return a dict of statistics."""
-        raise NotImplementedError
+        """Rewrite ``graph`` in place; return a dict of statistics or None."""
+        raise NotImplementedError(f"{type(self).__name__}.run")
+
+
+@dataclass
+class PassRecord:
+    name: str
+    seconds: float
+    stats: dict | None
 
 
 class PassManager:
-    def __init__(self, passes, print_after_all=False, verify_each=True):
+    def __init__(self, passes, print_after_all=False, verify_each=True, stream=None):
         self.passes = list(passes)
         self.print_after_all = print_after_all
         self.verify_each = verify_each
-        self.timings: dict = {}
-        self.stats: dict = {}
+        self.stream = stream
+        self.history: list = []
 
     def run(self, graph: Graph) -> Graph:
         for p in self.passes:
-            t0 = time.perf_counter()
-            stats = p.run(graph)
-            self.timings[p.name] = self.timings.get(p.name, 0.0) + (time.perf_counter() - t0)
-            if stats:
-                self.stats[p.name] = stats
+            started = time.perf_counter()
+            result = p.run(graph)
+            self.history.append(PassRecord(p.name, time.perf_counter() - started, result or None))
             if self.verify_each:
                 verify(graph)
             if self.print_after_all:
-                print(f"// ----- IR after {p.name} -----\n{graph}")
+                print(f"// ----- IR after {p.name} -----", graph, sep="\n", file=self.stream or sys.stdout)
         return graph
+
+    @property
+    def timings(self) -> dict:
+        total = {}
+        for rec in self.history:
+            total[rec.name] = total.get(rec.name, 0.0) + rec.seconds
+        return total
+
+    @property
+    def stats(self) -> dict:
+        return {rec.name: rec.stats for rec in self.history if rec.stats}

@@ -1,6 +1,7 @@
-"""One op per kernel: the ``fusion=False`` ablation baseline
-(reference: kiln/passes/partition.py:23-35). Views and constants never belong
-to a kernel."""
+"""``fusion=False``: every compute node is its own kernel (Kiln's ablation
+baseline, the reference's kiln/passes/partition.py:23-35). Views and
+constants belong to no kernel; kernels are numbered k0, k1, ... in program
+order."""
 
 from __future__ import annotations
 
@@ -15,11 +16,8 @@ class OneOpPerKernel(Pass):
     name = "partition"
 
     def run(self, graph: Graph):
-        graph.kernels = []
-        for n in graph.nodes:
-            k = ops.kind(n.op)
-            if k in COMPUTE_KINDS:
-                kern = Kernel(f"k{len(graph.kernels)}", k, [n])
-                n.attrs["kernel"] = kern.name
-                graph.kernels.append(kern)
+        compute = [n for n in graph.nodes if ops.kind(n.op) in COMPUTE_KINDS]
+        graph.kernels = [Kernel(f"k{i}", ops.kind(n.op), [n]) for i, n in enumerate(compute)]
+        for node, kernel in zip(compute, graph.kernels):
+            node.attrs["kernel"] = kernel.name
         return {"kernels": len(graph.kernels)}
