@@ -235,6 +235,15 @@ int kh_plan_run_one(kh_plan *plan, int index, void *const *inputs, int n_inputs,
  * (GPUExecutable._capture, runtime.py:191-204) and replay it on `stream`. */
 int kh_plan_capture(kh_plan *plan, void *const *inputs, int n_inputs, void *const *outputs, int n_outputs);
 int kh_plan_replay(kh_plan *plan, void *stream);
+/* GPU seconds per execution of launch `index` (every launch when index = -1),
+ * the reference's kernel_seconds method (kiln/gpu/runtime.py:93-132) done in
+ * the library: after two plain launches on `stream`, `repeats` executions are
+ * captured into a hipGraph of their own (the plan's replay graph is left
+ * alone), replayed once, then `rounds` replays are timed with hipEvents on
+ * `stream`; *seconds = the fastest replay / repeats. Synchronises `stream`.
+ * The autotuner times candidate plans with it. */
+int kh_plan_time(kh_plan *plan, int index, void *const *inputs, int n_inputs, void *const *outputs, int n_outputs,
+                 int repeats, int rounds, void *stream, double *seconds);
 int kh_plan_destroy(kh_plan *plan);
 
 #ifdef __cplusplus

@@ -386,6 +386,67 @@ int kh_plan_capture(kh_plan *plan, void *const *inputs, int n_inputs, void *cons
   return KH_OK;
 }
 
+namespace {
+
+// Owns the graph, executable and events of one kh_plan_time call.
+struct TimingGraph {
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  hipEvent_t start = nullptr, stop = nullptr;
+  ~TimingGraph() {
+    if (start) (void)hipEventDestroy(start);
+    if (stop) (void)hipEventDestroy(stop);
+    if (exec) (void)hipGraphExecDestroy(exec);
+    if (graph) (void)hipGraphDestroy(graph);
+  }
+};
+
+}  // namespace
+
+int kh_plan_time(kh_plan *plan, int index, void *const *inputs, int n_inputs, void *const *outputs, int n_outputs,
+                 int repeats, int rounds, void *stream, double *seconds) {
+  if (!plan || !seconds) return fail(KH_ERR_INVALID, "null argument");
+  const int n = (int)plan->ops.size();
+  if (index < -1 || index >= n) return fail(KH_ERR_INVALID, "bad launch index");
+  if (repeats < 1 || repeats > 4096 || rounds < 1 || rounds > 64)
+    return fail(KH_ERR_INVALID, "repeats must be 1..4096 and rounds 1..64");
+  const int begin = index < 0 ? 0 : index, end = index < 0 ? n : index + 1;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e;
+  // two launches outside the graph first (first-launch costs, caches)
+  for (int w = 0; w < 2; ++w) {
+    const int rc = run_range(plan, begin, end, inputs, n_inputs, outputs, n_outputs, s, plan->workspace);
+    if (rc != KH_OK) return rc;
+  }
+  if (!plan->capture_stream && (e = hipStreamCreateWithFlags(&plan->capture_stream, hipStreamNonBlocking)) != hipSuccess)
+    return kh::hip_fail(e, "hipStreamCreateWithFlags");
+  TimingGraph t;
+  if ((e = hipStreamBeginCapture(plan->capture_stream, hipStreamCaptureModeThreadLocal)) != hipSuccess)
+    return kh::hip_fail(e, "hipStreamBeginCapture");
+  int rc = KH_OK;
+  for (int r = 0; r < repeats && rc == KH_OK; ++r)
+    rc = run_range(plan, begin, end, inputs, n_inputs, outputs, n_outputs, plan->capture_stream, plan->workspace);
+  e = hipStreamEndCapture(plan->capture_stream, &t.graph);
+  if (rc != KH_OK) return rc;
+  if (e != hipSuccess) return kh::hip_fail(e, "hipStreamEndCapture");
+  if ((e = hipGraphInstantiate(&t.exec, t.graph, nullptr, nullptr, 0)) != hipSuccess)
+    return kh::hip_fail(e, "hipGraphInstantiate");
+  if ((e = hipEventCreate(&t.start)) != hipSuccess || (e = hipEventCreate(&t.stop)) != hipSuccess)
+    return kh::hip_fail(e, "hipEventCreate");
+  if ((e = hipGraphLaunch(t.exec, s)) != hipSuccess) return kh::hip_fail(e, "hipGraphLaunch");  // warm-up replay
+  float best = 0.0f;
+  for (int r = 0; r < rounds; ++r) {
+    float ms = 0.0f;
+    if ((e = hipEventRecord(t.start, s)) != hipSuccess || (e = hipGraphLaunch(t.exec, s)) != hipSuccess ||
+        (e = hipEventRecord(t.stop, s)) != hipSuccess || (e = hipEventSynchronize(t.stop)) != hipSuccess ||
+        (e = hipEventElapsedTime(&ms, t.start, t.stop)) != hipSuccess)
+      return kh::hip_fail(e, "timing replay");
+    if (r == 0 || ms < best) best = ms;
+  }
+  *seconds = (double)best * 1e-3 / repeats;
+  return KH_OK;
+}
+
 int kh_plan_replay(kh_plan *plan, void *stream) {
   if (!plan || !plan->exec) return fail(KH_ERR_INVALID, "plan has no captured graph");
   const hipError_t e = hipGraphLaunch(plan->exec, static_cast<hipStream_t>(stream));

@@ -1,23 +1,21 @@
-"""torch.compile backend for the MI355X HIP path.
+"""``torch.compile(model, backend=kiln.backend, dynamic=False)`` on the MI355X.
 
-    compiled = torch.compile(model, backend=kiln.backend, dynamic=False)
+Kiln's Dynamo bridge contract (the reference's kiln/backend.py:31-54): the
+graphs TorchDynamo captures are traced to ATen by aot_autograd, which also
+lifts the parameters into graph inputs; each forward graph is imported
+(``import_fx``) and built by ``compile_graph``. The reference bridge builds
+for the CPU; this one builds for the GPU.
 
-Same contract as the reference bridge (kiln/backend.py:31-54): aot_autograd
-traces each graph TorchDynamo captures down to ATen ops and lifts the
-parameters into graph inputs; the forward graph is imported
-(frontend.fx_import.import_fx) and compiled by compile_graph. Dynamo does not
-say which inputs are weights, so freezing is off: weights stay runtime
-inputs, read in their original layout (a transposed view feeds the GEMM as a
-strided operand), and in-place updates to them are seen by later calls. For
-inference deployments prefer ``kiln.compile``, which exports the model and
-freezes it (pre-transposed constants, bf16 weight copies when asked).
+Dynamo does not say which inputs are weights, so nothing is frozen: weights
+stay runtime inputs in their own layout (a transposed view reaches the GEMM as
+a strided operand) and in-place updates to them are seen by later calls. For
+deployment, ``kiln.compile`` exports and freezes the model instead
+(pre-transposed constants, bf16 weight copies on request).
 
-This build compiles for the GPU only: graphs whose tensor inputs are on the
-CUDA device are built for it; any other graph (CPU inputs, symbolic shapes,
-an op without a lowering) falls back to eager PyTorch with a warning.
-
-Environment variables:
-    KILN_STRICT=1   raise on unsupported graphs instead of falling back to eager
+A graph is built only when every input is a tensor on the GPU. Anything else
+(CPU inputs, symbolic sizes, an op without a translation) runs as Dynamo
+captured it, in eager PyTorch, after a warning, and counts in
+``stats["fallback"]``; with ``KILN_STRICT=1`` it raises instead.
 """
 
 from __future__ import annotations
@@ -32,48 +30,50 @@ from torch._subclasses.fake_tensor import unset_fake_temporarily
 stats = {"compiled": 0, "fallback": 0}
 
 
-def _strict() -> bool:
-    return os.environ.get("KILN_STRICT", "0") not in ("", "0", "false", "False")
+class KilnForwardCompiler:
+    """aot_autograd's forward compiler: returns a callable for each graph."""
 
+    def __init__(self, counters: dict):
+        self.counters = counters
 
-def _device_of(example_inputs) -> str:
-    from kiln.frontend.fx_import import Unsupported
+    @staticmethod
+    def strict() -> bool:
+        return os.environ.get("KILN_STRICT", "0") not in ("", "0", "false", "False")
 
-    tensors = [t for t in example_inputs if isinstance(t, torch.Tensor)]
-    if len(tensors) != len(example_inputs):
-        raise Unsupported("non-tensor graph inputs (symbolic shapes?)")
-    if tensors and all(t.device.type == "cuda" for t in tensors):
-        return "cuda"
-    raise Unsupported("this build of Kiln compiles for the MI355X GPU only; graph inputs are not all on the "
-                      "CUDA device")
+    @staticmethod
+    def check_inputs(example_inputs):
+        from kiln.frontend.fx_import import Unsupported
 
+        if not all(isinstance(t, torch.Tensor) for t in example_inputs):
+            raise Unsupported("non-tensor graph inputs (symbolic shapes?)")
+        if not all(t.device.type == "cuda" for t in example_inputs):
+            raise Unsupported("this build of Kiln compiles for the MI355X GPU only; graph inputs are not all on "
+                              "the CUDA device")
 
-def kiln_compiler(gm: torch.fx.GraphModule, example_inputs):
-    """aot_autograd forward compiler: an executable for `gm`, or gm.forward."""
-    from kiln.api import Options, compile_graph
-    from kiln.frontend.fx_import import import_fx
+    def build(self, gm: torch.fx.GraphModule, example_inputs):
+        from kiln.api import Options, compile_graph
+        from kiln.frontend.fx_import import import_fx
 
-    try:
-        device = _device_of(example_inputs)
+        self.check_inputs(example_inputs)
         graph = import_fx(gm)
-        # the compiler is called inside the tracer's fake-tensor mode; the
-        # executable's arena, workspace and plan need real device memory
+        # called under the tracer's fake-tensor mode: the executable's arena,
+        # constants and plan need real device memory
         with unset_fake_temporarily():
-            exe, _ = compile_graph(graph, Options(device=device, freeze=False))
-    except NotImplementedError as err:
-        if _strict():
-            raise
-        warnings.warn(f"Kiln: falling back to eager PyTorch ({err})")
-        stats["fallback"] += 1
-        return gm.forward
+            exe, _ = compile_graph(graph, Options(device="cuda", freeze=False))
+        return exe
 
-    stats["compiled"] += 1
+    def __call__(self, gm: torch.fx.GraphModule, example_inputs):
+        try:
+            exe = self.build(gm, example_inputs)
+        except NotImplementedError as why:
+            if self.strict():
+                raise
+            warnings.warn(f"Kiln: falling back to eager PyTorch ({why})")
+            self.counters["fallback"] += 1
+            return gm.forward
+        self.counters["compiled"] += 1
+        return lambda *args: exe(*args)
 
-    def run(*args):
-        return exe(*args)
 
-    return run
-
-
-# aot_autograd traces down to ATen ops and lifts parameters into graph inputs.
+kiln_compiler = KilnForwardCompiler(stats)
 backend = aot_autograd(fw_compiler=kiln_compiler)

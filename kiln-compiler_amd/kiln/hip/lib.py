@@ -103,6 +103,8 @@ def load():
         "kh_plan_run_one": (ip, [vp, ip, ctypes.POINTER(vp), ip, ctypes.POINTER(vp), ip, vp]),
         "kh_plan_capture": (ip, [vp, ctypes.POINTER(vp), ip, ctypes.POINTER(vp), ip]),
         "kh_plan_replay": (ip, [vp, vp]),
+        "kh_plan_time": (ip, [vp, ip, ctypes.POINTER(vp), ip, ctypes.POINTER(vp), ip, ip, ip, vp,
+                              ctypes.POINTER(ctypes.c_double)]),
         "kh_plan_destroy": (ip, [vp]),
     }
     for name, (res, args) in sig.items():
@@ -122,7 +124,7 @@ def load():
 EXPORTED = ("kh_version", "kh_abi_sizes", "kh_last_error", "kh_init", "kh_device_info", "kh_gemm_config_count", "kh_gemm_config",
             "kh_plan_create", "kh_plan_workspace_bytes", "kh_plan_bind", "kh_plan_run", "kh_plan_run_noalloc",
             "kh_plan_run_one",
-            "kh_plan_capture", "kh_plan_replay", "kh_plan_destroy")
+            "kh_plan_capture", "kh_plan_replay", "kh_plan_time", "kh_plan_destroy")
 
 
 def check(rc: int, what: str = ""):
@@ -202,6 +204,14 @@ class Plan:
 
     def replay(self, stream):
         check(self.lib.kh_plan_replay(self.handle, stream), "kh_plan_replay")
+
+    def time(self, in_ptrs, out_ptrs, stream, index=-1, repeats=20, rounds=5) -> float:
+        """GPU seconds per execution of one launch (or of all: index -1)."""
+        ins, outs = pointer_array(in_ptrs), pointer_array(out_ptrs)
+        sec = ctypes.c_double()
+        check(self.lib.kh_plan_time(self.handle, index, ins, len(in_ptrs), outs, len(out_ptrs), repeats, rounds,
+                                    stream, ctypes.byref(sec)), "kh_plan_time")
+        return sec.value
 
     def __del__(self):
         h = getattr(self, "handle", None)

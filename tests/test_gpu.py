@@ -225,6 +225,42 @@ def test_graph_replays_with_new_inputs():
             torch.testing.assert_close(c(x).cpu(), model(x), rtol=RTOL, atol=ATOL)
 
 
+def test_stored_plan_is_reused_and_bit_identical():
+    # the second compile of the same model finds the plan the first one
+    # stored (no lowering, no tuning) and computes the same bits
+    model = gpt2_init_(Block(256, 4, 64), seed=3).eval()
+    x = torch.randn(64, 256)
+    first = kiln.compile(model, (x,), device="cuda", autotune=True)
+    second = kiln.compile(model, (x,), device="cuda", autotune=True)
+    assert first.report.lowering["plan_cache"] == "lowered"
+    assert second.report.lowering["plan_cache"] == "stored"
+    assert second.report.lowering["source"] == first.report.lowering["source"]
+    assert [bytes(l.desc) for l in second._exe.program.launches] == \
+        [bytes(l.desc) for l in first._exe.program.launches]
+    assert all(e["source"] == "cache" for e in second.report.autotune)
+    assert torch.equal(first(x), second(x))
+    fresh = kiln.compile(model, (x,), device="cuda", autotune=True, plan_cache=False)
+    assert fresh.report.lowering["plan_cache"] == "lowered" and torch.equal(fresh(x), first(x))
+
+
+def test_native_launch_timing():
+    # kh_plan_time: per-launch and whole-plan GPU time from hipGraph replays
+    model = gpt2_init_(Block(256, 4, 64), seed=3).eval()
+    x = torch.randn(64, 256)
+    c = kiln.compile(model, (x,), device="cuda")
+    rows = c.profile(x)
+    assert [r[0] for r in rows] == c._exe.kernel_names and all(0 < r[3] < 1.0 for r in rows)
+    exe = c._exe
+    ins = exe._prepare((x,))
+    outs = [torch.empty(s, device="cuda") for s in exe.output_shapes]
+    from kiln.hip.runtime import current_stream_handle
+
+    total = exe.plan.time([t.data_ptr() for t in ins], [t.data_ptr() for t in outs], current_stream_handle())
+    assert 0 < total < 1e-3
+    with torch.no_grad():
+        torch.testing.assert_close(outs[0].cpu(), model(x), rtol=RTOL, atol=ATOL)
+
+
 def test_split_k_is_deterministic():
     # split-K partials are summed in split order by whichever workgroup
     # finishes last: repeated runs must be bit-identical.

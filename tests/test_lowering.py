@@ -150,7 +150,7 @@ def test_gemv_weights_are_k_contiguous_copies():
     # a constant GEMV weight is read as a derived [N][K] copy (the nn.Linear
     # layout) holding exactly the frozen W^T's values; K not a multiple of 4
     # keeps the [K][N] constant
-    from kiln.hip.runtime import HIPExecutable, nk_copy
+    from kiln.hip.runtime import host_constant, nk_copy
 
     lin = torch.nn.Linear(768, 300)
     g, prog = lowered(lin, torch.randn(1, 768))
@@ -161,7 +161,7 @@ def test_gemv_weights_are_k_contiguous_copies():
     copy = nk_copy(g.constants[src], offset, strides, batch, k, n)
     assert copy.shape == (1, 300, 768) and copy.flags.c_contiguous
     np.testing.assert_array_equal(copy[0], lin.weight.detach().numpy())
-    assert HIPExecutable._host_constant(prog, g.constants, name).shape == (1, 300, 768)
+    assert host_constant(prog, g.constants, name).shape == (1, 300, 768)
     # the frozen W^T itself is read only through the copy: it gets no slot
     assert name in prog.consts and src not in prog.consts
     _, prog = lowered(torch.nn.Linear(37, 30), torch.randn(1, 37))
@@ -359,3 +359,25 @@ def test_tuner_never_times_a_spilling_configuration():
     for shape in ((1, 2048, 3072, 768), (1, 128, 768, 3072), (1, 300, 452, 96)):
         assert not any(c["tile"] in autotune.SPILLING for c in autotune.candidates(*shape, cus=256))
         assert autotune.default_config_for(*shape, cus=256)["tile"] not in autotune.SPILLING
+
+
+def test_plans_round_trip_through_the_store(tmp_path, monkeypatch):
+    # a stored plan reloads to byte-identical descriptors, the same constant
+    # slots, derived-constant recipes and listing; a different key misses
+    from kiln.hip import plans
+
+    monkeypatch.setenv("KILN_CACHE_DIR", str(tmp_path))
+    lin = torch.nn.Sequential(torch.nn.LayerNorm(768), torch.nn.Linear(768, 300), torch.nn.GELU())
+    g, prog = lowered(lin, torch.randn(1, 768))
+    assert prog.derived
+    key = plans.plan_key(str(g), "fp32", "default", kl.device_info())
+    listing = plans.save(key, prog, [])
+    assert listing.read_text() == prog.source
+    back, log = plans.load(key)
+    assert log == [] and back.consts == prog.consts and back.derived == prog.derived
+    assert [bytes(l.desc) for l in back.launches] == [bytes(l.desc) for l in prog.launches]
+    assert back.source == prog.source and back.precision == prog.precision
+    assert plans.load(plans.plan_key(str(g), "bf16", "default", kl.device_info())) is None
+    # a damaged file is ignored, not trusted
+    (tmp_path / "hip" / "plans" / f"{key}.json").write_text("{broken")
+    assert plans.load(key) is None
