@@ -423,45 +423,69 @@ def test_config_gpt2_block(T):
 
 @pytest.mark.parametrize("T", [1024, 2048])
 def test_config_gpt2_block_long(T):
-    # Causal attention: the first P output rows depend only on the first P
-    # input rows, so the full-size result is checked on a prefix against the
-    # oracle, and in full against eager PyTorch fp32.
+    # the whole [T, 768] output against the C oracle (float64 inside), and
+    # against eager PyTorch fp32
     model = _block(T)
     x = torch.randn(T, 768)
     c = kiln.compile(model, (x,), device="cuda")
-    out = c(x)
-    P = 128
+    out = c(x).cpu()
     params = {k: v.numpy() for k, v in model.state_dict().items()}
-    ref = oracle.block(x[:P].numpy(), params, 12)
-    np.testing.assert_allclose(out[:P].cpu().numpy(), ref, rtol=RTOL, atol=ATOL)
+    ref = oracle.block(x.numpy(), params, 12)
+    np.testing.assert_allclose(out.numpy(), ref, rtol=RTOL, atol=ATOL)
     with torch.no_grad():
-        torch.testing.assert_close(out.cpu(), model(x), rtol=RTOL, atol=ATOL)
+        torch.testing.assert_close(out, model(x), rtol=RTOL, atol=ATOL)
 
 
-def test_config_stack_12_layers():
+class _LayerTaps(torch.nn.Module):
+    """A Stack that returns every block's output and the final LayerNorm's."""
+
+    def __init__(self, stack):
+        super().__init__()
+        self.stack = stack
+
+    def forward(self, x):
+        outs = []
+        for blk in self.stack.blocks:
+            x = blk(x)
+            outs.append(x)
+        outs.append(self.stack.ln_f(x))
+        return tuple(outs)
+
+
+# Per-layer error of the 12-layer stack, as max |y - y64| / max |y64| against
+# a float64 run of the same weights and input (torch float64 on the CPU).
+# Eager PyTorch fp32 has an error of its own against float64 (fp32 rounding
+# compounding through 12 layers); kiln must stay within STACK_ERR_FACTOR of
+# eager's error at every layer, and the final output within the per-kernel
+# bar (rtol 1e-4, atol 1e-5) of float64, element by element.
+STACK_ERR_FACTOR = 2.0
+STACK_ERR_FLOOR = 1e-6
+
+
+@pytest.mark.parametrize("T", [1024, 1], ids=["prefill_1024", "decode_1"])
+def test_config_stack_12_layers_against_float64(T):
+    import copy
+
     torch.manual_seed(0)
-    model = gpt2_init_(Stack(12, 768, 12, 1024), seed=0).eval()
-    x = torch.randn(1024, 768)
-    c = kiln.compile(model, (x,), device="cuda")
-    out = c(x)
-    # fp32 rounding compounds over 12 layers; the per-kernel bar is rtol 1e-4,
-    # the stack is checked against eager fp32 with rtol 1e-3 / atol 1e-4.
+    model = gpt2_init_(Stack(12, 768, 12, T), seed=0).eval()
+    x = torch.randn(T, 768)
+    taps = _LayerTaps(model).eval()
+    c = kiln.compile(taps, (x,), device="cuda")
+    if T == 1:
+        assert any(l.family == 4 for l in c._exe.program.launches)   # the GEMV path
+    got = [t.cpu().double() for t in c(x)]
     with torch.no_grad():
-        torch.testing.assert_close(out.cpu(), model(x), rtol=1e-3, atol=1e-4)
-
-
-def test_config_stack_decode():
-    torch.manual_seed(0)
-    model = gpt2_init_(Stack(12, 768, 12, 1), seed=0).eval()
-    x = torch.randn(1, 768)
-    c = kiln.compile(model, (x,), device="cuda")
-    assert any(l.family == 4 for l in c._exe.program.launches)   # the GEMV path
-    h = x.numpy()
-    for blk in model.blocks:
-        h = oracle.block(h, {k: v.numpy() for k, v in blk.state_dict().items()}, 12)
-    sd = model.ln_f.state_dict()
-    ref = oracle.layernorm(h, sd["weight"].numpy(), sd["bias"].numpy())
-    np.testing.assert_allclose(c(x).cpu().numpy(), ref, rtol=1e-3, atol=1e-4)
+        ref = _LayerTaps(copy.deepcopy(model).double()).eval()(x.double())
+        eager = [t.cpu().double() for t in copy.deepcopy(taps).cuda()(x.cuda())]
+    worst = 0.0
+    for layer, (g, r, e) in enumerate(zip(got, ref, eager)):
+        scale = float(r.abs().max())
+        k_err, e_err = float((g - r).abs().max()) / scale, float((e - r).abs().max()) / scale
+        print(f"stack T={T} layer {layer}: kiln {k_err:.2e}, eager fp32 {e_err:.2e} of max |y64|", flush=True)
+        assert k_err <= max(STACK_ERR_FACTOR * e_err, STACK_ERR_FLOOR), (layer, k_err, e_err)
+        worst = max(worst, k_err / max(e_err, 1e-12))
+    np.testing.assert_allclose(got[-1].numpy(), ref[-1].numpy(), rtol=RTOL, atol=ATOL)
+    print(f"stack T={T}: worst kiln/eager error ratio {worst:.2f}", flush=True)
 
 
 @pytest.mark.parametrize("k, n, affine, bias", [(768, 2304, True, True), (61, 37, True, False),
