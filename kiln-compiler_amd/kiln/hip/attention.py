@@ -29,7 +29,7 @@ import numpy as np
 from kiln.hip import lib as kl
 from kiln.ir import ops
 from kiln.ir.core import Graph, Kernel
-from kiln.passes.buffers import _order_kernels, compute_layouts, kernel_outputs
+from kiln.passes.buffers import compute_layouts, kernel_outputs, order_kernels
 from kiln.passes.manager import Pass
 
 HEAD_DIMS = (32, 64)   # head dimensions the HIP attention kernel is built for
@@ -251,7 +251,7 @@ class FuseAttention(Pass):
             graph.kernels.insert(first, merged)
         if not matches:
             return None
-        _order_kernels(graph)
+        order_kernels(graph)
         lay = compute_layouts(graph)
         for n in graph.nodes:
             if ops.kind(n.op) == "view" and n.out not in lay:

@@ -1,19 +1,19 @@
-"""Static memory planning: pack every arena buffer into one allocation.
+"""Static memory plan: every arena buffer gets a fixed offset in one allocation.
 
-Same plan as the reference (kiln/passes/memory_plan.py:43-112), since the
-``memory_plan.kir`` fixture pins offsets and the Block's arena must equal the
-peak-live lower bound (tests/test_memory_plan.py:42-51):
+The plan is Kiln's (the reference's kiln/passes/memory_plan.py:43-112): the
+memory_plan.kir fixture pins its offsets, and for the GPT-2 block the arena
+equals the peak-live lower bound (the reference's
+tests/test_memory_plan.py:42-51):
 
-  * a buffer is live over the closed interval [writer kernel, last reader
-    kernel]; reading through a view keeps the viewed buffer alive;
-  * buffers are placed largest first (ties by start), each at the lowest
-    64-byte-aligned offset that overlaps no placed buffer whose interval
-    intersects its own (greedy-by-size first fit);
-  * ``reuse=False`` gives every buffer its own slot (the ablation baseline).
+  * a buffer is busy from the kernel that writes it to the last kernel that
+    reads it, directly or through a view, both included (kernel indices);
+  * buffers are placed one by one, largest first (equal sizes: the earlier
+    writer first), each at the lowest 64-byte-aligned offset where it
+    overlaps no already placed buffer that is busy at the same time;
+  * ``reuse=False`` places them end to end instead (the ablation baseline).
 
-On MI355X the arena is one ``hipMalloc`` (a torch uint8 tensor); the plan is
-what makes the whole compiled graph replayable as one hipGraph with fixed
-addresses.
+On the MI355X the arena is one device allocation, and the fixed offsets are
+what let a whole compiled graph be captured once and replayed as a hipGraph.
 """
 
 from __future__ import annotations
@@ -24,34 +24,55 @@ from kiln.passes.manager import Pass
 
 
 def align(nbytes: int) -> int:
-    return -(-nbytes // ALIGNMENT) * ALIGNMENT
+    return (nbytes + ALIGNMENT - 1) // ALIGNMENT * ALIGNMENT
 
 
 def live_ranges(graph: Graph) -> dict:
-    """{owner Value: [first, last]} in kernel indices for every arena buffer."""
-    lay = compute_layouts(graph)
-    index = {n: i for i, k in enumerate(graph.kernels) for n in k.nodes}
-    ranges = {v: [index[v.node]] * 2 for v, l in lay.items() if l.base[0] == "arena" and l.base[1] is v}
+    """{buffer-owning Value: [first kernel, last kernel]} for arena buffers."""
+    layouts = compute_layouts(graph)
+    kernel_index = {n: i for i, k in enumerate(graph.kernels) for n in k.nodes}
+    spans = {}
+    for v, lay in layouts.items():
+        if lay.base == ("arena", v):
+            spans[v] = [kernel_index[v.node], kernel_index[v.node]]
     for i, k in enumerate(graph.kernels):
         for v in kernel_inputs(graph, k):
-            l = lay.get(v)
-            if l is not None and l.base[0] == "arena":
-                r = ranges[l.base[1]]
-                r[1] = max(r[1], i)
-    return ranges
+            lay = layouts.get(v)
+            if lay is not None and lay.base[0] == "arena":
+                span = spans[lay.base[1]]
+                span[1] = max(span[1], i)
+    return spans
 
 
 def overlaps(a, b) -> bool:
-    return a[0] <= b[1] and b[0] <= a[1]
+    """Do two closed [first, last] kernel intervals share a kernel?"""
+    return max(a[0], b[0]) <= min(a[1], b[1])
 
 
 def peak_live_bytes(ranges) -> int:
-    """Lower bound: the most aligned bytes live during any single kernel."""
-    if not ranges:
-        return 0
-    end = max(r[1] for r in ranges.values())
-    return max(sum(align(v.type.nbytes) for v, r in ranges.items() if r[0] <= t <= r[1])
-               for t in range(end + 1))
+    """The most (aligned) bytes busy during any one kernel: no plan can be
+    smaller. Computed as a sweep over interval start / end events."""
+    events = {}
+    for v, (first, last) in ranges.items():
+        size = align(v.type.nbytes)
+        events[first] = events.get(first, 0) + size
+        events[last + 1] = events.get(last + 1, 0) - size
+    peak = live = 0
+    for t in sorted(events):
+        live += events[t]
+        peak = max(peak, live)
+    return peak
+
+
+def _lowest_gap(size: int, taken) -> int:
+    """Lowest offset where [offset, offset + size) avoids every [lo, hi) in
+    ``taken`` (offsets of multiples of the alignment stay aligned)."""
+    offset = 0
+    for lo, hi in sorted(taken):
+        if offset + size <= lo:
+            break
+        offset = max(offset, hi)
+    return offset
 
 
 class MemoryPlan(Pass):
@@ -62,24 +83,21 @@ class MemoryPlan(Pass):
 
     def run(self, graph: Graph):
         ranges = live_ranges(graph)
-        placed = []   # (offset, size, range)
+        placements = []   # (offset, size, busy interval)
+        end = 0
         for v in sorted(ranges, key=lambda v: (-v.type.nbytes, ranges[v][0])):
-            size = align(v.type.nbytes)
+            size, busy = align(v.type.nbytes), ranges[v]
             if self.reuse:
-                offset = 0
-                for lo, hi in sorted((o, o + s) for o, s, r in placed if overlaps(r, ranges[v])):
-                    if offset + size <= lo:
-                        break
-                    offset = max(offset, hi)
+                offset = _lowest_gap(size, [(o, o + s) for o, s, b in placements if overlaps(b, busy)])
             else:
-                offset = sum(s for _, s, _ in placed)
-            placed.append((offset, size, ranges[v]))
+                offset = end
+            placements.append((offset, size, busy))
+            end = max(end, offset + size)
             v.node.attrs["offset"] = offset
-        arena = max((o + s for o, s, _ in placed), default=0)
-        graph.attrs["arena_bytes"] = arena
+        graph.attrs["arena_bytes"] = end
         return {
-            "buffers": len(placed),
-            "arena_bytes": arena,
-            "naive_bytes": sum(s for _, s, _ in placed),
+            "buffers": len(placements),
+            "arena_bytes": end,
+            "naive_bytes": sum(size for _, size, _ in placements),
             "lower_bound_bytes": peak_live_bytes(ranges),
         }
