@@ -676,6 +676,9 @@ def main():
     if not torch.cuda.is_available():
         sys.exit("bench.py needs an MI355X (no ROCm GPU visible)")
     from kiln.hip import lib as kl
+    from kiln.hip.interpret import refuse
+
+    refuse("bench.py")
 
     if args.traffic_probe:
         traffic_probe(args)

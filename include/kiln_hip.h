@@ -228,6 +228,16 @@ int kh_plan_run(kh_plan *plan, void *const *inputs, int n_inputs, void *const *o
 #define KH_NOALLOC_WORKSPACE_BYTES (16u << 20)
 int kh_plan_run_noalloc(kh_plan *plan, void *const *inputs, int n_inputs, void *const *outputs, int n_outputs,
                         void *stream);
+/* The plan's meaning executed on the CPU: every launch, in order, element by
+ * element, over HOST memory (inputs, outputs, and the constants and arena
+ * bound with kh_plan_bind must all be host pointers; no workspace is used).
+ * The counterpart of the reference's interpreter switch
+ * (kiln/gpu/runtime.py:39-50, Triton's TRITON_INTERPRET): it lets the CPU test
+ * suite check the lowering's descriptors, addressing and tapes against the
+ * oracle without a GPU. A test instrument: the GPU path never calls it.
+ * Products and attention accumulate in double, so results agree with the
+ * GPU kernels to rounding, not bit for bit. */
+int kh_plan_run_host(kh_plan *plan, void *const *inputs, int n_inputs, void *const *outputs, int n_outputs);
 /* Run one launch (per-kernel profiling). */
 int kh_plan_run_one(kh_plan *plan, int index, void *const *inputs, int n_inputs, void *const *outputs,
                     int n_outputs, void *stream);

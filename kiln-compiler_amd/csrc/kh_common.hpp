@@ -2,15 +2,13 @@
 // scalar math of the fused op set, the instruction-tape interpreter, wave64
 // reductions and fast integer division for index decomposition.
 //
-// The op semantics follow the reference's op table (kiln/ir/ops.py:48-97) and
-// its GPU forms (kiln/gpu/codegen.py:53-88, 223-248). Where this file uses a
-// different but more accurate formula it says so.
 #pragma once
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 #include "kiln_hip.h"
+#include "kh_semantics.hpp"
 
 namespace kh {
 
@@ -37,27 +35,8 @@ __device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv &f) {
   return (__umulhi(n, f.m) + n) >> f.s;
 }
 
-// ---------------------------------------------------------------------------
-// Scalar math. exp/erf/tanh use the device library's accurate forms.
-// GELU(tanh) is evaluated as x * sigmoid(2u) = x / (1 + exp(-2u)),
-// u = sqrt(2/pi) (x + 0.044715 x^3): algebraically equal to
-// 0.5 x (1 + tanh(u)) but free of the 1 - e cancellation of the tanh form.
-// Its exponential is the hardware base-2 one (v_exp_f32 of -2u * log2(e),
-// relative error ~1e-6 for |2u| < 88, exact overflow to inf / underflow to 0)
-// and the quotient a hardware reciprocal (v_rcp_f32, 1 ulp): GELU is the
-// elementwise hot op of the MLP, and the error stays far inside the 1e-4
-// tolerance its results are checked at.
-__device__ __forceinline__ float op_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
-
-__device__ __forceinline__ float op_gelu_tanh(float x) {
-  const float u = 0.7978845608028654f * fmaf(0.044715f * x, x * x, x);
-  const float e = __builtin_amdgcn_exp2f(-2.8853900817779268f * u);  // exp(-2u) = 2^(-2u log2 e)
-  return x * __builtin_amdgcn_rcpf(1.0f + e);
-}
-
-__device__ __forceinline__ float op_gelu_erf(float x) {
-  return 0.5f * x * (1.0f + erff(x * 0.7071067811865476f));
-}
+// Scalar math of the op set (op_scalar, nan_max, GELU forms ...) lives in
+// kh_semantics.hpp, shared with the host interpreter of plans.
 
 // 128-bit load marked non-temporal
 __device__ __forceinline__ float4 load_stream4(const float *p) {
@@ -72,13 +51,6 @@ __device__ __forceinline__ void store_stream(float *p, float x, float y, float z
   typedef float f32x4_t __attribute__((ext_vector_type(4)));
   const f32x4_t v = {x, y, z, w};
   __builtin_nontemporal_store(v, reinterpret_cast<f32x4_t *>(p));
-}
-
-__device__ __forceinline__ float nan_max(float a, float b) {
-  return (a != a) ? a : ((b != b) ? b : fmaxf(a, b));
-}
-__device__ __forceinline__ float nan_min(float a, float b) {
-  return (a != a) ? a : ((b != b) ? b : fminf(a, b));
 }
 
 // ---------------------------------------------------------------------------
@@ -146,36 +118,23 @@ __device__ __forceinline__ void bank_set(float (&b)[N], int s, const Vec<4> &v) 
   for (int i = 0; i < 4; ++i) b[(s & (N / 4 - 1)) * 4 + i] = v.v[i];
 }
 
-// One tape instruction (not STORE/RSUM/RMAX) on 4 lanes of data.
+// One tape instruction (not STORE/RSUM/RMAX) on 4 lanes of data. The switch
+// on the (wave-uniform) opcode is outside the element loop; each case calls
+// op_scalar with a constant opcode, which folds to that op's expression.
 __device__ __forceinline__ Vec<4> apply4(int op, const Vec<4> &x, const Vec<4> &y) {
   Vec<4> r;
-#define KH_EACH(expr)                             \
-  _Pragma("unroll") for (int i = 0; i < 4; ++i) { \
-    const float u = x.v[i], w = y.v[i];           \
-    (void)w;                                      \
-    r.v[i] = (expr);                              \
-  }                                               \
-  break;
+#define KH_OP_CASE(OP)                                                    \
+  case OP:                                                                \
+    _Pragma("unroll") for (int i = 0; i < 4; ++i) r.v[i] = op_scalar(OP, x.v[i], y.v[i]); \
+    break;
   switch (op) {
-    case KH_OP_ADD: KH_EACH(u + w)
-    case KH_OP_SUB: KH_EACH(u - w)
-    case KH_OP_MUL: KH_EACH(u * w)
-    case KH_OP_DIV: KH_EACH(u / w)
-    case KH_OP_MAX: KH_EACH(nan_max(u, w))
-    case KH_OP_MIN: KH_EACH(nan_min(u, w))
-    case KH_OP_NEG: KH_EACH(-u)
-    case KH_OP_RELU: KH_EACH(u != u ? u : fmaxf(u, 0.0f))
-    case KH_OP_EXP: KH_EACH(expf(u))
-    case KH_OP_TANH: KH_EACH(tanhf(u))
-    case KH_OP_SIGMOID: KH_EACH(op_sigmoid(u))
-    case KH_OP_ERF: KH_EACH(erff(u))
-    case KH_OP_GELU_TANH: KH_EACH(op_gelu_tanh(u))
-    case KH_OP_GELU_ERF: KH_EACH(op_gelu_erf(u))
-    case KH_OP_RSQRT: KH_EACH(rsqrtf(u))
-    case KH_OP_SQRT: KH_EACH(sqrtf(u))
-    default: KH_EACH(u)
+    KH_OP_CASE(KH_OP_ADD) KH_OP_CASE(KH_OP_SUB) KH_OP_CASE(KH_OP_MUL) KH_OP_CASE(KH_OP_DIV)
+    KH_OP_CASE(KH_OP_MAX) KH_OP_CASE(KH_OP_MIN) KH_OP_CASE(KH_OP_NEG) KH_OP_CASE(KH_OP_RELU)
+    KH_OP_CASE(KH_OP_EXP) KH_OP_CASE(KH_OP_TANH) KH_OP_CASE(KH_OP_SIGMOID) KH_OP_CASE(KH_OP_ERF)
+    KH_OP_CASE(KH_OP_GELU_TANH) KH_OP_CASE(KH_OP_GELU_ERF) KH_OP_CASE(KH_OP_RSQRT) KH_OP_CASE(KH_OP_SQRT)
+    default: r = x;
   }
-#undef KH_EACH
+#undef KH_OP_CASE
   return r;
 }
 

@@ -41,6 +41,10 @@ std::unique_ptr<Op> make_gemv(const kh_launch &L, std::string &err, bool &unsupp
 std::unique_ptr<Op> make_red(const kh_launch &L, std::string &err, bool &unsupported);
 std::unique_ptr<Op> make_attn(const kh_launch &L, std::string &err, bool &unsupported);
 
+// The meaning of launch L, executed on the CPU over host pointers
+// (kh_host.hip); false with `err` set for a family it cannot run.
+bool run_launch_host(const kh_launch &L, float *const *ptrs, std::string &err);
+
 int gemm_config_count();
 bool gemm_config(int id, int32_t out8[8]);
 

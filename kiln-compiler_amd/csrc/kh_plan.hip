@@ -349,6 +349,19 @@ int kh_plan_run_noalloc(kh_plan *plan, void *const *inputs, int n_inputs, void *
                    static_cast<hipStream_t>(stream), ws);
 }
 
+int kh_plan_run_host(kh_plan *plan, void *const *inputs, int n_inputs, void *const *outputs, int n_outputs) {
+  if (!plan) return fail(KH_ERR_INVALID, "null plan");
+  if (!plan->bound) return fail(KH_ERR_INVALID, "plan is not bound (call kh_plan_bind)");
+  float *ptrs[KH_MAX_REFS];
+  for (int i = 0; i < (int)plan->desc.size(); ++i) {
+    const int rc = resolve(plan, i, inputs, n_inputs, outputs, n_outputs, ptrs);
+    if (rc != KH_OK) return rc;
+    std::string err;
+    if (!kh::run_launch_host(plan->desc[i], ptrs, err)) return fail(KH_ERR_UNSUPPORTED, err);
+  }
+  return KH_OK;
+}
+
 int kh_plan_run_one(kh_plan *plan, int index, void *const *inputs, int n_inputs, void *const *outputs,
                     int n_outputs, void *stream) {
   if (!plan || index < 0 || index >= (int)plan->ops.size()) return fail(KH_ERR_INVALID, "bad launch index");

@@ -161,9 +161,11 @@ class _GpuBuild:
     def config_source(self):
         """(fn(graph, kernel) -> config or None, its name for the plan key or
         None when the plans it makes cannot be keyed, the tuner or None)."""
+        from kiln.hip.interpret import interpreting
+
         if self.options.gpu_matmul_config is not None:
             return self.options.gpu_matmul_config, None, None
-        if self.options.autotune:
+        if self.options.autotune and not interpreting():   # nothing to measure on the host interpreter
             from kiln.hip.autotune import GPUAutotuner
 
             tuner = GPUAutotuner(precision=self.precision)
@@ -190,13 +192,16 @@ class _GpuBuild:
         return program, log, plans.save(key, program, log), "lowered"
 
     def run(self):
+        from kiln.hip.interpret import HostExecutable, interpreting
         from kiln.hip.lib import FAMILY_NAMES
         from kiln.hip.runtime import HIPExecutable
 
         self.optimise()
         program, autotune_log, listing, origin = self.plan()
         g = self.graph
-        exe = HIPExecutable(program, g.attrs.get("arena_bytes", 0), g.constants, [a.shape for a in g.args],
+        # KILN_HIP_INTERPRET=1 (tests only): the plan's meaning on the CPU
+        executable = HostExecutable if interpreting() else HIPExecutable
+        exe = executable(program, g.attrs.get("arena_bytes", 0), g.constants, [a.shape for a in g.args],
                             [r.shape for r in g.results], cuda_graphs=self.options.cuda_graphs,
                             debug=self.options.debug, source_path=listing)
         if self.options.dump_mlir:

@@ -100,6 +100,7 @@ def load():
         "kh_plan_bind": (ip, [vp, ctypes.POINTER(vp), ip, vp, vp, ctypes.c_size_t]),
         "kh_plan_run": (ip, [vp, ctypes.POINTER(vp), ip, ctypes.POINTER(vp), ip, vp]),
         "kh_plan_run_noalloc": (ip, [vp, ctypes.POINTER(vp), ip, ctypes.POINTER(vp), ip, vp]),
+        "kh_plan_run_host": (ip, [vp, ctypes.POINTER(vp), ip, ctypes.POINTER(vp), ip]),
         "kh_plan_run_one": (ip, [vp, ip, ctypes.POINTER(vp), ip, ctypes.POINTER(vp), ip, vp]),
         "kh_plan_capture": (ip, [vp, ctypes.POINTER(vp), ip, ctypes.POINTER(vp), ip]),
         "kh_plan_replay": (ip, [vp, vp]),
@@ -123,6 +124,7 @@ def load():
 
 EXPORTED = ("kh_version", "kh_abi_sizes", "kh_last_error", "kh_init", "kh_device_info", "kh_gemm_config_count", "kh_gemm_config",
             "kh_plan_create", "kh_plan_workspace_bytes", "kh_plan_bind", "kh_plan_run", "kh_plan_run_noalloc",
+            "kh_plan_run_host",
             "kh_plan_run_one",
             "kh_plan_capture", "kh_plan_replay", "kh_plan_time", "kh_plan_destroy")
 
@@ -192,6 +194,11 @@ class Plan:
     def run(self, in_ptrs, out_ptrs, stream):
         ins, outs = pointer_array(in_ptrs), pointer_array(out_ptrs)
         check(self.lib.kh_plan_run(self.handle, ins, len(in_ptrs), outs, len(out_ptrs), stream), "kh_plan_run")
+
+    def run_host(self, in_ptrs, out_ptrs):
+        """The plan executed on the CPU over host buffers (kh_plan_run_host)."""
+        ins, outs = pointer_array(in_ptrs), pointer_array(out_ptrs)
+        check(self.lib.kh_plan_run_host(self.handle, ins, len(in_ptrs), outs, len(out_ptrs)), "kh_plan_run_host")
 
     def run_one(self, index, in_ptrs, out_ptrs, stream):
         ins, outs = pointer_array(in_ptrs), pointer_array(out_ptrs)

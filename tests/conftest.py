@@ -17,6 +17,17 @@ def pytest_configure(config):
 
 
 @pytest.fixture(autouse=True)
+def _gpu_tests_run_on_the_gpu(request):
+    # the host interpreter (KILN_HIP_INTERPRET) is a CPU test instrument; a
+    # GPU-marked test must exercise the HIP path
+    if request.node.get_closest_marker("gpu") is not None:
+        from kiln.hip.interpret import refuse
+
+        refuse(request.node.nodeid)
+    yield
+
+
+@pytest.fixture(autouse=True)
 def _deterministic():
     torch.manual_seed(0)
     yield

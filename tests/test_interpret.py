@@ -1,0 +1,128 @@
+"""The plan's meaning on the CPU (``KILN_HIP_INTERPRET=1``: the library's
+kh_plan_run_host). Every case goes through the real compile path - passes,
+lowering, plan validation in the library - and the host interpreter then
+executes the descriptors, addressing and tapes element by element; results
+are checked against the oracle at the GPU tests' tolerance. This is how the
+CPU suite catches a lowering or addressing mistake without a GPU, as the
+reference's interpreter switch does for its GPU tests (tests/conftest.py:11-15
+there)."""
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import kiln
+import oracle
+from kiln.hip import bf16
+from models.transformer import Block, Stack, gpt2_init_
+from oracle import interp
+from test_gpu import ATOL, CASES, RTOL, as_tuple, imported, random_graph
+
+
+@pytest.fixture(autouse=True)
+def _interpreting(monkeypatch):
+    monkeypatch.setenv("KILN_HIP_INTERPRET", "1")
+    yield
+
+
+def check(fn, *xs, rtol=RTOL, atol=ATOL, **flags):
+    compiled = kiln.compile(fn, xs, device="cuda", **flags)
+    ref = interp.run(imported(fn, xs), *[x.numpy() for x in xs])
+    got = as_tuple(compiled(*xs))
+    assert len(got) == len(ref)
+    for a, r in zip(got, ref):
+        assert a.device.type == "cpu"
+        np.testing.assert_allclose(a.numpy().astype(np.float64), r, rtol=rtol, atol=atol)
+    return compiled
+
+
+@pytest.mark.parametrize("name", list(CASES))
+@pytest.mark.parametrize("fusion", [True, False], ids=["fused", "unfused"])
+def test_reference_cases(name, fusion):
+    fn, xs = CASES[name]
+    check(fn, *xs, fusion=fusion)
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2, 3, 4, 5, 37, 45, 59])
+def test_random_graphs(seed):
+    import random
+
+    from kiln.api import Options
+
+    rng = random.Random(seed)
+    g = random_graph(rng, n_ops=rng.randint(6, 22))
+    x = np.random.default_rng(seed).standard_normal(g.args[0].shape).astype(np.float32) * 0.5
+    expected = interp.run(g, x)
+    exe, _ = kiln.compile_graph(g, Options(device="cuda"))
+    for out, ref in zip(exe(torch.from_numpy(x)), expected):
+        np.testing.assert_allclose(out.numpy(), ref, rtol=RTOL, atol=ATOL)
+
+
+def test_long_rows_run_in_chunks():
+    # chunked multi-pass rows: the interpreter poisons per-column values
+    # between passes, so a pass reading a stale value would show as NaN
+    x = torch.randn(2, 5000)
+    c = check(lambda t: F.softmax(t, -1), x)
+    assert "(chunked)" in open(c.report.lowering["source"]).read()
+    check(torch.nn.LayerNorm(6000).eval(), torch.randn(3, 6000))
+
+
+def test_max_reductions_propagate_nan():
+    x = torch.randn(300, 7)
+    x[123, 2] = float("nan")
+    for dim in (0, -1):
+        fn = lambda t: t.amax(dim, keepdim=True) + 0.0 * t
+        ref = interp.run(imported(fn, (x,)), x.numpy())[0]
+        np.testing.assert_allclose(kiln.compile(fn, (x,), device="cuda")(x).numpy(), ref, equal_nan=True)
+
+
+@pytest.mark.parametrize("T", [16, 48])
+def test_gpt2_block_against_the_c_oracle(T):
+    torch.manual_seed(0)
+    model = gpt2_init_(Block(128, 4, T), seed=0).eval()
+    x = torch.randn(T, 128)
+    c = kiln.compile(model, (x,), device="cuda")
+    assert c.report.lowering["families"].get("attention") == 1
+    params = {k: v.numpy() for k, v in model.state_dict().items()}
+    np.testing.assert_allclose(c(x).numpy(), oracle.block(x.numpy(), params, 4), rtol=RTOL, atol=ATOL)
+
+
+def test_decode_stack_runs_gemv_prologues():
+    # M = 1: LayerNorm and one-query attention as GEMV prologues, K-contiguous weights
+    torch.manual_seed(0)
+    model = gpt2_init_(Stack(2, 128, 4, 1), seed=0).eval()
+    x = torch.randn(1, 128)
+    c = kiln.compile(model, (x,), device="cuda")
+    src = open(c.report.lowering["source"]).read()
+    assert "prologue: layernorm" in src and "prologue: attention" in src
+    h = x.numpy()
+    for blk in model.blocks:
+        h = oracle.block(h, {k: v.numpy() for k, v in blk.state_dict().items()}, 4)
+    sd = model.ln_f.state_dict()
+    ref = oracle.layernorm(h, sd["weight"].numpy(), sd["bias"].numpy())
+    np.testing.assert_allclose(c(x).numpy(), ref, rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.parametrize("precision", ["bf16", "bf16x3"])
+def test_bf16_products_round_as_the_mfma_variants(precision):
+    torch.manual_seed(0)
+    lin = gpt2_init_(torch.nn.Linear(96, 40), seed=2).eval()
+    x = torch.randn(24, 96)
+    c = kiln.compile(lin, (x,), device="cuda", matmul_precision=precision)
+    w = lin.weight.detach().numpy().T
+    if precision == "bf16":
+        # against the product of the bf16-rounded inputs, in float64
+        xr, wr = bf16.bf16_value(bf16.bf16_bits(x.numpy())), bf16.bf16_value(bf16.bf16_bits(w))
+        ref = xr.astype(np.float64) @ wr.astype(np.float64) + lin.bias.detach().numpy()
+        np.testing.assert_allclose(c(x).numpy(), ref, rtol=1e-5, atol=1e-6)
+    else:
+        ref = oracle.linear(x.numpy(), w, lin.bias.detach().numpy())
+        np.testing.assert_allclose(c(x).numpy(), ref, rtol=RTOL, atol=ATOL)
+
+
+def test_interpreter_is_never_a_gpu_path():
+    from kiln.hip.interpret import refuse
+
+    with pytest.raises(RuntimeError, match="KILN_HIP_INTERPRET"):
+        refuse("bench.py")
