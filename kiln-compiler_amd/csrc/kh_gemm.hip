@@ -802,10 +802,185 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void gemm3_f32_kernel(const GemmAr
 }
 
 // ---------------------------------------------------------------------------
+// Skinny-M GEMM (kind 4), for products with few rows (M up to a few hundred)
+// where tiles that fill 256 CUs are too small to keep the LDS pipeline busy
+// and splitting K across workgroups needs a second kernel. One workgroup owns
+// one BM x BN output tile and its WK waves split K between them. Operands go
+// straight from global memory into registers, no LDS staging: A is row-major
+// [M][K] and B the [batch][N][K] copy of a constant weight (the nn.Linear
+// layout, K contiguous), so lane (row li, group g) loads the 16-byte pieces
+// A[m][k + 4g .. + 3] and B[n][k + 4g .. + 3], and the four MFMA steps of a
+// 16-deep chunk take its four values in turn (K is permuted the same way for
+// A and B; a dot product does not depend on the order of its terms).
+//
+// Loads are buffer loads: a piece outside the wave's share of K (or past the
+// end of K) gets an offset beyond the resource's extent and reads as zeros,
+// so no load is conditional and the compiler can count the loads in flight
+// exactly. Rows and columns past M and N are clamped to the last one (their
+// results are never stored). Each wave runs a ring of DEPTH chunks: the MFMAs
+// of a chunk, then the loads of the chunk DEPTH later into the same slot;
+// the ring is unrolled over at most kSkinnyIters turns (the host checks that a
+// wave's share of K fits), so the code is straight-line and every wait is
+// for exactly the chunk it needs.
+// The waves' partial tiles are then summed through LDS in wave order (the
+// result does not depend on scheduling) and the epilogue runs on
+// row-contiguous groups of 4 columns: directly for bias / residual /
+// activation, else through the epilogue tape.
+constexpr int kBufferRaw = 0x00020000;   // buffer resource word 3, gfx9 raw buffer: 32-bit data format
+constexpr uint32_t kOutside = 0x80000000u;  // an offset past any resource's extent: reads zeros
+constexpr int kSkinnyIters = 4;              // turns of a wave's ring
+
+template <int BM, int BN, int WK, int DEPTH>
+__global__ __launch_bounds__(64 * WK) void gemm_skinny_kernel(const GemmArgs a) {
+  constexpr int FM = BM / 16, FN = BN / 16;
+  constexpr int CS = BN + 4;   // LDS row stride: 16-byte aligned rows
+  static_assert(BM % 16 == 0 && BN % 16 == 0, "tile of whole MFMA blocks");
+  static_assert(WK * BM * CS * 4 <= 160 * 1024, "LDS");
+  __shared__ __attribute__((aligned(16))) float red[WK * BM * CS];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int li = lane & 15, g = lane >> 4;
+  int tm, tn;
+  tile_coords(blockIdx.x, a, tm, tn);
+  const int bidx = blockIdx.y;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int chunks = (a.K + 15) / 16;
+  const int per_wave = (chunks + WK - 1) / WK;
+  const int c_begin = wave * per_wave;
+  const int c_end = min(chunks, c_begin + per_wave);
+  const int n_iter = (max(0, c_end - c_begin) + DEPTH - 1) / DEPTH;
+
+  // extents in bytes (the host checks both spans are below 2^29 elements)
+  const __amdgpu_buffer_rsrc_t ares = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)(a.A + (int64_t)bidx * a.sa_b), (short)0, (int)(((uint32_t)(a.M - 1) * (uint32_t)a.sa_m + a.K) * 4),
+      kBufferRaw);
+  const __amdgpu_buffer_rsrc_t bres = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)(a.B + (int64_t)bidx * a.sb_b), (short)0, (int)(((uint32_t)(a.N - 1) * (uint32_t)a.sb_n + a.K) * 4),
+      kBufferRaw);
+  uint32_t row_a[FM], row_b[FN];
+#pragma unroll
+  for (int fm = 0; fm < FM; ++fm) row_a[fm] = (uint32_t)min(m0 + fm * 16 + li, a.M - 1) * (uint32_t)a.sa_m * 4;
+#pragma unroll
+  for (int fn = 0; fn < FN; ++fn) row_b[fn] = (uint32_t)min(n0 + fn * 16 + li, a.N - 1) * (uint32_t)a.sb_n * 4;
+
+  float4 ra[DEPTH][FM], rb[DEPTH][FN];
+  auto load = [&](int c, int s) {   // chunk c_begin + c into ring slot s
+    const int k = (c_begin + c) * 16 + 4 * g;
+    const uint32_t kb = (c_begin + c < c_end && k < a.K) ? (uint32_t)k * 4 : kOutside;
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) {
+      const auto x = __builtin_amdgcn_raw_buffer_load_b128(ares, kb == kOutside ? kOutside : row_a[fm] + kb, 0, 0);
+      ra[s][fm] = make_float4(__uint_as_float(x[0]), __uint_as_float(x[1]), __uint_as_float(x[2]),
+                              __uint_as_float(x[3]));
+    }
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) {
+      const auto x = __builtin_amdgcn_raw_buffer_load_b128(bres, kb == kOutside ? kOutside : row_b[fn] + kb, 0, 0);
+      rb[s][fn] = make_float4(__uint_as_float(x[0]), __uint_as_float(x[1]), __uint_as_float(x[2]),
+                              __uint_as_float(x[3]));
+    }
+  };
+  auto part = [](const float4 &v, int j) { return j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w; };
+
+  f32x4 acc[FM][FN];
+#pragma unroll
+  for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) acc[fm][fn] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < DEPTH; ++s) load(s, s);
+  __builtin_amdgcn_sched_barrier(0);   // every first-turn load is issued before the first MFMA
+#pragma unroll
+  for (int it = 0; it < kSkinnyIters; ++it) {
+    if (it >= n_iter) break;
+#pragma unroll
+    for (int s = 0; s < DEPTH; ++s) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+          for (int fn = 0; fn < FN; ++fn)
+            acc[fm][fn] = Mfma<16>::mma(part(ra[s][fm], j), part(rb[s][fn], j), acc[fm][fn]);
+      // refill the slot right away (past the share: zeros, never used); the
+      // scheduling barrier keeps the compiler from sinking the loads to the
+      // end of the iteration, so DEPTH - 1 chunks stay in flight
+      __builtin_amdgcn_sched_barrier(0);
+      load((it + 1) * DEPTH + s, s);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  float *mine = red + wave * BM * CS;
+#pragma unroll
+  for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) mine[(fm * 16 + Mfma<16>::row(i, lane)) * CS + fn * 16 + li] = acc[fm][fn][i];
+  __syncthreads();
+  for (int q = threadIdx.x; q < BM * BN / 4; q += 64 * WK) {
+    const int r = q / (BN / 4), c = (q % (BN / 4)) * 4;
+    const int m = m0 + r, n = n0 + c;
+    if (m >= a.M || n >= a.N) continue;
+    float4 sum = *reinterpret_cast<const float4 *>(red + r * CS + c);
+#pragma unroll
+    for (int w = 1; w < WK; ++w) {
+      const float4 p = *reinterpret_cast<const float4 *>(red + w * BM * CS + r * CS + c);
+      sum.x += p.x, sum.y += p.y, sum.z += p.z, sum.w += p.w;
+    }
+    const int valid = min(4, a.N - n);
+    Vec<4> v;
+    v.v[0] = sum.x, v.v[1] = sum.y, v.v[2] = sum.z, v.v[3] = sum.w;
+    if (!a.direct) {
+      run_epilogue(a, bidx, m, n, valid, v);
+      continue;
+    }
+    // out = act((acc [+ bias]) [+ res]), as the tape computes it
+    auto operand = [&](int j) -> Vec<4> {
+      const float *p = a.eptr[j] + (int64_t)bidx * a.estride[j][0] + (int64_t)m * a.estride[j][1];
+      Vec<4> o;
+      if ((a.e_vec_mask >> j & 1) && valid == 4) {
+        const float4 t = *reinterpret_cast<const float4 *>(p + n);
+        o.v[0] = t.x, o.v[1] = t.y, o.v[2] = t.z, o.v[3] = t.w;
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o.v[i] = i < valid ? p[(int64_t)(n + i) * a.estride[j][2]] : 0.0f;
+      }
+      return o;
+    };
+    if (a.d_bias >= 0) {
+      const Vec<4> bv = operand(a.d_bias);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v.v[i] += bv.v[i];
+    }
+    if (a.d_res >= 0) {
+      const Vec<4> rv = operand(a.d_res);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v.v[i] = rv.v[i] + v.v[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (a.d_act == KH_OP_GELU_TANH) v.v[i] = op_gelu_tanh(v.v[i]);
+      else if (a.d_act == KH_OP_GELU_ERF) v.v[i] = op_gelu_erf(v.v[i]);
+      else if (a.d_act == KH_OP_RELU) v.v[i] = v.v[i] != v.v[i] ? v.v[i] : fmaxf(v.v[i], 0.0f);
+    }
+    float *o = a.eptr[a.d_out] + (int64_t)bidx * a.estride[a.d_out][0] + (int64_t)m * a.estride[a.d_out][1];
+    if ((a.e_vec_mask >> a.d_out & 1) && valid == 4) {
+      *reinterpret_cast<float4 *>(o + n) = make_float4(v.v[0], v.v[1], v.v[2], v.v[3]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (i < valid) o[(int64_t)(n + i) * a.estride[a.d_out][2]] = v.v[i];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Host side.
 
 struct TileCfg {
-  int bm, bn, bk, wm, wn, wk, mt, kind, stages, prec;  // kind 1: register-staged loads; 3: LDS-copy pipeline
+  int bm, bn, bk, wm, wn, wk, mt, kind, stages, prec;  // kind 1: register-staged loads; 3: LDS-copy pipeline;
+                                                       // 4: skinny-M direct loads ([N][K] B)
 };
 
 // Configurations by id. Ids 0-7: the copy pipeline (BK = 32, MFMA
@@ -889,6 +1064,17 @@ struct TileCfg {
   X(24, 128, 192, 64, 2, 4, 2)   \
   X(25, 64, 96, 64, 2, 2, 2)
 
+// skinny-M direct-load tiles (kind 4): BM x BN, WK waves splitting K
+#define KH_GEMM_SKINNY_CONFIGS(X) \
+  X(47, 16, 32, 8, 8)             \
+  X(48, 16, 32, 16, 4)            \
+  X(49, 32, 32, 8, 8)             \
+  X(50, 16, 64, 8, 4)             \
+  X(51, 32, 32, 16, 4)            \
+  X(52, 16, 16, 8, 8)             \
+  X(53, 32, 64, 8, 4)             \
+  X(54, 16, 32, 4, 8)
+
 // the register-staged configuration a pipelined tile falls back to for
 // operands too large for 32-bit copy offsets
 constexpr int kFallbackConfig = 8;
@@ -921,6 +1107,9 @@ constexpr TileCfg kConfigs[] = {
 #define KH_CFG3_ROW(id, bm, bn, bk, wm, wn, ns) {bm, bn, bk, wm, wn, 1, 16, 3, ns, KH_PREC_FP32},
     KH_GEMM3_W96_CONFIGS(KH_CFG3_ROW)
 #undef KH_CFG3_ROW
+#define KH_CFGS_ROW(id, bm, bn, wk, depth) {bm, bn, 16, 1, 1, wk, 16, 4, depth, KH_PREC_FP32},
+    KH_GEMM_SKINNY_CONFIGS(KH_CFGS_ROW)
+#undef KH_CFGS_ROW
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
@@ -946,6 +1135,12 @@ int tile_group(const TileCfg &t, int tiles_m) {
 
 hipError_t launch_config(int id, const GemmArgs &a, dim3 grid, hipStream_t stream) {
   switch (id) {
+#define KH_CFGS_CASE(cid, bm, bn, wk, depth)                                                            \
+  case cid:                                                                                            \
+    hipLaunchKernelGGL((gemm_skinny_kernel<bm, bn, wk, depth>), grid, dim3(64 * wk), 0, stream, a);       \
+    break;
+    KH_GEMM_SKINNY_CONFIGS(KH_CFGS_CASE)
+#undef KH_CFGS_CASE
 #define KH_CFG_CASE(cid, bm, bn, bk, wm, wn, wk, mt)                                                          \
   case cid:                                                                                                  \
     hipLaunchKernelGGL((gemm_f32_kernel<bm, bn, bk, wm, wn, wk, mt>), grid, dim3(64 * wm * wn * wk), 0, stream, \
@@ -1015,6 +1210,7 @@ class GemmOp final : public Op {
   dim3 grid;
   size_t n_partials = 0;
   bool a_vec_layout = false, b_vec_layout = false;
+  bool skinny = false;
   uint32_t e_vec_candidates = 0;
 
   hipError_t launch(float *const *ptrs, float *partials, hipStream_t stream) override {
@@ -1032,6 +1228,8 @@ class GemmOp final : public Op {
     a.ws_partial = partials;
     if (a.M == 0 || a.N == 0 || a.batch == 0) return hipSuccess;
     if (a.splitk > 1 && !partials) return hipErrorInvalidValue;
+    // the skinny kernel reads A and B only as 16-byte pieces
+    if (skinny && !(a.a_vec && a.b_vec)) return hipErrorInvalidValue;
     const hipError_t e = launch_config(cfg, a, grid, stream);
     if (e != hipSuccess || a.splitk == 1) return e;
     return launch_splitk_reduce(a, current_device().cus, stream);
@@ -1206,6 +1404,32 @@ std::unique_ptr<Op> make_gemm(const kh_launch &L, std::string &err, bool &unsupp
     }
     op->b_vec_layout = true;
   }
+  if (t.kind == 4) {
+    // skinny-M direct loads: A row-major with unit K stride, B the
+    // [batch][N][K] copy, both read as whole 16-byte pieces; K is not split
+    const kh_ref &ra = L.refs[0], &rb = L.refs[1];
+    op->b_vec_layout = a.sb_k == 1 && rb.offset % 4 == 0 && a.sb_n % 4 == 0 && a.sb_b % 4 == 0 && a.sb_n >= K;
+    if (!op->a_vec_layout || !op->b_vec_layout || K % 4 || ra.offset % 4) {
+      err = "matmul: skinny configuration " + std::to_string(cfg) +
+            " needs A [.., M, K] and B [batch][N][K] with unit K stride, 16-byte aligned rows and K % 4 == 0";
+      return nullptr;
+    }
+    // buffer-load byte offsets are 32-bit (and must stay below the
+    // out-of-range marker)
+    const int64_t span_a = std::max<int64_t>(0, M - 1) * a.sa_m + K, span_b = std::max<int64_t>(0, N - 1) * a.sb_n + K;
+    if (span_a >= (1ll << 29) || span_b >= (1ll << 29)) {
+      unsupported = true;
+      err = "matmul: skinny configuration with an operand spanning 2^29 elements or more";
+      return nullptr;
+    }
+    // a wave's share of K must fit the unrolled ring
+    const int64_t share = ((K + 15) / 16 + t.wk - 1) / t.wk;
+    if (share > (int64_t)t.stages * kSkinnyIters) {
+      unsupported = true;
+      err = "matmul: K = " + std::to_string(K) + " is too deep for skinny configuration " + std::to_string(cfg);
+      return nullptr;
+    }
+  }
   if (t.kind == 3) {
     // 128-bit copies never straddle the end of a row or of K
     op->a_vec_layout = op->a_vec_layout && K % 4 == 0;
@@ -1226,7 +1450,7 @@ std::unique_ptr<Op> make_gemm(const kh_launch &L, std::string &err, bool &unsupp
   const TileCfg &tr = kConfigs[cfg_run];
   a.tiles_m = (int)((M + tr.bm - 1) / tr.bm);
   a.tiles_n = (int)((N + tr.bn - 1) / tr.bn);
-  int splitk = std::max(1, L.cfg[2]);
+  int splitk = tr.kind == 4 ? 1 : std::max(1, L.cfg[2]);
   const int k_steps = (int)std::max<int64_t>(1, (K + tr.bk - 1) / tr.bk);
   splitk = std::min(splitk, k_steps);
   a.k_per_split = ((k_steps + splitk - 1) / splitk) * tr.bk;
@@ -1240,6 +1464,7 @@ std::unique_ptr<Op> make_gemm(const kh_launch &L, std::string &err, bool &unsupp
     return nullptr;
   }
   a.group_m = tile_group(tr, a.tiles_m);
+  op->skinny = tr.kind == 4;
   op->cfg = cfg_run;
   op->grid = dim3((unsigned)n_tiles, (unsigned)batch, (unsigned)splitk);
   if (splitk > 1) {

@@ -647,11 +647,13 @@ class _Lowerer:
         d = self.new_desc(kl.FAM_GEMV if gemv else kl.FAM_GEMM, "gemv" if gemv else "matmul", k, space3)
         d.gemm[0], d.gemm[1], d.gemm[2], d.gemm[3] = batch, m, n, kk
         d.refs[0] = ref3(a_src, (batch, m, kk))
-        derived_b = prec in ("bf16", "bf16x3") or (gemv and self.layouts[b].base[0] == "const" and kk % 4 == 0)
+        skinny = not gemv and int(cfg.get("tile", -1)) in autotune.SKINNY
+        nk = (gemv and self.layouts[b].base[0] == "const" and kk % 4 == 0) or skinny
+        derived_b = prec in ("bf16", "bf16x3") or nk
         d.refs[1] = ref3(b, (batch, kk, n), register=not derived_b)
         if prec in ("bf16", "bf16x3"):
             d.refs[1] = self.bf16_weight(b, d.refs[1], batch, kk, n, split=prec == "bf16x3")
-        elif gemv and self.layouts[b].base[0] == "const" and kk % 4 == 0:
+        elif nk:
             d.refs[1] = self.nk_weight(b, d.refs[1], batch, kk, n)
         externals = []
         for nd in k.nodes:
@@ -769,8 +771,24 @@ class _Lowerer:
                 # bf16 inputs need B as a build-time bf16 copy of a constant; a
                 # matmul on two activations stays on the fp32 path (more exact)
                 prec = "fp32"
+            tile = int(cfg.get("tile", -1))
+            if tile in autotune.SKINNY and not (self.skinny_ok(mm) and
+                                                autotune.skinny_fits(mm.inputs[0].shape[-2], mm.inputs[0].shape[-1], tile)):
+                a, b = mm.inputs
+                batch = math.prod(a.shape[:-2]) if a.type.rank == 3 else 1
+                cfg = autotune.default_config_for(batch, a.shape[-2], b.shape[-1], a.shape[-1], precision=prec,
+                                                  skinny=False)
             self._cfg[k] = (cfg, prec)
         return self._cfg[k]
+
+    def skinny_ok(self, mm) -> bool:
+        """The skinny-M GEMM reads B as a build-time [batch][N][K] copy of a
+        constant and A as 16-byte pieces along K (unit K stride)."""
+        a, b = mm.inputs
+        la, lb = self.layouts.get(a), self.layouts.get(b)
+        return (la is not None and lb is not None and lb.base[0] == "const" and a.shape[-1] % 4 == 0
+                and la.strides[-1] == 1 and la.offset % 4 == 0
+                and all(st % 4 == 0 for st, ext in zip(la.strides[:-1], la.shape[:-1]) if ext > 1))
 
     def _arena_range(self, v):
         """Byte range [lo, hi) of v's storage in the arena, or None."""
@@ -840,8 +858,9 @@ class _Lowerer:
 
     def nk_weight(self, b, ref, batch, kk, n):
         """Ref of an fp32 [batch][N][K] copy of constant view `b` (fp32 ref
-        `ref` over (b, k, n)) for the GEMV family: each output column's
-        weights become one contiguous row, which the K-contiguous GEMV kernel
+        `ref` over (b, k, n)) for the GEMV family and the skinny-M GEMM: each
+        output column's weights become one contiguous row, which the
+        K-contiguous GEMV kernel
         reads 1 KiB per wave load. Registered as a derived constant, made when
         the executable is built."""
         src = self.layouts[b].base[1]

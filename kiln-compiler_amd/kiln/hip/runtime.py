@@ -171,6 +171,8 @@ class HIPExecutable:
                 raise ValueError(f"Kiln was compiled for input shape {shape}, got {tuple(t.shape)} (input {i})")
             if t.device != self.device or t.dtype != torch.float32 or not t.is_contiguous():
                 t = t.detach().to(device=self.device, dtype=torch.float32).contiguous()
+            if t.data_ptr() % 16:   # kernels read rows as 16-byte pieces
+                t = t.clone()
             ready.append(t)
         return ready
 

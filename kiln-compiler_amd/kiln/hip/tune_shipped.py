@@ -49,16 +49,21 @@ def main(argv=None):
     p.add_argument("--out", default=str(autotune.SHIPPED_PATH))
     p.add_argument("--precision", nargs="+", choices=("fp32", "bf16", "bf16x3"), default=None,
                    help="re-tune only these precisions and keep the table's other entries")
+    p.add_argument("--max-m", type=int, default=None,
+                   help="re-tune only shapes with at most this many rows and keep the table's other entries")
     args = p.parse_args(argv)
     warm_up()
+    shapes = [s for s in SHAPES if args.max_m is None or s[0] <= args.max_m]
+    precisions = args.precision or ("fp32", "bf16", "bf16x3")
     table = {}
-    if args.precision:
-        keep = autotune.shipped_configs()
-        table = {k: v for k, v in keep.items() if k.split("|")[-2] not in args.precision}
-    for precision in args.precision or ("fp32", "bf16", "bf16x3"):
+    if args.precision or args.max_m is not None:
+        retuned = {(p_, f"1x{m}x{n}x{k}") for p_ in precisions for m, n, k in shapes}
+        table = {key: v for key, v in autotune.shipped_configs().items()
+                 if (key.split("|")[-2], key.split("|")[-1]) not in retuned}
+    for precision in precisions:
         tuner = autotune.GPUAutotuner(precision=precision, use_cache=False, use_shipped=False)
         device = tuner.device_key()
-        for m, n, k in SHAPES:
+        for m, n, k in shapes:
             entry = tuner.tune(1, m, n, k, autotune.default_config_for(1, m, n, k, precision=precision))
             if entry["candidates"]:
                 table[f"{device}|{precision}|1x{m}x{n}x{k}"] = entry

@@ -290,6 +290,31 @@ def test_every_gemm_tile_configuration(tile):
             np.testing.assert_allclose(out, ref, rtol=RTOL, atol=ATOL)
 
 
+@pytest.mark.parametrize("tile", sorted(autotune.SKINNY))
+def test_every_skinny_gemm_configuration(tile):
+    # skinny-M direct-load kernel: ragged M / N, K a multiple of 4 but not of
+    # 16 or of the waves' share, batched constant weights, bias + residual and
+    # GELU epilogues; repeated launches agree bit for bit (the waves' partial
+    # tiles are summed in a fixed order)
+    cfg = lambda *_: {"tile": tile, "splitk": 1}
+    for m, n, k in ((21, 40, 68), (128, 768, 768), (77, 133, 1000)):
+        torch.manual_seed(m + n + k)
+        lin = gpt2_init_(torch.nn.Linear(k, n), seed=k).eval()
+        x, r = torch.randn(m, k), torch.randn(m, n)
+        fn = lambda t, res: lin(t) + res
+        c = kiln.compile(fn, (x, r), device="cuda", cuda_graphs=False, gpu_matmul_config=cfg)
+        assert f"tile {tile} splitk 1" in c._exe.program.launches[0].summary
+        out = c(x, r)
+        ref = oracle.linear(x.numpy(), lin.weight.detach().numpy().T, lin.bias.detach().numpy(), r.numpy())
+        np.testing.assert_allclose(out.cpu().numpy(), ref, rtol=RTOL, atol=ATOL)
+        for _ in range(3):
+            assert torch.equal(c(x, r), out)
+    model = _BatchedConstant(3, 96, 50).eval()
+    x = torch.randn(3, 24, 96)
+    c = check(model, x, gpu_matmul_config=cfg)
+    assert f"tile {tile} splitk 1" in c._exe.program.launches[0].summary
+
+
 @pytest.mark.parametrize("variant", range(6))
 def test_gemv_variants_and_ragged_sizes(variant):
     # M = 1: every column-block width (0 = chosen from the shape), with and

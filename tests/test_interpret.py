@@ -126,3 +126,18 @@ def test_interpreter_is_never_a_gpu_path():
 
     with pytest.raises(RuntimeError, match="KILN_HIP_INTERPRET"):
         refuse("bench.py")
+
+
+@pytest.mark.parametrize("tile", [47, 49, 53])
+def test_skinny_gemm_lowering(tile):
+    # skinny-M configurations read the weight as a [N][K] copy; a product of
+    # two activations cannot use them and keeps a tiled configuration
+    lin = gpt2_init_(torch.nn.Linear(68, 40), seed=1).eval()
+    x = torch.randn(21, 68)
+    model = torch.nn.Sequential(lin, torch.nn.GELU(approximate="tanh")).eval()
+    c = check(model, x, gpu_matmul_config=lambda *_: {"tile": tile, "splitk": 3})
+    (launch,) = c._exe.program.launches
+    assert f"tile {tile} splitk" in launch.summary and any("@nk:" in n for n in c._exe.program.derived)
+    c2 = check(lambda a, b: a @ b, torch.randn(21, 68), torch.randn(68, 40),
+               gpu_matmul_config=lambda *_: {"tile": tile, "splitk": 1})
+    assert f"tile {tile} " not in c2._exe.program.launches[0].summary
