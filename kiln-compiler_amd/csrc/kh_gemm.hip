@@ -39,56 +39,11 @@
 
 #include "kh_common.hpp"
 #include "kh_gemm_args.hpp"
+#include "kh_gemm_dev.hpp"
 #include "kh_internal.hpp"
 
 namespace kh {
 namespace {
-
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-
-template <int MT>
-struct Mfma;
-
-template <>
-struct Mfma<32> {
-  typedef f32x16 acc_t;
-  static constexpr int kRegs = 16;
-  __device__ static acc_t mma(float a, float b, acc_t c) { return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0); }
-  // Row within the 32x32 block held by accumulator register i of `lane`
-  // (the column is lane % 32).
-  __device__ static int row(int i, int lane) { return (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3); }
-};
-
-template <>
-struct Mfma<16> {
-  typedef f32x4 acc_t;
-  static constexpr int kRegs = 4;
-  __device__ static acc_t mma(float a, float b, acc_t c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); }
-  __device__ static int row(int i, int lane) { return (lane >> 4) * 4 + i; }
-};
-
-// XCD-aware tile order: hardware hands consecutive workgroup ids to the 8 XCDs
-// round-robin; remap so XCD x sees a contiguous range of tiles.
-__device__ __forceinline__ int xcd_remap(int id, int n) {
-  constexpr int kXcd = 8;
-  if (n % kXcd) return id;
-  return (id % kXcd) * (n / kXcd) + id / kXcd;
-}
-
-// Tile coordinates of workgroup `id`: the XCD remap, then the tile range
-// walked `group_m` tile rows at a time, column-major inside a group, so the
-// workgroups one XCD holds at once share a few A row panels and a narrow band
-// of B column panels (both stay in that XCD's 4 MB L2). group_m = 1 is
-// row-major order.
-__device__ __forceinline__ void tile_coords(int id, const GemmArgs &a, int &tm, int &tn) {
-  const int tile = xcd_remap(id, a.tiles_m * a.tiles_n);
-  const int span = a.group_m * a.tiles_n;
-  const int g = tile / span, r = tile - g * span;
-  const int rows = min(a.group_m, a.tiles_m - g * a.group_m);
-  tm = g * a.group_m + r % rows;
-  tn = r / rows;
-}
 
 template <int BM, int BN, int BK, int WM, int WN, int WK, int MT>
 __global__ __launch_bounds__(64 * WM * WN * WK) void gemm_f32_kernel(const GemmArgs a) {
@@ -361,60 +316,6 @@ __global__ __launch_bounds__(64 * WM * WN * WK) void gemm_f32_kernel(const GemmA
 //   * the epilogue stages the accumulators through LDS per 16-row block and
 //     runs the tape on row-contiguous groups of 4 (coalesced 128-bit operand
 //     loads and stores).
-typedef __attribute__((address_space(3))) void lds_void_t;
-
-__device__ __forceinline__ int swz_a(int r) { return (r ^ (r >> 3)) & 7; }
-// A rows of CH 16-byte chunks (CH = 8 for 32 floats, 16 for 64)
-template <int CH>
-__device__ __forceinline__ int swz_rows(int r) {
-  if constexpr (CH == 8) return swz_a(r);
-  else return (r ^ (r >> 4)) & (CH - 1);
-}
-
-// One wave-wide copy: lane l's VW floats at base + voff bytes go to LDS
-// byte address lds + l * 4 * VW (M0 holds the wave's LDS destination, `base`
-// is wave-uniform in SGPRs, `voff` a per-lane 32-bit byte offset). Issued as
-// inline assembly: the compiler's wait insertion would otherwise make every
-// LDS read wait for all copies in flight (it cannot tell the stages apart),
-// which would undo the two-step lead; the kernel waits for the copies it
-// needs itself.
-template <int VW>
-__device__ __forceinline__ void copy_to_lds(const float *base, uint32_t voff, uint32_t lds_addr) {
-  const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_addr);
-  if constexpr (VW == 4)
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds)
-                 : "memory", "m0");
-  else
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(base), "s"(lds)
-                 : "memory", "m0");
-}
-
-__device__ __forceinline__ const float *uniform_ptr(const float *p) {
-  const uint64_t v = (uint64_t)(uintptr_t)p;
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-  return (const float *)(uintptr_t)(((uint64_t)hi << 32) | lo);
-}
-
-// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
-// vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
-// Workgroup barrier for the copy pipeline: LDS writes of this wave complete,
-// then s_barrier. Unlike __syncthreads() it does not wait for outstanding
-// global loads (the copies of the step after next stay in flight); the
-// copies a stage depends on are waited for explicitly (wait_vmcnt) before it.
-__device__ __forceinline__ void stage_barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt((3 << 14) | (7 << 4) | 15);  // lgkmcnt(0); vmcnt, expcnt unconstrained
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
 // B rows of a bf16 stage are BK K values = BK / 8 chunks of 16 bytes; row n
 // puts chunk c at c ^ swz_b16<CB>(n), so the 16 rows one 128-bit fragment
 // read touches hit distinct banks (64 banks of 4 bytes: 4, 2 or 1 rows of
@@ -826,8 +727,6 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void gemm3_f32_kernel(const GemmAr
 // result does not depend on scheduling) and the epilogue runs on
 // row-contiguous groups of 4 columns: directly for bias / residual /
 // activation, else through the epilogue tape.
-constexpr int kBufferRaw = 0x00020000;   // buffer resource word 3, gfx9 raw buffer: 32-bit data format
-constexpr uint32_t kOutside = 0x80000000u;  // an offset past any resource's extent: reads zeros
 constexpr int kSkinnyIters = 4;              // turns of a wave's ring
 
 template <int BM, int BN, int WK, int DEPTH>
@@ -980,7 +879,8 @@ __global__ __launch_bounds__(64 * WK) void gemm_skinny_kernel(const GemmArgs a) 
 
 struct TileCfg {
   int bm, bn, bk, wm, wn, wk, mt, kind, stages, prec;  // kind 1: register-staged loads; 3: LDS-copy pipeline;
-                                                       // 4: skinny-M direct loads ([N][K] B)
+                                                       // 4: skinny-M direct loads ([N][K] B); 5: one
+                                                       // workgroup per CU, A and B K-contiguous ([N][K] B)
 };
 
 // Configurations by id. Ids 0-7: the copy pipeline (BK = 32, MFMA
@@ -1110,6 +1010,9 @@ constexpr TileCfg kConfigs[] = {
 #define KH_CFGS_ROW(id, bm, bn, wk, depth) {bm, bn, 16, 1, 1, wk, 16, 4, depth, KH_PREC_FP32},
     KH_GEMM_SKINNY_CONFIGS(KH_CFGS_ROW)
 #undef KH_CFGS_ROW
+#define KH_CFGNT_ROW(id, bm, bn, wm, wn, ns) {bm, bn, 32, wm, wn, 1, 16, 5, ns, KH_PREC_FP32},
+    KH_GEMM_NT_CONFIGS(KH_CFGNT_ROW)
+#undef KH_CFGNT_ROW
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
@@ -1121,7 +1024,8 @@ constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 // on the GPT-2 block's shapes against row-major order (interleaved, warm
 // GPU): 2048x3072x768 on the 32x64 tile 5% faster, the others within 1%.
 int tile_group(const TileCfg &t, int tiles_m) {
-  const int lds = t.kind == 3 ? 4 * t.stages * (t.bm * t.bk + (t.prec == KH_PREC_FP32 ? t.bk * t.bn
+  const int lds = t.kind == 5 ? 4 * t.stages * t.bk * (t.bm + t.bn)
+                  : t.kind == 3 ? 4 * t.stages * (t.bm * t.bk + (t.prec == KH_PREC_FP32 ? t.bk * t.bn
                                                                  : t.bn * t.bk / 2 * (t.prec == KH_PREC_BF16X3 ? 2 : 1)))
                               : 8 * (t.bm * (t.bk + 4) + t.bn * (t.bk + 2));
   const int per_cu = std::max(1, std::min(4, 163840 / std::max(1, lds)));
@@ -1198,7 +1102,7 @@ hipError_t launch_config(int id, const GemmArgs &a, dim3 grid, hipStream_t strea
 #undef KH_CFGBD_CASE
 #undef KH_CFGXD_CASE
 #undef KH_CFGD_CASE
-    default: return hipErrorInvalidValue;
+    default: return launch_gemm_nt(id, a, grid, stream);
   }
   return hipGetLastError();
 }
@@ -1210,7 +1114,7 @@ class GemmOp final : public Op {
   dim3 grid;
   size_t n_partials = 0;
   bool a_vec_layout = false, b_vec_layout = false;
-  bool skinny = false;
+  bool k_major = false;   // kinds 4 and 5: A and B both K-contiguous
   uint32_t e_vec_candidates = 0;
 
   hipError_t launch(float *const *ptrs, float *partials, hipStream_t stream) override {
@@ -1228,8 +1132,8 @@ class GemmOp final : public Op {
     a.ws_partial = partials;
     if (a.M == 0 || a.N == 0 || a.batch == 0) return hipSuccess;
     if (a.splitk > 1 && !partials) return hipErrorInvalidValue;
-    // the skinny kernel reads A and B only as 16-byte pieces
-    if (skinny && !(a.a_vec && a.b_vec)) return hipErrorInvalidValue;
+    // the skinny and K-contiguous kernels read A and B only as 16-byte pieces
+    if (k_major && !(a.a_vec && a.b_vec)) return hipErrorInvalidValue;
     const hipError_t e = launch_config(cfg, a, grid, stream);
     if (e != hipSuccess || a.splitk == 1) return e;
     return launch_splitk_reduce(a, current_device().cus, stream);
@@ -1404,14 +1308,16 @@ std::unique_ptr<Op> make_gemm(const kh_launch &L, std::string &err, bool &unsupp
     }
     op->b_vec_layout = true;
   }
-  if (t.kind == 4) {
-    // skinny-M direct loads: A row-major with unit K stride, B the
-    // [batch][N][K] copy, both read as whole 16-byte pieces; K is not split
+  if (t.kind == 4 || t.kind == 5) {
+    // skinny-M direct loads / K-contiguous pipeline: A row-major with unit K
+    // stride, B the [batch][N][K] copy, both read as whole 16-byte pieces; K
+    // is not split (and is a whole number of 32-deep steps for kind 5)
     const kh_ref &ra = L.refs[0], &rb = L.refs[1];
     op->b_vec_layout = a.sb_k == 1 && rb.offset % 4 == 0 && a.sb_n % 4 == 0 && a.sb_b % 4 == 0 && a.sb_n >= K;
-    if (!op->a_vec_layout || !op->b_vec_layout || K % 4 || ra.offset % 4) {
-      err = "matmul: skinny configuration " + std::to_string(cfg) +
-            " needs A [.., M, K] and B [batch][N][K] with unit K stride, 16-byte aligned rows and K % 4 == 0";
+    if (!op->a_vec_layout || !op->b_vec_layout || K % (t.kind == 5 ? 32 : 4) || ra.offset % 4) {
+      err = "matmul: configuration " + std::to_string(cfg) +
+            " needs A [.., M, K] and B [batch][N][K] with unit K stride, 16-byte aligned rows and K a multiple of " +
+            std::to_string(t.kind == 5 ? 32 : 4);
       return nullptr;
     }
     // buffer-load byte offsets are 32-bit (and must stay below the
@@ -1419,12 +1325,12 @@ std::unique_ptr<Op> make_gemm(const kh_launch &L, std::string &err, bool &unsupp
     const int64_t span_a = std::max<int64_t>(0, M - 1) * a.sa_m + K, span_b = std::max<int64_t>(0, N - 1) * a.sb_n + K;
     if (span_a >= (1ll << 29) || span_b >= (1ll << 29)) {
       unsupported = true;
-      err = "matmul: skinny configuration with an operand spanning 2^29 elements or more";
+      err = "matmul: K-contiguous configuration with an operand spanning 2^29 elements or more";
       return nullptr;
     }
-    // a wave's share of K must fit the unrolled ring
+    // a skinny wave's share of K must fit the unrolled ring
     const int64_t share = ((K + 15) / 16 + t.wk - 1) / t.wk;
-    if (share > (int64_t)t.stages * kSkinnyIters) {
+    if (t.kind == 4 && share > (int64_t)t.stages * kSkinnyIters) {
       unsupported = true;
       err = "matmul: K = " + std::to_string(K) + " is too deep for skinny configuration " + std::to_string(cfg);
       return nullptr;
@@ -1450,7 +1356,7 @@ std::unique_ptr<Op> make_gemm(const kh_launch &L, std::string &err, bool &unsupp
   const TileCfg &tr = kConfigs[cfg_run];
   a.tiles_m = (int)((M + tr.bm - 1) / tr.bm);
   a.tiles_n = (int)((N + tr.bn - 1) / tr.bn);
-  int splitk = tr.kind == 4 ? 1 : std::max(1, L.cfg[2]);
+  int splitk = tr.kind == 4 || tr.kind == 5 ? 1 : std::max(1, L.cfg[2]);
   const int k_steps = (int)std::max<int64_t>(1, (K + tr.bk - 1) / tr.bk);
   splitk = std::min(splitk, k_steps);
   a.k_per_split = ((k_steps + splitk - 1) / splitk) * tr.bk;
@@ -1464,7 +1370,7 @@ std::unique_ptr<Op> make_gemm(const kh_launch &L, std::string &err, bool &unsupp
     return nullptr;
   }
   a.group_m = tile_group(tr, a.tiles_m);
-  op->skinny = tr.kind == 4;
+  op->k_major = tr.kind == 4 || tr.kind == 5;
   op->cfg = cfg_run;
   op->grid = dim3((unsigned)n_tiles, (unsigned)batch, (unsigned)splitk);
   if (splitk > 1) {

@@ -128,6 +128,22 @@ inline hipError_t launch_splitk_reduce(const GemmArgs &a, int cus, hipStream_t s
 }
 }  // namespace
 
+// Configurations of the K-contiguous fp32 kernel (kind 5, kh_gemm_nt.hip):
+// id, macro tile BM x BN (K step 32), waves WM x WN (one or two per SIMD,
+// one workgroup per CU), LDS stages NS.
+#define KH_GEMM_NT_CONFIGS(X) \
+  X(55, 128, 192, 2, 2, 3)    \
+  X(56, 64, 288, 2, 2, 3)     \
+  X(57, 64, 96, 2, 2, 3)      \
+  X(58, 128, 96, 2, 2, 3)     \
+  X(59, 128, 128, 2, 2, 3)    \
+  X(60, 64, 192, 2, 2, 3)     \
+  X(61, 128, 192, 2, 4, 3)    \
+  X(62, 64, 128, 2, 2, 3)
+
+// Launch configuration `id` of kind 5 (hipErrorInvalidValue for another id).
+hipError_t launch_gemm_nt(int id, const GemmArgs &a, dim3 grid, hipStream_t stream);
+
 // Host: validate the epilogue refs/tape of a matmul descriptor into `a`.
 bool fill_epilogue(const kh_launch &L, GemmArgs &a, uint32_t &vec_candidates, std::string &err);
 // Recognise the tape out = act((acc [+ bias]) [+ res]) and fill the direct

@@ -1,0 +1,121 @@
+// kh_gemm_dev.hpp - device helpers shared by the matmul kernels: MFMA
+// shapes, the XCD-aware tile order, and the global -> LDS copy pipeline
+// primitives (copy instructions, counter waits, the stage barrier, LDS chunk
+// swizzles).
+#pragma once
+
+#include "kh_gemm_args.hpp"
+
+namespace kh {
+namespace {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+template <int MT>
+struct Mfma;
+
+template <>
+struct Mfma<32> {
+  typedef f32x16 acc_t;
+  static constexpr int kRegs = 16;
+  __device__ static acc_t mma(float a, float b, acc_t c) { return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0); }
+  // Row within the 32x32 block held by accumulator register i of `lane`
+  // (the column is lane % 32).
+  __device__ static int row(int i, int lane) { return (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3); }
+};
+
+template <>
+struct Mfma<16> {
+  typedef f32x4 acc_t;
+  static constexpr int kRegs = 4;
+  __device__ static acc_t mma(float a, float b, acc_t c) { return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0); }
+  __device__ static int row(int i, int lane) { return (lane >> 4) * 4 + i; }
+};
+
+// XCD-aware tile order: hardware hands consecutive workgroup ids to the 8 XCDs
+// round-robin; remap so XCD x sees a contiguous range of tiles.
+__device__ __forceinline__ int xcd_remap(int id, int n) {
+  constexpr int kXcd = 8;
+  if (n % kXcd) return id;
+  return (id % kXcd) * (n / kXcd) + id / kXcd;
+}
+
+// Tile coordinates of workgroup `id`: the XCD remap, then the tile range
+// walked `group_m` tile rows at a time, column-major inside a group, so the
+// workgroups one XCD holds at once share a few A row panels and a narrow band
+// of B column panels (both stay in that XCD's 4 MB L2). group_m = 1 is
+// row-major order.
+__device__ __forceinline__ void tile_coords(int id, const GemmArgs &a, int &tm, int &tn) {
+  const int tile = xcd_remap(id, a.tiles_m * a.tiles_n);
+  const int span = a.group_m * a.tiles_n;
+  const int g = tile / span, r = tile - g * span;
+  const int rows = min(a.group_m, a.tiles_m - g * a.group_m);
+  tm = g * a.group_m + r % rows;
+  tn = r / rows;
+}
+
+// ---------------------------------------------------------------------------
+// Copy-pipeline primitives. Global memory is copied straight into LDS
+// (global_load_lds, 128-bit per lane for aligned row-major operands, 32-bit
+// for any other strides); LDS holds 16-byte chunks, XOR-swizzled per row so
+// the 128-bit fragment reads of 16 consecutive rows hit distinct banks.
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+__device__ __forceinline__ int swz_a(int r) { return (r ^ (r >> 3)) & 7; }
+// A rows of CH 16-byte chunks (CH = 8 for 32 floats, 16 for 64)
+template <int CH>
+__device__ __forceinline__ int swz_rows(int r) {
+  if constexpr (CH == 8) return swz_a(r);
+  else return (r ^ (r >> 4)) & (CH - 1);
+}
+
+// One wave-wide copy: lane l's VW floats at base + voff bytes go to LDS
+// byte address lds + l * 4 * VW (M0 holds the wave's LDS destination, `base`
+// is wave-uniform in SGPRs, `voff` a per-lane 32-bit byte offset). Issued as
+// inline assembly: the compiler's wait insertion would otherwise make every
+// LDS read wait for all copies in flight (it cannot tell the stages apart),
+// which would undo the two-step lead; the kernel waits for the copies it
+// needs itself.
+template <int VW>
+__device__ __forceinline__ void copy_to_lds(const float *base, uint32_t voff, uint32_t lds_addr) {
+  const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_addr);
+  if constexpr (VW == 4)
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds)
+                 : "memory", "m0");
+  else
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(base), "s"(lds)
+                 : "memory", "m0");
+}
+
+__device__ __forceinline__ const float *uniform_ptr(const float *p) {
+  const uint64_t v = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (const float *)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
+// vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt_hi[15:14]).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Workgroup barrier for the copy pipeline: LDS writes of this wave complete,
+// then s_barrier. Unlike __syncthreads() it does not wait for outstanding
+// global loads (the copies of the step after next stay in flight); the
+// copies a stage depends on are waited for explicitly (wait_vmcnt) before it.
+__device__ __forceinline__ void stage_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt((3 << 14) | (7 << 4) | 15);  // lgkmcnt(0); vmcnt, expcnt unconstrained
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+constexpr int kBufferRaw = 0x00020000;   // buffer resource word 3, gfx9 raw buffer: 32-bit data format
+constexpr uint32_t kOutside = 0x80000000u;  // an offset past any resource's extent: reads zeros
+
+}  // namespace
+}  // namespace kh

@@ -1,0 +1,254 @@
+// kh_gemm_nt.hip - fp32 matmul over a constant weight read through its
+// [batch][N][K] copy (configuration kind 5), for the large products of a
+// transformer block: C[b] = epilogue(A[b] @ B[b]) with both operands
+// K-contiguous in memory.
+//
+// Same contract as the other members of the matmul family (the reference's
+// tl.dot kernel with fused epilogue, kiln/gpu/codegen.py:484-530); what
+// differs is the shape of the work on a CU:
+//   * one workgroup per CU, its waves one per SIMD (or two), each owning a
+//     large wave tile (up to 64 x 96: 24 MFMA blocks of 16 x 16), so a K step
+//     of 32 is 8 x FM x FN v_mfma_f32_16x16x4_f32 per wave between barriers
+//     (192 for the largest tile, ~6000 matrix cycles);
+//   * A and B rows both hold K contiguously, so both are copied into LDS with
+//     the same 128-bit global_load_lds pattern (rows of 32 floats = 8 chunks
+//     of 16 bytes, chunk c of row r at c ^ swz_a(r)) and both fragments are
+//     read as two 128-bit LDS vectors per row: lane (row li, group g) takes K
+//     values 8g .. 8g+7 of its A row and of its B row, and MFMA j of a step
+//     consumes value 8g + j in every group (the K order is permuted the same
+//     way for A and B; a dot product does not depend on it);
+//   * a ring of NS LDS stages, copies issued NS - 1 steps ahead; the barrier
+//     that publishes stage s + 1 sits in the middle of step s's MFMAs, and
+//     the fragment reads of stage s + 1 follow it, so they run under the
+//     second half of step s's MFMAs and the next step starts with its
+//     operands in registers (two register sets of fragments, one per half
+//     step, each loaded while the other feeds the MFMAs);
+//   * the epilogue runs straight from the accumulators for bias / residual /
+//     activation tapes, else stages 16-row blocks through LDS for the tape.
+// K must be a multiple of 32 and the operands' spans below 2^29 elements (the
+// host checks both; other shapes use the other kernels of the family).
+#include <algorithm>
+
+#include "kh_common.hpp"
+#include "kh_gemm_args.hpp"
+#include "kh_gemm_dev.hpp"
+#include "kh_internal.hpp"
+
+namespace kh {
+namespace {
+
+template <int BM, int BN, int WM, int WN, int NS>
+__global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM * WN / 4, WM * WN / 4)))
+void gemm_nt_kernel(const GemmArgs a) {
+  constexpr int BK = 32, MT = 16, ACH = BK / 4;
+  constexpr int kWaves = WM * WN;
+  constexpr int TM = BM / WM, TN = BN / WN, FM = TM / MT, FN = TN / MT;
+  constexpr int A_FLOATS = BM * BK, STAGE = (BM + BN) * BK;
+  constexpr int A_PER_WAVE = BM * ACH / 64 / kWaves, B_PER_WAVE = BN * ACH / 64 / kWaves;
+  constexpr int COPIES = A_PER_WAVE + B_PER_WAVE;
+  static_assert(TM % MT == 0 && TN % MT == 0, "wave tile of whole MFMA blocks");
+  static_assert((BM * ACH) % (64 * kWaves) == 0 && (BN * ACH) % (64 * kWaves) == 0, "copy mapping");
+  static_assert(NS >= 2 && NS <= 4 && (NS - 2) * COPIES < 64, "ring depth / vmcnt range");
+  static_assert(NS * STAGE * 4 <= 160 * 1024, "LDS");
+  static_assert(kWaves % 4 == 0, "whole SIMDs");
+
+  __shared__ float4 ring[NS * STAGE / 4];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  const int wm = wave / WN, wn = wave % WN;
+  int tm, tn;
+  tile_coords(blockIdx.x, a, tm, tn);
+  const int bidx = blockIdx.y;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const float *Ab = a.A + (int64_t)bidx * a.sa_b;
+  const float *Bb = a.B + (int64_t)bidx * a.sb_b;
+  const int n_steps = a.K / BK;
+
+  // per-lane copy sources: byte offsets from the step's first K column (rows
+  // past M / N clamped to the last one; their results are never stored)
+  uint32_t a_off[A_PER_WAVE], b_off[B_PER_WAVE];
+#pragma unroll
+  for (int i = 0; i < A_PER_WAVE; ++i) {
+    const int p = (wave * A_PER_WAVE + i) * 64 + lane;
+    const int r = p / ACH;
+    a_off[i] = (uint32_t)(min(m0 + r, a.M - 1) * (int)a.sa_m + ((p % ACH) ^ swz_a(r)) * 4) * 4u;
+  }
+#pragma unroll
+  for (int i = 0; i < B_PER_WAVE; ++i) {
+    const int p = (wave * B_PER_WAVE + i) * 64 + lane;
+    const int r = p / ACH;
+    b_off[i] = (uint32_t)(min(n0 + r, a.N - 1) * (int)a.sb_n + ((p % ACH) ^ swz_a(r)) * 4) * 4u;
+  }
+  auto slot_ptr = [&](int step) { return ring + (step % NS) * (STAGE / 4); };
+  auto issue = [&](int step) {
+    const float *abase = uniform_ptr(Ab + step * BK);
+    const float *bbase = uniform_ptr(Bb + step * BK);
+    const uint32_t lds = (uint32_t)(uintptr_t)(lds_void_t *)slot_ptr(step);
+#pragma unroll
+    for (int i = 0; i < A_PER_WAVE; ++i) copy_to_lds<4>(abase, a_off[i], lds + (wave_u * A_PER_WAVE + i) * 1024);
+#pragma unroll
+    for (int i = 0; i < B_PER_WAVE; ++i)
+      copy_to_lds<4>(bbase, b_off[i], lds + A_FLOATS * 4 + (wave_u * B_PER_WAVE + i) * 1024);
+  };
+  // this wave's copies of a step have landed, `later` steps' copies being
+  // issued after them
+  auto wait_landed = [&](int later) {
+    if (later <= 0) wait_vmcnt<0>();
+    else if (later == 1 || NS < 4) wait_vmcnt<COPIES>();
+    else wait_vmcnt<2 * COPIES>();
+  };
+
+  // fragment offsets (floats, within a stage): two 128-bit reads per row
+  const int li = lane & 15, g = lane >> 4;
+  int fa_off[FM][2], fb_off[FN][2];
+#pragma unroll
+  for (int fm = 0; fm < FM; ++fm) {
+    const int r = wm * TM + fm * MT + li;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) fa_off[fm][h] = r * BK + ((2 * g + h) ^ swz_a(r)) * 4;
+  }
+#pragma unroll
+  for (int fn = 0; fn < FN; ++fn) {
+    const int r = wn * TN + fn * MT + li;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) fb_off[fn][h] = A_FLOATS + r * BK + ((2 * g + h) ^ swz_a(r)) * 4;
+  }
+
+  f32x4 acc[FM][FN];
+#pragma unroll
+  for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) acc[fm][fn] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // Fragments in two register sets, one per half step: set h holds K values
+  // 8g + 4h .. 8g + 4h + 3 of the lane's A rows and B rows (one 128-bit LDS
+  // read per row).
+  float4 f0a[FM], f0b[FN], f1a[FM], f1b[FN];
+  // (the scheduling barrier keeps the compiler from sinking the reads towards
+  // their first use at the start of the next half, where the wave would then
+  // wait for them)
+  auto read_half = [&](int step, int h, float4 (&xa)[FM], float4 (&xb)[FN]) {
+    const float *st = reinterpret_cast<const float *>(slot_ptr(step));
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) xa[fm] = *reinterpret_cast<const float4 *>(st + fa_off[fm][h]);
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) xb[fn] = *reinterpret_cast<const float4 *>(st + fb_off[fn][h]);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto part = [](const float4 &v, int j) { return j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w; };
+  auto mfmas = [&](const float4 (&xa)[FM], const float4 (&xb)[FN]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn)
+          acc[fm][fn] = __builtin_amdgcn_mfma_f32_16x16x4f32(part(xa[fm], j), part(xb[fn], j), acc[fm][fn], 0, 0, 0);
+  };
+
+  if (n_steps > 0) {
+    for (int p = 0; p < NS - 1 && p < n_steps; ++p) issue(p);
+    wait_landed(min(NS - 2, n_steps - 1));
+    stage_barrier();
+    read_half(0, 0, f0a, f0b);
+    // every step but the last (the loop body has no conditional LDS reads, so
+    // the compiler's counter waits before the second half stay exact)
+    for (int s = 0; s + 1 < n_steps; ++s) {
+      // first half of step s (set 0) under the reads of its second half
+      if (s + NS - 1 < n_steps) issue(s + NS - 1);
+      read_half(s, 1, f1a, f1b);
+      mfmas(f0a, f0b);
+      // stage s + 1 landed everywhere: its first half is read under the
+      // second half of step s (set 1)
+      wait_landed(min(NS - 2, n_steps - 2 - s));
+      stage_barrier();
+      read_half(s + 1, 0, f0a, f0b);
+      mfmas(f1a, f1b);
+    }
+    read_half(n_steps - 1, 1, f1a, f1b);
+    mfmas(f0a, f0b);
+    mfmas(f1a, f1b);
+  }
+
+  // Direct epilogue (bias / activation / residual recognised on the host):
+  // straight from the accumulators, 4 consecutive rows of one column per
+  // lane and MFMA block.
+  if (a.direct) {
+    const int col_base = n0 + wn * TN + li, row_base = m0 + wm * TM + 4 * g;
+    const float *bias = a.d_bias >= 0 ? a.eptr[a.d_bias] + (int64_t)bidx * a.estride[a.d_bias][0] : nullptr;
+    const float *res = a.d_res >= 0 ? a.eptr[a.d_res] + (int64_t)bidx * a.estride[a.d_res][0] : nullptr;
+    float *out = a.eptr[a.d_out] + (int64_t)bidx * a.estride[a.d_out][0];
+    const int64_t bn = bias ? a.estride[a.d_bias][2] : 0;
+    const int64_t rm = res ? a.estride[a.d_res][1] : 0, rn = res ? a.estride[a.d_res][2] : 0;
+    const int64_t om = a.estride[a.d_out][1], on = a.estride[a.d_out][2];
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) {
+      const int n = col_base + fn * MT;
+      if (n >= a.N) continue;
+      const float bv = bias ? bias[n * bn] : 0.0f;
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int m = row_base + fm * MT + i;
+          if (m >= a.M) continue;
+          float v = acc[fm][fn][i];
+          if (bias) v += bv;
+          if (res) v = res[m * rm + n * rn] + v;
+          if (a.d_act == KH_OP_GELU_TANH) v = op_gelu_tanh(v);
+          else if (a.d_act == KH_OP_GELU_ERF) v = op_gelu_erf(v);
+          else if (a.d_act == KH_OP_RELU) v = v != v ? v : fmaxf(v, 0.0f);
+          out[m * om + n * on] = v;
+        }
+      }
+    }
+    return;
+  }
+
+  // Tape epilogue: each wave stages its accumulators through LDS one 16-row
+  // block (16 x TN) at a time and reads them back as row-contiguous groups of
+  // 4 columns. Every wave has finished reading the ring first.
+  constexpr int CS = TN + 4;
+  static_assert(kWaves * MT * CS <= NS * STAGE, "epilogue staging");
+  __syncthreads();
+  float *Cw = reinterpret_cast<float *>(ring) + wave * MT * CS;
+  const int row0 = m0 + wm * TM, col0 = n0 + wn * TN;
+#pragma unroll
+  for (int fm = 0; fm < FM; ++fm) {
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) Cw[(4 * g + i) * CS + fn * MT + li] = acc[fm][fn][i];
+    __syncthreads();
+#pragma unroll 1
+    for (int q = lane; q < MT * TN / 4; q += 64) {
+      const int r = q / (TN / 4), c = (q % (TN / 4)) * 4;
+      const int m = row0 + fm * MT + r, n = col0 + c;
+      if (m >= a.M || n >= a.N) continue;
+      const float4 p = *reinterpret_cast<const float4 *>(Cw + r * CS + c);
+      Vec<4> v;
+      v.v[0] = p.x, v.v[1] = p.y, v.v[2] = p.z, v.v[3] = p.w;
+      run_epilogue(a, bidx, m, n, min(4, a.N - n), v);
+    }
+    __syncthreads();
+  }
+}
+
+}  // namespace
+
+hipError_t launch_gemm_nt(int id, const GemmArgs &a, dim3 grid, hipStream_t stream) {
+  switch (id) {
+#define KH_CFGNT_CASE(cid, bm, bn, wm, wn, ns)                                                         \
+  case cid:                                                                                           \
+    hipLaunchKernelGGL((gemm_nt_kernel<bm, bn, wm, wn, ns>), grid, dim3(64 * wm * wn), 0, stream, a); \
+    break;
+    KH_GEMM_NT_CONFIGS(KH_CFGNT_CASE)
+#undef KH_CFGNT_CASE
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace kh

@@ -647,8 +647,8 @@ class _Lowerer:
         d = self.new_desc(kl.FAM_GEMV if gemv else kl.FAM_GEMM, "gemv" if gemv else "matmul", k, space3)
         d.gemm[0], d.gemm[1], d.gemm[2], d.gemm[3] = batch, m, n, kk
         d.refs[0] = ref3(a_src, (batch, m, kk))
-        skinny = not gemv and int(cfg.get("tile", -1)) in autotune.SKINNY
-        nk = (gemv and self.layouts[b].base[0] == "const" and kk % 4 == 0) or skinny
+        k_major = not gemv and int(cfg.get("tile", -1)) in autotune.NK_B
+        nk = (gemv and self.layouts[b].base[0] == "const" and kk % 4 == 0) or k_major
         derived_b = prec in ("bf16", "bf16x3") or nk
         d.refs[1] = ref3(b, (batch, kk, n), register=not derived_b)
         if prec in ("bf16", "bf16x3"):
@@ -772,8 +772,8 @@ class _Lowerer:
                 # matmul on two activations stays on the fp32 path (more exact)
                 prec = "fp32"
             tile = int(cfg.get("tile", -1))
-            if tile in autotune.SKINNY and not (self.skinny_ok(mm) and
-                                                autotune.skinny_fits(mm.inputs[0].shape[-2], mm.inputs[0].shape[-1], tile)):
+            if tile in autotune.NK_B and not (self.skinny_ok(mm) and autotune.k_major_fits(
+                    mm.inputs[0].shape[-2], mm.inputs[0].shape[-1], tile)):
                 a, b = mm.inputs
                 batch = math.prod(a.shape[:-2]) if a.type.rank == 3 else 1
                 cfg = autotune.default_config_for(batch, a.shape[-2], b.shape[-1], a.shape[-1], precision=prec,
@@ -782,8 +782,9 @@ class _Lowerer:
         return self._cfg[k]
 
     def skinny_ok(self, mm) -> bool:
-        """The skinny-M GEMM reads B as a build-time [batch][N][K] copy of a
-        constant and A as 16-byte pieces along K (unit K stride)."""
+        """The skinny-M and K-contiguous GEMMs read B as a build-time
+        [batch][N][K] copy of a constant and A as 16-byte pieces along K (unit
+        K stride)."""
         a, b = mm.inputs
         la, lb = self.layouts.get(a), self.layouts.get(b)
         return (la is not None and lb is not None and lb.base[0] == "const" and a.shape[-1] % 4 == 0
@@ -858,7 +859,8 @@ class _Lowerer:
 
     def nk_weight(self, b, ref, batch, kk, n):
         """Ref of an fp32 [batch][N][K] copy of constant view `b` (fp32 ref
-        `ref` over (b, k, n)) for the GEMV family and the skinny-M GEMM: each
+        `ref` over (b, k, n)) for the GEMV family and the skinny-M and
+        K-contiguous GEMMs: each
         output column's weights become one contiguous row, which the
         K-contiguous GEMV kernel
         reads 1 KiB per wave load. Registered as a derived constant, made when

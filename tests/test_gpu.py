@@ -315,6 +315,36 @@ def test_every_skinny_gemm_configuration(tile):
     assert f"tile {tile} splitk 1" in c._exe.program.launches[0].summary
 
 
+@pytest.mark.parametrize("tile", sorted(autotune.K_CONTIGUOUS))
+def test_every_k_contiguous_gemm_configuration(tile):
+    # K-contiguous pipeline (one workgroup per CU, B read as a [N][K] copy):
+    # ragged M / N (rows and columns past the edge clamped), K a multiple of
+    # 32 from one step to a multiple of the ring depth; direct epilogues
+    # (bias + residual, bias + GELU) and the staged tape epilogue (a scale);
+    # batched constant weights; repeated launches agree bit for bit
+    cfg = lambda *_: {"tile": tile, "splitk": 1}
+    for m, n, k in ((21, 40, 32), (77, 133, 96), (300, 452, 160), (256, 768, 768)):
+        torch.manual_seed(m + n + k)
+        lin = gpt2_init_(torch.nn.Linear(k, n), seed=k).eval()
+        x, r = torch.randn(m, k), torch.randn(m, n)
+        wt, b = lin.weight.detach().numpy().T, lin.bias.detach().numpy()
+        cases = ((lambda t, res: lin(t) + res, (x, r), oracle.linear(x.numpy(), wt, b, r.numpy())),
+                 (lambda t: torch.nn.functional.gelu(lin(t), approximate="tanh"), (x,),
+                  oracle.linear(x.numpy(), wt, b, act="tanh")),
+                 (lambda t, res: lin(t) * 0.5 - res, (x, r), oracle.linear(x.numpy(), wt, b) * 0.5 - r.numpy()))
+        for fn, args, ref in cases:
+            c = kiln.compile(fn, args, device="cuda", cuda_graphs=False, gpu_matmul_config=cfg)
+            assert f"tile {tile} splitk 1" in c._exe.program.launches[0].summary
+            out = c(*args)
+            np.testing.assert_allclose(out.cpu().numpy(), ref, rtol=RTOL, atol=ATOL)
+            for _ in range(2):
+                assert torch.equal(c(*args), out)
+    model = _BatchedConstant(3, 96, 50).eval()
+    x = torch.randn(3, 24, 96)
+    c = check(model, x, gpu_matmul_config=cfg)
+    assert f"tile {tile} splitk 1" in c._exe.program.launches[0].summary
+
+
 @pytest.mark.parametrize("variant", range(6))
 def test_gemv_variants_and_ragged_sizes(variant):
     # M = 1: every column-block width (0 = chosen from the shape), with and
