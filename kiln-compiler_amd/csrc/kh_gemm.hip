@@ -317,13 +317,16 @@ __global__ __launch_bounds__(64 * WM * WN * WK) void gemm_f32_kernel(const GemmA
 //     runs the tape on row-contiguous groups of 4 (coalesced 128-bit operand
 //     loads and stores).
 // B rows of a bf16 stage are BK K values = BK / 8 chunks of 16 bytes; row n
-// puts chunk c at c ^ swz_b16<CB>(n), so the 16 rows one 128-bit fragment
-// read touches hit distinct banks (64 banks of 4 bytes: 4, 2 or 1 rows of
-// 64, 128 or 256 bytes share a bank cycle).
+// puts chunk c at c ^ swz_b16<CB>(n), chosen so the 16 consecutive rows one
+// 128-bit fragment read touches land in distinct 16-byte bank slots whether
+// the LDS serves such a read 8 lanes (128 bytes) or 16 lanes (256 bytes) at a
+// time: rows of 64 bytes pair up in a 128-byte bank row (n & 1 picks the
+// half), rows of 128 bytes take the A rows' swizzle, rows of 256 bytes span
+// the banks on their own.
 template <int CB>
 __device__ __forceinline__ int swz_b16(int n) {
   if constexpr (CB == 4) return ((n >> 1) ^ (n >> 3)) & 3;
-  else if constexpr (CB == 8) return (n >> 1) & 7;
+  else if constexpr (CB == 8) return swz_a(n);
   else return n & 15;
 }
 
@@ -788,18 +791,22 @@ __global__ __launch_bounds__(64 * WK) void gemm_skinny_kernel(const GemmArgs a) 
 #pragma unroll
   for (int s = 0; s < DEPTH; ++s) load(s, s);
   __builtin_amdgcn_sched_barrier(0);   // every first-turn load is issued before the first MFMA
+  const int n_chunks = max(0, c_end - c_begin);
 #pragma unroll
   for (int it = 0; it < kSkinnyIters; ++it) {
     if (it >= n_iter) break;
 #pragma unroll
     for (int s = 0; s < DEPTH; ++s) {
+      // slots past the wave's share hold zeros: no MFMAs for them
+      if (it * DEPTH + s < n_chunks) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int fm = 0; fm < FM; ++fm)
+          for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
-          for (int fn = 0; fn < FN; ++fn)
-            acc[fm][fn] = Mfma<16>::mma(part(ra[s][fm], j), part(rb[s][fn], j), acc[fm][fn]);
+            for (int fn = 0; fn < FN; ++fn)
+              acc[fm][fn] = Mfma<16>::mma(part(ra[s][fm], j), part(rb[s][fn], j), acc[fm][fn]);
+      }
       // refill the slot right away (past the share: zeros, never used); the
       // scheduling barrier keeps the compiler from sinking the loads to the
       // end of the iteration, so DEPTH - 1 chunks stay in flight
