@@ -631,36 +631,61 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void gemm3_f32_kernel(const GemmAr
   }
 
   // Direct epilogue (bias / activation / residual recognised on the host):
-  // straight from the accumulators, 4 consecutive rows of one column per
-  // lane and MFMA block; the bias element is read once per column.
+  // each wave stages its accumulators through its own LDS slice one 16-row
+  // block at a time (every wave passed the last stage barrier, so the ring
+  // is free) and reads them back as row-contiguous groups of 4 columns, so
+  // the operands are read and the output written with 128-bit accesses. LDS
+  // operations of one wave complete in order: no workgroup barrier.
   if (a.direct && a.splitk == 1) {
-    const int col_base = n0 + wn * TN + li, row_base = m0 + wm * TM + 4 * g;
-    const float *bias = a.d_bias >= 0 ? a.eptr[a.d_bias] + (int64_t)bidx * a.estride[a.d_bias][0] : nullptr;
-    const float *res = a.d_res >= 0 ? a.eptr[a.d_res] + (int64_t)bidx * a.estride[a.d_res][0] : nullptr;
-    float *out = a.eptr[a.d_out] + (int64_t)bidx * a.estride[a.d_out][0];
-    const int64_t bn = bias ? a.estride[a.d_bias][2] : 0;
-    const int64_t rm = res ? a.estride[a.d_res][1] : 0, rn = res ? a.estride[a.d_res][2] : 0;
-    const int64_t om = a.estride[a.d_out][1], on = a.estride[a.d_out][2];
+    constexpr int DS = TN + 4;
+    static_assert(kWaves * MT * DS <= NS * STAGE, "epilogue staging");
+    float *Cw = reinterpret_cast<float *>(ring) + wave * MT * DS;
+    const int row0 = m0 + wm * TM, col0 = n0 + wn * TN;
+    auto load4 = [&](int j, int m, int n, int valid) {
+      const float *p = a.eptr[j] + (int64_t)bidx * a.estride[j][0] + (int64_t)m * a.estride[j][1];
+      if ((a.e_vec_mask >> j & 1) && valid == 4) return *reinterpret_cast<const float4 *>(p + n);
+      float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      for (int i = 0; i < valid; ++i) v[i] = p[(int64_t)(n + i) * a.estride[j][2]];
+      return make_float4(v[0], v[1], v[2], v[3]);
+    };
 #pragma unroll
-    for (int fn = 0; fn < FN; ++fn) {
-      const int n = col_base + fn * MT;
-      if (n >= a.N) continue;
-      const float bv = bias ? bias[n * bn] : 0.0f;
+    for (int fm = 0; fm < FM; ++fm) {
 #pragma unroll
-      for (int fm = 0; fm < FM; ++fm) {
+      for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+        for (int r = 0; r < M::kRegs; ++r) Cw[M::row(r, lane) * DS + fn * MT + li] = acc[fm][fn][r];
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int q = lane; q < MT * TN / 4; q += 64) {
+        const int r = q / (TN / 4), c = (q % (TN / 4)) * 4;
+        const int m = row0 + fm * MT + r, n = col0 + c;
+        if (m >= a.M || n >= a.N) continue;
+        const float4 p = *reinterpret_cast<const float4 *>(Cw + r * DS + c);
+        const int valid = min(4, a.N - n);
+        // out = act((acc [+ bias]) [+ res]), in the tape's order
+        float v[4] = {p.x, p.y, p.z, p.w};
+        if (a.d_bias >= 0) {
+          const float4 bv = load4(a.d_bias, m, n, valid);
+          v[0] += bv.x, v[1] += bv.y, v[2] += bv.z, v[3] += bv.w;
+        }
+        if (a.d_res >= 0) {
+          const float4 rv = load4(a.d_res, m, n, valid);
+          v[0] = rv.x + v[0], v[1] = rv.y + v[1], v[2] = rv.z + v[2], v[3] = rv.w + v[3];
+        }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int m = row_base + fm * MT + i;
-          if (m >= a.M) continue;
-          float v = acc[fm][fn][i];
-          if (bias) v += bv;
-          if (res) v = res[m * rm + n * rn] + v;
-          if (a.d_act == KH_OP_GELU_TANH) v = op_gelu_tanh(v);
-          else if (a.d_act == KH_OP_GELU_ERF) v = op_gelu_erf(v);
-          else if (a.d_act == KH_OP_RELU) v = v != v ? v : fmaxf(v, 0.0f);
-          out[m * om + n * on] = v;
+          if (a.d_act == KH_OP_GELU_TANH) v[i] = op_gelu_tanh(v[i]);
+          else if (a.d_act == KH_OP_GELU_ERF) v[i] = op_gelu_erf(v[i]);
+          else if (a.d_act == KH_OP_RELU) v[i] = v[i] != v[i] ? v[i] : fmaxf(v[i], 0.0f);
+        }
+        float *o = a.eptr[a.d_out] + (int64_t)bidx * a.estride[a.d_out][0] + (int64_t)m * a.estride[a.d_out][1];
+        if ((a.e_vec_mask >> a.d_out & 1) && valid == 4) {
+          *reinterpret_cast<float4 *>(o + n) = make_float4(v[0], v[1], v[2], v[3]);
+        } else {
+          for (int i = 0; i < valid; ++i) o[(int64_t)(n + i) * a.estride[a.d_out][2]] = v[i];
         }
       }
+      __builtin_amdgcn_wave_barrier();
     }
     return;
   }
@@ -1321,7 +1346,8 @@ std::unique_ptr<Op> make_gemm(const kh_launch &L, std::string &err, bool &unsupp
     // is not split (and is a whole number of 32-deep steps for kind 5)
     const kh_ref &ra = L.refs[0], &rb = L.refs[1];
     op->b_vec_layout = a.sb_k == 1 && rb.offset % 4 == 0 && a.sb_n % 4 == 0 && a.sb_b % 4 == 0 && a.sb_n >= K;
-    if (!op->a_vec_layout || !op->b_vec_layout || K % (t.kind == 5 ? 32 : 4) || ra.offset % 4) {
+    if (!op->a_vec_layout || !op->b_vec_layout || K % (t.kind == 5 ? 32 : 4) || (t.kind == 5 && K == 0) ||
+        ra.offset % 4) {
       err = "matmul: configuration " + std::to_string(cfg) +
             " needs A [.., M, K] and B [batch][N][K] with unit K stride, 16-byte aligned rows and K a multiple of " +
             std::to_string(t.kind == 5 ? 32 : 4);
@@ -1379,7 +1405,10 @@ std::unique_ptr<Op> make_gemm(const kh_launch &L, std::string &err, bool &unsupp
   a.group_m = tile_group(tr, a.tiles_m);
   op->k_major = tr.kind == 4 || tr.kind == 5;
   op->cfg = cfg_run;
-  op->grid = dim3((unsigned)n_tiles, (unsigned)batch, (unsigned)splitk);
+  // the K-contiguous kernel with a direct epilogue is persistent: at most
+  // one workgroup per CU, each walking its tiles
+  const int64_t grid_x = tr.kind == 5 && a.direct ? std::min<int64_t>(n_tiles, current_device().cus) : n_tiles;
+  op->grid = dim3((unsigned)std::max<int64_t>(1, grid_x), (unsigned)batch, (unsigned)splitk);
   if (splitk > 1) {
     op->n_partials = (size_t)splitk * batch * M * N;
   }

@@ -129,17 +129,19 @@ inline hipError_t launch_splitk_reduce(const GemmArgs &a, int cus, hipStream_t s
 }  // namespace
 
 // Configurations of the K-contiguous fp32 kernel (kind 5, kh_gemm_nt.hip):
-// id, macro tile BM x BN (K step 32), waves WM x WN (one or two per SIMD,
-// one workgroup per CU), LDS stages NS.
+// id, macro tile BM x BN (K step 32), waves WM x WN (one or two per SIMD;
+// persistent, at most one workgroup per CU), LDS stages NS.
 #define KH_GEMM_NT_CONFIGS(X) \
   X(55, 128, 192, 2, 2, 3)    \
-  X(56, 64, 288, 2, 2, 3)     \
+  X(56, 64, 288, 2, 2, 2)     \
   X(57, 64, 96, 2, 2, 3)      \
   X(58, 128, 96, 2, 2, 3)     \
-  X(59, 128, 128, 2, 2, 3)    \
-  X(60, 64, 192, 2, 2, 3)     \
+  X(59, 128, 128, 2, 4, 3)    \
+  X(60, 64, 192, 2, 4, 3)     \
   X(61, 128, 192, 2, 4, 3)    \
-  X(62, 64, 128, 2, 2, 3)
+  X(62, 64, 128, 2, 4, 3)     \
+  X(63, 32, 96, 2, 2, 3)      \
+  X(64, 64, 64, 2, 2, 3)
 
 // Launch configuration `id` of kind 5 (hipErrorInvalidValue for another id).
 hipError_t launch_gemm_nt(int id, const GemmArgs &a, dim3 grid, hipStream_t stream);

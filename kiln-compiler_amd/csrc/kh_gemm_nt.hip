@@ -23,10 +23,18 @@
 //     second half of step s's MFMAs and the next step starts with its
 //     operands in registers (two register sets of fragments, one per half
 //     step, each loaded while the other feeds the MFMAs);
-//   * the epilogue runs straight from the accumulators for bias / residual /
-//     activation tapes, else stages 16-row blocks through LDS for the tape.
-// K must be a multiple of 32 and the operands' spans below 2^29 elements (the
-// host checks both; other shapes use the other kernels of the family).
+//   * persistent (for bias / residual / activation epilogues): the grid is at
+//     most one workgroup per CU and each workgroup walks its tiles, issuing
+//     the next tile's first stages before the current tile's epilogue, so the
+//     loads are in flight while the epilogue runs and the stores drain under
+//     the next main loop (other epilogue tapes: one tile per workgroup);
+//   * the epilogue stages 16-row blocks of the accumulators through a per-wave
+//     LDS slice and reads, computes and writes row-contiguous groups of 4
+//     columns with 128-bit accesses (bias / residual / activation directly,
+//     other tapes through the tape interpreter).
+// K must be a positive multiple of 32 and the operands' spans below 2^29
+// elements (the host checks both; other shapes use the other kernels of the
+// family).
 #include <algorithm>
 
 #include "kh_common.hpp"
@@ -37,7 +45,11 @@
 namespace kh {
 namespace {
 
-template <int BM, int BN, int WM, int WN, int NS>
+// TAPE = false: persistent over tiles, direct epilogue (bias / residual /
+// activation, recognised on the host); TAPE = true: one tile per workgroup
+// and the general epilogue tape after the main loop (kept out of the tile
+// loop so the tape interpreter is not replicated into it).
+template <int BM, int BN, int WM, int WN, int NS, bool TAPE>
 __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM * WN / 4, WM * WN / 4)))
 void gemm_nt_kernel(const GemmArgs a) {
   constexpr int BK = 32, MT = 16, ACH = BK / 4;
@@ -49,38 +61,47 @@ void gemm_nt_kernel(const GemmArgs a) {
   static_assert(TM % MT == 0 && TN % MT == 0, "wave tile of whole MFMA blocks");
   static_assert((BM * ACH) % (64 * kWaves) == 0 && (BN * ACH) % (64 * kWaves) == 0, "copy mapping");
   static_assert(NS >= 2 && NS <= 4 && (NS - 2) * COPIES < 64, "ring depth / vmcnt range");
-  static_assert(NS * STAGE * 4 <= 160 * 1024, "LDS");
   static_assert(kWaves % 4 == 0, "whole SIMDs");
 
+  constexpr int CS = TN + 4;   // epilogue staging row stride (floats, 16-byte aligned rows)
+  static_assert(NS * STAGE * 4 + kWaves * MT * CS * 4 <= 160 * 1024, "LDS: ring and epilogue staging");
+
   __shared__ float4 ring[NS * STAGE / 4];
+  __shared__ float4 staging[kWaves * MT * CS / 4];
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   const int wm = wave / WN, wn = wave % WN;
-  int tm, tn;
-  tile_coords(blockIdx.x, a, tm, tn);
+  const int li = lane & 15, g = lane >> 4;
   const int bidx = blockIdx.y;
-  const int m0 = tm * BM, n0 = tn * BN;
   const float *Ab = a.A + (int64_t)bidx * a.sa_b;
   const float *Bb = a.B + (int64_t)bidx * a.sb_b;
-  const int n_steps = a.K / BK;
+  const int n_steps = a.K / BK;   // the host checks K % 32 == 0 and K > 0
+  const int n_tiles = a.tiles_m * a.tiles_n;
 
-  // per-lane copy sources: byte offsets from the step's first K column (rows
-  // past M / N clamped to the last one; their results are never stored)
+  // per-lane copy sources of the current tile: byte offsets from the step's
+  // first K column (rows past M / N clamped to the last one; their results
+  // are never stored)
   uint32_t a_off[A_PER_WAVE], b_off[B_PER_WAVE];
+  int m0 = 0, n0 = 0;
+  auto set_tile = [&](int t) {
+    int tm, tn;
+    tile_coords(t, a, tm, tn);
+    m0 = tm * BM, n0 = tn * BN;
 #pragma unroll
-  for (int i = 0; i < A_PER_WAVE; ++i) {
-    const int p = (wave * A_PER_WAVE + i) * 64 + lane;
-    const int r = p / ACH;
-    a_off[i] = (uint32_t)(min(m0 + r, a.M - 1) * (int)a.sa_m + ((p % ACH) ^ swz_a(r)) * 4) * 4u;
-  }
+    for (int i = 0; i < A_PER_WAVE; ++i) {
+      const int p = (wave * A_PER_WAVE + i) * 64 + lane;
+      const int r = p / ACH;
+      a_off[i] = (uint32_t)(min(m0 + r, a.M - 1) * (int)a.sa_m + ((p % ACH) ^ swz_a(r)) * 4) * 4u;
+    }
 #pragma unroll
-  for (int i = 0; i < B_PER_WAVE; ++i) {
-    const int p = (wave * B_PER_WAVE + i) * 64 + lane;
-    const int r = p / ACH;
-    b_off[i] = (uint32_t)(min(n0 + r, a.N - 1) * (int)a.sb_n + ((p % ACH) ^ swz_a(r)) * 4) * 4u;
-  }
+    for (int i = 0; i < B_PER_WAVE; ++i) {
+      const int p = (wave * B_PER_WAVE + i) * 64 + lane;
+      const int r = p / ACH;
+      b_off[i] = (uint32_t)(min(n0 + r, a.N - 1) * (int)a.sb_n + ((p % ACH) ^ swz_a(r)) * 4) * 4u;
+    }
+  };
   auto slot_ptr = [&](int step) { return ring + (step % NS) * (STAGE / 4); };
   auto issue = [&](int step) {
     const float *abase = uniform_ptr(Ab + step * BK);
@@ -93,7 +114,7 @@ void gemm_nt_kernel(const GemmArgs a) {
       copy_to_lds<4>(bbase, b_off[i], lds + A_FLOATS * 4 + (wave_u * B_PER_WAVE + i) * 1024);
   };
   // this wave's copies of a step have landed, `later` steps' copies being
-  // issued after them
+  // issued after them (and no other vector memory operation after those)
   auto wait_landed = [&](int later) {
     if (later <= 0) wait_vmcnt<0>();
     else if (later == 1 || NS < 4) wait_vmcnt<COPIES>();
@@ -101,7 +122,6 @@ void gemm_nt_kernel(const GemmArgs a) {
   };
 
   // fragment offsets (floats, within a stage): two 128-bit reads per row
-  const int li = lane & 15, g = lane >> 4;
   int fa_off[FM][2], fb_off[FN][2];
 #pragma unroll
   for (int fm = 0; fm < FM; ++fm) {
@@ -117,11 +137,6 @@ void gemm_nt_kernel(const GemmArgs a) {
   }
 
   f32x4 acc[FM][FN];
-#pragma unroll
-  for (int fm = 0; fm < FM; ++fm)
-#pragma unroll
-    for (int fn = 0; fn < FN; ++fn) acc[fm][fn] = f32x4{0.f, 0.f, 0.f, 0.f};
-
   // Fragments in two register sets, one per half step: set h holds K values
   // 8g + 4h .. 8g + 4h + 3 of the lane's A rows and B rows (one 128-bit LDS
   // read per row).
@@ -148,10 +163,96 @@ void gemm_nt_kernel(const GemmArgs a) {
           acc[fm][fn] = __builtin_amdgcn_mfma_f32_16x16x4f32(part(xa[fm], j), part(xb[fn], j), acc[fm][fn], 0, 0, 0);
   };
 
-  if (n_steps > 0) {
-    for (int p = 0; p < NS - 1 && p < n_steps; ++p) issue(p);
-    wait_landed(min(NS - 2, n_steps - 1));
+  // Epilogue of the tile at (tm0, tn0): each wave stages its accumulators
+  // through its own LDS slice one 16-row block (16 x TN) at a time and reads
+  // them back as row-contiguous groups of 4 columns, so operands are read and
+  // the output written with 128-bit accesses. The slice is the wave's own and
+  // LDS operations of one wave complete in order, so no barrier is needed.
+  float *Cw = reinterpret_cast<float *>(staging) + wave * MT * CS;
+  auto load4 = [&](int j, int m, int n, int valid) {
+    const float *p = a.eptr[j] + (int64_t)bidx * a.estride[j][0] + (int64_t)m * a.estride[j][1];
+    if ((a.e_vec_mask >> j & 1) && valid == 4) return *reinterpret_cast<const float4 *>(p + n);
+    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i = 0; i < valid; ++i) v[i] = p[(int64_t)(n + i) * a.estride[j][2]];
+    return make_float4(v[0], v[1], v[2], v[3]);
+  };
+  auto act = [&](float v) {
+    if (a.d_act == KH_OP_GELU_TANH) return op_gelu_tanh(v);
+    if (a.d_act == KH_OP_GELU_ERF) return op_gelu_erf(v);
+    if (a.d_act == KH_OP_RELU) return v != v ? v : fmaxf(v, 0.0f);
+    return v;
+  };
+  auto epilogue = [&](int tm0, int tn0) {
+    const int row0 = tm0 + wm * TM, col0 = tn0 + wn * TN;
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) {
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) Cw[(4 * g + i) * CS + fn * MT + li] = acc[fm][fn][i];
+      __builtin_amdgcn_wave_barrier();
+      auto emit = [&](int q) {
+        const int r = q / (TN / 4), c = (q % (TN / 4)) * 4;
+        const int m = row0 + fm * MT + r, n = col0 + c;
+        if (m >= a.M || n >= a.N) return;
+        const float4 p = *reinterpret_cast<const float4 *>(Cw + r * CS + c);
+        const int valid = min(4, a.N - n);
+        if constexpr (TAPE) {
+          Vec<4> v;
+          v.v[0] = p.x, v.v[1] = p.y, v.v[2] = p.z, v.v[3] = p.w;
+          run_epilogue(a, bidx, m, n, valid, v);
+        } else {
+          // out = act((acc [+ bias]) [+ res]), in the tape's order
+          float v[4] = {p.x, p.y, p.z, p.w};
+          if (a.d_bias >= 0) {
+            const float4 bv = load4(a.d_bias, m, n, valid);
+            v[0] += bv.x, v[1] += bv.y, v[2] += bv.z, v[3] += bv.w;
+          }
+          if (a.d_res >= 0) {
+            const float4 rv = load4(a.d_res, m, n, valid);
+            v[0] = rv.x + v[0], v[1] = rv.y + v[1], v[2] = rv.z + v[2], v[3] = rv.w + v[3];
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v[i] = act(v[i]);
+          float *o = a.eptr[a.d_out] + (int64_t)bidx * a.estride[a.d_out][0] + (int64_t)m * a.estride[a.d_out][1];
+          if ((a.e_vec_mask >> a.d_out & 1) && valid == 4) {
+            *reinterpret_cast<float4 *>(o + n) = make_float4(v[0], v[1], v[2], v[3]);
+          } else {
+            for (int i = 0; i < valid; ++i) o[(int64_t)(n + i) * a.estride[a.d_out][2]] = v[i];
+          }
+        }
+      };
+      // the tape interpreter once, in a loop; the direct form unrolled
+      if constexpr (TAPE) {
+#pragma unroll 1
+        for (int q = lane; q < MT * TN / 4; q += 64) emit(q);
+      } else {
+#pragma unroll
+        for (int q = lane; q < MT * TN / 4; q += 64) emit(q);
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+  };
+
+  // Persistent loop: workgroup w takes tiles w, w + grid, ... The next tile's
+  // first NS - 1 stages are issued as soon as every wave is done with the
+  // ring, before this tile's epilogue, so its loads are in flight while the
+  // epilogue runs and the output stores drain under the next main loop.
+  int t = blockIdx.x;
+  if (t >= n_tiles) return;
+  set_tile(t);
+  for (int p = 0; p < NS - 1 && p < n_steps; ++p) issue(p);
+  bool first = true;
+  while (true) {
+    // stage 0 of this tile landed everywhere (after a previous tile, whose
+    // epilogue issued memory operations behind these copies, wait for all)
+    if (first) wait_landed(min(NS - 2, n_steps - 1));
+    else wait_vmcnt<0>();
     stage_barrier();
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn) acc[fm][fn] = f32x4{0.f, 0.f, 0.f, 0.f};
     read_half(0, 0, f0a, f0b);
     // every step but the last (the loop body has no conditional LDS reads, so
     // the compiler's counter waits before the second half stay exact)
@@ -170,69 +271,18 @@ void gemm_nt_kernel(const GemmArgs a) {
     read_half(n_steps - 1, 1, f1a, f1b);
     mfmas(f0a, f0b);
     mfmas(f1a, f1b);
-  }
 
-  // Direct epilogue (bias / activation / residual recognised on the host):
-  // straight from the accumulators, 4 consecutive rows of one column per
-  // lane and MFMA block.
-  if (a.direct) {
-    const int col_base = n0 + wn * TN + li, row_base = m0 + wm * TM + 4 * g;
-    const float *bias = a.d_bias >= 0 ? a.eptr[a.d_bias] + (int64_t)bidx * a.estride[a.d_bias][0] : nullptr;
-    const float *res = a.d_res >= 0 ? a.eptr[a.d_res] + (int64_t)bidx * a.estride[a.d_res][0] : nullptr;
-    float *out = a.eptr[a.d_out] + (int64_t)bidx * a.estride[a.d_out][0];
-    const int64_t bn = bias ? a.estride[a.d_bias][2] : 0;
-    const int64_t rm = res ? a.estride[a.d_res][1] : 0, rn = res ? a.estride[a.d_res][2] : 0;
-    const int64_t om = a.estride[a.d_out][1], on = a.estride[a.d_out][2];
-#pragma unroll
-    for (int fn = 0; fn < FN; ++fn) {
-      const int n = col_base + fn * MT;
-      if (n >= a.N) continue;
-      const float bv = bias ? bias[n * bn] : 0.0f;
-#pragma unroll
-      for (int fm = 0; fm < FM; ++fm) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int m = row_base + fm * MT + i;
-          if (m >= a.M) continue;
-          float v = acc[fm][fn][i];
-          if (bias) v += bv;
-          if (res) v = res[m * rm + n * rn] + v;
-          if (a.d_act == KH_OP_GELU_TANH) v = op_gelu_tanh(v);
-          else if (a.d_act == KH_OP_GELU_ERF) v = op_gelu_erf(v);
-          else if (a.d_act == KH_OP_RELU) v = v != v ? v : fmaxf(v, 0.0f);
-          out[m * om + n * on] = v;
-        }
-      }
+    const int tm0 = m0, tn0 = n0;
+    const int t_next = TAPE ? n_tiles : t + (int)gridDim.x;
+    if (t_next < n_tiles) {
+      __syncthreads();   // every wave's fragment reads of the ring have completed
+      set_tile(t_next);
+      for (int p = 0; p < NS - 1 && p < n_steps; ++p) issue(p);
     }
-    return;
-  }
-
-  // Tape epilogue: each wave stages its accumulators through LDS one 16-row
-  // block (16 x TN) at a time and reads them back as row-contiguous groups of
-  // 4 columns. Every wave has finished reading the ring first.
-  constexpr int CS = TN + 4;
-  static_assert(kWaves * MT * CS <= NS * STAGE, "epilogue staging");
-  __syncthreads();
-  float *Cw = reinterpret_cast<float *>(ring) + wave * MT * CS;
-  const int row0 = m0 + wm * TM, col0 = n0 + wn * TN;
-#pragma unroll
-  for (int fm = 0; fm < FM; ++fm) {
-#pragma unroll
-    for (int fn = 0; fn < FN; ++fn)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) Cw[(4 * g + i) * CS + fn * MT + li] = acc[fm][fn][i];
-    __syncthreads();
-#pragma unroll 1
-    for (int q = lane; q < MT * TN / 4; q += 64) {
-      const int r = q / (TN / 4), c = (q % (TN / 4)) * 4;
-      const int m = row0 + fm * MT + r, n = col0 + c;
-      if (m >= a.M || n >= a.N) continue;
-      const float4 p = *reinterpret_cast<const float4 *>(Cw + r * CS + c);
-      Vec<4> v;
-      v.v[0] = p.x, v.v[1] = p.y, v.v[2] = p.z, v.v[3] = p.w;
-      run_epilogue(a, bidx, m, n, min(4, a.N - n), v);
-    }
-    __syncthreads();
+    epilogue(tm0, tn0);
+    if (t_next >= n_tiles) break;
+    t = t_next;
+    first = false;
   }
 }
 
@@ -240,9 +290,12 @@ void gemm_nt_kernel(const GemmArgs a) {
 
 hipError_t launch_gemm_nt(int id, const GemmArgs &a, dim3 grid, hipStream_t stream) {
   switch (id) {
-#define KH_CFGNT_CASE(cid, bm, bn, wm, wn, ns)                                                         \
-  case cid:                                                                                           \
-    hipLaunchKernelGGL((gemm_nt_kernel<bm, bn, wm, wn, ns>), grid, dim3(64 * wm * wn), 0, stream, a); \
+#define KH_CFGNT_CASE(cid, bm, bn, wm, wn, ns)                                                                 \
+  case cid:                                                                                                   \
+    if (a.direct)                                                                                             \
+      hipLaunchKernelGGL((gemm_nt_kernel<bm, bn, wm, wn, ns, false>), grid, dim3(64 * wm * wn), 0, stream, a); \
+    else                                                                                                      \
+      hipLaunchKernelGGL((gemm_nt_kernel<bm, bn, wm, wn, ns, true>), grid, dim3(64 * wm * wn), 0, stream, a);  \
     break;
     KH_GEMM_NT_CONFIGS(KH_CFGNT_CASE)
 #undef KH_CFGNT_CASE
