@@ -912,7 +912,8 @@ __global__ __launch_bounds__(64 * WK) void gemm_skinny_kernel(const GemmArgs a) 
 struct TileCfg {
   int bm, bn, bk, wm, wn, wk, mt, kind, stages, prec;  // kind 1: register-staged loads; 3: LDS-copy pipeline;
                                                        // 4: skinny-M direct loads ([N][K] B); 5: one
-                                                       // workgroup per CU, A and B K-contiguous ([N][K] B)
+                                                       // workgroup per CU, A and B K-contiguous ([N][K] B);
+                                                       // 6: small tiles, waves split K ([N][K] B)
 };
 
 // Configurations by id. Ids 0-7: the copy pipeline (BK = 32, MFMA
@@ -1045,6 +1046,9 @@ constexpr TileCfg kConfigs[] = {
 #define KH_CFGNT_ROW(id, bm, bn, wm, wn, ns) {bm, bn, 32, wm, wn, 1, 16, 5, ns, KH_PREC_FP32},
     KH_GEMM_NT_CONFIGS(KH_CFGNT_ROW)
 #undef KH_CFGNT_ROW
+#define KH_CFGSM_ROW(id, bm, bn, wk, ns) {bm, bn, 32, 1, 1, wk, 16, 6, ns, KH_PREC_FP32},
+    KH_GEMM_SMALL_CONFIGS(KH_CFGSM_ROW)
+#undef KH_CFGSM_ROW
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
@@ -1056,7 +1060,8 @@ constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 // on the GPT-2 block's shapes against row-major order (interleaved, warm
 // GPU): 2048x3072x768 on the 32x64 tile 5% faster, the others within 1%.
 int tile_group(const TileCfg &t, int tiles_m) {
-  const int lds = t.kind == 5 ? 4 * t.stages * t.bk * (t.bm + t.bn)
+  const int lds = t.kind == 6   ? 4 * t.stages * t.bk * (t.bm + t.bn) * t.wk
+                  : t.kind == 5 ? 4 * t.stages * t.bk * (t.bm + t.bn)
                   : t.kind == 3 ? 4 * t.stages * (t.bm * t.bk + (t.prec == KH_PREC_FP32 ? t.bk * t.bn
                                                                  : t.bn * t.bk / 2 * (t.prec == KH_PREC_BF16X3 ? 2 : 1)))
                               : 8 * (t.bm * (t.bk + 4) + t.bn * (t.bk + 2));
@@ -1070,6 +1075,8 @@ int tile_group(const TileCfg &t, int tiles_m) {
 }
 
 hipError_t launch_config(int id, const GemmArgs &a, dim3 grid, hipStream_t stream) {
+  if (kConfigs[id].kind == 5) return launch_gemm_nt(id, a, grid, stream);
+  if (kConfigs[id].kind == 6) return launch_gemm_small(id, a, grid, stream);
   switch (id) {
 #define KH_CFGS_CASE(cid, bm, bn, wk, depth)                                                            \
   case cid:                                                                                            \
@@ -1134,7 +1141,7 @@ hipError_t launch_config(int id, const GemmArgs &a, dim3 grid, hipStream_t strea
 #undef KH_CFGBD_CASE
 #undef KH_CFGXD_CASE
 #undef KH_CFGD_CASE
-    default: return launch_gemm_nt(id, a, grid, stream);
+    default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
@@ -1146,7 +1153,7 @@ class GemmOp final : public Op {
   dim3 grid;
   size_t n_partials = 0;
   bool a_vec_layout = false, b_vec_layout = false;
-  bool k_major = false;   // kinds 4 and 5: A and B both K-contiguous
+  bool k_major = false;   // kinds 4, 5 and 6: A and B both K-contiguous
   uint32_t e_vec_candidates = 0;
 
   hipError_t launch(float *const *ptrs, float *partials, hipStream_t stream) override {
@@ -1340,17 +1347,18 @@ std::unique_ptr<Op> make_gemm(const kh_launch &L, std::string &err, bool &unsupp
     }
     op->b_vec_layout = true;
   }
-  if (t.kind == 4 || t.kind == 5) {
-    // skinny-M direct loads / K-contiguous pipeline: A row-major with unit K
+  if (t.kind == 4 || t.kind == 5 || t.kind == 6) {
+    // skinny-M direct loads / K-contiguous pipelines: A row-major with unit K
     // stride, B the [batch][N][K] copy, both read as whole 16-byte pieces; K
-    // is not split (and is a whole number of 32-deep steps for kind 5)
+    // is not split across workgroups (and is a positive whole number of
+    // 32-deep steps for kinds 5 and 6)
     const kh_ref &ra = L.refs[0], &rb = L.refs[1];
+    const bool steps = t.kind == 5 || t.kind == 6;
     op->b_vec_layout = a.sb_k == 1 && rb.offset % 4 == 0 && a.sb_n % 4 == 0 && a.sb_b % 4 == 0 && a.sb_n >= K;
-    if (!op->a_vec_layout || !op->b_vec_layout || K % (t.kind == 5 ? 32 : 4) || (t.kind == 5 && K == 0) ||
-        ra.offset % 4) {
+    if (!op->a_vec_layout || !op->b_vec_layout || K % (steps ? 32 : 4) || (steps && K == 0) || ra.offset % 4) {
       err = "matmul: configuration " + std::to_string(cfg) +
-            " needs A [.., M, K] and B [batch][N][K] with unit K stride, 16-byte aligned rows and K a multiple of " +
-            std::to_string(t.kind == 5 ? 32 : 4);
+            " needs A [.., M, K] and B [batch][N][K] with unit K stride, 16-byte aligned rows and K a " +
+            (steps ? std::string("positive multiple of 32") : std::string("multiple of 4"));
       return nullptr;
     }
     // buffer-load byte offsets are 32-bit (and must stay below the
@@ -1389,7 +1397,7 @@ std::unique_ptr<Op> make_gemm(const kh_launch &L, std::string &err, bool &unsupp
   const TileCfg &tr = kConfigs[cfg_run];
   a.tiles_m = (int)((M + tr.bm - 1) / tr.bm);
   a.tiles_n = (int)((N + tr.bn - 1) / tr.bn);
-  int splitk = tr.kind == 4 || tr.kind == 5 ? 1 : std::max(1, L.cfg[2]);
+  int splitk = tr.kind >= 4 ? 1 : std::max(1, L.cfg[2]);
   const int k_steps = (int)std::max<int64_t>(1, (K + tr.bk - 1) / tr.bk);
   splitk = std::min(splitk, k_steps);
   a.k_per_split = ((k_steps + splitk - 1) / splitk) * tr.bk;
@@ -1403,7 +1411,7 @@ std::unique_ptr<Op> make_gemm(const kh_launch &L, std::string &err, bool &unsupp
     return nullptr;
   }
   a.group_m = tile_group(tr, a.tiles_m);
-  op->k_major = tr.kind == 4 || tr.kind == 5;
+  op->k_major = tr.kind >= 4;
   op->cfg = cfg_run;
   // the K-contiguous kernel with a direct epilogue is persistent: at most
   // one workgroup per CU, each walking its tiles

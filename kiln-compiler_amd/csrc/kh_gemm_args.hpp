@@ -146,6 +146,23 @@ inline hipError_t launch_splitk_reduce(const GemmArgs &a, int cus, hipStream_t s
 // Launch configuration `id` of kind 5 (hipErrorInvalidValue for another id).
 hipError_t launch_gemm_nt(int id, const GemmArgs &a, dim3 grid, hipStream_t stream);
 
+// Configurations of the small-M kernel (kind 6, kh_gemm_small.hip): id, tile
+// BM x BN, WK waves splitting K (each with a private LDS ring), NS stages.
+#define KH_GEMM_SMALL_CONFIGS(X) \
+  X(65, 16, 32, 4, 3)            \
+  X(66, 16, 32, 4, 2)            \
+  X(67, 16, 16, 4, 3)            \
+  X(68, 16, 64, 4, 2)            \
+  X(69, 32, 32, 4, 2)            \
+  X(70, 16, 32, 8, 2)            \
+  X(71, 16, 16, 8, 2)            \
+  X(72, 32, 64, 4, 2)            \
+  X(73, 32, 32, 8, 2)            \
+  X(74, 16, 16, 4, 2)
+
+// Launch configuration `id` of kind 6 (hipErrorInvalidValue for another id).
+hipError_t launch_gemm_small(int id, const GemmArgs &a, dim3 grid, hipStream_t stream);
+
 // Host: validate the epilogue refs/tape of a matmul descriptor into `a`.
 bool fill_epilogue(const kh_launch &L, GemmArgs &a, uint32_t &vec_candidates, std::string &err);
 // Recognise the tape out = act((acc [+ bias]) [+ res]) and fill the direct

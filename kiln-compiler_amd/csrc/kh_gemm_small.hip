@@ -1,0 +1,250 @@
+// kh_gemm_small.hip - fp32 matmul for products with few rows (configuration
+// kind 6): C[b] = epilogue(A[b] @ B[b]) with A [.., M, K] row-major and B the
+// [batch][N][K] copy of a constant weight, both K-contiguous.
+//
+// Same contract as the rest of the matmul family (the reference's tl.dot
+// kernel with fused epilogue, kiln/gpu/codegen.py:484-530). A product with a
+// few hundred rows has too little work per output tile to keep a CU's four
+// SIMDs busy when each tile goes to one wave, and tiles large enough to do so
+// leave most of the 256 CUs idle; splitting K across workgroups needs a
+// second kernel. Here a workgroup owns one small BM x BN tile and its WK
+// waves split K between them, so a product is many small workgroups and every
+// SIMD of every CU gets a wave:
+//   * each wave streams its own K range through a private ring of NS LDS
+//     stages with 128-bit global_load_lds copies (rows of 32 floats = 8
+//     chunks, chunk c of row r at c ^ swz_a(r); A rows then B rows in a
+//     stage), NS - 1 steps ahead of its MFMAs; a wave waits only for its own
+//     copies (vmcnt) and no other wave reads its ring, so the main loop has no
+//     workgroup barrier;
+//   * fragments are two 128-bit LDS reads per row: lane (row li, group g)
+//     takes K values 8g .. 8g+7 of its A row and its B row, and MFMA j of a
+//     step (v_mfma_f32_16x16x4_f32) consumes value 8g + j in every group (the
+//     K order is permuted the same way for A and B);
+//   * the waves' partial tiles are then summed through LDS in wave order (the
+//     result does not depend on scheduling) and the epilogue runs on
+//     row-contiguous groups of 4 columns with 128-bit accesses: bias /
+//     residual / activation directly, other tapes through the tape
+//     interpreter; the direct operands are loaded before the partial sums so
+//     their latency overlaps the reduction.
+// K must be a positive multiple of 32 and the operands' spans below 2^29
+// elements (the host checks both).
+#include <algorithm>
+
+#include "kh_common.hpp"
+#include "kh_gemm_args.hpp"
+#include "kh_gemm_dev.hpp"
+#include "kh_internal.hpp"
+
+namespace kh {
+namespace {
+
+template <int BM, int BN, int WK, int NS>
+__global__ __launch_bounds__(64 * WK) void gemm_small_kernel(const GemmArgs a) {
+  constexpr int BK = 32, MT = 16, ACH = BK / 4;
+  constexpr int FM = BM / MT, FN = BN / MT;
+  constexpr int STAGE = (BM + BN) * BK;         // floats per stage: A rows, then B rows
+  constexpr int A_COPIES = BM * ACH / 64, B_COPIES = BN * ACH / 64;
+  constexpr int COPIES = A_COPIES + B_COPIES;   // copy instructions per stage and wave
+  constexpr int CS = BN + 4;                    // partial-tile row stride (16-byte aligned rows)
+  static_assert(BM % MT == 0 && BN % MT == 0, "tile of whole MFMA blocks");
+  static_assert((BM * ACH) % 64 == 0 && (BN * ACH) % 64 == 0, "whole copy instructions");
+  static_assert(NS >= 2 && NS <= 4 && (NS - 2) * COPIES < 64, "ring depth / vmcnt range");
+  static_assert(BM * CS <= NS * STAGE, "partial tile fits the wave's ring");
+  static_assert(WK * NS * STAGE * 4 <= 160 * 1024, "LDS");
+
+  __shared__ float4 rings[WK * NS * STAGE / 4];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  const int li = lane & 15, g = lane >> 4;
+  int tm, tn;
+  tile_coords(blockIdx.x, a, tm, tn);
+  const int bidx = blockIdx.y;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const float *Ab = a.A + (int64_t)bidx * a.sa_b;
+  const float *Bb = a.B + (int64_t)bidx * a.sb_b;
+  // this wave's K steps (the host checks K % 32 == 0 and K > 0)
+  const int steps = a.K / BK;
+  const int per_wave = (steps + WK - 1) / WK;
+  const int s_begin = wave_u * per_wave;
+  const int n_steps = max(0, min(steps, s_begin + per_wave) - s_begin);
+
+  float4 *ring = rings + wave_u * (NS * STAGE / 4);
+  const uint32_t ring_lds = (uint32_t)(uintptr_t)(lds_void_t *)ring;
+  // per-lane copy sources: byte offsets from the step's first K column (rows
+  // past M / N clamped to the last one; their results are never stored)
+  uint32_t a_off[A_COPIES], b_off[B_COPIES];
+#pragma unroll
+  for (int i = 0; i < A_COPIES; ++i) {
+    const int p = i * 64 + lane, r = p / ACH;
+    a_off[i] = (uint32_t)(min(m0 + r, a.M - 1) * (int)a.sa_m + ((p % ACH) ^ swz_a(r)) * 4) * 4u;
+  }
+#pragma unroll
+  for (int i = 0; i < B_COPIES; ++i) {
+    const int p = i * 64 + lane, r = p / ACH;   // B row r of the tile sits at stage row BM + r
+    b_off[i] = (uint32_t)(min(n0 + r, a.N - 1) * (int)a.sb_n + ((p % ACH) ^ swz_a(BM + r)) * 4) * 4u;
+  }
+  auto issue = [&](int s) {   // this wave's step s (0-based within its range)
+    const int k0 = (s_begin + s) * BK;
+    const float *abase = uniform_ptr(Ab + k0);
+    const float *bbase = uniform_ptr(Bb + k0);
+    const uint32_t lds = ring_lds + (uint32_t)((s % NS) * STAGE * 4);
+#pragma unroll
+    for (int i = 0; i < A_COPIES; ++i) copy_to_lds<4>(abase, a_off[i], lds + i * 1024);
+#pragma unroll
+    for (int i = 0; i < B_COPIES; ++i) copy_to_lds<4>(bbase, b_off[i], lds + BM * BK * 4 + i * 1024);
+  };
+  // this wave's copies of a step have landed, `later` steps' copies being
+  // issued after them
+  auto wait_landed = [&](int later) {
+    if (later <= 0) wait_vmcnt<0>();
+    else if (later == 1 || NS < 4) wait_vmcnt<COPIES>();
+    else wait_vmcnt<2 * COPIES>();
+  };
+
+  int fa_off[FM][2], fb_off[FN][2];
+#pragma unroll
+  for (int fm = 0; fm < FM; ++fm) {
+    const int r = fm * MT + li;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) fa_off[fm][h] = r * BK + ((2 * g + h) ^ swz_a(r)) * 4;
+  }
+#pragma unroll
+  for (int fn = 0; fn < FN; ++fn) {
+    const int r = BM + fn * MT + li;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) fb_off[fn][h] = r * BK + ((2 * g + h) ^ swz_a(r)) * 4;
+  }
+
+  f32x4 acc[FM][FN];
+#pragma unroll
+  for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) acc[fm][fn] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto part = [](const float4 &v, int j) { return j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w; };
+
+  for (int p = 0; p < NS - 1 && p < n_steps; ++p) issue(p);
+  for (int s = 0; s < n_steps; ++s) {
+    wait_landed(min(NS - 2, n_steps - 1 - s));
+    // the wave's own LDS: its copies landed (vmcnt), nothing else writes it
+    __builtin_amdgcn_wave_barrier();
+    const float *st = reinterpret_cast<const float *>(ring + (s % NS) * (STAGE / 4));
+    float4 xa[FM][2], xb[FN][2];
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) xa[fm][h] = *reinterpret_cast<const float4 *>(st + fa_off[fm][h]);
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) xb[fn][h] = *reinterpret_cast<const float4 *>(st + fb_off[fn][h]);
+    // the slot read now is refilled NS steps later: its fragment reads must
+    // have completed before this wave issues that copy (next iterations)
+    __builtin_amdgcn_s_waitcnt((3 << 14) | (7 << 4) | 15);  // lgkmcnt(0); vmcnt, expcnt unconstrained
+    if (s + NS - 1 < n_steps) issue(s + NS - 1);
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+          for (int fn = 0; fn < FN; ++fn)
+            acc[fm][fn] = __builtin_amdgcn_mfma_f32_16x16x4f32(part(xa[fm][h], j), part(xb[fn][h], j), acc[fm][fn],
+                                                               0, 0, 0);
+  }
+  wait_vmcnt<0>();   // (no copy of this wave is outstanding past here)
+
+  // direct epilogue: this thread's first output group's operands, loaded
+  // before the partial tiles are summed
+  constexpr int GROUPS = BM * BN / 4;
+  const int q0 = threadIdx.x;
+  auto group_mn = [&](int q, int &m, int &n) {
+    m = m0 + q / (BN / 4);
+    n = n0 + (q % (BN / 4)) * 4;
+  };
+  auto load4 = [&](int j, int m, int n, int valid) {
+    const float *p = a.eptr[j] + (int64_t)bidx * a.estride[j][0] + (int64_t)m * a.estride[j][1];
+    if ((a.e_vec_mask >> j & 1) && valid == 4) return *reinterpret_cast<const float4 *>(p + n);
+    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i = 0; i < valid; ++i) v[i] = p[(int64_t)(n + i) * a.estride[j][2]];
+    return make_float4(v[0], v[1], v[2], v[3]);
+  };
+  float4 pre_b = make_float4(0.f, 0.f, 0.f, 0.f), pre_r = pre_b;
+  if (a.direct && q0 < GROUPS) {
+    int m, n;
+    group_mn(q0, m, n);
+    if (m < a.M && n < a.N) {
+      const int valid = min(4, a.N - n);
+      if (a.d_bias >= 0) pre_b = load4(a.d_bias, m, n, valid);
+      if (a.d_res >= 0) pre_r = load4(a.d_res, m, n, valid);
+    }
+  }
+
+  // partial tiles through LDS (each wave into its own ring), summed in wave
+  // order
+  float *mine = reinterpret_cast<float *>(ring);
+#pragma unroll
+  for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) mine[(fm * MT + 4 * g + i) * CS + fn * MT + li] = acc[fm][fn][i];
+  __syncthreads();
+  const float *parts = reinterpret_cast<const float *>(rings);
+  for (int q = q0; q < GROUPS; q += 64 * WK) {
+    int m, n;
+    group_mn(q, m, n);
+    if (m >= a.M || n >= a.N) continue;
+    const int off = (m - m0) * CS + (n - n0);
+    float4 sum = *reinterpret_cast<const float4 *>(parts + off);
+#pragma unroll
+    for (int w = 1; w < WK; ++w) {
+      const float4 p = *reinterpret_cast<const float4 *>(parts + w * NS * STAGE + off);
+      sum.x += p.x, sum.y += p.y, sum.z += p.z, sum.w += p.w;
+    }
+    const int valid = min(4, a.N - n);
+    if (!a.direct) {
+      Vec<4> v;
+      v.v[0] = sum.x, v.v[1] = sum.y, v.v[2] = sum.z, v.v[3] = sum.w;
+      run_epilogue(a, bidx, m, n, valid, v);
+      continue;
+    }
+    // out = act((acc [+ bias]) [+ res]), in the tape's order
+    const float4 bv = q == q0 ? pre_b : (a.d_bias >= 0 ? load4(a.d_bias, m, n, valid) : pre_b);
+    const float4 rv = q == q0 ? pre_r : (a.d_res >= 0 ? load4(a.d_res, m, n, valid) : pre_r);
+    float v[4] = {sum.x, sum.y, sum.z, sum.w};
+    if (a.d_bias >= 0) v[0] += bv.x, v[1] += bv.y, v[2] += bv.z, v[3] += bv.w;
+    if (a.d_res >= 0) v[0] = rv.x + v[0], v[1] = rv.y + v[1], v[2] = rv.z + v[2], v[3] = rv.w + v[3];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (a.d_act == KH_OP_GELU_TANH) v[i] = op_gelu_tanh(v[i]);
+      else if (a.d_act == KH_OP_GELU_ERF) v[i] = op_gelu_erf(v[i]);
+      else if (a.d_act == KH_OP_RELU) v[i] = v[i] != v[i] ? v[i] : fmaxf(v[i], 0.0f);
+    }
+    float *o = a.eptr[a.d_out] + (int64_t)bidx * a.estride[a.d_out][0] + (int64_t)m * a.estride[a.d_out][1];
+    if ((a.e_vec_mask >> a.d_out & 1) && valid == 4) {
+      *reinterpret_cast<float4 *>(o + n) = make_float4(v[0], v[1], v[2], v[3]);
+    } else {
+      for (int i = 0; i < valid; ++i) o[(int64_t)(n + i) * a.estride[a.d_out][2]] = v[i];
+    }
+  }
+}
+
+}  // namespace
+
+hipError_t launch_gemm_small(int id, const GemmArgs &a, dim3 grid, hipStream_t stream) {
+  switch (id) {
+#define KH_CFGSM_CASE(cid, bm, bn, wk, ns)                                                      \
+  case cid:                                                                                    \
+    hipLaunchKernelGGL((gemm_small_kernel<bm, bn, wk, ns>), grid, dim3(64 * wk), 0, stream, a); \
+    break;
+    KH_GEMM_SMALL_CONFIGS(KH_CFGSM_CASE)
+#undef KH_CFGSM_CASE
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace kh

@@ -121,6 +121,17 @@ TILES = {
     62: (64, 128, 32, 2, 4, 1, 16),
     63: (32, 96, 32, 2, 2, 1, 16),
     64: (64, 64, 32, 2, 2, 1, 16),
+    # small tiles, WK waves splitting K, each with a private LDS ring (B as [N][K])
+    65: (16, 32, 32, 1, 1, 4, 16),
+    66: (16, 32, 32, 1, 1, 4, 16),
+    67: (16, 16, 32, 1, 1, 4, 16),
+    68: (16, 64, 32, 1, 1, 4, 16),
+    69: (32, 32, 32, 1, 1, 4, 16),
+    70: (16, 32, 32, 1, 1, 8, 16),
+    71: (16, 16, 32, 1, 1, 8, 16),
+    72: (32, 64, 32, 1, 1, 4, 16),
+    73: (32, 32, 32, 1, 1, 8, 16),
+    74: (16, 16, 32, 1, 1, 4, 16),
 }
 # configurations of the skinny-M kernel: A row-major with unit K stride and
 # K % 4 == 0, B a constant read through its [batch][N][K] copy, no split-K;
@@ -130,8 +141,13 @@ SKINNY = frozenset(range(47, 55))
 # configurations of the K-contiguous pipeline: A as for the skinny kernel, B
 # the [batch][N][K] copy of a constant, K a multiple of 32, no split-K
 K_CONTIGUOUS = frozenset(range(55, 65))
+# configurations of the small-M kernel: as the K-contiguous pipeline (B the
+# [batch][N][K] copy, K a positive multiple of 32, no split-K), for products
+# with at most SMALL_M_MAX rows
+SMALL_M = frozenset(range(65, 75))
+SMALL_M_MAX = 1024
 # configurations that read B through its [batch][N][K] copy
-NK_B = SKINNY | K_CONTIGUOUS
+NK_B = SKINNY | K_CONTIGUOUS | SMALL_M
 SKINNY_DEPTH = {47: 8, 48: 4, 49: 8, 50: 4, 51: 4, 52: 8, 53: 4, 54: 8}
 SKINNY_TURNS = 4
 # input precision of each configuration: 15-20 and 34-41 bf16 (A rounded in
@@ -148,7 +164,8 @@ OCCUPANCY = {0: 2, 1: 2, 2: 3, 3: 2, 4: 4, 5: 2, 6: 1, 7: 1, 8: 4, 9: 4, 10: 4, 
              26: 1, 27: 2, 28: 2, 29: 3, 30: 4, 31: 1, 32: 1, 33: 1,
              34: 1, 35: 2, 36: 2, 37: 2, 38: 3, 39: 1, 40: 2, 41: 1, 42: 1, 43: 1, 44: 2, 45: 2, 46: 3,
              47: 2, 48: 1, 49: 2, 50: 2, 51: 1, 52: 2, 53: 2, 54: 4,
-             55: 1, 56: 1, 57: 1, 58: 1, 59: 1, 60: 1, 61: 1, 62: 1, 63: 1, 64: 1}
+             55: 1, 56: 1, 57: 1, 58: 1, 59: 1, 60: 1, 61: 1, 62: 1, 63: 1, 64: 1,
+             65: 2, 66: 3, 67: 3, 68: 1, 69: 2, 70: 1, 71: 2, 72: 1, 73: 1, 74: 4}
 EFFICIENCY = {0: 0.62, 1: 0.6, 2: 0.62, 3: 0.58, 4: 0.66, 5: 0.62, 6: 0.67, 7: 0.55,
               8: 0.55, 9: 0.55, 10: 0.5, 11: 0.5, 12: 0.45, 13: 0.5, 14: 0.55,
               15: 0.15, 16: 0.15, 17: 0.15, 18: 0.15, 19: 0.15, 20: 0.15,
@@ -157,7 +174,8 @@ EFFICIENCY = {0: 0.62, 1: 0.6, 2: 0.62, 3: 0.58, 4: 0.66, 5: 0.62, 6: 0.67, 7: 0
               34: 0.2, 35: 0.2, 36: 0.2, 37: 0.2, 38: 0.2, 39: 0.2, 40: 0.2, 41: 0.2,
               42: 0.35, 43: 0.35, 44: 0.35, 45: 0.35, 46: 0.62,
               47: 0.45, 48: 0.45, 49: 0.5, 50: 0.5, 51: 0.5, 52: 0.4, 53: 0.5, 54: 0.45,
-              55: 0.7, 56: 0.7, 57: 0.7, 58: 0.7, 59: 0.75, 60: 0.75, 61: 0.78, 62: 0.72, 63: 0.65, 64: 0.68}
+              55: 0.7, 56: 0.7, 57: 0.7, 58: 0.7, 59: 0.75, 60: 0.75, 61: 0.78, 62: 0.72, 63: 0.65, 64: 0.68,
+              65: 0.5, 66: 0.5, 67: 0.45, 68: 0.5, 69: 0.5, 70: 0.5, 71: 0.45, 72: 0.5, 73: 0.5, 74: 0.45}
 # MFMA rate of a CU relative to fp32, per precision
 RATE = {"fp32": 1.0, "bf16": 16.0, "bf16x3": 16.0 / 3}
 CU_MFLOP_PER_US = 0.614          # fp32 MFMA: 256 flop/clk/CU at 2.4 GHz
@@ -198,6 +216,8 @@ def k_major_fits(m, k, tile) -> bool:
     product with m rows and depth k."""
     if tile in SKINNY:
         return skinny_fits(m, k, tile)
+    if tile in SMALL_M and m > SMALL_M_MAX:
+        return False
     return k % 32 == 0 and k > 0
 
 

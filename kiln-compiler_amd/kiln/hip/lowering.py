@@ -716,9 +716,6 @@ class _Lowerer:
         if best is None:
             raise NotImplementedError("HIP backend: matmul epilogue needs more than 8 registers")
         _encode(best[0], best[1], d, ref_offset=2)
-        if not gemv and autotune.PRECISION.get(int(cfg.get("tile", -1))) != prec:
-            # a configuration of another precision (e.g. the fp32 fallback above)
-            cfg = {**cfg, **autotune.default_config_for(batch, m, n, kk, precision=prec)}
         if gemv:
             # GEMV family: "tile" picks the workgroup variant of the [K][N]
             # kernel (0 = from the shape, 1-5), split-K 0 = from the shape
@@ -753,10 +750,12 @@ class _Lowerer:
         multiple of 8 (whole 16-byte weight chunks); other bf16 / bf16x3
         one-row products run on the GEMM tiles."""
         mm = next(n for n in k.nodes if n.op == "matmul")
+        return self._gemv_at(mm, self.matmul_choice(k)[1])
+
+    def _gemv_at(self, mm, prec) -> bool:
         a, b = mm.inputs
         if a.shape[-2] != 1:
             return False
-        _, prec = self.matmul_choice(k)
         if prec == "fp32":
             return True
         return prec == "bf16" and self.layouts[b].base[0] == "const" and a.shape[-1] % 8 == 0
@@ -771,13 +770,19 @@ class _Lowerer:
                 # bf16 inputs need B as a build-time bf16 copy of a constant; a
                 # matmul on two activations stays on the fp32 path (more exact)
                 prec = "fp32"
+            a, b = mm.inputs
+            batch = math.prod(a.shape[:-2]) if a.type.rank == 3 else 1
+            m, n, kk = a.shape[-2], b.shape[-1], a.shape[-1]
             tile = int(cfg.get("tile", -1))
-            if tile in autotune.NK_B and not (self.skinny_ok(mm) and autotune.k_major_fits(
-                    mm.inputs[0].shape[-2], mm.inputs[0].shape[-1], tile)):
-                a, b = mm.inputs
-                batch = math.prod(a.shape[:-2]) if a.type.rank == 3 else 1
-                cfg = autotune.default_config_for(batch, a.shape[-2], b.shape[-1], a.shape[-1], precision=prec,
-                                                  skinny=False)
+            if not self._gemv_at(mm, prec) and autotune.PRECISION.get(tile) != prec:
+                # a configuration of another precision (e.g. the fp32 fallback
+                # above): the default of this one, [N][K] configurations only
+                # when B can be copied that way
+                cfg = {**cfg, **autotune.default_config_for(batch, m, n, kk, precision=prec,
+                                                            skinny=self.skinny_ok(mm))}
+                tile = int(cfg.get("tile", -1))
+            if tile in autotune.NK_B and not (self.skinny_ok(mm) and autotune.k_major_fits(m, kk, tile)):
+                cfg = autotune.default_config_for(batch, m, n, kk, precision=prec, skinny=False)
             self._cfg[k] = (cfg, prec)
         return self._cfg[k]
 

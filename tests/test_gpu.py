@@ -315,15 +315,16 @@ def test_every_skinny_gemm_configuration(tile):
     assert f"tile {tile} splitk 1" in c._exe.program.launches[0].summary
 
 
-@pytest.mark.parametrize("tile", sorted(autotune.K_CONTIGUOUS))
+@pytest.mark.parametrize("tile", sorted(autotune.K_CONTIGUOUS | autotune.SMALL_M))
 def test_every_k_contiguous_gemm_configuration(tile):
-    # K-contiguous pipeline (one workgroup per CU, B read as a [N][K] copy):
+    # K-contiguous pipelines reading B as a [N][K] copy (the persistent
+    # one-workgroup-per-CU kernel and the small-M kernel whose waves split K):
     # ragged M / N (rows and columns past the edge clamped), K a multiple of
-    # 32 from one step to a multiple of the ring depth; direct epilogues
-    # (bias + residual, bias + GELU) and the staged tape epilogue (a scale);
-    # batched constant weights; repeated launches agree bit for bit
+    # 32 from one step (fewer steps than waves) to many steps per wave; direct
+    # epilogues (bias + residual, bias + GELU) and the tape epilogue (a
+    # scale); batched constant weights; repeated launches agree bit for bit
     cfg = lambda *_: {"tile": tile, "splitk": 1}
-    for m, n, k in ((21, 40, 32), (77, 133, 96), (300, 452, 160), (256, 768, 768)):
+    for m, n, k in ((21, 40, 32), (77, 133, 96), (300, 452, 160), (256, 768, 768), (128, 200, 3072)):
         torch.manual_seed(m + n + k)
         lin = gpt2_init_(torch.nn.Linear(k, n), seed=k).eval()
         x, r = torch.randn(m, k), torch.randn(m, n)

@@ -128,6 +128,21 @@ def test_interpreter_is_never_a_gpu_path():
         refuse("bench.py")
 
 
+@pytest.mark.parametrize("tile", [15, 34, 26])
+def test_other_precision_config_on_two_activations(tile):
+    # a configuration of another precision (bf16 / bf16x3 tiles asked for an
+    # fp32 product) falls back to the fp32 default; with two activations that
+    # default must not be a configuration reading B as a [N][K] constant copy
+    from kiln.hip import autotune
+
+    for m in (77, 128, 300):
+        a, b = torch.randn(m, 96), torch.randn(96, 130)
+        c = check(lambda x, y: x @ y, a, b, gpu_matmul_config=lambda *_: {"tile": tile, "splitk": 1})
+        (launch,) = c._exe.program.launches
+        chosen = int(launch.summary.split(" tile ")[1].split()[0])
+        assert chosen not in autotune.NK_B and autotune.PRECISION[chosen] == "fp32"
+
+
 @pytest.mark.parametrize("tile", [47, 49, 53])
 def test_skinny_gemm_lowering(tile):
     # skinny-M configurations read the weight as a [N][K] copy; a product of
