@@ -316,21 +316,6 @@ __global__ __launch_bounds__(64 * WM * WN * WK) void gemm_f32_kernel(const GemmA
 //   * the epilogue stages the accumulators through LDS per 16-row block and
 //     runs the tape on row-contiguous groups of 4 (coalesced 128-bit operand
 //     loads and stores).
-// B rows of a bf16 stage are BK K values = BK / 8 chunks of 16 bytes; row n
-// puts chunk c at c ^ swz_b16<CB>(n), chosen so the 16 consecutive rows one
-// 128-bit fragment read touches land in distinct 16-byte bank slots whether
-// the LDS serves such a read 8 lanes (128 bytes) or 16 lanes (256 bytes) at a
-// time: rows of 64 bytes pair up in a 128-byte bank row (n & 1 picks the
-// half), rows of 128 bytes take the A rows' swizzle, rows of 256 bytes span
-// the banks on their own.
-template <int CB>
-__device__ __forceinline__ int swz_b16(int n) {
-  if constexpr (CB == 4) return ((n >> 1) ^ (n >> 3)) & 3;
-  else if constexpr (CB == 8) return swz_a(n);
-  else return n & 15;
-}
-
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 // BF16B: B is a bf16 copy of a constant in [batch][N][K'] layout (K' = K
 // rounded up to 8, zero padded) and the products run on
@@ -1046,7 +1031,8 @@ constexpr TileCfg kConfigs[] = {
 #define KH_CFGNT_ROW(id, bm, bn, wm, wn, ns) {bm, bn, 32, wm, wn, 1, 16, 5, ns, KH_PREC_FP32},
     KH_GEMM_NT_CONFIGS(KH_CFGNT_ROW)
 #undef KH_CFGNT_ROW
-#define KH_CFGSM_ROW(id, bm, bn, wk, ns) {bm, bn, 32, 1, 1, wk, 16, 6, ns, KH_PREC_FP32},
+#define KH_CFGSM_ROW(id, bm, bn, wk, ns, prec) \
+  {bm, bn, 32, 1, 1, wk, 16, 6, ns, prec == 0 ? KH_PREC_FP32 : prec == 1 ? KH_PREC_BF16 : KH_PREC_BF16X3},
     KH_GEMM_SMALL_CONFIGS(KH_CFGSM_ROW)
 #undef KH_CFGSM_ROW
 };
@@ -1060,7 +1046,7 @@ constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 // on the GPT-2 block's shapes against row-major order (interleaved, warm
 // GPU): 2048x3072x768 on the 32x64 tile 5% faster, the others within 1%.
 int tile_group(const TileCfg &t, int tiles_m) {
-  const int lds = t.kind == 6   ? 4 * t.stages * t.bk * (t.bm + t.bn) * t.wk
+  const int lds = t.kind == 6   ? 4 * t.stages * t.bk * (t.bm + t.bn) * t.wk   // (fp32 bound)
                   : t.kind == 5 ? 4 * t.stages * t.bk * (t.bm + t.bn)
                   : t.kind == 3 ? 4 * t.stages * (t.bm * t.bk + (t.prec == KH_PREC_FP32 ? t.bk * t.bn
                                                                  : t.bn * t.bk / 2 * (t.prec == KH_PREC_BF16X3 ? 2 : 1)))

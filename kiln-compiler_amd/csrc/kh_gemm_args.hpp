@@ -147,18 +147,31 @@ inline hipError_t launch_splitk_reduce(const GemmArgs &a, int cus, hipStream_t s
 hipError_t launch_gemm_nt(int id, const GemmArgs &a, dim3 grid, hipStream_t stream);
 
 // Configurations of the small-M kernel (kind 6, kh_gemm_small.hip): id, tile
-// BM x BN, WK waves splitting K (each with a private LDS ring), NS stages.
+// BM x BN, WK waves splitting K (each with a private LDS ring), NS stages,
+// precision (0 fp32, 1 bf16, 2 three-pass bf16).
 #define KH_GEMM_SMALL_CONFIGS(X) \
-  X(65, 16, 32, 4, 3)            \
-  X(66, 16, 32, 4, 2)            \
-  X(67, 16, 16, 4, 3)            \
-  X(68, 16, 64, 4, 2)            \
-  X(69, 32, 32, 4, 2)            \
-  X(70, 16, 32, 8, 2)            \
-  X(71, 16, 16, 8, 2)            \
-  X(72, 32, 64, 4, 2)            \
-  X(73, 32, 32, 8, 2)            \
-  X(74, 16, 16, 4, 2)
+  X(65, 16, 32, 4, 3, 0)         \
+  X(66, 16, 32, 4, 2, 0)         \
+  X(67, 16, 16, 4, 3, 0)         \
+  X(68, 16, 64, 4, 2, 0)         \
+  X(69, 32, 32, 4, 2, 0)         \
+  X(70, 16, 32, 8, 2, 0)         \
+  X(71, 16, 16, 8, 2, 0)         \
+  X(72, 32, 64, 4, 2, 0)         \
+  X(73, 32, 32, 8, 2, 0)         \
+  X(74, 16, 16, 4, 2, 0)         \
+  X(75, 16, 32, 4, 2, 1)         \
+  X(76, 16, 32, 8, 2, 1)         \
+  X(77, 32, 32, 4, 2, 1)         \
+  X(78, 16, 64, 4, 2, 1)         \
+  X(79, 16, 16, 4, 2, 1)         \
+  X(80, 16, 32, 4, 2, 2)         \
+  X(81, 16, 32, 8, 2, 2)         \
+  X(82, 32, 32, 4, 2, 2)         \
+  X(83, 16, 16, 4, 2, 2)         \
+  X(84, 16, 16, 8, 2, 1)         \
+  X(85, 32, 32, 8, 2, 1)         \
+  X(86, 16, 16, 8, 2, 2)
 
 // Launch configuration `id` of kind 6 (hipErrorInvalidValue for another id).
 hipError_t launch_gemm_small(int id, const GemmArgs &a, dim3 grid, hipStream_t stream);

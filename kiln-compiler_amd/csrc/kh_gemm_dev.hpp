@@ -117,5 +117,21 @@ __device__ __forceinline__ void stage_barrier() {
 constexpr int kBufferRaw = 0x00020000;   // buffer resource word 3, gfx9 raw buffer: 32-bit data format
 constexpr uint32_t kOutside = 0x80000000u;  // an offset past any resource's extent: reads zeros
 
+// B rows of a bf16 stage are BK K values = BK / 8 chunks of 16 bytes; row n
+// puts chunk c at c ^ swz_b16<CB>(n), chosen so the 16 consecutive rows one
+// 128-bit fragment read touches land in distinct 16-byte bank slots whether
+// the LDS serves such a read 8 lanes (128 bytes) or 16 lanes (256 bytes) at a
+// time: rows of 64 bytes pair up in a 128-byte bank row (n & 1 picks the
+// half), rows of 128 bytes take the A rows' swizzle, rows of 256 bytes span
+// the banks on their own.
+template <int CB>
+__device__ __forceinline__ int swz_b16(int n) {
+  if constexpr (CB == 4) return ((n >> 1) ^ (n >> 3)) & 3;
+  else if constexpr (CB == 8) return swz_a(n);
+  else return n & 15;
+}
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
 }  // namespace
 }  // namespace kh

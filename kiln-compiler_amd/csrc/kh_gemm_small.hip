@@ -1,6 +1,7 @@
-// kh_gemm_small.hip - fp32 matmul for products with few rows (configuration
-// kind 6): C[b] = epilogue(A[b] @ B[b]) with A [.., M, K] row-major and B the
-// [batch][N][K] copy of a constant weight, both K-contiguous.
+// kh_gemm_small.hip - matmul for products with few rows (configuration kind
+// 6): C[b] = epilogue(A[b] @ B[b]) with A [.., M, K] row-major fp32 and B the
+// [batch][N][K] copy of a constant weight (fp32, or the bf16 / three-pass
+// bf16 copies), both K-contiguous.
 //
 // Same contract as the rest of the matmul family (the reference's tl.dot
 // kernel with fused epilogue, kiln/gpu/codegen.py:484-530). A product with a
@@ -38,16 +39,26 @@
 namespace kh {
 namespace {
 
-template <int BM, int BN, int WK, int NS>
+// PREC: 0 fp32 (v_mfma_f32_16x16x4_f32, eight per output block and step);
+// 1 bf16 - B the bf16 [batch][N][K'] copy, A rounded to bf16 as its
+// fragments are read, one v_mfma_f32_16x16x32_bf16 per block and step, fp32
+// accumulation (the arithmetic of the other bf16 GEMMs); 2 three-pass bf16 -
+// B the [batch][N][2K'] copy holding bf16(w) then bf16(w - bf16(w)) per row,
+// A split the same way, a.b = a_lo.b_hi + a_hi.b_lo + a_hi.b_hi.
+template <int BM, int BN, int WK, int NS, int PREC>
 __global__ __launch_bounds__(64 * WK) void gemm_small_kernel(const GemmArgs a) {
   constexpr int BK = 32, MT = 16, ACH = BK / 4;
   constexpr int FM = BM / MT, FN = BN / MT;
-  constexpr int STAGE = (BM + BN) * BK;         // floats per stage: A rows, then B rows
-  constexpr int A_COPIES = BM * ACH / 64, B_COPIES = BN * ACH / 64;
+  constexpr bool BF = PREC != 0;
+  constexpr int B_HALF = BN * BK / 2;           // words of one bf16 copy of a stage's B rows
+  constexpr int A_FLOATS = BM * BK;
+  constexpr int STAGE = A_FLOATS + (BF ? B_HALF * (PREC == 2 ? 2 : 1) : BN * BK);   // words: A rows, then B rows
+  constexpr int B_CHUNKS = BF ? BN * 4 * (PREC == 2 ? 2 : 1) : BN * ACH;   // 16-byte chunks of B per stage
+  constexpr int A_COPIES = BM * ACH / 64, B_COPIES = B_CHUNKS / 64;
   constexpr int COPIES = A_COPIES + B_COPIES;   // copy instructions per stage and wave
   constexpr int CS = BN + 4;                    // partial-tile row stride (16-byte aligned rows)
   static_assert(BM % MT == 0 && BN % MT == 0, "tile of whole MFMA blocks");
-  static_assert((BM * ACH) % 64 == 0 && (BN * ACH) % 64 == 0, "whole copy instructions");
+  static_assert((BM * ACH) % 64 == 0 && B_CHUNKS % 64 == 0, "whole copy instructions");
   static_assert(NS >= 2 && NS <= 4 && (NS - 2) * COPIES < 64, "ring depth / vmcnt range");
   static_assert(BM * CS <= NS * STAGE, "partial tile fits the wave's ring");
   static_assert(WK * NS * STAGE * 4 <= 160 * 1024, "LDS");
@@ -63,7 +74,6 @@ __global__ __launch_bounds__(64 * WK) void gemm_small_kernel(const GemmArgs a) {
   const int bidx = blockIdx.y;
   const int m0 = tm * BM, n0 = tn * BN;
   const float *Ab = a.A + (int64_t)bidx * a.sa_b;
-  const float *Bb = a.B + (int64_t)bidx * a.sb_b;
   // this wave's K steps (the host checks K % 32 == 0 and K > 0)
   const int steps = a.K / BK;
   const int per_wave = (steps + WK - 1) / WK;
@@ -82,18 +92,30 @@ __global__ __launch_bounds__(64 * WK) void gemm_small_kernel(const GemmArgs a) {
   }
 #pragma unroll
   for (int i = 0; i < B_COPIES; ++i) {
-    const int p = i * 64 + lane, r = p / ACH;   // B row r of the tile sits at stage row BM + r
-    b_off[i] = (uint32_t)(min(n0 + r, a.N - 1) * (int)a.sb_n + ((p % ACH) ^ swz_a(BM + r)) * 4) * 4u;
+    const int p = i * 64 + lane;
+    if constexpr (BF) {
+      // bf16 row n: 4 chunks of 8 K values, chunk c at c ^ swz_b16<4>(n);
+      // three-pass: the lo rows (K' further along the copy's row) follow
+      const int half = p / (BN * 4), pp = p % (BN * 4), r = pp / 4;
+      const int64_t row = (int64_t)min(n0 + r, a.N - 1) * a.sb_n + half * (a.sb_n / 2);
+      b_off[i] = (uint32_t)(row + ((pp % 4) ^ swz_b16<4>(r)) * 8) * 2u;
+    } else {
+      const int r = p / ACH;   // B row r of the tile sits at stage row BM + r
+      b_off[i] = (uint32_t)(min(n0 + r, a.N - 1) * (int)a.sb_n + ((p % ACH) ^ swz_a(BM + r)) * 4) * 4u;
+    }
   }
   auto issue = [&](int s) {   // this wave's step s (0-based within its range)
     const int k0 = (s_begin + s) * BK;
     const float *abase = uniform_ptr(Ab + k0);
-    const float *bbase = uniform_ptr(Bb + k0);
+    const float *bbase =
+        BF ? uniform_ptr(reinterpret_cast<const float *>(reinterpret_cast<const __bf16 *>(a.B) +
+                                                          (int64_t)bidx * a.sb_b + k0))
+           : uniform_ptr(a.B + (int64_t)bidx * a.sb_b + k0);
     const uint32_t lds = ring_lds + (uint32_t)((s % NS) * STAGE * 4);
 #pragma unroll
     for (int i = 0; i < A_COPIES; ++i) copy_to_lds<4>(abase, a_off[i], lds + i * 1024);
 #pragma unroll
-    for (int i = 0; i < B_COPIES; ++i) copy_to_lds<4>(bbase, b_off[i], lds + BM * BK * 4 + i * 1024);
+    for (int i = 0; i < B_COPIES; ++i) copy_to_lds<4>(bbase, b_off[i], lds + A_FLOATS * 4 + i * 1024);
   };
   // this wave's copies of a step have landed, `later` steps' copies being
   // issued after them
@@ -103,6 +125,9 @@ __global__ __launch_bounds__(64 * WK) void gemm_small_kernel(const GemmArgs a) {
     else wait_vmcnt<2 * COPIES>();
   };
 
+  // fragment offsets (words, within a stage): lane (li, g) reads K values
+  // 8g .. 8g+7 of its A row (two 128-bit reads) and of its B row (two fp32
+  // reads, or one 16-byte bf16 chunk)
   int fa_off[FM][2], fb_off[FN][2];
 #pragma unroll
   for (int fm = 0; fm < FM; ++fm) {
@@ -112,9 +137,14 @@ __global__ __launch_bounds__(64 * WK) void gemm_small_kernel(const GemmArgs a) {
   }
 #pragma unroll
   for (int fn = 0; fn < FN; ++fn) {
-    const int r = BM + fn * MT + li;
+    const int r = fn * MT + li;
+    if constexpr (BF) {
+      fb_off[fn][0] = A_FLOATS + r * (BK / 2) + ((g ^ swz_b16<4>(r)) * 4);
+      fb_off[fn][1] = fb_off[fn][0] + B_HALF;   // three-pass: the lo row
+    } else {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) fb_off[fn][h] = r * BK + ((2 * g + h) ^ swz_a(r)) * 4;
+      for (int h = 0; h < 2; ++h) fb_off[fn][h] = (BM + r) * BK + ((2 * g + h) ^ swz_a(BM + r)) * 4;
+    }
   }
 
   f32x4 acc[FM][FN];
@@ -138,21 +168,49 @@ __global__ __launch_bounds__(64 * WK) void gemm_small_kernel(const GemmArgs a) {
 #pragma unroll
     for (int fn = 0; fn < FN; ++fn)
 #pragma unroll
-      for (int h = 0; h < 2; ++h) xb[fn][h] = *reinterpret_cast<const float4 *>(st + fb_off[fn][h]);
+      for (int h = 0; h < (PREC == 1 ? 1 : 2); ++h) xb[fn][h] = *reinterpret_cast<const float4 *>(st + fb_off[fn][h]);
     // the slot read now is refilled NS steps later: its fragment reads must
     // have completed before this wave issues that copy (next iterations)
     __builtin_amdgcn_s_waitcnt((3 << 14) | (7 << 4) | 15);  // lgkmcnt(0); vmcnt, expcnt unconstrained
     if (s + NS - 1 < n_steps) issue(s + NS - 1);
+    if constexpr (BF) {
+      bf16x8 ah[FM], al[FM];
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+      for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+        for (int e = 0; e < 8; ++e) {
+          const float x = part(xa[fm][e / 4], e % 4);
+          ah[fm][e] = (__bf16)x;
+          if constexpr (PREC == 2) {
+            // the difference is exact in fp32; a non-finite hi part keeps lo 0
+            const float hv = (float)ah[fm][e];
+            al[fm][e] = (__bf16)(__builtin_isfinite(hv) ? x - hv : 0.0f);
+          }
+        }
 #pragma unroll
-        for (int fm = 0; fm < FM; ++fm)
+      for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
-          for (int fn = 0; fn < FN; ++fn)
-            acc[fm][fn] = __builtin_amdgcn_mfma_f32_16x16x4f32(part(xa[fm][h], j), part(xb[fn][h], j), acc[fm][fn],
-                                                               0, 0, 0);
+        for (int fn = 0; fn < FN; ++fn) {
+          const bf16x8 bh = *reinterpret_cast<const bf16x8 *>(&xb[fn][0]);
+          if constexpr (PREC == 2) {
+            const bf16x8 bl = *reinterpret_cast<const bf16x8 *>(&xb[fn][1]);
+            acc[fm][fn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[fm], bh, acc[fm][fn], 0, 0, 0);
+            acc[fm][fn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[fm], bl, acc[fm][fn], 0, 0, 0);
+          }
+          acc[fm][fn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[fm], bh, acc[fm][fn], 0, 0, 0);
+        }
+    } else {
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+            for (int fn = 0; fn < FN; ++fn)
+              acc[fm][fn] = __builtin_amdgcn_mfma_f32_16x16x4f32(part(xa[fm][h], j), part(xb[fn][h], j),
+                                                                 acc[fm][fn], 0, 0, 0);
+    }
   }
   wait_vmcnt<0>();   // (no copy of this wave is outstanding past here)
 
@@ -236,9 +294,9 @@ __global__ __launch_bounds__(64 * WK) void gemm_small_kernel(const GemmArgs a) {
 
 hipError_t launch_gemm_small(int id, const GemmArgs &a, dim3 grid, hipStream_t stream) {
   switch (id) {
-#define KH_CFGSM_CASE(cid, bm, bn, wk, ns)                                                      \
-  case cid:                                                                                    \
-    hipLaunchKernelGGL((gemm_small_kernel<bm, bn, wk, ns>), grid, dim3(64 * wk), 0, stream, a); \
+#define KH_CFGSM_CASE(cid, bm, bn, wk, ns, prec)                                                      \
+  case cid:                                                                                          \
+    hipLaunchKernelGGL((gemm_small_kernel<bm, bn, wk, ns, prec>), grid, dim3(64 * wk), 0, stream, a); \
     break;
     KH_GEMM_SMALL_CONFIGS(KH_CFGSM_CASE)
 #undef KH_CFGSM_CASE

@@ -315,7 +315,8 @@ def test_every_skinny_gemm_configuration(tile):
     assert f"tile {tile} splitk 1" in c._exe.program.launches[0].summary
 
 
-@pytest.mark.parametrize("tile", sorted(autotune.K_CONTIGUOUS | autotune.SMALL_M))
+@pytest.mark.parametrize("tile", [t for t in sorted(autotune.K_CONTIGUOUS | autotune.SMALL_M)
+                                  if autotune.PRECISION[t] == "fp32"])
 def test_every_k_contiguous_gemm_configuration(tile):
     # K-contiguous pipelines reading B as a [N][K] copy (the persistent
     # one-workgroup-per-CU kernel and the small-M kernel whose waves split K):

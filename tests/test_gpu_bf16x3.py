@@ -69,8 +69,9 @@ def test_config_gemm_sweep_bf16x3(mnk):
 @pytest.mark.parametrize("tile", [t for t in sorted(autotune.TILES) if autotune.PRECISION[t] == "bf16x3"])
 def test_every_bf16x3_tile_configuration(tile):
     # ragged sizes (K = 61: not a multiple of 4 or 8), then interior tiles with
-    # ragged edges; bias + residual epilogue; split-K 1 and 2
-    for m, n, k in ((77, 133, 61), (300, 452, 96)):
+    # ragged edges; bias + residual epilogue; split-K 1 and 2; a deeper K
+    # (several steps per wave for the small-M kernel)
+    for m, n, k in ((77, 133, 61), (300, 452, 96), (128, 200, 768)):
         torch.manual_seed(tile)
         w = torch.randn(n, k) * 0.1
         b, r = torch.randn(n), torch.randn(m, n)
