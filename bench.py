@@ -685,19 +685,27 @@ def stack_bench(autotune):
     from models.transformer import Stack, gpt2_init_
 
     out = {}
-    for name, T in (("prefill_1024", 1024), ("decode_1", 1)):
+    # decode_1_chain: the same decode with its 48 GEMVs as one persistent
+    # launch (gemv_chains, opt-in), measured beside the default
+    for name, T, chains in (("prefill_1024", 1024, False), ("decode_1", 1, False), ("decode_1_chain", 1, True)):
         torch.manual_seed(0)
         model = gpt2_init_(Stack(12, 768, 12, T), seed=0).eval().cuda()
         x = torch.randn(T, 768, device="cuda")
-        c = kiln.compile(model, (x,), device="cuda", autotune=autotune)
+        c = kiln.compile(model, (x,), device="cuda", autotune=autotune, gemv_chains=chains)
         with torch.no_grad():
             torch.testing.assert_close(c(x), model(x), rtol=1e-4, atol=1e-5)
             k_ms = ms_per_call(lambda: c(x))
             e_ms = ms_per_call(lambda: model(x))
         flops = 12 * block_flops(T)
         out[name] = {"kiln_ms": round(k_ms, 4), "eager_ms": round(e_ms, 4), "tflops": round(flops / k_ms / 1e9, 2),
-                     "launches": c.report.lowering["launches"]}
-        log(f"stack {name}: kiln {k_ms:.4f} ms, eager {e_ms:.4f} ms")
+                     "launches": c.report.lowering["launches"],
+                     "kernel_launches": c.report.lowering["kernel_launches"]}
+        if T == 1:   # the algorithmic bytes of every launch (weights once each), per call
+            nbytes = sum(launch.bytes for launch in c._exe.program.launches)
+            out[name]["bytes"] = nbytes
+            out[name]["gbs"] = round(nbytes / k_ms / 1e6, 1)
+        log(f"stack {name}: kiln {k_ms:.4f} ms ({c.report.lowering['kernel_launches']} kernel launches), "
+            f"eager {e_ms:.4f} ms" + (f", {out[name]['gbs']} GB/s of {out[name]['bytes'] / 1e6:.1f} MB" if T == 1 else ""))
     return out
 
 

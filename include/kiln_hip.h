@@ -77,6 +77,10 @@ enum { KH_ROW_GENERIC = 0, KH_ROW_LAYERNORM = 1, KH_ROW_SOFTMAX = 2 };
 enum { KH_PREC_FP32 = 0, KH_PREC_BF16 = 1, KH_PREC_BF16X3 = 2 };
 /* GEMV prologues (kh_launch.cfg[4] of a KH_FAM_GEMV launch) */
 enum { KH_GEMV_PRO_NONE = 0, KH_GEMV_PRO_LAYERNORM = 1, KH_GEMV_PRO_ATTN = 2 };
+/* GEMV launch flag (kh_launch.variant of a KH_FAM_GEMV launch): the launch
+ * may run inside a persistent chain with the flagged GEMV launches next to it
+ * (kh_plan_chains); no counterpart in the reference. */
+enum { KH_GEMV_CHAIN = 1 };
 
 /*
  * Tape: a straight-line program over KH_NREGS slots, each slot holding the
@@ -254,6 +258,25 @@ int kh_plan_replay(kh_plan *plan, void *stream);
  * The autotuner times candidate plans with it. */
 int kh_plan_time(kh_plan *plan, int index, void *const *inputs, int n_inputs, void *const *outputs, int n_outputs,
                  int repeats, int rounds, void *stream, double *seconds);
+/*
+ * Persistent GEMV chains. No counterpart in the reference, which launches
+ * every kernel on its own. Consecutive launches flagged KH_GEMV_CHAIN whose
+ * operands allow it (each reads the whole output of the one before: decode's
+ * GEMV after GEMV) run as ONE launch in which each stage's weights stream
+ * while the previous stage's outputs are handed over. kh_plan_bind sets up a
+ * chain's device state (it allocates: descriptors, one 8-byte hand-over word
+ * per output column of every stage, an epoch); a chain that could not be
+ * bound (no GPU) runs launch by launch. kh_plan_run, kh_plan_run_noalloc,
+ * kh_plan_capture and kh_plan_time(index -1) take the one launch;
+ * kh_plan_run_one and kh_plan_time of one index run the launch alone.
+ * kh_plan_chains: *n_chains = the number of chains; ranges receives up to
+ * max_chains triples {first launch, number of launches, active}.
+ */
+int kh_plan_chains(const kh_plan *plan, int32_t *ranges, int max_chains, int *n_chains);
+/* Waits inside the plan's chains that gave up (a bounded wait that ran out:
+ * its workgroup left the kernel and later values are stale; none is expected).
+ * Synchronises the device. */
+int kh_plan_chain_timeouts(kh_plan *plan, uint64_t *timeouts);
 int kh_plan_destroy(kh_plan *plan);
 
 #ifdef __cplusplus

@@ -60,14 +60,31 @@ __device__ __forceinline__ float dpp(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
 }
 
+// The two cross-row steps exchange register values between rows with
+// v_permlane16_swap (rows 2k and 2k + 1) and v_permlane32_swap (lane halves)
+// instead of LDS permutes: each returns the pair (value of the even row or
+// low half, value of the odd row or high half) in every lane of the pair, so
+// combining the two gives every lane the same value, and the result is the
+// one the xor butterfly over lanes l ^ 16, l ^ 32 gives (the same two
+// operands per step; fp addition and max are commutative).
+__device__ __forceinline__ float2 row_pair(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float2 half_pair(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
   v += dpp<0xB1>(v);   // quad_perm [1,0,3,2]
   v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]
   v += dpp<0x141>(v);  // row_half_mirror
   v += dpp<0x140>(v);  // row_mirror
-  v += __shfl_xor(v, 16, kWave);
-  v += __shfl_xor(v, 32, kWave);
-  return v;
+  float2 p = row_pair(v);
+  v = p.x + p.y;
+  p = half_pair(v);
+  return p.x + p.y;
 }
 
 // NaN-propagating at every step (v_max_f32 alone returns the non-NaN operand),
@@ -77,9 +94,10 @@ __device__ __forceinline__ float wave_max(float v) {
   v = nan_max(v, dpp<0x4E>(v));
   v = nan_max(v, dpp<0x141>(v));
   v = nan_max(v, dpp<0x140>(v));
-  v = nan_max(v, __shfl_xor(v, 16, kWave));
-  v = nan_max(v, __shfl_xor(v, 32, kWave));
-  return v;
+  float2 p = row_pair(v);
+  v = nan_max(p.x, p.y);
+  p = half_pair(v);
+  return nan_max(p.x, p.y);
 }
 
 // ---------------------------------------------------------------------------

@@ -510,6 +510,10 @@ class GemvOp final : public Op {
     return launch_splitk_reduce(a, current_device().cus, stream);
   }
   size_t partial_floats() const override { return n_partials; }
+  bool gemv_facts(GemvFacts &f) const override {
+    f.args = &args, f.nk_r = nk_r, f.bf16 = bf16;
+    return true;
+  }
 
   static bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
@@ -563,6 +567,10 @@ std::unique_ptr<Op> make_gemv(const kh_launch &L, std::string &err, bool &unsupp
     return nullptr;
   }
   const int64_t batch = L.gemm[0], M = L.gemm[1], N = L.gemm[2], K = L.gemm[3];
+  if (L.variant != 0 && L.variant != KH_GEMV_CHAIN) {
+    err = "gemv: unknown launch flags " + std::to_string(L.variant);
+    return nullptr;
+  }
   if (M != 1) {
     err = "gemv: M must be 1";
     return nullptr;

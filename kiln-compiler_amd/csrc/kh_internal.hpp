@@ -8,10 +8,13 @@
 
 #include <memory>
 #include <string>
+#include <vector>
 
 #include "kiln_hip.h"
 
 namespace kh {
+
+struct GemmArgs;
 
 struct Device {
   int id = -1;
@@ -30,7 +33,36 @@ class Op {
   // asks for none. Every op writes all the partials it reads back.
   virtual hipError_t launch(float *const *ptrs, float *partials, hipStream_t stream) = 0;
   virtual size_t partial_floats() const { return 0; }
+  // GEMV ops: the parsed arguments and kernel choice (for chaining); false
+  // for every other family.
+  virtual bool gemv_facts(struct GemvFacts &) const { return false; }
 };
+
+struct GemvFacts {
+  const GemmArgs *args = nullptr;
+  int nk_r = 0;       // > 0: the K-contiguous kernel ([N][K] weights) runs it
+  bool bf16 = false;  // bf16 weights
+};
+
+// Consecutive GEMV launches [first(), end()) of a plan that run as one
+// persistent launch (kh_chain.hip). bind() resolves the operands and sets up
+// the chain's device state (it allocates); launch() resolves the plan's
+// inputs and outputs and launches.
+class Chain {
+ public:
+  virtual ~Chain() = default;
+  virtual int first() const = 0;
+  virtual int end() const = 0;
+  virtual bool active() const = 0;  // bound on a GPU
+  virtual int bind(void *const *consts, int n_consts, void *arena, std::string &err) = 0;
+  virtual hipError_t launch(void *const *inputs, int n_in, void *const *outputs, int n_out, hipStream_t stream) = 0;
+  virtual int timeouts(unsigned long long *out) = 0;
+};
+
+// The chains of a plan's launches (only GEMV launches marked KH_GEMV_CHAIN
+// whose operands allow it; at least two launches each).
+std::vector<std::unique_ptr<Chain>> find_chains(const std::vector<kh_launch> &desc,
+                                                const std::vector<std::unique_ptr<Op>> &ops);
 
 // Each factory returns nullptr and sets `err` when the descriptor is invalid or
 // unsupported; `unsupported` distinguishes the two for the status code.

@@ -141,6 +141,8 @@ bool check_tape(const kh_launch &L, int begin, int end, bool allow_row_ops, Tape
 struct kh_plan {
   std::vector<kh_launch> desc;
   std::vector<std::unique_ptr<kh::Op>> ops;
+  std::vector<std::unique_ptr<kh::Chain>> chains;  // persistent GEMV chains over runs of launches
+  std::vector<int> chain_start;                    // launch index -> chain starting there, or -1
   size_t ws_needed = 0;
   std::vector<void *> consts;
   void *arena = nullptr;
@@ -201,12 +203,21 @@ int run_range(kh_plan *p, int begin, int end, void *const *inputs, int n_in, voi
     return fail(KH_ERR_CAPACITY, "plan needs a workspace of " + std::to_string(p->ws_needed) +
                                      " bytes: bind one (kh_plan_bind) or run it with kh_plan_run_noalloc");
   float *ptrs[KH_MAX_REFS];
-  for (int i = begin; i < end; ++i) {
+  for (int i = begin; i < end;) {
+    // a chain the range covers whole runs as its one launch
+    const int c = p->chain_start[i];
+    if (c >= 0 && p->chains[c]->active() && p->chains[c]->end() <= end) {
+      const hipError_t e = p->chains[c]->launch(inputs, n_in, outputs, n_out, stream);
+      if (e != hipSuccess) return kh::hip_fail(e, "GEMV chain");
+      i = p->chains[c]->end();
+      continue;
+    }
     const int rc = resolve(p, i, inputs, n_in, outputs, n_out, ptrs);
     if (rc != KH_OK) return rc;
     float *partials = p->ops[i]->partial_floats() ? static_cast<float *>(workspace) : nullptr;
     const hipError_t e = p->ops[i]->launch(ptrs, partials, stream);
     if (e != hipSuccess) return kh::hip_fail(e, p->desc[i].name);
+    ++i;
   }
   return KH_OK;
 }
@@ -299,6 +310,9 @@ int kh_plan_create(const kh_launch *launches, int n_launches, kh_plan **out) {
   size_t partials = 0;
   for (auto &op : p->ops) partials = std::max(partials, op->partial_floats());
   p->ws_needed = partials * sizeof(float);
+  p->chains = kh::find_chains(p->desc, p->ops);
+  p->chain_start.assign(p->desc.size(), -1);
+  for (int c = 0; c < (int)p->chains.size(); ++c) p->chain_start[p->chains[c]->first()] = c;
   *out = p.release();
   return KH_OK;
 }
@@ -322,6 +336,35 @@ int kh_plan_bind(kh_plan *plan, void *const *consts, int n_consts, void *arena, 
   plan->workspace = workspace;
   plan->ws_size = workspace_bytes;
   plan->bound = true;
+  // chains bind their device state here; one that cannot (no GPU: a plan
+  // bound for kh_plan_run_host) stays inactive and its launches run one by one
+  for (auto &c : plan->chains) {
+    std::string err;
+    (void)c->bind(consts, n_consts, arena, err);
+  }
+  return KH_OK;
+}
+
+int kh_plan_chains(const kh_plan *plan, int32_t *ranges, int max_chains, int *n_chains) {
+  if (!plan || !n_chains || max_chains < 0 || (max_chains > 0 && !ranges)) return fail(KH_ERR_INVALID, "bad arguments");
+  *n_chains = (int)plan->chains.size();
+  for (int c = 0; c < std::min(max_chains, *n_chains); ++c) {
+    const kh::Chain &ch = *plan->chains[c];
+    ranges[3 * c] = ch.first();
+    ranges[3 * c + 1] = ch.end() - ch.first();
+    ranges[3 * c + 2] = ch.active() ? 1 : 0;
+  }
+  return KH_OK;
+}
+
+int kh_plan_chain_timeouts(kh_plan *plan, uint64_t *timeouts) {
+  if (!plan || !timeouts) return fail(KH_ERR_INVALID, "bad arguments");
+  *timeouts = 0;
+  for (auto &c : plan->chains) {
+    unsigned long long n = 0;
+    if (c->timeouts(&n) != KH_OK) return fail(KH_ERR_HIP, "reading a chain's state");
+    *timeouts += n;
+  }
   return KH_OK;
 }
 

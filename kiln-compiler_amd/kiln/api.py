@@ -48,6 +48,8 @@ class Options:
     debug: bool = False          # NaN-poison the arena, synchronise after every run
     fused_attention: bool = True # scores -> softmax -> (x V) as one launch (needs fusion)
     plan_cache: bool = True      # reuse plans lowered earlier for the same graph and settings
+    gemv_chains: bool = False    # consecutive one-row matmuls (decode) as one persistent launch (measured
+                                 # slower than launch by launch at the GPT-2 decode sizes, so opt-in)
 
     @classmethod
     def none(cls, **overrides):
@@ -180,12 +182,14 @@ class _GpuBuild:
         config_for, source_name, tuner = self.config_source()
         key = None
         if self.options.plan_cache and source_name is not None:
-            key = plans.plan_key(str(self.graph), self.precision, source_name, kl.device_info())
+            source = source_name + "|gemv-chains" if self.options.gemv_chains else source_name
+            key = plans.plan_key(str(self.graph), self.precision, source, kl.device_info())
             stored = plans.load(key)
             if stored is not None:
                 program, log = stored
                 return program, log, plans.listing_path(key), "stored"
-        program = lower_graph(self.graph, precision=self.precision, matmul_config=config_for)
+        program = lower_graph(self.graph, precision=self.precision, matmul_config=config_for,
+                              gemv_chains=self.options.gemv_chains)
         log = tuner.log if tuner is not None else []
         if key is None:   # a caller's config function: the plan cannot be keyed, only listed
             return program, log, plans.write_listing("unkeyed-" + program.digest(), program), "lowered"
@@ -211,11 +215,16 @@ class _GpuBuild:
             name = FAMILY_NAMES[launch.family]
             families[name] = families.get(name, 0) + 1
         memory = self.pm.stats.get("memory-plan", {})
+        # persistent GEMV chains the library formed: each runs as one kernel launch
+        plan = getattr(exe, "plan", None)
+        chains = plan.chains() if plan is not None else []
+        kernel_launches = len(program.launches) - sum(n - 1 for _, n, active in chains if active)
         report = Report(
             passes=self.pm.stats, timings=self.pm.timings,
             lowering={"backend": "hip", "launches": len(program.launches), "source": str(listing),
                       "cuda_graphs": exe.use_cuda_graphs, "tf32": self.options.allow_tf32,
-                      "precision": self.precision, "families": families, "plan_cache": origin},
+                      "precision": self.precision, "families": families, "plan_cache": origin,
+                      "gemv_chains": [(first, n) for first, n, _ in chains], "kernel_launches": kernel_launches},
             kernels=[f"{k.name} {k.kind:<11} {' '.join(n.op for n in k.nodes)}" for k in g.kernels],
             arena_bytes=g.attrs.get("arena_bytes", 0), naive_bytes=memory.get("naive_bytes", 0),
             lower_bound_bytes=memory.get("lower_bound_bytes", 0), autotune=list(autotune_log))

@@ -25,6 +25,7 @@ BASE_INPUT, BASE_OUTPUT, BASE_CONST, BASE_ARENA, BASE_WORKSPACE = range(5)
 FAM_EW, FAM_ROW, FAM_GEMM, FAM_GEMV, FAM_RED, FAM_ATTN = 1, 2, 3, 4, 5, 6
 ATTN_MASK_NONE, ATTN_MASK_CAUSAL, ATTN_MASK_ADD = 0, 1, 2
 GEMV_PRO_NONE, GEMV_PRO_LAYERNORM, GEMV_PRO_ATTN = 0, 1, 2
+GEMV_CHAIN = 1   # KH_GEMV_CHAIN: kh_launch.variant flag of a GEMV launch
 ATTN_SCALE_NONE, ATTN_SCALE_MUL, ATTN_SCALE_DIV = 0, 1, 2
 ROW_GENERIC, ROW_LAYERNORM, ROW_SOFTMAX = 0, 1, 2
 PREC_FP32, PREC_BF16, PREC_BF16X3 = 0, 1, 2
@@ -106,6 +107,8 @@ def load():
         "kh_plan_replay": (ip, [vp, vp]),
         "kh_plan_time": (ip, [vp, ip, ctypes.POINTER(vp), ip, ctypes.POINTER(vp), ip, ip, ip, vp,
                               ctypes.POINTER(ctypes.c_double)]),
+        "kh_plan_chains": (ip, [vp, ctypes.POINTER(ctypes.c_int32), ip, ctypes.POINTER(ip)]),
+        "kh_plan_chain_timeouts": (ip, [vp, ctypes.POINTER(ctypes.c_uint64)]),
         "kh_plan_destroy": (ip, [vp]),
     }
     for name, (res, args) in sig.items():
@@ -126,7 +129,8 @@ EXPORTED = ("kh_version", "kh_abi_sizes", "kh_last_error", "kh_init", "kh_device
             "kh_plan_create", "kh_plan_workspace_bytes", "kh_plan_bind", "kh_plan_run", "kh_plan_run_noalloc",
             "kh_plan_run_host",
             "kh_plan_run_one",
-            "kh_plan_capture", "kh_plan_replay", "kh_plan_time", "kh_plan_destroy")
+            "kh_plan_capture", "kh_plan_replay", "kh_plan_time", "kh_plan_chains", "kh_plan_chain_timeouts",
+            "kh_plan_destroy")
 
 
 def check(rc: int, what: str = ""):
@@ -219,6 +223,20 @@ class Plan:
         check(self.lib.kh_plan_time(self.handle, index, ins, len(in_ptrs), outs, len(out_ptrs), repeats, rounds,
                                     stream, ctypes.byref(sec)), "kh_plan_time")
         return sec.value
+
+    def chains(self):
+        """[(first launch, launches, active)] of the plan's persistent GEMV chains."""
+        n = ctypes.c_int()
+        check(self.lib.kh_plan_chains(self.handle, None, 0, ctypes.byref(n)), "kh_plan_chains")
+        buf = (ctypes.c_int32 * max(1, 3 * n.value))()
+        check(self.lib.kh_plan_chains(self.handle, buf, n.value, ctypes.byref(n)), "kh_plan_chains")
+        return [tuple(buf[3 * i:3 * i + 3]) for i in range(n.value)]
+
+    def chain_timeouts(self) -> int:
+        """Waits inside the plan's chains that gave up (none expected); synchronises the device."""
+        n = ctypes.c_uint64()
+        check(self.lib.kh_plan_chain_timeouts(self.handle, ctypes.byref(n)), "kh_plan_chain_timeouts")
+        return n.value
 
     def __del__(self):
         h = getattr(self, "handle", None)

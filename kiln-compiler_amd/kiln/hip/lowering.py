@@ -176,8 +176,9 @@ def _encode(tape: _Tape, slot, desc: kl.LaunchDesc, ref_offset=0):
 # ----------------------------------------------------------------------------------
 
 class _Lowerer:
-    def __init__(self, graph: Graph, precision: str, matmul_config):
+    def __init__(self, graph: Graph, precision: str, matmul_config, gemv_chains: bool = True):
         self.g = graph
+        self.gemv_chains = gemv_chains
         self.layouts = compute_layouts(graph)
         self.users = graph.users()
         self.precision = precision
@@ -645,6 +646,8 @@ class _Lowerer:
         pro = self.prologue.get(k) if gemv else None
         a_src = pro[0] if pro else a   # the LayerNorm's input when the GEMV runs it as its prologue
         d = self.new_desc(kl.FAM_GEMV if gemv else kl.FAM_GEMM, "gemv" if gemv else "matmul", k, space3)
+        if gemv and self.gemv_chains:
+            d.variant = kl.GEMV_CHAIN   # the library may run it in a persistent chain with its GEMV neighbours
         d.gemm[0], d.gemm[1], d.gemm[2], d.gemm[3] = batch, m, n, kk
         d.refs[0] = ref3(a_src, (batch, m, kk))
         k_major = not gemv and int(cfg.get("tile", -1)) in autotune.NK_B
@@ -1047,8 +1050,10 @@ class _Lowerer:
         return self.program
 
 
-def lower_graph(graph: Graph, precision: str = "fp32", matmul_config=None) -> Program:
-    """Fused, buffer-assigned, memory-planned graph -> Program (launch list)."""
+def lower_graph(graph: Graph, precision: str = "fp32", matmul_config=None, gemv_chains: bool = True) -> Program:
+    """Fused, buffer-assigned, memory-planned graph -> Program (launch list).
+    gemv_chains: mark one-row matmuls KH_GEMV_CHAIN, so the library may run
+    consecutive ones as one persistent launch."""
     from kiln.hip.autotune import default_matmul_config
 
-    return _Lowerer(graph, precision, matmul_config or default_matmul_config).run()
+    return _Lowerer(graph, precision, matmul_config or default_matmul_config, gemv_chains).run()

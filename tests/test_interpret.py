@@ -156,3 +156,39 @@ def test_skinny_gemm_lowering(tile):
     c2 = check(lambda a, b: a @ b, torch.randn(21, 68), torch.randn(68, 40),
                gpu_matmul_config=lambda *_: {"tile": tile, "splitk": 1})
     assert f"tile {tile} " not in c2._exe.program.launches[0].summary
+
+
+def test_decode_stack_forms_one_gemv_chain():
+    # every GEMV of the decode stack reads the whole output of the one before
+    # (x, or q / k / v of the attention prologue), so the library chains all of
+    # them; the final LayerNorm is a row launch after the chain. On the host
+    # the chain is not bound (no GPU) and the launches run one by one.
+    torch.manual_seed(0)
+    model = gpt2_init_(Stack(3, 128, 4, 1), seed=0).eval()
+    x = torch.randn(1, 128)
+    c = kiln.compile(model, (x,), device="cuda", gemv_chains=True)
+    low = c.report.lowering
+    assert low["launches"] == 13
+    assert low["gemv_chains"] == [(0, 12)]
+    off = kiln.compile(model, (x,), device="cuda")   # chains are opt-in
+    assert off.report.lowering["gemv_chains"] == []
+    np.testing.assert_array_equal(c(x).numpy(), off(x).numpy())
+
+
+def test_gemv_chain_needs_the_whole_previous_output():
+    # the second product reads half of the first one's output: not chained
+    # (a stage's waves must have waited for every output of the stage before)
+    w1 = torch.randn(64, 96) * 0.1
+    w2 = torch.randn(16, 32) * 0.1
+    w3 = torch.randn(16, 64) * 0.1
+
+    def half(x):
+        y = F.linear(x, w1)
+        return F.linear(y[:, :32], w2)
+
+    def whole(x):
+        return F.linear(F.linear(x, w1), w3)
+
+    x = torch.randn(1, 96)
+    assert check(half, x, gemv_chains=True).report.lowering["gemv_chains"] == []
+    assert check(whole, x, gemv_chains=True).report.lowering["gemv_chains"] == [(0, 2)]
