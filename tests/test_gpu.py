@@ -223,6 +223,15 @@ def test_graph_replays_with_new_inputs():
         x = torch.randn(16, 64)
         with torch.no_grad():
             torch.testing.assert_close(c(x).cpu(), model(x), rtol=RTOL, atol=ATOL)
+    # calls take graph replay or direct launches, whichever measured faster at
+    # the first call; both run the same kernels and give the same bits
+    assert c._exe.mode in ("graph", "direct")
+    x = torch.randn(16, 64)
+    outs = {}
+    for mode in ("graph", "direct", "graph"):
+        c._exe.mode = mode
+        outs.setdefault(mode, []).append(c(x))
+    assert torch.equal(outs["graph"][0], outs["direct"][0]) and torch.equal(outs["graph"][0], outs["graph"][1])
 
 
 def test_stored_plan_is_reused_and_bit_identical():
