@@ -1035,6 +1035,10 @@ constexpr TileCfg kConfigs[] = {
   {bm, bn, 32, 1, 1, wk, 16, 6, ns, prec == 0 ? KH_PREC_FP32 : prec == 1 ? KH_PREC_BF16 : KH_PREC_BF16X3},
     KH_GEMM_SMALL_CONFIGS(KH_CFGSM_ROW)
 #undef KH_CFGSM_ROW
+#define KH_CFGNTB_ROW(id, bm, bn, wm, wn, ns, prec) \
+  {bm, bn, 32, wm, wn, 1, 16, 5, ns, prec == 1 ? KH_PREC_BF16 : KH_PREC_BF16X3},
+    KH_GEMM_NT_BF16_CONFIGS(KH_CFGNTB_ROW)
+#undef KH_CFGNTB_ROW
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
@@ -1047,7 +1051,7 @@ constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 // GPU): 2048x3072x768 on the 32x64 tile 5% faster, the others within 1%.
 int tile_group(const TileCfg &t, int tiles_m) {
   const int lds = t.kind == 6   ? 4 * t.stages * t.bk * (t.bm + t.bn) * t.wk   // (fp32 bound)
-                  : t.kind == 5 ? 4 * t.stages * t.bk * (t.bm + t.bn)
+                  : t.kind == 5 ? 4 * t.stages * t.bk * (t.bm + t.bn)   // (fp32 bound)
                   : t.kind == 3 ? 4 * t.stages * (t.bm * t.bk + (t.prec == KH_PREC_FP32 ? t.bk * t.bn
                                                                  : t.bn * t.bk / 2 * (t.prec == KH_PREC_BF16X3 ? 2 : 1)))
                               : 8 * (t.bm * (t.bk + 4) + t.bn * (t.bk + 2));

@@ -143,6 +143,18 @@ inline hipError_t launch_splitk_reduce(const GemmArgs &a, int cus, hipStream_t s
   X(63, 32, 96, 2, 2, 3)      \
   X(64, 64, 64, 2, 2, 3)
 
+// The same kernel over the bf16 (prec 1) and three-pass bf16 (prec 2) weight
+// copies: id, BM x BN, waves WM x WN, stages NS, prec.
+#define KH_GEMM_NT_BF16_CONFIGS(X) \
+  X(87, 128, 256, 2, 4, 3, 1)      \
+  X(88, 128, 192, 2, 2, 4, 1)      \
+  X(89, 256, 128, 4, 2, 3, 1)      \
+  X(90, 128, 128, 2, 4, 4, 1)      \
+  X(91, 64, 192, 2, 2, 4, 1)       \
+  X(92, 128, 256, 2, 4, 2, 2)      \
+  X(93, 128, 192, 2, 2, 3, 2)      \
+  X(94, 128, 128, 2, 4, 3, 2)
+
 // Launch configuration `id` of kind 5 (hipErrorInvalidValue for another id).
 hipError_t launch_gemm_nt(int id, const GemmArgs &a, dim3 grid, hipStream_t stream);
 

@@ -1,7 +1,7 @@
-// kh_gemm_nt.hip - fp32 matmul over a constant weight read through its
-// [batch][N][K] copy (configuration kind 5), for the large products of a
-// transformer block: C[b] = epilogue(A[b] @ B[b]) with both operands
-// K-contiguous in memory.
+// kh_gemm_nt.hip - matmul over a constant weight read through its
+// [batch][N][K] copy (configuration kind 5; fp32, or the bf16 / three-pass
+// bf16 copies), for the large products of a transformer block:
+// C[b] = epilogue(A[b] @ B[b]) with both operands K-contiguous in memory.
 //
 // Same contract as the other members of the matmul family (the reference's
 // tl.dot kernel with fused epilogue, kiln/gpu/codegen.py:484-530); what
@@ -32,6 +32,18 @@
 //     LDS slice and reads, computes and writes row-contiguous groups of 4
 //     columns with 128-bit accesses (bias / residual / activation directly,
 //     other tapes through the tape interpreter).
+// bf16 inputs (PREC 1, the arithmetic of the other bf16 GEMMs): B is the
+// bf16 [batch][N][K'] copy (rows of 32 K values = 4 chunks of 16 bytes in a
+// stage, chunk c of row n at c ^ swz_b16<4>(n)), A is read as fp32 like the
+// fp32 kernel and rounded to bf16 as its fragments are read; each step is one
+// v_mfma_f32_16x16x32_bf16 per output block (lane (li, g) supplies K values
+// 8g .. 8g+7 of its A row and its B row), fp32 accumulation. Three-pass bf16
+// (PREC 2): B the [batch][N][2K'] copy, hi then lo rows in a stage, A split
+// the same way, a.b = a_lo.b_hi + a_hi.b_lo + a_hi.b_hi. With an MFMA step
+// this short the fp32 kernel's mid-step barrier does not pay: a bf16 step
+// waits for its stage, passes the barrier, refills the slot the previous step
+// read and then reads and multiplies (two workgroup waves per SIMD, or one
+// wave with the next copies NS - 1 steps ahead).
 // K must be a positive multiple of 32 and the operands' spans below 2^29
 // elements (the host checks both; other shapes use the other kernels of the
 // family).
@@ -49,17 +61,22 @@ namespace {
 // activation, recognised on the host); TAPE = true: one tile per workgroup
 // and the general epilogue tape after the main loop (kept out of the tile
 // loop so the tape interpreter is not replicated into it).
-template <int BM, int BN, int WM, int WN, int NS, bool TAPE>
+template <int BM, int BN, int WM, int WN, int NS, bool TAPE, int PREC>
 __global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(WM * WN / 4, WM * WN / 4)))
 void gemm_nt_kernel(const GemmArgs a) {
   constexpr int BK = 32, MT = 16, ACH = BK / 4;
+  constexpr bool BF = PREC != 0;
+  constexpr int NB = PREC == 2 ? 2 : 1;                      // bf16 copies of B rows per stage (hi, lo)
   constexpr int kWaves = WM * WN;
   constexpr int TM = BM / WM, TN = BN / WN, FM = TM / MT, FN = TN / MT;
-  constexpr int A_FLOATS = BM * BK, STAGE = (BM + BN) * BK;
-  constexpr int A_PER_WAVE = BM * ACH / 64 / kWaves, B_PER_WAVE = BN * ACH / 64 / kWaves;
+  constexpr int A_FLOATS = BM * BK;
+  constexpr int B_HALF = BN * BK / 2;                        // words of one bf16 copy of a stage's B rows
+  constexpr int STAGE = A_FLOATS + (BF ? B_HALF * NB : BN * BK);
+  constexpr int B_CHUNKS = BF ? BN * 4 * NB : BN * ACH;      // 16-byte chunks of B per stage
+  constexpr int A_PER_WAVE = BM * ACH / 64 / kWaves, B_PER_WAVE = B_CHUNKS / 64 / kWaves;
   constexpr int COPIES = A_PER_WAVE + B_PER_WAVE;
   static_assert(TM % MT == 0 && TN % MT == 0, "wave tile of whole MFMA blocks");
-  static_assert((BM * ACH) % (64 * kWaves) == 0 && (BN * ACH) % (64 * kWaves) == 0, "copy mapping");
+  static_assert((BM * ACH) % (64 * kWaves) == 0 && B_CHUNKS % (64 * kWaves) == 0, "copy mapping");
   static_assert(NS >= 2 && NS <= 4 && (NS - 2) * COPIES < 64, "ring depth / vmcnt range");
   static_assert(kWaves % 4 == 0, "whole SIMDs");
 
@@ -76,7 +93,8 @@ void gemm_nt_kernel(const GemmArgs a) {
   const int li = lane & 15, g = lane >> 4;
   const int bidx = blockIdx.y;
   const float *Ab = a.A + (int64_t)bidx * a.sa_b;
-  const float *Bb = a.B + (int64_t)bidx * a.sb_b;
+  // (B in its element type: fp32, or the bf16 copy)
+  const char *Bb = reinterpret_cast<const char *>(a.B) + (int64_t)bidx * a.sb_b * (BF ? 2 : 4);
   const int n_steps = a.K / BK;   // the host checks K % 32 == 0 and K > 0
   const int n_tiles = a.tiles_m * a.tiles_n;
 
@@ -98,14 +116,22 @@ void gemm_nt_kernel(const GemmArgs a) {
 #pragma unroll
     for (int i = 0; i < B_PER_WAVE; ++i) {
       const int p = (wave * B_PER_WAVE + i) * 64 + lane;
-      const int r = p / ACH;
-      b_off[i] = (uint32_t)(min(n0 + r, a.N - 1) * (int)a.sb_n + ((p % ACH) ^ swz_a(r)) * 4) * 4u;
+      if constexpr (BF) {
+        // bf16 row r: 4 chunks of 8 K values; three-pass: the lo rows (K'
+        // further along the copy's row) follow the hi rows
+        const int half = p / (BN * 4), pp = p % (BN * 4), r = pp / 4;
+        const int row = min(n0 + r, a.N - 1) * (int)a.sb_n + half * ((int)a.sb_n / 2);
+        b_off[i] = (uint32_t)(row + ((pp % 4) ^ swz_b16<4>(r)) * 8) * 2u;
+      } else {
+        const int r = p / ACH;
+        b_off[i] = (uint32_t)(min(n0 + r, a.N - 1) * (int)a.sb_n + ((p % ACH) ^ swz_a(r)) * 4) * 4u;
+      }
     }
   };
   auto slot_ptr = [&](int step) { return ring + (step % NS) * (STAGE / 4); };
   auto issue = [&](int step) {
     const float *abase = uniform_ptr(Ab + step * BK);
-    const float *bbase = uniform_ptr(Bb + step * BK);
+    const float *bbase = uniform_ptr(reinterpret_cast<const float *>(Bb + step * BK * (BF ? 2 : 4)));
     const uint32_t lds = (uint32_t)(uintptr_t)(lds_void_t *)slot_ptr(step);
 #pragma unroll
     for (int i = 0; i < A_PER_WAVE; ++i) copy_to_lds<4>(abase, a_off[i], lds + (wave_u * A_PER_WAVE + i) * 1024);
@@ -132,8 +158,14 @@ void gemm_nt_kernel(const GemmArgs a) {
 #pragma unroll
   for (int fn = 0; fn < FN; ++fn) {
     const int r = wn * TN + fn * MT + li;
+    if constexpr (BF) {
+      // one 16-byte bf16 chunk per row (and the lo row's for three-pass)
+      fb_off[fn][0] = A_FLOATS + r * (BK / 2) + ((g ^ swz_b16<4>(r)) * 4);
+      fb_off[fn][1] = fb_off[fn][0] + B_HALF;
+    } else {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) fb_off[fn][h] = A_FLOATS + r * BK + ((2 * g + h) ^ swz_a(r)) * 4;
+      for (int h = 0; h < 2; ++h) fb_off[fn][h] = A_FLOATS + r * BK + ((2 * g + h) ^ swz_a(r)) * 4;
+    }
   }
 
   f32x4 acc[FM][FN];
@@ -244,33 +276,81 @@ void gemm_nt_kernel(const GemmArgs a) {
   for (int p = 0; p < NS - 1 && p < n_steps; ++p) issue(p);
   bool first = true;
   while (true) {
-    // stage 0 of this tile landed everywhere (after a previous tile, whose
-    // epilogue issued memory operations behind these copies, wait for all)
-    if (first) wait_landed(min(NS - 2, n_steps - 1));
-    else wait_vmcnt<0>();
-    stage_barrier();
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
       for (int fn = 0; fn < FN; ++fn) acc[fm][fn] = f32x4{0.f, 0.f, 0.f, 0.f};
-    read_half(0, 0, f0a, f0b);
-    // every step but the last (the loop body has no conditional LDS reads, so
-    // the compiler's counter waits before the second half stay exact)
-    for (int s = 0; s + 1 < n_steps; ++s) {
-      // first half of step s (set 0) under the reads of its second half
-      if (s + NS - 1 < n_steps) issue(s + NS - 1);
-      read_half(s, 1, f1a, f1b);
-      mfmas(f0a, f0b);
-      // stage s + 1 landed everywhere: its first half is read under the
-      // second half of step s (set 1)
-      wait_landed(min(NS - 2, n_steps - 2 - s));
+    if constexpr (BF) {
+      for (int s = 0; s < n_steps; ++s) {
+        // stage s landed everywhere (after a previous tile, whose epilogue
+        // issued memory operations behind the first copies, wait for all),
+        // and every wave is done reading stage s - 1, whose slot the copies
+        // of step s + NS - 1 refill
+        if (s == 0 && !first) wait_vmcnt<0>();
+        else wait_landed(min(NS - 2, n_steps - 1 - s));
+        stage_barrier();
+        if (s + NS - 1 < n_steps) issue(s + NS - 1);
+        const float *st = reinterpret_cast<const float *>(slot_ptr(s));
+        float4 xa[FM][2], xb[FN][NB];
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) xa[fm][h] = *reinterpret_cast<const float4 *>(st + fa_off[fm][h]);
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+          for (int h = 0; h < NB; ++h) xb[fn][h] = *reinterpret_cast<const float4 *>(st + fb_off[fn][h]);
+        bf16x8 ah[FM], al[FM];
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float x = part(xa[fm][e / 4], e % 4);
+            ah[fm][e] = (__bf16)x;
+            if constexpr (PREC == 2) {
+              // the difference is exact in fp32; a non-finite hi part keeps lo 0
+              const float hv = (float)ah[fm][e];
+              al[fm][e] = (__bf16)(__builtin_isfinite(hv) ? x - hv : 0.0f);
+            }
+          }
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+          for (int fn = 0; fn < FN; ++fn) {
+            const bf16x8 bh = *reinterpret_cast<const bf16x8 *>(&xb[fn][0]);
+            if constexpr (PREC == 2) {
+              const bf16x8 bl = *reinterpret_cast<const bf16x8 *>(&xb[fn][NB - 1]);
+              acc[fm][fn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al[fm], bh, acc[fm][fn], 0, 0, 0);
+              acc[fm][fn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[fm], bl, acc[fm][fn], 0, 0, 0);
+            }
+            acc[fm][fn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah[fm], bh, acc[fm][fn], 0, 0, 0);
+          }
+      }
+    } else {
+      // stage 0 of this tile landed everywhere (after a previous tile, whose
+      // epilogue issued memory operations behind these copies, wait for all)
+      if (first) wait_landed(min(NS - 2, n_steps - 1));
+      else wait_vmcnt<0>();
       stage_barrier();
-      read_half(s + 1, 0, f0a, f0b);
+      read_half(0, 0, f0a, f0b);
+      // every step but the last (the loop body has no conditional LDS reads, so
+      // the compiler's counter waits before the second half stay exact)
+      for (int s = 0; s + 1 < n_steps; ++s) {
+        // first half of step s (set 0) under the reads of its second half
+        if (s + NS - 1 < n_steps) issue(s + NS - 1);
+        read_half(s, 1, f1a, f1b);
+        mfmas(f0a, f0b);
+        // stage s + 1 landed everywhere: its first half is read under the
+        // second half of step s (set 1)
+        wait_landed(min(NS - 2, n_steps - 2 - s));
+        stage_barrier();
+        read_half(s + 1, 0, f0a, f0b);
+        mfmas(f1a, f1b);
+      }
+      read_half(n_steps - 1, 1, f1a, f1b);
+      mfmas(f0a, f0b);
       mfmas(f1a, f1b);
     }
-    read_half(n_steps - 1, 1, f1a, f1b);
-    mfmas(f0a, f0b);
-    mfmas(f1a, f1b);
 
     const int tm0 = m0, tn0 = n0;
     const int t_next = TAPE ? n_tiles : t + (int)gridDim.x;
@@ -290,15 +370,18 @@ void gemm_nt_kernel(const GemmArgs a) {
 
 hipError_t launch_gemm_nt(int id, const GemmArgs &a, dim3 grid, hipStream_t stream) {
   switch (id) {
-#define KH_CFGNT_CASE(cid, bm, bn, wm, wn, ns)                                                                 \
-  case cid:                                                                                                   \
-    if (a.direct)                                                                                             \
-      hipLaunchKernelGGL((gemm_nt_kernel<bm, bn, wm, wn, ns, false>), grid, dim3(64 * wm * wn), 0, stream, a); \
-    else                                                                                                      \
-      hipLaunchKernelGGL((gemm_nt_kernel<bm, bn, wm, wn, ns, true>), grid, dim3(64 * wm * wn), 0, stream, a);  \
+#define KH_CFGNTP_CASE(cid, bm, bn, wm, wn, ns, prec)                                                                  \
+  case cid:                                                                                                          \
+    if (a.direct)                                                                                                    \
+      hipLaunchKernelGGL((gemm_nt_kernel<bm, bn, wm, wn, ns, false, prec>), grid, dim3(64 * wm * wn), 0, stream, a); \
+    else                                                                                                             \
+      hipLaunchKernelGGL((gemm_nt_kernel<bm, bn, wm, wn, ns, true, prec>), grid, dim3(64 * wm * wn), 0, stream, a);  \
     break;
+#define KH_CFGNT_CASE(cid, bm, bn, wm, wn, ns) KH_CFGNTP_CASE(cid, bm, bn, wm, wn, ns, 0)
     KH_GEMM_NT_CONFIGS(KH_CFGNT_CASE)
+    KH_GEMM_NT_BF16_CONFIGS(KH_CFGNTP_CASE)
 #undef KH_CFGNT_CASE
+#undef KH_CFGNTP_CASE
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

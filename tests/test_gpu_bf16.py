@@ -91,6 +91,31 @@ def test_every_bf16_tile_configuration(tile):
             close_to_scale(c(x, r).cpu().numpy(), ref, EXACT)
 
 
+@pytest.mark.parametrize("tile", [t for t in sorted(autotune.K_CONTIGUOUS) if autotune.PRECISION[t] == "bf16"])
+def test_k_contiguous_bf16_tiles_walk_several_tiles(tile):
+    # the persistent K-contiguous kernel over the bf16 weight copy: more tiles
+    # than CUs (each workgroup walks several, the next tile's first stages
+    # issued before the current epilogue) with ragged edges, fewer steps than
+    # ring stages and many steps; direct epilogue (bias + residual) and the
+    # tape epilogue (a scale); repeated calls agree bit for bit
+    cfg = lambda *_: {"tile": tile, "splitk": 1}
+    for m, n, k in ((4200, 2600, 64), (4200, 2600, 160), (300, 452, 768)):
+        torch.manual_seed(m + k)
+        lin = gpt2_init_(torch.nn.Linear(k, n), seed=k).eval()
+        x, r = torch.randn(m, k), torch.randn(m, n)
+        w, b = lin.weight.detach().numpy(), lin.bias.detach().numpy().astype(np.float64)
+        prod = r16(x.numpy()) @ r16(w).T
+        cases = ((lambda t, res: lin(t) + res, (x, r), prod + b + r.numpy()),
+                 (lambda t, res: lin(t) * 0.5 - res, (x, r), (prod + b) * 0.5 - r.numpy()))
+        for fn, args, ref in cases:
+            c = kiln.compile(fn, args, device="cuda", cuda_graphs=False, matmul_precision="bf16",
+                             gpu_matmul_config=cfg)
+            assert f"tile {tile} splitk 1" in c._exe.program.launches[0].summary
+            out = c(*args)
+            close_to_scale(out.cpu().numpy(), ref, EXACT)
+            assert torch.equal(c(*args), out)
+
+
 @pytest.mark.parametrize("k, n, ln", [(768, 2304, True), (3072, 768, False), (64, 130, False), (16, 5, True)])
 def test_bf16_gemv(k, n, ln):
     # one-row products with a constant weight run on the K-contiguous GEMV over

@@ -88,6 +88,29 @@ def test_every_bf16x3_tile_configuration(tile):
             close_to_scale(c(x, r).cpu().numpy(), ref, SPLIT_EXACT)
 
 
+@pytest.mark.parametrize("tile", [t for t in sorted(autotune.K_CONTIGUOUS) if autotune.PRECISION[t] == "bf16x3"])
+def test_k_contiguous_bf16x3_tiles_walk_several_tiles(tile):
+    # the persistent K-contiguous kernel over the three-pass copy (hi and lo
+    # rows per stage): more tiles than CUs with ragged edges, short and long
+    # K; direct and tape epilogues; repeated calls agree bit for bit
+    cfg = lambda *_: {"tile": tile, "splitk": 1}
+    for m, n, k in ((4200, 2600, 64), (300, 452, 768)):
+        torch.manual_seed(m + k)
+        lin = gpt2_init_(torch.nn.Linear(k, n), seed=k).eval()
+        x, r = torch.randn(m, k), torch.randn(m, n)
+        w, b = lin.weight.detach().numpy(), lin.bias.detach().numpy().astype(np.float64)
+        prod = three_pass(x.numpy(), w.T)
+        cases = ((lambda t, res: lin(t) + res, (x, r), prod + b + r.numpy()),
+                 (lambda t, res: lin(t) * 0.5 - res, (x, r), (prod + b) * 0.5 - r.numpy()))
+        for fn, args, ref in cases:
+            c = kiln.compile(fn, args, device="cuda", cuda_graphs=False, matmul_precision="bf16x3",
+                             gpu_matmul_config=cfg)
+            assert f"tile {tile} splitk 1" in c._exe.program.launches[0].summary
+            out = c(*args)
+            close_to_scale(out.cpu().numpy(), ref, SPLIT_EXACT)
+            assert torch.equal(c(*args), out)
+
+
 @pytest.mark.parametrize("T", [128, 512])
 def test_gpt2_block_allow_tf32(T):
     torch.manual_seed(0)
