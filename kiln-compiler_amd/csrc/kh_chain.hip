@@ -12,7 +12,8 @@
 //     beta it needs), so the weight stream of a stage overlaps the hand-over
 //     of the previous one;
 //   * stage outputs are handed over as 64-bit words (value, epoch) written
-//     with device-scope stores; a consumer polls the words of its input
+//     with device-scope stores by a fifth wave of the workgroup that only
+//     stores (below); a consumer polls the words of its input
 //     with device-scope loads until every epoch is the current call's, so a
 //     value and the proof that it is ready arrive in one load - no counter,
 //     no fence, no atomics on shared addresses (a shared arrival counter was
@@ -24,7 +25,14 @@
 //     read the old one, so the next call's tags never match a stale word;
 //   * every wait is bounded (wall clock); a wait that gives up counts a
 //     timeout in the plan's state and its workgroup leaves the kernel, so the
-//     grid always drains (kh_plan_chain_timeouts reports the count).
+//     grid always drains (kh_plan_chain_timeouts reports the count);
+//   * the four compute waves never store: one counter (vmcnt) tracks a
+//     wave's loads and stores together and in issue order, so a wave that
+//     stored its outputs would wait for the stores' device-scope
+//     acknowledgement (a memory round trip) at its next wait for a load -
+//     before the next stage's weights or hand-over words could be used. They
+//     leave their outputs in LDS and pass a barrier; the store wave, which
+//     issues no loads, stores them.
 // Stage t's in-chain operands (x, q / k / v of the attention prologue, the
 // residual) are read from the hand-over words of the stage that produced
 // them; operands from outside the chain are read from memory. A stage also
@@ -52,8 +60,9 @@ namespace kh {
 namespace {
 
 constexpr int kSlots = 12;                    // 16-byte weight chunks per lane and pass
-constexpr int kThreads = 256;                 // 4 waves per workgroup
+constexpr int kThreads = 256;                 // 4 compute waves per workgroup
 constexpr int kWaves = kThreads / 64;
+constexpr int kBlock = kThreads + 64;         // and the store wave
 constexpr int kMaxK = 4096;                   // x row staged in LDS
 constexpr int kPerThread = kMaxK / kThreads;  // x words per thread
 constexpr int kAttRounds = 4;                 // attention prologue: head rounds per wave
@@ -155,7 +164,10 @@ __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w 
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 __device__ __forceinline__ float round_bf16(float x) { return (float)(__bf16)x; }
 
-// Sum over the workgroup in a fixed order (wave tree, then waves 0..3).
+// Sum over the compute waves in a fixed order (wave tree, then waves 0..3).
+// Two barriers; the LayerNorm prologue takes two sums, and the store wave
+// passes the same kLnBarriers barriers.
+constexpr int kLnBarriers = 4;
 __device__ __forceinline__ float group_sum(float v, float *red) {
   v = wave_sum(v);
   __syncthreads();  // `red` may still be read from a previous sum
@@ -212,7 +224,6 @@ struct Carry {
   uint4 w[kSlots];
   float pb, prp;   // bias; residual read from memory
   uint64_t pr;     // residual hand-over word
-  float pg[kPerThread], pbe[kPerThread];
 };
 
 // Columns of stage S that wave gw owns: gw, gw + nwaves, ...
@@ -248,11 +259,11 @@ __device__ __forceinline__ void prefetch_t(const Hot &S, int gw, int nwaves, int
 }
 
 // The wave's dot products from the weight chunks in registers and x in LDS,
-// then in lane c the epilogue of column c, its store to memory (when the
-// stage's output is read after the chain) and its hand-over word.
+// then in lane c the epilogue of column c, left in outs[64 * wave + c] for
+// the store wave.
 template <int P, bool BF16>
 __device__ __forceinline__ void compute_t(const Hot &S, int gw, int nwaves, int lane, uint32_t epoch, Carry &cr,
-                                          const float *xs, ChainState *state) {
+                                          const float *xs, float *outs, ChainState *state) {
   constexpr int CMAX = kSlots / P;
   const int U = S.K / (BF16 ? 8 : 4);
   const int nc = wave_columns(S, gw, nwaves);
@@ -312,8 +323,7 @@ __device__ __forceinline__ void compute_t(const Hot &S, int gw, int nwaves, int 
   if (S.act == KH_OP_GELU_TANH) v = op_gelu_tanh(v);
   else if (S.act == KH_OP_GELU_ERF) v = op_gelu_erf(v);
   else if (S.act == KH_OP_RELU) v = v != v ? v : fmaxf(v, 0.0f);
-  if (S.plain_out) gbl_w(S.out)[col * S.out_sn] = v;
-  ll_put(S.out_ll + col, ll_word(v, epoch));
+  outs[threadIdx.x] = v;   // (threadIdx.x = 64 * wave + lane: an address the compiler need not keep)
 }
 
 #define KH_CHAIN_KINDS(X) \
@@ -327,28 +337,31 @@ __device__ __forceinline__ void prefetch(const Hot &S, int gw, int nwaves, int l
     KH_CHAIN_KINDS(KH_X)
 #undef KH_X
   }
-  if (S.pro == KH_GEMV_PRO_LAYERNORM && (int)blockIdx.x * kWaves < S.N) {
-    // unconditional loads as above: clamped indices, absent gamma / beta read
-    // a stand-in and are ignored at use
-    const int rounds = (S.K + kThreads - 1) / kThreads;
-#pragma unroll
-    for (int i = 0; i < kPerThread; ++i) {
-      if (i < rounds) {
-        const int k = min((int)threadIdx.x + i * kThreads, S.K - 1);
-        cr.pg[i] = ld(S.gamma, k), cr.pbe[i] = ld(S.beta, k);
-      }
-    }
-  }
 }
 
 __device__ __forceinline__ void compute(const Hot &S, int gw, int nwaves, int lane, uint32_t epoch, Carry &cr,
-                                        const float *xs, ChainState *state) {
+                                        const float *xs, float *outs, ChainState *state) {
   switch (S.kind) {
 #define KH_X(k, P, B) \
-  case k: compute_t<P, B>(S, gw, nwaves, lane, epoch, cr, xs, state); break;
+  case k: compute_t<P, B>(S, gw, nwaves, lane, epoch, cr, xs, outs, state); break;
     KH_CHAIN_KINDS(KH_X)
 #undef KH_X
   }
+}
+
+// The store wave: lane 16w + c stores column c of compute wave w's outputs
+// (its memory copy when the stage's output is read after the chain, and its
+// hand-over word).
+__device__ __forceinline__ void store_outputs(const Hot &S, int nwaves, int lane, uint32_t epoch,
+                                              const float *outs) {
+  const int w = lane >> 4, c = lane & 15;
+  const int gw = (int)blockIdx.x * kWaves + w;
+  const int nc = min(wave_columns(S, gw, nwaves), kSlots / kKindP[S.kind % kNumP]);
+  if (w >= kWaves || c >= nc) return;
+  const int64_t col = gw + (int64_t)c * nwaves;
+  const float v = outs[w * 64 + c];
+  if (S.plain_out) gbl_w(S.out)[col * S.out_sn] = v;
+  ll_put(S.out_ll + col, ll_word(v, epoch));
 }
 
 // Poll n words until each carries `epoch` or the wait's time runs out;
@@ -377,11 +390,22 @@ __device__ __forceinline__ bool poll(uint64_t (&v)[N], uint32_t epoch, Need need
 
 // The stage's row x into LDS: from the producer's hand-over words (or
 // memory), with the LayerNorm prologue applied. false: a wait gave up.
-__device__ __forceinline__ bool acquire_x(const CStage &S, const ChainDyn &dyn, uint32_t epoch, const Carry &cr,
+__device__ __forceinline__ bool acquire_x(const CStage &S, const Hot &hot, const ChainDyn &dyn, uint32_t epoch,
                                           float *xs, float *red) {
   uint64_t v[kPerThread];
   const float *xp = S.x_ll ? nullptr : cptr(S.x, dyn);
   const int tid = threadIdx.x;
+  // the LayerNorm's gamma / beta, issued with the first polls (unconditional
+  // loads: clamped indices, an absent gamma / beta reads a stand-in and is
+  // ignored at use)
+  float pg[kPerThread], pbe[kPerThread];
+  if (S.pro == KH_GEMV_PRO_LAYERNORM) {
+#pragma unroll
+    for (int i = 0; i < kPerThread; ++i) {
+      const int k = min(tid + i * kThreads, S.K - 1);
+      if (tid + i * kThreads < S.K) pg[i] = ld(hot.gamma, k), pbe[i] = ld(hot.beta, k);
+    }
+  }
 #pragma unroll
   for (int i = 0; i < kPerThread; ++i) {
     const int k = tid + i * kThreads;
@@ -411,8 +435,8 @@ __device__ __forceinline__ bool acquire_x(const CStage &S, const ChainDyn &dyn, 
       const int k = tid + i * kThreads;
       if (k < S.K) {
         float y = (ll_val(v[i]) - mean) * rstd;
-        if (S.has_gamma) y *= cr.pg[i];
-        if (S.has_beta) y += cr.pbe[i];
+        if (S.has_gamma) y *= pg[i];
+        if (S.has_beta) y += pbe[i];
         xs[k] = y;
       }
     }
@@ -499,10 +523,11 @@ __device__ __forceinline__ bool attend(const CStage &S, const ChainDyn &dyn, uin
   return good;
 }
 
-__global__ __launch_bounds__(kThreads) void gemv_chain_kernel(const CStage *st, int n_stages,
+__global__ __launch_bounds__(kBlock) void gemv_chain_kernel(const CStage *st, int n_stages,
                                                               ChainDyn dyn, ChainState *state) {
   __shared__ float4 xs4[kMaxK / 4];
   __shared__ float red[kWaves];
+  __shared__ float outs[kWaves * 64];   // the compute waves' stage outputs, for the store wave
   __shared__ int alive;
   // the stage descriptors, copied once: a stage's fields are then LDS reads
   // instead of scalar loads that miss the scalar cache stage after stage
@@ -517,36 +542,54 @@ __global__ __launch_bounds__(kThreads) void gemv_chain_kernel(const CStage *st, 
     const u32x4_t *from = reinterpret_cast<const u32x4_t *>(st);
     u32x4_t *to = reinterpret_cast<u32x4_t *>(st_lds);
     const int pieces = n_stages * (int)(sizeof(CStage) / 16);
-    for (int i = tid; i < pieces; i += kThreads) to[i] = gbl(from)[i];
+    for (int i = tid; i < pieces; i += kBlock) to[i] = gbl(from)[i];
     __syncthreads();
     st = st_lds;
   }
   const uint32_t epoch = __hip_atomic_load(&state->epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
-  if (tid == 0) {
-    alive = 1;
-    ll_put(&state->started[blockIdx.x], (uint64_t)epoch << 32 | blockIdx.x);
+  const bool storer = wave == kWaves;
+  if (tid == 0) alive = 1;
+  if (storer && lane == 0) ll_put(&state->started[blockIdx.x], (uint64_t)epoch << 32 | blockIdx.x);
+  // Every wave passes the same barriers per stage: B1 at the start, the
+  // LayerNorm prologue's, B2 once x is in LDS, B3 once the outputs are in
+  // `outs`. The store wave has a loop of its own (values of the compute
+  // loop merged into it would be copied between registers, and each copy
+  // would wait for the stores before it).
+  if (storer) {
+    for (int s = 0; s < n_stages; ++s) {
+      const CStage &S = st[s];
+      if ((int)blockIdx.x * kWaves >= S.N) continue;
+      __syncthreads();                                 // B1
+      if (S.pro == KH_GEMV_PRO_LAYERNORM)
+        for (int i = 0; i < kLnBarriers; ++i) __syncthreads();
+      __syncthreads();                                 // B2
+      if (!alive) break;
+      __syncthreads();                                 // B3
+      store_outputs(hot_of(S, dyn), nwaves, lane, epoch, outs);   // `outs` is rewritten only after the next B2
+    }
+    return;
   }
-  Carry cr;
-  cr.pb = 0.0f, cr.prp = 0.0f, cr.pr = 0;
-  Hot hot = hot_of(st[0], dyn);
-  prefetch(hot, gw, nwaves, lane, cr);
   for (int s = 0; s < n_stages; ++s) {
     const CStage &S = st[s];
-    if ((int)blockIdx.x * kWaves < S.N) {  // this workgroup owns columns of stage s
-      __syncthreads();                       // the previous stage's reads of xs are done
-      const bool good = S.pro == KH_GEMV_PRO_ATTN ? attend(S, dyn, epoch, xs) : acquire_x(S, dyn, epoch, cr, xs, red);
-      if (!good) alive = 0;
-      __syncthreads();
-      if (!alive) {
-        if (tid == 0) atomicAdd(&state->timeouts, 1ull);
-        break;
-      }
-      compute(hot, gw, nwaves, lane, epoch, cr, xs, state);
+    if ((int)blockIdx.x * kWaves >= S.N) continue;  // this workgroup owns no columns of stage s
+    const Hot hot = hot_of(S, dyn);
+    // The stage's weights and epilogue operands are loaded before its input
+    // is awaited. They live in registers of this iteration only: a value
+    // carried to the next stage would be copied between registers at the end
+    // of the stage, and the copy's wait for the load would also wait for
+    // every memory operation issued before it.
+    Carry cr;
+    prefetch(hot, gw, nwaves, lane, cr);
+    __syncthreads();                                   // B1: the previous stage's reads of xs are done
+    const bool good = S.pro == KH_GEMV_PRO_ATTN ? attend(S, dyn, epoch, xs) : acquire_x(S, hot, dyn, epoch, xs, red);
+    if (!good) alive = 0;
+    __syncthreads();                                   // B2
+    if (!alive) {
+      if (tid == 0) atomicAdd(&state->timeouts, 1ull);
+      break;
     }
-    if (s + 1 < n_stages) {
-      hot = hot_of(st[s + 1], dyn);
-      prefetch(hot, gw, nwaves, lane, cr);
-    }
+    compute(hot, gw, nwaves, lane, epoch, cr, xs, outs, state);
+    __syncthreads();                                   // B3
   }
   if (blockIdx.x == 0 && wave == 0) {
     // every workgroup has read the old epoch before the new one is stored
@@ -703,7 +746,7 @@ class GemvChain final : public Chain {
       return KH_ERR_HIP;
     }
     int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gemv_chain_kernel, kThreads, 0) != hipSuccess ||
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gemv_chain_kernel, kBlock, 0) != hipSuccess ||
         per_cu < 1) {
       (void)hipGetLastError();
       err = "chain: the kernel does not fit a CU";
@@ -734,7 +777,7 @@ class GemvChain final : public Chain {
       if (!p) return hipErrorInvalidValue;
       dyn.p[i] = static_cast<float *>(p);
     }
-    hipLaunchKernelGGL(gemv_chain_kernel, dim3(groups), dim3(kThreads), 0, stream, d_stages, (int)st.size(), dyn,
+    hipLaunchKernelGGL(gemv_chain_kernel, dim3(groups), dim3(kBlock), 0, stream, d_stages, (int)st.size(), dyn,
                        d_state);
     return hipGetLastError();
   }
