@@ -39,6 +39,17 @@ def r16(a):
     return oracle.bf16_round(np.asarray(a, np.float32)).astype(np.float64)
 
 
+class _Batched(torch.nn.Module):
+    """x @ w[b] * 0.5 over a constant batch of weights."""
+
+    def __init__(self, w):
+        super().__init__()
+        self.w = torch.nn.Parameter(w)
+
+    def forward(self, x):
+        return torch.matmul(x, self.w) * 0.5
+
+
 def close_to_scale(out, ref, tol):
     out, ref = np.asarray(out, np.float64), np.asarray(ref, np.float64)
     scale = max(np.abs(ref).max(), 1e-30)
@@ -114,6 +125,15 @@ def test_k_contiguous_bf16_tiles_walk_several_tiles(tile):
             out = c(*args)
             close_to_scale(out.cpu().numpy(), ref, EXACT)
             assert torch.equal(c(*args), out)
+    # batched constant weights: each batch reads its own slice of the copy
+    torch.manual_seed(tile)
+    model = _Batched(torch.randn(3, 96, 50) * 0.1).eval()
+    w = model.w.detach()
+    x = torch.randn(3, 300, 96)
+    c = kiln.compile(model, (x,), device="cuda", matmul_precision="bf16", gpu_matmul_config=cfg)
+    assert f"tile {tile} splitk 1" in c._exe.program.launches[0].summary
+    ref = np.stack([r16(x[i].numpy()) @ r16(w[i].numpy()) for i in range(3)]) * 0.5
+    close_to_scale(c(x).cpu().numpy(), ref, EXACT)
 
 
 @pytest.mark.parametrize("k, n, ln", [(768, 2304, True), (3072, 768, False), (64, 130, False), (16, 5, True)])

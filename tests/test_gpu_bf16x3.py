@@ -44,6 +44,17 @@ def three_pass(x, w_kn):
     return xl @ wh + xh @ wl + xh @ wh
 
 
+class _Batched(torch.nn.Module):
+    """x @ w[b] * 0.5 over a constant batch of weights."""
+
+    def __init__(self, w):
+        super().__init__()
+        self.w = torch.nn.Parameter(w)
+
+    def forward(self, x):
+        return torch.matmul(x, self.w) * 0.5
+
+
 def close_to_scale(out, ref, tol):
     out, ref = np.asarray(out, np.float64), np.asarray(ref, np.float64)
     scale = max(np.abs(ref).max(), 1e-30)
@@ -109,6 +120,15 @@ def test_k_contiguous_bf16x3_tiles_walk_several_tiles(tile):
             out = c(*args)
             close_to_scale(out.cpu().numpy(), ref, SPLIT_EXACT)
             assert torch.equal(c(*args), out)
+    # batched constant weights: each batch reads its own slice of the copy
+    torch.manual_seed(tile)
+    model = _Batched(torch.randn(3, 96, 50) * 0.1).eval()
+    w = model.w.detach()
+    x = torch.randn(3, 300, 96)
+    c = kiln.compile(model, (x,), device="cuda", matmul_precision="bf16x3", gpu_matmul_config=cfg)
+    assert f"tile {tile} splitk 1" in c._exe.program.launches[0].summary
+    ref = np.stack([three_pass(x[i].numpy(), w[i].numpy()) for i in range(3)]) * 0.5
+    close_to_scale(c(x).cpu().numpy(), ref, SPLIT_EXACT)
 
 
 @pytest.mark.parametrize("T", [128, 512])
