@@ -506,7 +506,7 @@ GEMM_SHAPES = [(2048, 3072, 768), (128, 2304, 768), (128, 768, 768), (128, 3072,
 
 
 def gemm_sweep(autotune):
-    """BASELINE's nn.Linear sweep (bias epilogue), fp32 and, reported
+    """The benchmark's nn.Linear sweep (bias epilogue), fp32 and, reported
     separately, the bf16-input / fp32-accumulate variant. TFLOP/s from GPU time
     of a 20-call graph replay; eager torch beside each (bf16 with inputs
     already cast, its best case). bf16 also reports the fraction of the
@@ -569,7 +569,7 @@ def gemm_sweep(autotune):
 
 
 def linear_gelu(autotune):
-    """BASELINE's C1: nn.Linear(768, 3072) + bias + GELU at [128, 768], with
+    """The benchmark's C1: nn.Linear(768, 3072) + bias + GELU at [128, 768], with
     nn.GELU's default (erf) form and the tanh form the Block uses; GPU time of
     a 20-call graph replay, eager torch beside each."""
     import torch

@@ -293,7 +293,7 @@ __global__ __launch_bounds__(64 * WM * WN * WK) void gemm_f32_kernel(const GemmA
 // (global_load_lds, 128-bit per lane for aligned row-major operands, 32-bit
 // for any other strides) through a ring of NS LDS stages, NS - 1 steps ahead
 // of the matrix cores, so no VGPRs hold data in flight and a load has NS - 1
-// MFMA phases to arrive. (Rings deeper than 3 were measured on the BASELINE
+// MFMA phases to arrive. (Rings deeper than 3 were measured on the benchmark
 // shapes and won nowhere, so every configuration uses NS = 3.)
 //   * K advances in steps of 32. Within a step, lane group g of an MFMA
 //     (lanes l / 16) owns K values 8g .. 8g+7 and MFMA j consumes value 8g + j

@@ -4,7 +4,7 @@
 
 Runs the measured autotuner (kiln.hip.autotune.GPUAutotuner, no cache, no
 shipped table) on one MI355X for every GEMM shape of the GPT-2-small block at
-T = 128, 512, 1024 and 2048 tokens, the 12-layer stack and the BASELINE GEMM
+T = 128, 512, 1024 and 2048 tokens, the 12-layer stack and the benchmark GEMM
 sweep, in fp32 and bf16, and writes the winners keyed like the on-disk cache
 (device|CUs|precision|BxMxNxK). The table is what makes a plan the same on
 every MI355X: compiled models look their shapes up there before measuring.
@@ -21,7 +21,7 @@ from kiln.hip import autotune
 SHAPES = sorted({
     # GPT-2 block: qkv, attention projection, MLP up, MLP down, at each token count
     *((t, n, k) for t in (128, 512, 1024, 2048) for n, k in ((2304, 768), (768, 768), (3072, 768), (768, 3072))),
-    # BASELINE GEMM sweep (the M = 1 decode shape is a GEMV in fp32)
+    # the benchmark GEMM sweep (the M = 1 decode shape is a GEMV in fp32)
     (2048, 3072, 768), (128, 2304, 768), (128, 768, 768), (128, 3072, 768), (128, 768, 3072), (1, 3072, 768),
     (1, 2304, 768), (1, 768, 768), (1, 768, 3072),
 })

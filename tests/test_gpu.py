@@ -1,7 +1,7 @@
 """Parity of the MI355X HIP backend: every result must match the oracle.
 
 The cases mirror the reference's GPU tests (tests/test_gpu.py:52-169 of the
-reference) plus the BASELINE configurations at full size. Each compiled result
+reference) plus the benchmark configurations at full size. Each compiled result
 is compared with
   * the float64 oracle (oracle/interp.py on the imported graph, or the C
     oracle for the named configurations): rtol 1e-4, atol 1e-5 for fp32
@@ -420,7 +420,7 @@ def test_strided_and_broadcast_gemm_operands():
     check(fn, a, b)
 
 
-# -- BASELINE configurations at full size ------------------------------------------------
+# -- benchmark configurations at full size -----------------------------------------------
 
 def test_config_linear_bias_gelu():
     torch.manual_seed(0)
