@@ -75,7 +75,8 @@ enum { KH_ROW_GENERIC = 0, KH_ROW_LAYERNORM = 1, KH_ROW_SOFTMAX = 2 };
 
 /* GEMM precisions */
 enum { KH_PREC_FP32 = 0, KH_PREC_BF16 = 1, KH_PREC_BF16X3 = 2 };
-/* GEMV prologues (kh_launch.cfg[4] of a KH_FAM_GEMV launch) */
+/* Prologues (kh_launch.cfg[4] of a KH_FAM_GEMV launch; LayerNorm also of a
+ * KH_FAM_GEMM launch on an fp32 small-M configuration) */
 enum { KH_GEMV_PRO_NONE = 0, KH_GEMV_PRO_LAYERNORM = 1, KH_GEMV_PRO_ATTN = 2 };
 /* GEMV launch flag (kh_launch.variant of a KH_FAM_GEMV launch): the launch
  * may run inside a persistent chain with the flagged GEMV launches next to it
@@ -138,7 +139,13 @@ typedef struct kh_pass {
  *        refs[1] = B over (b, k, n); refs[2..] are the epilogue's operands with
  *        strides over (b, m, n). The tape starts with the accumulator in slot 0.
  *        cfg[1] = tile configuration id, cfg[2] = split-K (0: library picks),
- *        cfg[3] = precision.
+ *        cfg[3] = precision. cfg[4] = 1 (fp32 small-M configurations with at
+ *        most 4 rows per wave, K <= 1024): LayerNorm prologue - refs[0] is
+ *        the LayerNorm's input x and each row enters the product as (x -
+ *        mean) * rstd (mean, var and eps from fparams[0..2] as for the GEMV
+ *        below); gamma must already be folded into B and beta . B is the
+ *        per-column vector refs[cfg[6]] (strides 0 over M, 1 over N; -1:
+ *        none) added to the accumulator before the tape; cfg[5] = -1.
  *   GEMV as GEMM with M = 1; cfg[1] = workgroup variant of the [K][N] kernel
  *        (0: library picks from the shape; 1-3: 32/16/8 columns x 256 threads;
  *        4-5: 32/16 columns x 1024 threads), cfg[2] = split-K (0: library

@@ -1317,6 +1317,35 @@ std::unique_ptr<Op> make_gemm(const kh_launch &L, std::string &err, bool &unsupp
   if (!fill_epilogue(L, a, op->e_vec_candidates, err)) return nullptr;
   a.direct = 0, a.d_bias = a.d_res = a.d_out = a.d_act = -1;
   match_direct_epilogue(L, a);
+  // LayerNorm prologue (cfg[4] = 1; fp32 small-M configurations holding at
+  // most 4 rows per wave, K <= kLnMaxK): every A row enters the product as
+  // (x - mean) * rstd, mean = sum(x) * fparams[0], rstd = rsqrt(sum((x -
+  // mean)^2) * fparams[1] + fparams[2]); the LayerNorm's gamma is folded into
+  // B and its beta . B into the per-column vector refs[cfg[6]] (strides 0
+  // over M, 1 over N; -1: none), added to the accumulator before the
+  // epilogue; cfg[5] must be -1
+  a.pro = L.cfg[4], a.pro_g = -1, a.pro_b = -1;
+  if (a.pro != KH_GEMV_PRO_NONE) {
+    if (a.pro != KH_GEMV_PRO_LAYERNORM || t.kind != 6 || t.prec != KH_PREC_FP32 || t.bm > 4 * t.wk ||
+        L.cfg[5] != -1) {
+      err = "matmul: a LayerNorm prologue needs an fp32 small-M configuration with at most 4 rows per wave";
+      return nullptr;
+    }
+    if (K > kLnMaxK) {
+      unsupported = true;
+      err = "matmul: LayerNorm prologue rows longer than " + std::to_string(kLnMaxK);
+      return nullptr;
+    }
+    const int r = L.cfg[6];
+    if (r != -1) {
+      if (r < 2 || r >= L.n_refs || L.refs[r].strides[1] != 0 || L.refs[r].strides[2] != 1) {
+        err = "matmul: the LayerNorm prologue's column vector must be an operand with strides 0 over M, 1 over N";
+        return nullptr;
+      }
+      a.pro_b = r - 2;
+    }
+    a.pro_c1 = L.fparams[0], a.pro_c2 = L.fparams[1], a.pro_eps = L.fparams[2];
+  }
   int cfg_run = cfg;
   if (t.prec == KH_PREC_BF16) {
     // B must be the library-layout bf16 copy: [batch][N][K'] with K' a

@@ -27,6 +27,16 @@
 //     residual / activation directly, other tapes through the tape
 //     interpreter; the direct operands are loaded before the partial sums so
 //     their latency overlaps the reduction.
+// LayerNorm prologue (LN, fp32; a LayerNorm whose only consumer is this
+// product's A operand): A is the LayerNorm's input x, gamma is folded into
+// B and beta . B into a per-column vector by the lowering, so the product
+// needs only each row's (x - mean) * rstd. Each wave loads its rows of the
+// tile once (after the ring's first copies are in flight), takes the mean,
+// then the variance of the centred values (the LayerNorm row kernel's
+// arithmetic), and leaves (rstd, -mean * rstd) per row in LDS; every A
+// fragment value then enters the MFMAs as x * rstd - mean * rstd (one FMA),
+// and the column vector is added to the summed tile before the epilogue.
+// The LayerNorm's launch and its output's round trip through memory go away.
 // K must be a positive multiple of 32 and the operands' spans below 2^29
 // elements (the host checks both).
 #include <algorithm>
@@ -45,11 +55,12 @@ namespace {
 // accumulation (the arithmetic of the other bf16 GEMMs); 2 three-pass bf16 -
 // B the [batch][N][2K'] copy holding bf16(w) then bf16(w - bf16(w)) per row,
 // A split the same way, a.b = a_lo.b_hi + a_hi.b_lo + a_hi.b_hi.
-template <int BM, int BN, int WK, int NS, int PREC>
+template <int BM, int BN, int WK, int NS, int PREC, bool LN>
 __global__ __launch_bounds__(64 * WK) void gemm_small_kernel(const GemmArgs a) {
   constexpr int BK = 32, MT = 16, ACH = BK / 4;
   constexpr int FM = BM / MT, FN = BN / MT;
   constexpr bool BF = PREC != 0;
+  static_assert(!LN || (!BF && BM % WK == 0 && BM / WK <= 4), "LayerNorm prologue: fp32, at most 4 rows per wave");
   constexpr int B_HALF = BN * BK / 2;           // words of one bf16 copy of a stage's B rows
   constexpr int A_FLOATS = BM * BK;
   constexpr int STAGE = A_FLOATS + (BF ? B_HALF * (PREC == 2 ? 2 : 1) : BN * BK);   // words: A rows, then B rows
@@ -64,6 +75,7 @@ __global__ __launch_bounds__(64 * WK) void gemm_small_kernel(const GemmArgs a) {
   static_assert(WK * NS * STAGE * 4 <= 160 * 1024, "LDS");
 
   __shared__ float4 rings[WK * NS * STAGE / 4];
+  __shared__ float2 ln_stats[LN ? BM : 1];   // LN: (rstd, -mean * rstd) per tile row
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -155,6 +167,44 @@ __global__ __launch_bounds__(64 * WK) void gemm_small_kernel(const GemmArgs a) {
   auto part = [](const float4 &v, int j) { return j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w; };
 
   for (int p = 0; p < NS - 1 && p < n_steps; ++p) issue(p);
+  float ln_sc[FM], ln_sh[FM];
+  if constexpr (LN) {
+    // every load of the wave's rows first (clamped, unconditional: values
+    // past K are dropped at use), then the two sums per row
+    constexpr int R = BM / WK, J = kLnMaxK / 256;
+    const int k4s = a.K / 4;
+    float4 xv[R][J];
+#pragma unroll
+    for (int rr = 0; rr < R; ++rr) {
+      const float4 *x = reinterpret_cast<const float4 *>(Ab + (int64_t)min(m0 + wave_u + rr * WK, a.M - 1) * a.sa_m);
+#pragma unroll
+      for (int j = 0; j < J; ++j) xv[rr][j] = x[min(lane + 64 * j, k4s - 1)];
+    }
+#pragma unroll
+    for (int rr = 0; rr < R; ++rr) {
+      float s1 = 0.0f;
+#pragma unroll
+      for (int j = 0; j < J; ++j)
+        if (lane + 64 * j < k4s) s1 += (xv[rr][j].x + xv[rr][j].y) + (xv[rr][j].z + xv[rr][j].w);
+      const float mean = wave_sum(s1) * a.pro_c1;
+      float s2 = 0.0f;
+#pragma unroll
+      for (int j = 0; j < J; ++j)
+        if (lane + 64 * j < k4s) {
+          const float dx = xv[rr][j].x - mean, dy = xv[rr][j].y - mean;
+          const float dz = xv[rr][j].z - mean, dw = xv[rr][j].w - mean;
+          s2 = fmaf(dx, dx, s2), s2 = fmaf(dy, dy, s2), s2 = fmaf(dz, dz, s2), s2 = fmaf(dw, dw, s2);
+        }
+      const float rstd = rsqrtf(wave_sum(s2) * a.pro_c2 + a.pro_eps);
+      if (lane == 0) ln_stats[wave_u + rr * WK] = make_float2(rstd, -mean * rstd);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) {
+      const float2 st = ln_stats[fm * MT + li];
+      ln_sc[fm] = st.x, ln_sh[fm] = st.y;
+    }
+  }
   for (int s = 0; s < n_steps; ++s) {
     wait_landed(min(NS - 2, n_steps - 1 - s));
     // the wave's own LDS: its copies landed (vmcnt), nothing else writes it
@@ -173,6 +223,16 @@ __global__ __launch_bounds__(64 * WK) void gemm_small_kernel(const GemmArgs a) {
     // have completed before this wave issues that copy (next iterations)
     __builtin_amdgcn_s_waitcnt((3 << 14) | (7 << 4) | 15);  // lgkmcnt(0); vmcnt, expcnt unconstrained
     if (s + NS - 1 < n_steps) issue(s + NS - 1);
+    if constexpr (LN) {
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          float4 &v = xa[fm][h];
+          v.x = fmaf(v.x, ln_sc[fm], ln_sh[fm]), v.y = fmaf(v.y, ln_sc[fm], ln_sh[fm]);
+          v.z = fmaf(v.z, ln_sc[fm], ln_sh[fm]), v.w = fmaf(v.w, ln_sc[fm], ln_sh[fm]);
+        }
+    }
     if constexpr (BF) {
       bf16x8 ah[FM], al[FM];
 #pragma unroll
@@ -263,6 +323,12 @@ __global__ __launch_bounds__(64 * WK) void gemm_small_kernel(const GemmArgs a) {
       sum.x += p.x, sum.y += p.y, sum.z += p.z, sum.w += p.w;
     }
     const int valid = min(4, a.N - n);
+    if constexpr (LN) {
+      if (a.pro_b >= 0) {   // the folded beta . B
+        const float4 c = load4(a.pro_b, m, n, valid);
+        sum.x += c.x, sum.y += c.y, sum.z += c.z, sum.w += c.w;
+      }
+    }
     if (!a.direct) {
       Vec<4> v;
       v.v[0] = sum.x, v.v[1] = sum.y, v.v[2] = sum.z, v.v[3] = sum.w;
@@ -294,9 +360,16 @@ __global__ __launch_bounds__(64 * WK) void gemm_small_kernel(const GemmArgs a) {
 
 hipError_t launch_gemm_small(int id, const GemmArgs &a, dim3 grid, hipStream_t stream) {
   switch (id) {
-#define KH_CFGSM_CASE(cid, bm, bn, wk, ns, prec)                                                      \
-  case cid:                                                                                          \
-    hipLaunchKernelGGL((gemm_small_kernel<bm, bn, wk, ns, prec>), grid, dim3(64 * wk), 0, stream, a); \
+#define KH_CFGSM_CASE(cid, bm, bn, wk, ns, prec)                                                             \
+  case cid:                                                                                                 \
+    if (a.pro == KH_GEMV_PRO_LAYERNORM) {                                                                   \
+      if constexpr (prec == 0 && bm <= 4 * wk && bm % wk == 0)                                              \
+        hipLaunchKernelGGL((gemm_small_kernel<bm, bn, wk, ns, prec, true>), grid, dim3(64 * wk), 0, stream, a); \
+      else                                                                                                  \
+        return hipErrorInvalidValue;                                                                        \
+    } else {                                                                                                \
+      hipLaunchKernelGGL((gemm_small_kernel<bm, bn, wk, ns, prec, false>), grid, dim3(64 * wk), 0, stream, a); \
+    }                                                                                                       \
     break;
     KH_GEMM_SMALL_CONFIGS(KH_CFGSM_CASE)
 #undef KH_CFGSM_CASE

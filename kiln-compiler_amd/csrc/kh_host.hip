@@ -226,8 +226,10 @@ void host_attn(const kh_launch &L, float *const *p) {
 
 // -- matrix products ----------------------------------------------------------------------
 
-// The A row (b, m, 0..K) the product reads: A itself, or what a GEMV prologue
-// makes of it (LayerNorm of the row; one query's head-merged attention).
+// The A row (b, m, 0..K) the product reads: A itself, or what a prologue
+// makes of it (a GEMV's LayerNorm of the row, or one query's head-merged
+// attention; a GEMM's LayerNorm prologue only normalises, (x - mean) * rstd:
+// its gamma and beta are folded into B and a per-column constant).
 void a_row(const kh_launch &L, float *const *p, int64_t b, int64_t m, std::vector<float> &row) {
   const int64_t K = L.gemm[3];
   const kh_ref &A = L.refs[0];
@@ -248,7 +250,7 @@ void a_row(const kh_launch &L, float *const *p, int64_t b, int64_t m, std::vecto
     return;
   }
   for (int64_t k = 0; k < K; ++k) row[(size_t)k] = p[0][b * A.strides[0] + m * A.strides[1] + k * A.strides[2]];
-  if (gemv && L.cfg[4] == KH_GEMV_PRO_LAYERNORM) {
+  if (L.cfg[4] == KH_GEMV_PRO_LAYERNORM) {
     double sum = 0.0;
     for (int64_t k = 0; k < K; ++k) sum += row[(size_t)k];
     const double mean = sum * L.fparams[0];
@@ -257,8 +259,8 @@ void a_row(const kh_launch &L, float *const *p, int64_t b, int64_t m, std::vecto
     const double rstd = 1.0 / std::sqrt(sq * L.fparams[1] + L.fparams[2]);
     for (int64_t k = 0; k < K; ++k) {
       double y = (row[(size_t)k] - mean) * rstd;
-      if (L.cfg[5] >= 0) y *= p[L.cfg[5]][b * L.refs[L.cfg[5]].strides[0] + k * L.refs[L.cfg[5]].strides[2]];
-      if (L.cfg[6] >= 0) y += p[L.cfg[6]][b * L.refs[L.cfg[6]].strides[0] + k * L.refs[L.cfg[6]].strides[2]];
+      if (gemv && L.cfg[5] >= 0) y *= p[L.cfg[5]][b * L.refs[L.cfg[5]].strides[0] + k * L.refs[L.cfg[5]].strides[2]];
+      if (gemv && L.cfg[6] >= 0) y += p[L.cfg[6]][b * L.refs[L.cfg[6]].strides[0] + k * L.refs[L.cfg[6]].strides[2]];
       row[(size_t)k] = (float)y;
     }
   }
@@ -292,6 +294,9 @@ void host_matmul(const kh_launch &L, float *const *p) {
           }
         }
         const int64_t idx[3] = {b, m, n};
+        // a GEMM's LayerNorm prologue: the folded beta . W, per column
+        const int c_ref = L.family == KH_FAM_GEMM && L.cfg[4] == KH_GEMV_PRO_LAYERNORM ? L.cfg[6] : -1;
+        if (c_ref >= 0) acc += (double)p[c_ref][offset_of(L.refs[c_ref], idx, 3)];
         slot[0] = (float)acc;
         run_tape(
             L, 0, L.n_insns, slot, [&](int j) { return p[j][offset_of(L.refs[j], idx, 3)]; },

@@ -643,8 +643,8 @@ class _Lowerer:
             raise NotImplementedError("HIP backend: matmul operand has no storage")
         cfg, prec = self.matmul_choice(k)
         gemv = self.is_gemv(k)
-        pro = self.prologue.get(k) if gemv else None
-        a_src = pro[0] if pro else a   # the LayerNorm's input when the GEMV runs it as its prologue
+        pro = self.prologue.get(k)
+        a_src = pro[0] if pro else a   # the LayerNorm's input when the product runs it as its prologue
         d = self.new_desc(kl.FAM_GEMV if gemv else kl.FAM_GEMM, "gemv" if gemv else "matmul", k, space3)
         if gemv and self.gemv_chains:
             d.variant = kl.GEMV_CHAIN   # the library may run it in a persistent chain with its GEMV neighbours
@@ -653,11 +653,11 @@ class _Lowerer:
         k_major = not gemv and int(cfg.get("tile", -1)) in autotune.NK_B
         nk = (gemv and self.layouts[b].base[0] == "const" and kk % 4 == 0) or k_major
         derived_b = prec in ("bf16", "bf16x3") or nk
-        d.refs[1] = ref3(b, (batch, kk, n), register=not derived_b)
+        d.refs[1] = b_ref = ref3(b, (batch, kk, n), register=not derived_b)
         if prec in ("bf16", "bf16x3"):
             d.refs[1] = self.bf16_weight(b, d.refs[1], batch, kk, n, split=prec == "bf16x3")
         elif nk:
-            d.refs[1] = self.nk_weight(b, d.refs[1], batch, kk, n)
+            d.refs[1] = self.nk_weight(b, b_ref, batch, kk, n, scale=pro[1] if pro and not gemv else None)
         externals = []
         for nd in k.nodes:
             if nd is mm:
@@ -681,10 +681,15 @@ class _Lowerer:
         if pro:
             x, gamma, beta, fparams = pro
             d.cfg[4], d.cfg[5], d.cfg[6] = 1, -1, -1
-            for w, p in ((5, gamma), (6, beta)):
-                if p is not None:
-                    d.cfg[w] = 2 + len(refs) + len(pro_refs)
-                    pro_refs.append(ref3(p, (batch, m, kk)))
+            if gemv:
+                for w, p in ((5, gamma), (6, beta)):
+                    if p is not None:
+                        d.cfg[w] = 2 + len(refs) + len(pro_refs)
+                        pro_refs.append(ref3(p, (batch, m, kk)))
+            elif beta is not None:
+                # gamma rides in the weight copy; beta . W is a column constant
+                d.cfg[6] = 2 + len(refs) + len(pro_refs)
+                pro_refs.append(self.ln_column(b, b_ref, batch, kk, n, beta))
             for i, f in enumerate(fparams):
                 d.fparams[i] = f
         self._check_refs(refs + pro_refs + [None, None])
@@ -810,10 +815,13 @@ class _Lowerer:
 
     def find_ln_prologues(self):
         """LayerNorm row kernels whose only consumer is the A operand of a
-        1-row fp32 matmul (decode: ln_1 -> qkv, ln_2 -> fc): the GEMV runs the
-        LayerNorm as its prologue and the row kernel is not launched. The
-        LayerNorm's input must stay intact until the GEMV, so no buffer that a
-        kernel from the LayerNorm up to the GEMV writes may overlap it."""
+        1-row fp32 matmul (decode: ln_1 -> qkv, ln_2 -> fc) or of a product on
+        an fp32 small-M configuration (short prefill: the same pairs at a few
+        hundred tokens): the GEMV / GEMM runs the LayerNorm as its prologue and
+        the row kernel is not launched (for the GEMM, gamma is folded into the
+        weight copy and beta . W into a per-column constant). The LayerNorm's
+        input must stay intact until the product, so no buffer that a kernel
+        from the LayerNorm up to the product writes may overlap it."""
         kernels = self.g.kernels
         owner = {n: k for k in kernels for n in k.nodes}
         results = set(self.g.results)
@@ -842,11 +850,13 @@ class _Lowerer:
             km = owner.get(mm)
             if km is None or km.kind != "matmul" or mm.inputs[0] is not y or mm.inputs[1] is y:
                 continue
-            if y.type.rank != 2 or y.shape[0] != 1 or tuple(x.shape) != tuple(y.shape):
+            if y.type.rank != 2 or tuple(x.shape) != tuple(y.shape):
                 continue
             if self._arena_range(y) is None and y not in self.layouts:
                 continue
-            if not self.is_gemv(km):
+            gamma = ordered[1] if has_g else None
+            beta = ordered[1 + has_g] if has_b else None
+            if not (self.is_gemv(km) if y.shape[0] == 1 else self._ln_gemm_ok(km, x, gamma, beta)):
                 continue
             j = kernels.index(km)
             xr = self._arena_range(x)
@@ -859,13 +869,58 @@ class _Lowerer:
                             clash = True
                 if clash:
                     continue
-            gamma = ordered[1] if has_g else None
-            beta = ordered[1 + has_g] if has_b else None
             self.prologue[km] = (x, gamma, beta, list(fparams))
             skip.add(k)
         return skip
 
-    def nk_weight(self, b, ref, batch, kk, n):
+    def _ln_gemm_ok(self, km, x, gamma, beta) -> bool:
+        """Whether matmul kernel km can run a LayerNorm of x (gamma, beta:
+        its parameters or None) as its prologue: an fp32 small-M configuration
+        (B the [N][K] copy of a constant, A read with unit K stride) holding at
+        most 4 rows per wave, K <= 1024, x laid out like the A operand it
+        replaces, and gamma / beta constants (folded into build-time copies)."""
+        cfg, prec = self.matmul_choice(km)
+        tile = int(cfg.get("tile", -1))
+        if prec != "fp32" or tile not in autotune.SMALL_M or autotune.PRECISION.get(tile) != "fp32":
+            return False
+        bm, wk = autotune.TILES[tile][0], autotune.TILES[tile][5]
+        mm = next(n for n in km.nodes if n.op == "matmul")
+        m, kk = mm.inputs[0].shape[-2], mm.inputs[0].shape[-1]
+        if bm % wk or bm > 4 * wk or kk > 1024:
+            return False
+        if not (self.skinny_ok(mm) and autotune.k_major_fits(m, kk, tile)):
+            return False
+        for p in (gamma, beta):
+            if p is not None and (p not in self.layouts or self.layouts[p].base[0] != "const"
+                                  or math.prod(p.shape) != kk):
+                return False
+        lay = self.layouts.get(x)
+        return (lay is not None and lay.strides[-1] == 1 and lay.offset % 4 == 0
+                and all(st % 4 == 0 for st, ext in zip(lay.strides[:-1], lay.shape[:-1]) if ext > 1))
+
+    def _vector_spec(self, v):
+        """(constant name, element offset, element stride) of a constant
+        vector's values, for a derived-constant recipe."""
+        lay = self.layouts[v]
+        return [lay.base[1], int(lay.offset), int(lay.strides[-1])]
+
+    def ln_column(self, b, ref, batch, kk, n, beta):
+        """Ref of the per-column constant beta . W over (b, m, n) (strides 0
+        over M) of a small-M GEMM's LayerNorm prologue, `ref` being W's fp32
+        ref over (b, k, n); registered as a derived constant."""
+        src = self.layouts[b].base[1]
+        strides = (int(ref.strides[0]), int(ref.strides[1]), int(ref.strides[2]))
+        spec = self._vector_spec(beta)
+        name = (f"{src}@lnc:{int(ref.offset)}:{strides[0]},{strides[1]},{strides[2]}:{batch}x{kk}x{n}:"
+                f"{spec[0]}:{spec[1]}:{spec[2]}")
+        self.program.derived[name] = (src, int(ref.offset), strides, batch, kk, n, spec)
+        r = kl.Ref()
+        r.base, r.index = self.slot_of(("const", name))
+        r.offset = 0
+        r.strides[0], r.strides[1], r.strides[2] = (n if batch > 1 else 0), 0, 1
+        return r
+
+    def nk_weight(self, b, ref, batch, kk, n, scale=None):
         """Ref of an fp32 [batch][N][K] copy of constant view `b` (fp32 ref
         `ref` over (b, k, n)) for the GEMV family and the skinny-M and
         K-contiguous GEMMs: each
@@ -876,7 +931,14 @@ class _Lowerer:
         src = self.layouts[b].base[1]
         strides = (int(ref.strides[0]), int(ref.strides[1]), int(ref.strides[2]))
         name = f"{src}@nk:{int(ref.offset)}:{strides[0]},{strides[1]},{strides[2]}:{batch}x{kk}x{n}"
-        self.program.derived[name] = (src, int(ref.offset), strides, batch, kk, n)
+        if scale is None:
+            self.program.derived[name] = (src, int(ref.offset), strides, batch, kk, n)
+        else:
+            # each row scaled by the vector `scale` over K (a LayerNorm's
+            # gamma folded into the product that follows it)
+            spec = self._vector_spec(scale)
+            name = name.replace("@nk:", "@nkg:") + f":{spec[0]}:{spec[1]}:{spec[2]}"
+            self.program.derived[name] = (src, int(ref.offset), strides, batch, kk, n, spec)
         r = kl.Ref()
         r.base, r.index = self.slot_of(("const", name))
         r.offset = 0

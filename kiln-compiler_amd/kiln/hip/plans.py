@@ -31,7 +31,7 @@ from pathlib import Path
 
 from kiln.hip import lib as kl
 
-FORMAT = 1
+FORMAT = 2
 
 
 def cache_dir() -> Path:
@@ -110,6 +110,14 @@ def save(key: str, program, autotune_log=()) -> Path:
     return write_listing(key, program)
 
 
+def _recipe(r) -> tuple:
+    """A derived-constant recipe read back from JSON: (source, offset,
+    strides, batch, k, n) and, for the folded LayerNorm constants, the
+    (constant, offset, stride) of the vector they fold in."""
+    head = (r[0], int(r[1]), tuple(r[2]), int(r[3]), int(r[4]), int(r[5]))
+    return head + ((str(r[6][0]), int(r[6][1]), int(r[6][2])),) if len(r) > 6 else head
+
+
 def load(key: str):
     """(Program, autotune log) stored under ``key``, or None."""
     from kiln.hip.lowering import Launch, Program
@@ -129,8 +137,7 @@ def load(key: str):
                                    kl.LaunchDesc.from_buffer_copy(raw), item["summary"], int(item["flops"]),
                                    int(item["bytes"])))
         program = Program(launches=launches, consts=list(record["consts"]), precision=record["precision"],
-                          derived={name: (r[0], int(r[1]), tuple(r[2]), int(r[3]), int(r[4]), int(r[5]))
-                                   for name, r in record["derived"].items()})
+                          derived={name: _recipe(r) for name, r in record["derived"].items()})
         log = [dict(e, shape=tuple(e["shape"]), source="cache") for e in record.get("autotune", [])]
         return program, log
     except (OSError, ValueError, KeyError, TypeError, IndexError):

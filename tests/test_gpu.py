@@ -376,6 +376,40 @@ def test_gemv_variants_and_ragged_sizes(variant):
                 assert torch.equal(c(x, wt, b), first)
 
 
+@pytest.mark.parametrize("tile", [t for t in sorted(autotune.SMALL_M) if autotune.PRECISION[t] == "fp32"
+                                  and autotune.TILES[t][0] <= 4 * autotune.TILES[t][5]])
+def test_layernorm_prologue_on_every_small_m_configuration(tile):
+    # LayerNorm -> Linear (+ residual) on a small-M configuration: the GEMM
+    # normalises its A rows itself (gamma folded into the weight copy, beta . W
+    # into a column constant) and the LayerNorm has no launch of its own;
+    # ragged M / N, K from one step to the longest prologue row (1024), with
+    # and without affine parameters, inputs with a large mean; repeated
+    # launches agree bit for bit
+    cfg = lambda *_: {"tile": tile, "splitk": 1}
+    for m, n, k, affine in ((77, 133, 32, True), (300, 452, 256, False), (128, 200, 768, True),
+                            (40, 64, 1024, True)):
+        torch.manual_seed(m + k)
+        ln = torch.nn.LayerNorm(k, elementwise_affine=affine)
+        if affine:
+            with torch.no_grad():
+                ln.weight.copy_(1.0 + 0.1 * torch.randn(k))
+                ln.bias.copy_(0.1 * torch.randn(k))
+        lin = gpt2_init_(torch.nn.Linear(k, n), seed=k).eval()
+        model = torch.nn.Sequential(ln, lin).eval()
+        fn = lambda t, res: model(t) + res
+        x, r = 3.0 + 2.0 * torch.randn(m, k), torch.randn(m, n)
+        c = kiln.compile(fn, (x, r), device="cuda", cuda_graphs=False, gpu_matmul_config=cfg)
+        summaries = [l.summary for l in c._exe.program.launches]
+        assert len(summaries) == 1 and f"tile {tile} " in summaries[0] and "prologue: layernorm" in summaries[0]
+        g = ln.weight.detach().numpy() if affine else None
+        bt = ln.bias.detach().numpy() if affine else None
+        ref = oracle.linear(oracle.layernorm(x.numpy(), g, bt), lin.weight.detach().numpy().T,
+                            lin.bias.detach().numpy(), r.numpy())
+        out = c(x, r)
+        np.testing.assert_allclose(out.cpu().numpy(), ref, rtol=RTOL, atol=ATOL)
+        assert torch.equal(c(x, r), out)
+
+
 class _BatchedConstant(torch.nn.Module):
     def __init__(self, batch, k, n):
         super().__init__()
@@ -480,7 +514,10 @@ def test_config_gpt2_block(T):
     model = _block(T)
     x = torch.randn(T, 768)
     c = kiln.compile(model, (x,), device="cuda")
-    assert c.report.lowering["launches"] == 7    # attention fused into one launch
+    # attention fused into one launch; a LayerNorm feeding a small-M GEMM
+    # runs as that GEMM's prologue (both at T = 128)
+    n_pro = sum("prologue: layernorm" in l.summary for l in c._exe.program.launches)
+    assert c.report.lowering["launches"] == 7 - n_pro and (T != 128 or n_pro == 2)
     out = c(x).cpu().numpy()
     params = {k: v.numpy() for k, v in model.state_dict().items()}
     ref = oracle.block(x.numpy(), params, 12)

@@ -188,7 +188,9 @@ def test_block_uses_one_attention_launch(T):
     c = kiln.compile(model, (x,), device="cuda")
     # at T = 1 both LayerNorms run as the prologue of the qkv / fc GEMV
     # at T = 1 the attention runs as the prologue of the c_proj GEMV
-    assert (c.report.lowering["launches"], n_attention(c)) == ((4, 0) if T == 1 else (7, 1))
+    # at T > 1 a LayerNorm feeding a small-M GEMM runs as that GEMM's prologue
+    n_pro = sum("prologue: layernorm" in l.summary for l in c._exe.program.launches)
+    assert (c.report.lowering["launches"], n_attention(c)) == ((4, 0) if T == 1 else (7 - n_pro, 1))
     # the scores never get arena memory: the peak is the MLP's (768 + 768 + 3072) T floats
     assert c.report.arena_bytes == 4 * 4608 * T
     params = {k: v.numpy() for k, v in model.state_dict().items()}

@@ -62,12 +62,14 @@ def test_gemm_config_table_matches_the_tuner():
 def test_block_lowers_to_the_expected_families():
     g, prog = lowered(Block(768, 12, 128), torch.randn(128, 768))
     fams = [kl.FAMILY_NAMES[l.family] for l in prog.launches]
-    assert fams == ["row", "gemm", "elementwise", "gemm", "row", "gemm", "elementwise", "gemm", "row", "gemm",
-                    "gemm"]
+    # both LayerNorms run as the prologue of the small-M GEMM that reads them
+    # (qkv, MLP up): no row launch of their own
+    assert fams == ["gemm", "elementwise", "gemm", "row", "gemm", "elementwise", "gemm", "gemm", "gemm"]
     variants = [l.desc.variant for l in prog.launches if l.family == kl.FAM_ROW]
-    assert variants == [kl.ROW_LAYERNORM, kl.ROW_SOFTMAX, kl.ROW_LAYERNORM]
+    assert variants == [kl.ROW_SOFTMAX]
+    assert [i for i, l in enumerate(prog.launches) if "prologue: layernorm" in l.summary] == [0, 7]
     plan = kl.Plan([l.desc for l in prog.launches])
-    assert plan.n_launches == 11
+    assert plan.n_launches == 9
 
 
 def test_block_attention_becomes_one_launch():
@@ -246,9 +248,53 @@ def test_layernorm_is_not_fused_when_its_output_has_other_users():
     assert not any(l.desc.cfg[4] for l in prog.launches if l.family == kl.FAM_GEMV)
 
 
-def test_layernorm_is_not_fused_into_a_multi_row_gemm():
-    _, prog = lowered(_ln_linear(), torch.randn(4, 64))
+@pytest.mark.parametrize("affine", [True, False])
+def test_layernorm_feeding_a_small_m_gemm_becomes_its_prologue(affine):
+    # a few rows: the product runs on an fp32 small-M configuration; A is the
+    # LayerNorm's input, gamma is folded into the [N][K] weight copy and
+    # beta . W into a per-column constant (ref cfg[6], strides 0 over M)
+    _, prog = lowered(_ln_linear(affine), torch.randn(40, 64))
+    assert [kl.FAMILY_NAMES[l.family] for l in prog.launches] == ["gemm"]
+    launch = prog.launches[0]
+    d = launch.desc
+    assert d.cfg[1] in autotune.SMALL_M and d.cfg[4] == 1 and d.cfg[5] == -1
+    assert "prologue: layernorm" in launch.summary and d.refs[0].base == kl.BASE_INPUT
+    assert list(d.fparams)[:3] == pytest.approx([1 / 64, 1 / 64, 1e-5])
+    names = [prog.consts[d.refs[j].index] for j in (1, d.cfg[6]) if j >= 0]
+    if affine:
+        assert 2 <= d.cfg[6] < d.n_refs and list(d.refs[d.cfg[6]].strides[:3]) == [0, 0, 1]
+        assert "@nkg:" in names[0] and "@lnc:" in names[1]
+    else:
+        assert d.cfg[6] == -1 and "@nk:" in names[0]
+    kl.Plan([l.desc for l in prog.launches])
+
+
+def test_folded_layernorm_constants():
+    # the scaled weight copy is W^T row n times gamma; the column constant is
+    # beta . W (float64 sums); a LayerNorm + Linear run through the host
+    # interpreter matches the float64 reference
+    from kiln.hip.runtime import host_constant
+
+    torch.manual_seed(3)
+    model = _ln_linear()
+    with torch.no_grad():
+        model[0].weight.copy_(1 + 0.1 * torch.randn(64))
+        model[0].bias.copy_(0.1 * torch.randn(64))
+    g, prog = lowered(model, torch.randn(40, 64))
+    d = prog.launches[0].desc
+    w = model[1].weight.detach().numpy().astype(np.float64)      # [N, K]
+    gam, bet = model[0].weight.detach().numpy(), model[0].bias.detach().numpy()
+    scaled = host_constant(prog, g.constants, prog.consts[d.refs[1].index])
+    np.testing.assert_array_equal(scaled[0], (w.astype(np.float32) * gam[None, :]).astype(np.float32))
+    col = host_constant(prog, g.constants, prog.consts[d.refs[d.cfg[6]].index])
+    np.testing.assert_allclose(col.reshape(-1), w @ bet.astype(np.float64), rtol=1e-6, atol=1e-7)
+
+
+def test_layernorm_stays_a_row_kernel_before_other_gemms():
+    # more rows than the small-M kernel takes: the LayerNorm keeps its launch
+    _, prog = lowered(_ln_linear(), torch.randn(1100, 64))
     assert [kl.FAMILY_NAMES[l.family] for l in prog.launches] == ["row", "gemm"]
+    assert prog.launches[1].desc.cfg[4] == 0
 
 
 @pytest.mark.parametrize("mutate, err", [
