@@ -143,9 +143,10 @@ typedef struct kh_pass {
  *        most 4 rows per wave, K <= 1024): LayerNorm prologue - refs[0] is
  *        the LayerNorm's input x and each row enters the product as (x -
  *        mean) * rstd (mean, var and eps from fparams[0..2] as for the GEMV
- *        below); gamma must already be folded into B and beta . B is the
- *        per-column vector refs[cfg[6]] (strides 0 over M, 1 over N; -1:
- *        none) added to the accumulator before the tape; cfg[5] = -1.
+ *        below); gamma must already be folded into B; refs[cfg[5]] = the
+ *        column sums of that B and refs[cfg[6]] = beta . B (-1: none), both
+ *        per-column vectors (strides 0 over M, 1 over N), the second added to
+ *        the accumulator before the tape.
  *   GEMV as GEMM with M = 1; cfg[1] = workgroup variant of the [K][N] kernel
  *        (0: library picks from the shape; 1-3: 32/16/8 columns x 256 threads;
  *        4-5: 32/16 columns x 1024 threads), cfg[2] = split-K (0: library

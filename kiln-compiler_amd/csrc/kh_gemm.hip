@@ -1318,16 +1318,17 @@ std::unique_ptr<Op> make_gemm(const kh_launch &L, std::string &err, bool &unsupp
   a.direct = 0, a.d_bias = a.d_res = a.d_out = a.d_act = -1;
   match_direct_epilogue(L, a);
   // LayerNorm prologue (cfg[4] = 1; fp32 small-M configurations holding at
-  // most 4 rows per wave, K <= kLnMaxK): every A row enters the product as
-  // (x - mean) * rstd, mean = sum(x) * fparams[0], rstd = rsqrt(sum((x -
-  // mean)^2) * fparams[1] + fparams[2]); the LayerNorm's gamma is folded into
-  // B and its beta . B into the per-column vector refs[cfg[6]] (strides 0
-  // over M, 1 over N; -1: none), added to the accumulator before the
-  // epilogue; cfg[5] must be -1
+  // most 4 rows per wave, K <= kLnMaxK): A is the LayerNorm's input x and
+  // the product is rstd * ((x - x0) . B - (mean - x0) * g) + c per row (x0
+  // the row's first value, mean = sum(x) * fparams[0], rstd = rsqrt(sum((x -
+  // mean)^2) * fparams[1] + fparams[2])), i.e. LayerNorm(x) . B with the
+  // LayerNorm's gamma folded into B: g = refs[cfg[5]] (column sums of B) and
+  // c = refs[cfg[6]] (beta . B before the folding; -1: none), both with
+  // strides 0 over M and 1 over N, added before the epilogue
   a.pro = L.cfg[4], a.pro_g = -1, a.pro_b = -1;
   if (a.pro != KH_GEMV_PRO_NONE) {
     if (a.pro != KH_GEMV_PRO_LAYERNORM || t.kind != 6 || t.prec != KH_PREC_FP32 || t.bm > 4 * t.wk ||
-        L.cfg[5] != -1) {
+        t.bm % t.wk) {
       err = "matmul: a LayerNorm prologue needs an fp32 small-M configuration with at most 4 rows per wave";
       return nullptr;
     }
@@ -1336,13 +1337,14 @@ std::unique_ptr<Op> make_gemm(const kh_launch &L, std::string &err, bool &unsupp
       err = "matmul: LayerNorm prologue rows longer than " + std::to_string(kLnMaxK);
       return nullptr;
     }
-    const int r = L.cfg[6];
-    if (r != -1) {
+    for (int w = 0; w < 2; ++w) {
+      const int r = L.cfg[5 + w];
+      if (r == -1 && w == 1) continue;
       if (r < 2 || r >= L.n_refs || L.refs[r].strides[1] != 0 || L.refs[r].strides[2] != 1) {
-        err = "matmul: the LayerNorm prologue's column vector must be an operand with strides 0 over M, 1 over N";
+        err = "matmul: the LayerNorm prologue's column vectors must be operands with strides 0 over M, 1 over N";
         return nullptr;
       }
-      a.pro_b = r - 2;
+      (w == 0 ? a.pro_g : a.pro_b) = r - 2;
     }
     a.pro_c1 = L.fparams[0], a.pro_c2 = L.fparams[1], a.pro_eps = L.fparams[2];
   }

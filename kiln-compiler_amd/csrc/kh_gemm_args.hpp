@@ -158,8 +158,7 @@ inline hipError_t launch_splitk_reduce(const GemmArgs &a, int cus, hipStream_t s
 // Launch configuration `id` of kind 5 (hipErrorInvalidValue for another id).
 hipError_t launch_gemm_nt(int id, const GemmArgs &a, dim3 grid, hipStream_t stream);
 
-// Longest row a small-M GEMM's LayerNorm prologue takes (each lane holds up
-// to kLnMaxK / 256 float4 of each of its wave's rows).
+// Longest row a small-M GEMM's LayerNorm prologue takes.
 constexpr int kLnMaxK = 1024;
 
 // Configurations of the small-M kernel (kind 6, kh_gemm_small.hip): id, tile

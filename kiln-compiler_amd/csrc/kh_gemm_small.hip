@@ -28,15 +28,17 @@
 //     interpreter; the direct operands are loaded before the partial sums so
 //     their latency overlaps the reduction.
 // LayerNorm prologue (LN, fp32; a LayerNorm whose only consumer is this
-// product's A operand): A is the LayerNorm's input x, gamma is folded into
-// B and beta . B into a per-column vector by the lowering, so the product
-// needs only each row's (x - mean) * rstd. Each wave loads its rows of the
-// tile once (after the ring's first copies are in flight), takes the mean,
-// then the variance of the centred values (the LayerNorm row kernel's
-// arithmetic), and leaves (rstd, -mean * rstd) per row in LDS; every A
-// fragment value then enters the MFMAs as x * rstd - mean * rstd (one FMA),
-// and the column vector is added to the summed tile before the epilogue.
-// The LayerNorm's launch and its output's round trip through memory go away.
+// product's A operand): A is the LayerNorm's input x; the lowering folds
+// gamma into B (B' = gamma * B) and provides g = column sums of B' and
+// c = beta . B. With x0 a row's first value,
+//     LayerNorm(x) . B = rstd * ((x - x0) . B' - (mean - x0) * g) + c,
+// so A fragments enter the MFMAs as x - x0 (the shift keeps the correction
+// term small whatever the row's mean) and the row statistics come from the
+// same fragments as the K loop streams them: each lane merges the mean and
+// the sum of squared deviations of its 8-value chunks (Chan's pairwise
+// update), lanes and then waves merge theirs in a fixed order, and the
+// epilogue applies the formula before the tape. The LayerNorm's launch and
+// its output's round trip through memory go away; A is read once.
 // K must be a positive multiple of 32 and the operands' spans below 2^29
 // elements (the host checks both).
 #include <algorithm>
@@ -75,7 +77,7 @@ __global__ __launch_bounds__(64 * WK) void gemm_small_kernel(const GemmArgs a) {
   static_assert(WK * NS * STAGE * 4 <= 160 * 1024, "LDS");
 
   __shared__ float4 rings[WK * NS * STAGE / 4];
-  __shared__ float2 ln_stats[LN ? BM : 1];   // LN: (rstd, -mean * rstd) per tile row
+  __shared__ float4 ln_part[LN ? WK : 1][LN ? BM : 1];   // LN: (count, mean, M2) per wave and tile row
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -167,44 +169,26 @@ __global__ __launch_bounds__(64 * WK) void gemm_small_kernel(const GemmArgs a) {
   auto part = [](const float4 &v, int j) { return j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w; };
 
   for (int p = 0; p < NS - 1 && p < n_steps; ++p) issue(p);
-  float ln_sc[FM], ln_sh[FM];
+  // LN: the row's first value (the shift) and this lane's running (count,
+  // mean, M2) of x - x0 per row of the tile
+  float ln_x0[FM], ln_n[FM], ln_mean[FM], ln_m2[FM];
   if constexpr (LN) {
-    // every load of the wave's rows first (clamped, unconditional: values
-    // past K are dropped at use), then the two sums per row
-    constexpr int R = BM / WK, J = kLnMaxK / 256;
-    const int k4s = a.K / 4;
-    float4 xv[R][J];
-#pragma unroll
-    for (int rr = 0; rr < R; ++rr) {
-      const float4 *x = reinterpret_cast<const float4 *>(Ab + (int64_t)min(m0 + wave_u + rr * WK, a.M - 1) * a.sa_m);
-#pragma unroll
-      for (int j = 0; j < J; ++j) xv[rr][j] = x[min(lane + 64 * j, k4s - 1)];
-    }
-#pragma unroll
-    for (int rr = 0; rr < R; ++rr) {
-      float s1 = 0.0f;
-#pragma unroll
-      for (int j = 0; j < J; ++j)
-        if (lane + 64 * j < k4s) s1 += (xv[rr][j].x + xv[rr][j].y) + (xv[rr][j].z + xv[rr][j].w);
-      const float mean = wave_sum(s1) * a.pro_c1;
-      float s2 = 0.0f;
-#pragma unroll
-      for (int j = 0; j < J; ++j)
-        if (lane + 64 * j < k4s) {
-          const float dx = xv[rr][j].x - mean, dy = xv[rr][j].y - mean;
-          const float dz = xv[rr][j].z - mean, dw = xv[rr][j].w - mean;
-          s2 = fmaf(dx, dx, s2), s2 = fmaf(dy, dy, s2), s2 = fmaf(dz, dz, s2), s2 = fmaf(dw, dw, s2);
-        }
-      const float rstd = rsqrtf(wave_sum(s2) * a.pro_c2 + a.pro_eps);
-      if (lane == 0) ln_stats[wave_u + rr * WK] = make_float2(rstd, -mean * rstd);
-    }
-    __syncthreads();
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm) {
-      const float2 st = ln_stats[fm * MT + li];
-      ln_sc[fm] = st.x, ln_sh[fm] = st.y;
+      ln_x0[fm] = Ab[(int64_t)min(m0 + fm * MT + li, a.M - 1) * a.sa_m];
+      ln_n[fm] = 0.0f, ln_mean[fm] = 0.0f, ln_m2[fm] = 0.0f;
     }
   }
+  // Chan's update: (n, mean, m2) += the statistics (nb, mb, m2b) of more values
+  auto merge = [](float &n, float &mean, float &m2, float nb, float mb, float m2b) {
+    const float nt = n + nb;
+    if (nt > 0.0f) {
+      const float d = mb - mean;
+      mean = fmaf(d, nb / nt, mean);
+      m2 = m2 + m2b + d * d * (n * nb / nt);
+      n = nt;
+    }
+  };
   for (int s = 0; s < n_steps; ++s) {
     wait_landed(min(NS - 2, n_steps - 1 - s));
     // the wave's own LDS: its copies landed (vmcnt), nothing else writes it
@@ -225,13 +209,18 @@ __global__ __launch_bounds__(64 * WK) void gemm_small_kernel(const GemmArgs a) {
     if (s + NS - 1 < n_steps) issue(s + NS - 1);
     if constexpr (LN) {
 #pragma unroll
-      for (int fm = 0; fm < FM; ++fm)
+      for (int fm = 0; fm < FM; ++fm) {
+        float v[8];
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          float4 &v = xa[fm][h];
-          v.x = fmaf(v.x, ln_sc[fm], ln_sh[fm]), v.y = fmaf(v.y, ln_sc[fm], ln_sh[fm]);
-          v.z = fmaf(v.z, ln_sc[fm], ln_sh[fm]), v.w = fmaf(v.w, ln_sc[fm], ln_sh[fm]);
-        }
+        for (int e = 0; e < 8; ++e) v[e] = part(xa[fm][e / 4], e % 4) - ln_x0[fm];
+        xa[fm][0] = make_float4(v[0], v[1], v[2], v[3]);
+        xa[fm][1] = make_float4(v[4], v[5], v[6], v[7]);
+        const float cm = (((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]))) * 0.125f;
+        float cm2 = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) cm2 = fmaf(v[e] - cm, v[e] - cm, cm2);
+        merge(ln_n[fm], ln_mean[fm], ln_m2[fm], 8.0f, cm, cm2);
+      }
     }
     if constexpr (BF) {
       bf16x8 ah[FM], al[FM];
@@ -309,6 +298,20 @@ __global__ __launch_bounds__(64 * WK) void gemm_small_kernel(const GemmArgs a) {
     for (int fn = 0; fn < FN; ++fn)
 #pragma unroll
       for (int i = 0; i < 4; ++i) mine[(fm * MT + 4 * g + i) * CS + fn * MT + li] = acc[fm][fn][i];
+  if constexpr (LN) {
+    // the row's statistics over this wave's K range: lanes li, li + 16,
+    // li + 32, li + 48 merged (lane group 0's result kept)
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) {
+#pragma unroll
+      for (int off = 16; off <= 32; off <<= 1) {
+        const float nb = __shfl_xor(ln_n[fm], off, 64), mb = __shfl_xor(ln_mean[fm], off, 64);
+        const float m2b = __shfl_xor(ln_m2[fm], off, 64);
+        merge(ln_n[fm], ln_mean[fm], ln_m2[fm], nb, mb, m2b);
+      }
+      if (g == 0) ln_part[wave_u][fm * MT + li] = make_float4(ln_n[fm], ln_mean[fm], ln_m2[fm], 0.0f);
+    }
+  }
   __syncthreads();
   const float *parts = reinterpret_cast<const float *>(rings);
   for (int q = q0; q < GROUPS; q += 64 * WK) {
@@ -324,6 +327,18 @@ __global__ __launch_bounds__(64 * WK) void gemm_small_kernel(const GemmArgs a) {
     }
     const int valid = min(4, a.N - n);
     if constexpr (LN) {
+      // the row's statistics over all of K (waves merged in order), then
+      // rstd * (sum - (mean - x0) * g) + c
+      float4 st = ln_part[0][m - m0];
+#pragma unroll
+      for (int w = 1; w < WK; ++w) {
+        const float4 o = ln_part[w][m - m0];
+        merge(st.x, st.y, st.z, o.x, o.y, o.z);
+      }
+      const float rstd = rsqrtf(st.z * a.pro_c2 + a.pro_eps), mu = st.y;
+      const float4 gs = load4(a.pro_g, m, n, valid);
+      sum.x = rstd * fmaf(-mu, gs.x, sum.x), sum.y = rstd * fmaf(-mu, gs.y, sum.y);
+      sum.z = rstd * fmaf(-mu, gs.z, sum.z), sum.w = rstd * fmaf(-mu, gs.w, sum.w);
       if (a.pro_b >= 0) {   // the folded beta . B
         const float4 c = load4(a.pro_b, m, n, valid);
         sum.x += c.x, sum.y += c.y, sum.z += c.z, sum.w += c.w;

@@ -686,10 +686,14 @@ class _Lowerer:
                     if p is not None:
                         d.cfg[w] = 2 + len(refs) + len(pro_refs)
                         pro_refs.append(ref3(p, (batch, m, kk)))
-            elif beta is not None:
-                # gamma rides in the weight copy; beta . W is a column constant
-                d.cfg[6] = 2 + len(refs) + len(pro_refs)
-                pro_refs.append(self.ln_column(b, b_ref, batch, kk, n, beta))
+            else:
+                # gamma rides in the weight copy; that copy's column sums and
+                # beta . W are column constants
+                d.cfg[5] = 2 + len(refs) + len(pro_refs)
+                pro_refs.append(self.ln_column(b, b_ref, batch, kk, n, gamma, "lng"))
+                if beta is not None:
+                    d.cfg[6] = 2 + len(refs) + len(pro_refs)
+                    pro_refs.append(self.ln_column(b, b_ref, batch, kk, n, beta, "lnc"))
             for i, f in enumerate(fparams):
                 d.fparams[i] = f
         self._check_refs(refs + pro_refs + [None, None])
@@ -904,14 +908,16 @@ class _Lowerer:
         lay = self.layouts[v]
         return [lay.base[1], int(lay.offset), int(lay.strides[-1])]
 
-    def ln_column(self, b, ref, batch, kk, n, beta):
-        """Ref of the per-column constant beta . W over (b, m, n) (strides 0
-        over M) of a small-M GEMM's LayerNorm prologue, `ref` being W's fp32
-        ref over (b, k, n); registered as a derived constant."""
+    def ln_column(self, b, ref, batch, kk, n, vec, kind):
+        """Ref of a per-column constant over (b, m, n) (strides 0 over M) of a
+        small-M GEMM's LayerNorm prologue, `ref` being W's fp32 ref over (b,
+        k, n): kind "lnc" = beta . W (vec = beta), "lng" = the column sums of
+        the gamma-scaled weight copy (vec = gamma, or None: of W); registered
+        as a derived constant."""
         src = self.layouts[b].base[1]
         strides = (int(ref.strides[0]), int(ref.strides[1]), int(ref.strides[2]))
-        spec = self._vector_spec(beta)
-        name = (f"{src}@lnc:{int(ref.offset)}:{strides[0]},{strides[1]},{strides[2]}:{batch}x{kk}x{n}:"
+        spec = self._vector_spec(vec) if vec is not None else ["", 0, 0]
+        name = (f"{src}@{kind}:{int(ref.offset)}:{strides[0]},{strides[1]},{strides[2]}:{batch}x{kk}x{n}:"
                 f"{spec[0]}:{spec[1]}:{spec[2]}")
         self.program.derived[name] = (src, int(ref.offset), strides, batch, kk, n, spec)
         r = kl.Ref()

@@ -121,15 +121,20 @@ def host_constant(program, constants: dict, name: str) -> np.ndarray:
     src, offset, strides, batch, k, n = recipe[:6]
     if "@nk:" in name:
         return nk_copy(constants[src], offset, strides, batch, k, n)
-    if "@nkg:" in name or "@lnc:" in name:
+    if "@nkg:" in name or "@lnc:" in name or "@lng:" in name:
         # a LayerNorm folded into the small-M GEMM that follows it: the
         # [batch][N][K] weight copy with every row scaled by gamma (one fp32
-        # product per element), or beta . W per column (float64 sums)
+        # product per element), that copy's column sums, or beta . W per
+        # column (sums in float64)
         vname, voff, vstride = recipe[6]
-        vec = np.ascontiguousarray(constants[vname], np.float32).reshape(-1)[voff + np.arange(k) * vstride]
         w = nk_copy(constants[src], offset, strides, batch, k, n)
+        vec = (np.ascontiguousarray(constants[vname], np.float32).reshape(-1)[voff + np.arange(k) * vstride]
+               if vname else None)
+        scaled = w if vec is None else w * vec[None, None, :]
         if "@nkg:" in name:
-            return np.ascontiguousarray(w * vec[None, None, :], dtype=np.float32)
+            return np.ascontiguousarray(scaled, dtype=np.float32)
+        if "@lng:" in name:
+            return np.ascontiguousarray(scaled.astype(np.float64).sum(-1).astype(np.float32))
         return np.ascontiguousarray((w.astype(np.float64) @ vec.astype(np.float64)).astype(np.float32))
     make = bf16.weight_copy_x3 if "@bf16x3:" in name else bf16.weight_copy
     return make(constants[src], offset, strides, batch, k, n).view(np.int16)

@@ -380,14 +380,17 @@ def test_gemv_variants_and_ragged_sizes(variant):
                                   and autotune.TILES[t][0] <= 4 * autotune.TILES[t][5]])
 def test_layernorm_prologue_on_every_small_m_configuration(tile):
     # LayerNorm -> Linear (+ residual) on a small-M configuration: the GEMM
-    # normalises its A rows itself (gamma folded into the weight copy, beta . W
-    # into a column constant) and the LayerNorm has no launch of its own;
-    # ragged M / N, K from one step to the longest prologue row (1024), with
-    # and without affine parameters, inputs with a large mean; repeated
-    # launches agree bit for bit
+    # takes the row statistics from the A fragments it streams and applies the
+    # LayerNorm algebraically (gamma folded into the weight copy, its column
+    # sums and beta . W as column constants); the LayerNorm has no launch of
+    # its own. Ragged M / N, K from one step to the longest prologue row
+    # (1024), with and without affine parameters, rows with mean 3 and with
+    # mean 100 (std 1: the shift by the row's first value keeps the result
+    # exact to fp32 rounding); repeated launches agree bit for bit
     cfg = lambda *_: {"tile": tile, "splitk": 1}
-    for m, n, k, affine in ((77, 133, 32, True), (300, 452, 256, False), (128, 200, 768, True),
-                            (40, 64, 1024, True)):
+    for m, n, k, affine, loc, sd in ((77, 133, 32, True, 3.0, 2.0), (300, 452, 256, False, 3.0, 2.0),
+                                     (128, 200, 768, True, 3.0, 2.0), (40, 64, 1024, True, 3.0, 2.0),
+                                     (64, 96, 768, True, 100.0, 1.0)):
         torch.manual_seed(m + k)
         ln = torch.nn.LayerNorm(k, elementwise_affine=affine)
         if affine:
@@ -397,7 +400,7 @@ def test_layernorm_prologue_on_every_small_m_configuration(tile):
         lin = gpt2_init_(torch.nn.Linear(k, n), seed=k).eval()
         model = torch.nn.Sequential(ln, lin).eval()
         fn = lambda t, res: model(t) + res
-        x, r = 3.0 + 2.0 * torch.randn(m, k), torch.randn(m, n)
+        x, r = loc + sd * torch.randn(m, k), torch.randn(m, n)
         c = kiln.compile(fn, (x, r), device="cuda", cuda_graphs=False, gpu_matmul_config=cfg)
         summaries = [l.summary for l in c._exe.program.launches]
         assert len(summaries) == 1 and f"tile {tile} " in summaries[0] and "prologue: layernorm" in summaries[0]

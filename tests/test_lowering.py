@@ -251,28 +251,30 @@ def test_layernorm_is_not_fused_when_its_output_has_other_users():
 @pytest.mark.parametrize("affine", [True, False])
 def test_layernorm_feeding_a_small_m_gemm_becomes_its_prologue(affine):
     # a few rows: the product runs on an fp32 small-M configuration; A is the
-    # LayerNorm's input, gamma is folded into the [N][K] weight copy and
-    # beta . W into a per-column constant (ref cfg[6], strides 0 over M)
+    # LayerNorm's input, gamma is folded into the [N][K] weight copy, whose
+    # column sums (ref cfg[5]) and beta . W (ref cfg[6]) are per-column
+    # constants (strides 0 over M)
     _, prog = lowered(_ln_linear(affine), torch.randn(40, 64))
     assert [kl.FAMILY_NAMES[l.family] for l in prog.launches] == ["gemm"]
     launch = prog.launches[0]
     d = launch.desc
-    assert d.cfg[1] in autotune.SMALL_M and d.cfg[4] == 1 and d.cfg[5] == -1
+    assert d.cfg[1] in autotune.SMALL_M and d.cfg[4] == 1 and 2 <= d.cfg[5] < d.n_refs
     assert "prologue: layernorm" in launch.summary and d.refs[0].base == kl.BASE_INPUT
     assert list(d.fparams)[:3] == pytest.approx([1 / 64, 1 / 64, 1e-5])
-    names = [prog.consts[d.refs[j].index] for j in (1, d.cfg[6]) if j >= 0]
+    assert list(d.refs[d.cfg[5]].strides[:3]) == [0, 0, 1]
+    names = [prog.consts[d.refs[j].index] for j in (1, d.cfg[5], d.cfg[6]) if j >= 0]
+    assert "@lng:" in names[1]
     if affine:
         assert 2 <= d.cfg[6] < d.n_refs and list(d.refs[d.cfg[6]].strides[:3]) == [0, 0, 1]
-        assert "@nkg:" in names[0] and "@lnc:" in names[1]
+        assert "@nkg:" in names[0] and "@lnc:" in names[2]
     else:
         assert d.cfg[6] == -1 and "@nk:" in names[0]
     kl.Plan([l.desc for l in prog.launches])
 
 
 def test_folded_layernorm_constants():
-    # the scaled weight copy is W^T row n times gamma; the column constant is
-    # beta . W (float64 sums); a LayerNorm + Linear run through the host
-    # interpreter matches the float64 reference
+    # the scaled weight copy is W^T row n times gamma; the column constants
+    # are beta . W and the scaled copy's row sums (float64 sums)
     from kiln.hip.runtime import host_constant
 
     torch.manual_seed(3)
@@ -288,6 +290,8 @@ def test_folded_layernorm_constants():
     np.testing.assert_array_equal(scaled[0], (w.astype(np.float32) * gam[None, :]).astype(np.float32))
     col = host_constant(prog, g.constants, prog.consts[d.refs[d.cfg[6]].index])
     np.testing.assert_allclose(col.reshape(-1), w @ bet.astype(np.float64), rtol=1e-6, atol=1e-7)
+    sums = host_constant(prog, g.constants, prog.consts[d.refs[d.cfg[5]].index])
+    np.testing.assert_allclose(sums.reshape(-1), scaled[0].astype(np.float64).sum(-1), rtol=1e-6, atol=1e-7)
 
 
 def test_layernorm_stays_a_row_kernel_before_other_gemms():
