@@ -208,6 +208,9 @@ __global__ __launch_bounds__(64 * WK) void gemm_small_kernel(const GemmArgs a) {
     __builtin_amdgcn_s_waitcnt((3 << 14) | (7 << 4) | 15);  // lgkmcnt(0); vmcnt, expcnt unconstrained
     if (s + NS - 1 < n_steps) issue(s + NS - 1);
     if constexpr (LN) {
+      // chunk s + 1 of 8 values joins s chunks: Chan's update with weight
+      // 8 / (8 (s + 1)) (one reciprocal per step for every row)
+      const float w1 = __builtin_amdgcn_rcpf((float)(s + 1)), w2 = 8.0f * (float)s * w1;
 #pragma unroll
       for (int fm = 0; fm < FM; ++fm) {
         float v[8];
@@ -219,7 +222,9 @@ __global__ __launch_bounds__(64 * WK) void gemm_small_kernel(const GemmArgs a) {
         float cm2 = 0.0f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) cm2 = fmaf(v[e] - cm, v[e] - cm, cm2);
-        merge(ln_n[fm], ln_mean[fm], ln_m2[fm], 8.0f, cm, cm2);
+        const float d = cm - ln_mean[fm];
+        ln_mean[fm] = fmaf(d, w1, ln_mean[fm]);
+        ln_m2[fm] = fmaf(d * d, w2, ln_m2[fm] + cm2);
       }
     }
     if constexpr (BF) {
@@ -303,6 +308,7 @@ __global__ __launch_bounds__(64 * WK) void gemm_small_kernel(const GemmArgs a) {
     // li + 32, li + 48 merged (lane group 0's result kept)
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm) {
+      ln_n[fm] = 8.0f * (float)n_steps;
 #pragma unroll
       for (int off = 16; off <= 32; off <<= 1) {
         const float nb = __shfl_xor(ln_n[fm], off, 64), mb = __shfl_xor(ln_mean[fm], off, 64);
