@@ -906,7 +906,7 @@ class _Lowerer:
         """(constant name, element offset, element stride) of a constant
         vector's values, for a derived-constant recipe."""
         lay = self.layouts[v]
-        return [lay.base[1], int(lay.offset), int(lay.strides[-1])]
+        return (lay.base[1], int(lay.offset), int(lay.strides[-1]))
 
     def ln_column(self, b, ref, batch, kk, n, vec, kind):
         """Ref of a per-column constant over (b, m, n) (strides 0 over M) of a
@@ -916,7 +916,7 @@ class _Lowerer:
         as a derived constant."""
         src = self.layouts[b].base[1]
         strides = (int(ref.strides[0]), int(ref.strides[1]), int(ref.strides[2]))
-        spec = self._vector_spec(vec) if vec is not None else ["", 0, 0]
+        spec = self._vector_spec(vec) if vec is not None else ("", 0, 0)
         name = (f"{src}@{kind}:{int(ref.offset)}:{strides[0]},{strides[1]},{strides[2]}:{batch}x{kk}x{n}:"
                 f"{spec[0]}:{spec[1]}:{spec[2]}")
         self.program.derived[name] = (src, int(ref.offset), strides, batch, kk, n, spec)

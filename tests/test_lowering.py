@@ -272,6 +272,18 @@ def test_layernorm_feeding_a_small_m_gemm_becomes_its_prologue(affine):
     kl.Plan([l.desc for l in prog.launches])
 
 
+def test_folded_layernorm_plan_round_trips_through_the_store(tmp_path, monkeypatch):
+    from kiln.hip import plans
+
+    monkeypatch.setenv("KILN_CACHE_DIR", str(tmp_path))
+    g, prog = lowered(_ln_linear(), torch.randn(40, 64))
+    key = plans.plan_key(str(g), "fp32", "default", kl.device_info())
+    plans.save(key, prog, [])
+    back, _ = plans.load(key)
+    assert back.derived == prog.derived and any("@lng:" in n for n in back.derived)
+    assert bytes(back.launches[0].desc) == bytes(prog.launches[0].desc)
+
+
 def test_folded_layernorm_constants():
     # the scaled weight copy is W^T row n times gamma; the column constants
     # are beta . W and the scaled copy's row sums (float64 sums)
