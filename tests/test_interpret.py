@@ -84,6 +84,10 @@ def test_gpt2_block_against_the_c_oracle(T):
     x = torch.randn(T, 128)
     c = kiln.compile(model, (x,), device="cuda")
     assert c.report.lowering["families"].get("attention") == 1
+    # both LayerNorms run inside the small-M GEMMs that read them (folded
+    # gamma / beta constants, row statistics in the product)
+    src = open(c.report.lowering["source"]).read()
+    assert src.count("prologue: layernorm") == 2 and "layernorm rows" not in src
     params = {k: v.numpy() for k, v in model.state_dict().items()}
     np.testing.assert_allclose(c(x).numpy(), oracle.block(x.numpy(), params, 4), rtol=RTOL, atol=ATOL)
 
