@@ -413,6 +413,40 @@ def test_layernorm_prologue_on_every_small_m_configuration(tile):
         assert torch.equal(c(x, r), out)
 
 
+@pytest.mark.parametrize("tile", [t for t in sorted(autotune.SMALL_M) if autotune.PRECISION[t] == "fp32"
+                                  and autotune.TILES[t][0] <= 4 * autotune.TILES[t][5]])
+def test_layernorm_prologue_non_finite_rows(tile):
+    # A row holding NaN, +inf, -inf or both infinities normalises to NaN in
+    # every element (the oracle's LayerNorm: its mean or variance is not
+    # finite), so its product row is NaN in every column, whichever element
+    # is not finite - also the row's first value, the shift the folded
+    # LayerNorm subtracts. The row statistics are merged per row across lanes
+    # and waves, so the other rows of the same tiles stay exact
+    cfg = lambda *_: {"tile": tile, "splitk": 1}
+    m, n, k = 70, 90, 256
+    torch.manual_seed(11)
+    ln = torch.nn.LayerNorm(k)
+    with torch.no_grad():
+        ln.weight.copy_(1.0 + 0.1 * torch.randn(k))
+        ln.bias.copy_(0.1 * torch.randn(k))
+    lin = gpt2_init_(torch.nn.Linear(k, n), seed=5).eval()
+    model = torch.nn.Sequential(ln, lin).eval()
+    x = 3.0 + 2.0 * torch.randn(m, k)
+    bad = {5: [(17, math.nan)], 20: [(0, math.inf)], 33: [(200, -math.inf)], 40: [(3, math.inf), (90, -math.inf)],
+           47: [(0, math.nan)], 69: [(255, math.nan)]}
+    for row, cells in bad.items():
+        for col, v in cells:
+            x[row, col] = v
+    c = kiln.compile(model, (x,), device="cuda", cuda_graphs=False, gpu_matmul_config=cfg)
+    summaries = [l.summary for l in c._exe.program.launches]
+    assert len(summaries) == 1 and f"tile {tile} " in summaries[0] and "prologue: layernorm" in summaries[0]
+    ref = oracle.linear(oracle.layernorm(x.numpy(), ln.weight.detach().numpy(), ln.bias.detach().numpy()),
+                        lin.weight.detach().numpy().T, lin.bias.detach().numpy())
+    assert np.isnan(ref[sorted(bad)]).all() and np.isfinite(np.delete(ref, sorted(bad), axis=0)).all()
+    out = c(x).cpu().numpy()
+    np.testing.assert_allclose(out, ref, rtol=RTOL, atol=ATOL, equal_nan=True)
+
+
 class _BatchedConstant(torch.nn.Module):
     def __init__(self, batch, k, n):
         super().__init__()
