@@ -643,3 +643,26 @@ def test_layernorm_prologue_of_a_gemv(k, n, affine, bias):
     x = 3.0 + 2.0 * torch.randn(1, k)
     c = check(model, x)
     assert c.report.lowering["launches"] == 1 and c.report.lowering["families"] == {"gemv": 1}
+
+
+@pytest.mark.parametrize("cells", [[(5, math.nan)], [(0, math.inf)], [(700, -math.inf)], [(3, math.inf), (9, -math.inf)]])
+def test_layernorm_prologue_of_a_gemv_non_finite_row(cells):
+    # a row holding NaN or infinities normalises to NaN in every element (the
+    # oracle's LayerNorm), so every output of the GEMV is NaN
+    torch.manual_seed(1)
+    k, n = 768, 300
+    ln = torch.nn.LayerNorm(k)
+    with torch.no_grad():
+        ln.weight.copy_(1 + 0.1 * torch.randn(k))
+        ln.bias.copy_(0.1 * torch.randn(k))
+    lin = torch.nn.Linear(k, n)
+    model = torch.nn.Sequential(ln, lin).eval()
+    x = 3.0 + 2.0 * torch.randn(1, k)
+    for col, v in cells:
+        x[0, col] = v
+    c = kiln.compile(model, (x,), device="cuda")
+    assert c.report.lowering["launches"] == 1 and c.report.lowering["families"] == {"gemv": 1}
+    ref = oracle.linear(oracle.layernorm(x.numpy(), ln.weight.detach().numpy(), ln.bias.detach().numpy()),
+                        lin.weight.detach().numpy().T, lin.bias.detach().numpy())
+    assert np.isnan(ref).all()
+    assert torch.isnan(c(x)).all()
