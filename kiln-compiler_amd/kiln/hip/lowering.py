@@ -33,7 +33,7 @@ from kiln.hip import autotune, bf16
 from kiln.hip import lib as kl
 from kiln.ir import ops
 from kiln.ir.core import Graph, Kernel
-from kiln.passes.buffers import compute_layouts, kernel_inputs, kernel_outputs
+from kiln.passes.buffers import Layout, compute_layouts, kernel_inputs, kernel_outputs
 from kiln.passes.fusion import is_row_reduction
 
 ROW_SINGLE_CHUNK = 1024   # rows up to this length are held in registers (workgroup x 4)
@@ -186,7 +186,7 @@ class _Lowerer:
         self.program = Program(precision=precision)
         self.const_slot = {}
         self._cfg = {}
-        self.prologue = {}   # matmul kernel -> (x, gamma, beta, fparams) of a fused LayerNorm
+        self.prologue = {}   # matmul kernel -> (x, gamma, beta, fparams, x as [rows, K]) of a fused LayerNorm
         self.attn_prologue = {}  # GEMV kernel -> (attention match, strides, mask mode, (heads, tk, dh))
 
     # operands ---------------------------------------------------------------------
@@ -625,12 +625,13 @@ class _Lowerer:
         outs = kernel_outputs(self.g, k, self.users)
         space3 = (batch, m, n)
 
-        def ref3(v, dims, register=True):
+        def ref3(v, dims, register=True, lay=None):
             """Strides of v over a 3-d space named by `dims` (v's own dims
-            right-aligned). register=False describes a constant that is only
+            right-aligned; `lay`: v's storage seen with other dims, the same
+            base and offset). register=False describes a constant that is only
             read through a derived copy, so it gets no slot (and is not
             uploaded)."""
-            lay = self.layouts[v]
+            lay = lay or self.layouts[v]
             r = kl.Ref()
             r.base, r.index = self.slot_of(lay.base) if register else (kl.BASE_CONST, -1)
             r.offset = self.element_offset(v)
@@ -649,7 +650,7 @@ class _Lowerer:
         if gemv and self.gemv_chains:
             d.variant = kl.GEMV_CHAIN   # the library may run it in a persistent chain with its GEMV neighbours
         d.gemm[0], d.gemm[1], d.gemm[2], d.gemm[3] = batch, m, n, kk
-        d.refs[0] = ref3(a_src, (batch, m, kk))
+        d.refs[0] = ref3(a_src, (batch, m, kk), lay=pro[4] if pro else None)
         k_major = not gemv and int(cfg.get("tile", -1)) in autotune.NK_B
         nk = (gemv and self.layouts[b].base[0] == "const" and kk % 4 == 0) or k_major
         derived_b = prec in ("bf16", "bf16x3") or nk
@@ -679,7 +680,7 @@ class _Lowerer:
         if gemv and k in self.attn_prologue:
             pro_refs, *attn_work = self.attn_prologue_refs(d, k, 2 + len(refs))
         if pro:
-            x, gamma, beta, fparams = pro
+            x, gamma, beta, fparams, _ = pro
             d.cfg[4], d.cfg[5], d.cfg[6] = 1, -1, -1
             if gemv:
                 for w, p in ((5, gamma), (6, beta)):
@@ -823,7 +824,10 @@ class _Lowerer:
         an fp32 small-M configuration (short prefill: the same pairs at a few
         hundred tokens): the GEMV / GEMM runs the LayerNorm as its prologue and
         the row kernel is not launched (for the GEMM, gamma is folded into the
-        weight copy and beta . W into a per-column constant). The LayerNorm's
+        weight copy and beta . W into a per-column constant). A reshape that
+        merges the LayerNorm's leading dims into the product's rows may sit
+        between them ([B, T, K] -> [B*T, K]); x must then merge the same way
+        (one row stride). The LayerNorm's
         input must stay intact until the product, so no buffer that a kernel
         from the LayerNorm up to the product writes may overlap it."""
         kernels = self.g.kernels
@@ -848,19 +852,28 @@ class _Lowerer:
                 continue
             y, x = outs[0], ordered[0]
             users = self.users.get(y, [])
-            if y in results or len(users) != 1 or users[0].op != "matmul":
+            if y in results or len(users) != 1 or tuple(x.shape) != tuple(y.shape):
+                continue
+            a_val = y
+            if users[0].op == "reshape" and y.type.rank > 2:
+                a_val = users[0].out
+                users = self.users.get(a_val, [])
+                if a_val in results or len(users) != 1:
+                    continue
+            if users[0].op != "matmul" or a_val.type.rank != 2:
                 continue
             mm = users[0]
             km = owner.get(mm)
-            if km is None or km.kind != "matmul" or mm.inputs[0] is not y or mm.inputs[1] is y:
-                continue
-            if y.type.rank != 2 or tuple(x.shape) != tuple(y.shape):
+            if km is None or km.kind != "matmul" or mm.inputs[0] is not a_val or mm.inputs[1] is a_val:
                 continue
             if self._arena_range(y) is None and y not in self.layouts:
                 continue
+            x_lay = self._rows_layout(x, a_val.shape)
+            if x_lay is None:
+                continue
             gamma = ordered[1] if has_g else None
             beta = ordered[1 + has_g] if has_b else None
-            if not (self.is_gemv(km) if y.shape[0] == 1 else self._ln_gemm_ok(km, x, gamma, beta)):
+            if not (self.is_gemv(km) if a_val.shape[0] == 1 else self._ln_gemm_ok(km, x_lay, gamma, beta)):
                 continue
             j = kernels.index(km)
             xr = self._arena_range(x)
@@ -873,16 +886,36 @@ class _Lowerer:
                             clash = True
                 if clash:
                     continue
-            self.prologue[km] = (x, gamma, beta, list(fparams))
+            self.prologue[km] = (x, gamma, beta, list(fparams), x_lay)
             skip.add(k)
         return skip
 
-    def _ln_gemm_ok(self, km, x, gamma, beta) -> bool:
+    def _rows_layout(self, x, shape):
+        """x's storage seen as the [rows, K] operand `shape` of a product: x
+        itself when it is 2-d, else its leading dims merged into one row
+        stride; None when x has no storage or its leading dims do not merge."""
+        lay = self.layouts.get(x)
+        if lay is None or len(shape) != 2 or tuple(shape) != (math.prod(x.shape[:-1]), x.shape[-1]):
+            return None
+        if len(lay.shape) == 2:
+            return lay
+        row, inner = None, None
+        for ext, st in reversed(list(zip(lay.shape[:-1], lay.strides[:-1]))):
+            if ext == 1:
+                continue
+            if inner is not None and st != inner[0] * inner[1]:
+                return None
+            row = st if row is None else row
+            inner = (ext, st)
+        return Layout(lay.base, lay.offset, tuple(shape), (lay.shape[-1] if row is None else row, lay.strides[-1]))
+
+    def _ln_gemm_ok(self, km, lay, gamma, beta) -> bool:
         """Whether matmul kernel km can run a LayerNorm of x (gamma, beta:
         its parameters or None) as its prologue: an fp32 small-M configuration
         (B the [N][K] copy of a constant, A read with unit K stride) holding at
         most 4 rows per wave, K <= 1024, x laid out like the A operand it
-        replaces, and gamma / beta constants (folded into build-time copies)."""
+        replaces (`lay`: x's storage as [rows, K]), and gamma / beta constants
+        (folded into build-time copies)."""
         cfg, prec = self.matmul_choice(km)
         tile = int(cfg.get("tile", -1))
         if prec != "fp32" or tile not in autotune.SMALL_M or autotune.PRECISION.get(tile) != "fp32":
@@ -898,8 +931,7 @@ class _Lowerer:
             if p is not None and (p not in self.layouts or self.layouts[p].base[0] != "const"
                                   or math.prod(p.shape) != kk):
                 return False
-        lay = self.layouts.get(x)
-        return (lay is not None and lay.strides[-1] == 1 and lay.offset % 4 == 0
+        return (lay.strides[-1] == 1 and lay.offset % 4 == 0
                 and all(st % 4 == 0 for st, ext in zip(lay.strides[:-1], lay.shape[:-1]) if ext > 1))
 
     def _vector_spec(self, v):

@@ -447,6 +447,31 @@ def test_layernorm_prologue_non_finite_rows(tile):
     np.testing.assert_allclose(out, ref, rtol=RTOL, atol=ATOL, equal_nan=True)
 
 
+@pytest.mark.parametrize("tile", [t for t in sorted(autotune.SMALL_M) if autotune.PRECISION[t] == "fp32"
+                                  and autotune.TILES[t][0] <= 4 * autotune.TILES[t][5]])
+def test_layernorm_prologue_through_a_row_reshape(tile):
+    # LayerNorm over [B, T, K] feeding a Linear (A = its output reshaped to
+    # [B*T, K]): the product reads the LayerNorm's input with the merged row
+    # stride and runs the LayerNorm as its prologue
+    cfg = lambda *_: {"tile": tile, "splitk": 1}
+    torch.manual_seed(tile)
+    ln = torch.nn.LayerNorm(256)
+    with torch.no_grad():
+        ln.weight.copy_(1.0 + 0.1 * torch.randn(256))
+        ln.bias.copy_(0.1 * torch.randn(256))
+    lin = gpt2_init_(torch.nn.Linear(256, 120), seed=2).eval()
+    model = torch.nn.Sequential(ln, lin).eval()
+    x = 3.0 + 2.0 * torch.randn(3, 45, 256)
+    c = kiln.compile(model, (x,), device="cuda", cuda_graphs=False, gpu_matmul_config=cfg)
+    summaries = [l.summary for l in c._exe.program.launches]
+    assert f"tile {tile} " in summaries[0] and "prologue: layernorm" in summaries[0]
+    assert not any("layernorm rows" in s for s in summaries)
+    ref = oracle.linear(oracle.layernorm(x.reshape(-1, 256).numpy(), ln.weight.detach().numpy(),
+                                         ln.bias.detach().numpy()),
+                        lin.weight.detach().numpy().T, lin.bias.detach().numpy()).reshape(3, 45, 120)
+    np.testing.assert_allclose(c(x).cpu().numpy(), ref, rtol=RTOL, atol=ATOL)
+
+
 class _BatchedConstant(torch.nn.Module):
     def __init__(self, batch, k, n):
         super().__init__()

@@ -108,6 +108,28 @@ def test_decode_stack_runs_gemv_prologues():
     np.testing.assert_allclose(c(x).numpy(), ref, rtol=RTOL, atol=ATOL)
 
 
+@pytest.mark.parametrize("shape, perm, fused", [((3, 20, 64), None, True), ((2, 5, 1, 64), None, True),
+                                                ((1, 1, 64), None, True), ((20, 3, 64), (1, 0, 2), False)])
+def test_layernorm_prologue_through_a_row_reshape(shape, perm, fused):
+    # LayerNorm over [B, T, K] feeding a Linear: the product's A is the
+    # LayerNorm's output reshaped to [B*T, K]; the product runs the LayerNorm as
+    # its prologue and reads x with the merged row stride - unless x's leading
+    # dims do not merge into one stride (a permuted input), when the LayerNorm
+    # stays a row kernel
+    torch.manual_seed(3)
+    ln = torch.nn.LayerNorm(64)
+    with torch.no_grad():
+        ln.weight.copy_(1 + 0.1 * torch.randn(64))
+        ln.bias.copy_(0.1 * torch.randn(64))
+    lin = torch.nn.Linear(64, 48)
+    model = torch.nn.Sequential(ln, lin).eval()
+    fn = (lambda t: model(t.permute(*perm))) if perm else model
+    x = 3.0 + 2.0 * torch.randn(*shape)
+    c = check(fn, x)
+    src = open(c.report.lowering["source"]).read()
+    assert ("prologue: layernorm" in src) == fused and ("layernorm rows" in src) != fused
+
+
 @pytest.mark.parametrize("precision", ["bf16", "bf16x3"])
 def test_bf16_products_round_as_the_mfma_variants(precision):
     torch.manual_seed(0)
