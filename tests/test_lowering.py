@@ -272,6 +272,17 @@ def test_layernorm_feeding_a_small_m_gemm_becomes_its_prologue(affine):
     kl.Plan([l.desc for l in prog.launches])
 
 
+def test_layernorm_prologue_reads_merged_rows_through_a_reshape():
+    # [3, 20, 64] -> LayerNorm -> reshape [60, 64] -> Linear: the product's A
+    # is the caller's input itself, rows 64 elements apart
+    _, prog = lowered(_ln_linear(), torch.randn(3, 20, 64))
+    launch = prog.launches[0]
+    assert kl.FAMILY_NAMES[launch.family] == "gemm" and "prologue: layernorm" in launch.summary
+    a = launch.desc.refs[0]
+    assert a.base == kl.BASE_INPUT and list(a.strides[:3]) == [0, 64, 1] and list(launch.desc.gemm)[:4] == [1, 60, 48, 64]
+    assert not any("layernorm rows" in l.summary for l in prog.launches)
+
+
 def test_folded_layernorm_plan_round_trips_through_the_store(tmp_path, monkeypatch):
     from kiln.hip import plans
 
