@@ -198,6 +198,12 @@ typedef struct kh_plan kh_plan;
 
 /* library -------------------------------------------------------------------- */
 int kh_version(void);
+/* Digest of the sources and flags the library was built from (build.py
+ * compiles it in): part of the key under which lowered plans are stored, the
+ * counterpart of the reference's content-addressed kernel cache
+ * (kiln/gpu/runtime.py:53-79), so no stored plan outlives a rebuild that may
+ * read its descriptors differently. */
+const char *kh_build_id(void);
 /* sizeof(kh_launch), sizeof(kh_ref), sizeof(kh_insn), sizeof(kh_pass): lets a
  * binding check its struct mirrors against the compiled library. */
 int kh_abi_sizes(size_t *sizes4);
@@ -281,10 +287,16 @@ int kh_plan_time(kh_plan *plan, int index, void *const *inputs, int n_inputs, vo
  * max_chains triples {first launch, number of launches, active}.
  */
 int kh_plan_chains(const kh_plan *plan, int32_t *ranges, int max_chains, int *n_chains);
-/* Waits inside the plan's chains that gave up (a bounded wait that ran out:
- * its workgroup left the kernel and later values are stale; none is expected).
- * Synchronises the device. */
+/* Waits inside the plan's chains that gave up, summed over the plan's life (a
+ * bounded wait that ran out; none is expected). The workgroup that gave up
+ * stored NaN as every output it still owed and left the kernel, so every
+ * value computed from those outputs is NaN. Synchronises the device. */
 int kh_plan_chain_timeouts(kh_plan *plan, uint64_t *timeouts);
+/* Bound on each wait of the plan's chains, in ticks of the 100 MHz wall clock
+ * (kh_plan_bind sets 2,000,000 = 20 ms); ticks < 0 makes every wait give up
+ * at once, so tests can drive the give-up path with every kernel exiting
+ * normally. No counterpart in the reference. */
+int kh_plan_chain_spin(kh_plan *plan, int64_t ticks);
 int kh_plan_destroy(kh_plan *plan);
 
 #ifdef __cplusplus

@@ -11,6 +11,7 @@ on every round, and objects of a stale source must never be reused.
 from __future__ import annotations
 
 import argparse
+import hashlib
 import os
 import shutil
 import subprocess
@@ -53,6 +54,17 @@ def _run(cmd, verbose):
     return res
 
 
+def source_digest() -> str:
+    """sha256 over every file the library is compiled from (csrc/, include/)
+    and the compiler flags: compiled into the library as kh_build_id(), so a
+    stored plan is never reused by a library built from other sources."""
+    h = hashlib.sha256()
+    for f in sorted([*CSRC.glob("*.hip"), *CSRC.glob("*.hpp"), *INCLUDE.glob("*.h")]):
+        h.update(f.name.encode() + b"\0" + f.read_bytes() + b"\0")
+    h.update(" ".join(HIPCC_FLAGS[:-2]).encode())
+    return h.hexdigest()[:32]
+
+
 def build(jobs: int | None = None, verbose: bool = False) -> Path:
     sources = sorted(CSRC.glob("*.hip"))
     if not sources:
@@ -60,7 +72,8 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     BUILD.mkdir(exist_ok=True)
     cc = hipcc()
     objects = [BUILD / (s.stem + ".o") for s in sources]
-    cmds = [[cc, *HIPCC_FLAGS, "-c", str(s), "-o", str(o)] for s, o in zip(sources, objects)]
+    flags = [*HIPCC_FLAGS, f'-DKH_BUILD_ID="{source_digest()}"']
+    cmds = [[cc, *flags, "-c", str(s), "-o", str(o)] for s, o in zip(sources, objects)]
     jobs = jobs or min(len(cmds), max(1, (os.cpu_count() or 4)))
     with ThreadPoolExecutor(max_workers=jobs) as pool:
         for fut in [pool.submit(_run, c, verbose) for c in cmds]:

@@ -23,9 +23,14 @@
 //     (+1 = this call's tag); workgroup 0 stores the new value as its last
 //     act, after every workgroup has reported (a `started` word each) that it
 //     read the old one, so the next call's tags never match a stale word;
-//   * every wait is bounded (wall clock); a wait that gives up counts a
-//     timeout in the plan's state and its workgroup leaves the kernel, so the
-//     grid always drains (kh_plan_chain_timeouts reports the count);
+//   * every wait is bounded (wall clock, `spin` ticks of the plan's state);
+//     a wait that gives up counts a timeout in the plan's state, and its
+//     workgroup stores NaN, under the current epoch, as every output it
+//     still owed (its columns of the stage that gave up and of every later
+//     stage) and leaves the kernel: the grid always drains, the workgroups
+//     that wait for those columns get them at once, and every value
+//     downstream of the give-up is NaN (kh_plan_chain_timeouts reports the
+//     count; the Python runtime raises on it);
 //   * the four compute waves never store: one counter (vmcnt) tracks a
 //     wave's loads and stores together and in issue order, so a wave that
 //     stored its outputs would wait for the stores' device-scope
@@ -69,7 +74,7 @@ constexpr int kAttRounds = 4;                 // attention prologue: head rounds
 constexpr int kMaxDyn = 8;                    // distinct input / output slots a chain reads or writes
 constexpr int kMaxGroups = 1024;              // workgroups (one per CU)
 constexpr int kMaxStages = 96;                // stages of one chain (their descriptors sit in LDS)
-constexpr long long kSpinTicks = 2000000;     // 20 ms of the 100 MHz wall clock per wait
+constexpr int64_t kSpinTicks = 2000000;     // default bound per wait: 20 ms of the 100 MHz wall clock
 
 // An operand address: the absolute address (constants, arena) resolved at
 // bind, or dynamic slot `slot` (a plan input or output) + `off` floats.
@@ -88,6 +93,7 @@ struct ChainState {
   uint32_t epoch;
   uint32_t pad;
   unsigned long long timeouts;
+  int64_t spin;                  // wall-clock ticks a wait may take; < 0: every wait gives up (test hook)
   uint64_t started[kMaxGroups];  // (epoch, group) words: group g has read the epoch
 };
 
@@ -263,7 +269,7 @@ __device__ __forceinline__ void prefetch_t(const Hot &S, int gw, int nwaves, int
 // the store wave.
 template <int P, bool BF16>
 __device__ __forceinline__ void compute_t(const Hot &S, int gw, int nwaves, int lane, uint32_t epoch, Carry &cr,
-                                          const float *xs, float *outs, ChainState *state) {
+                                          const float *xs, float *outs, ChainState *state, int64_t spin) {
   constexpr int CMAX = kSlots / P;
   const int U = S.K / (BF16 ? 8 : 4);
   const int nc = wave_columns(S, gw, nwaves);
@@ -310,8 +316,9 @@ __device__ __forceinline__ void compute_t(const Hot &S, int gw, int nwaves, int 
   if (S.has_res && S.res_ll && !ll_ok(pr, epoch)) {
     const long long t0 = wall_clock64();
     while (!ll_ok(pr = ll_get(S.res_ll + col * S.res_sn), epoch)) {
-      if (wall_clock64() - t0 > kSpinTicks) {
+      if (spin < 0 || wall_clock64() - t0 > spin) {
         atomicAdd(&state->timeouts, 1ull);
+        pr = ll_word(__builtin_nanf(""), epoch);   // the column's output becomes NaN
         break;
       }
     }
@@ -340,10 +347,10 @@ __device__ __forceinline__ void prefetch(const Hot &S, int gw, int nwaves, int l
 }
 
 __device__ __forceinline__ void compute(const Hot &S, int gw, int nwaves, int lane, uint32_t epoch, Carry &cr,
-                                        const float *xs, float *outs, ChainState *state) {
+                                        const float *xs, float *outs, ChainState *state, int64_t spin) {
   switch (S.kind) {
 #define KH_X(k, P, B) \
-  case k: compute_t<P, B>(S, gw, nwaves, lane, epoch, cr, xs, outs, state); break;
+  case k: compute_t<P, B>(S, gw, nwaves, lane, epoch, cr, xs, outs, state, spin); break;
     KH_CHAIN_KINDS(KH_X)
 #undef KH_X
   }
@@ -352,14 +359,15 @@ __device__ __forceinline__ void compute(const Hot &S, int gw, int nwaves, int la
 // The store wave: lane 16w + c stores column c of compute wave w's outputs
 // (its memory copy when the stage's output is read after the chain, and its
 // hand-over word).
+// `poison`: NaN instead of the computed value (a stage this workgroup gave up).
 __device__ __forceinline__ void store_outputs(const Hot &S, int nwaves, int lane, uint32_t epoch,
-                                              const float *outs) {
+                                              const float *outs, bool poison = false) {
   const int w = lane >> 4, c = lane & 15;
   const int gw = (int)blockIdx.x * kWaves + w;
   const int nc = min(wave_columns(S, gw, nwaves), kSlots / kKindP[S.kind % kNumP]);
   if (w >= kWaves || c >= nc) return;
   const int64_t col = gw + (int64_t)c * nwaves;
-  const float v = outs[w * 64 + c];
+  const float v = poison ? __builtin_nanf("") : outs[w * 64 + c];
   if (S.plain_out) gbl_w(S.out)[col * S.out_sn] = v;
   ll_put(S.out_ll + col, ll_word(v, epoch));
 }
@@ -369,7 +377,8 @@ __device__ __forceinline__ void store_outputs(const Hot &S, int nwaves, int lane
 // The wall clock (a scalar-memory read) is checked every 64 rounds only, so
 // a round costs one memory round trip.
 template <int N, class Need, class Reload>
-__device__ __forceinline__ bool poll(uint64_t (&v)[N], uint32_t epoch, Need need, Reload reload) {
+__device__ __forceinline__ bool poll(uint64_t (&v)[N], uint32_t epoch, int64_t spin, Need need, Reload reload) {
+  if (spin < 0) return false;
   long long t0 = 0;
   for (unsigned round = 0;; ++round) {
     bool all = true;
@@ -380,7 +389,7 @@ __device__ __forceinline__ bool poll(uint64_t (&v)[N], uint32_t epoch, Need need
     if ((round & 63) == 0) {
       const long long now = wall_clock64();
       if (round == 0) t0 = now;
-      else if (now - t0 > kSpinTicks) return false;
+      else if (now - t0 > spin) return false;
     }
 #pragma unroll
     for (int i = 0; i < N; ++i)
@@ -391,7 +400,7 @@ __device__ __forceinline__ bool poll(uint64_t (&v)[N], uint32_t epoch, Need need
 // The stage's row x into LDS: from the producer's hand-over words (or
 // memory), with the LayerNorm prologue applied. false: a wait gave up.
 __device__ __forceinline__ bool acquire_x(const CStage &S, const Hot &hot, const ChainDyn &dyn, uint32_t epoch,
-                                          float *xs, float *red) {
+                                          int64_t spin, float *xs, float *red) {
   uint64_t v[kPerThread];
   const float *xp = S.x_ll ? nullptr : cptr(S.x, dyn);
   const int tid = threadIdx.x;
@@ -412,7 +421,7 @@ __device__ __forceinline__ bool acquire_x(const CStage &S, const Hot &hot, const
     if (k < S.K) v[i] = S.x_ll ? ll_get(S.x_ll + k) : ll_word(ld(xp, k), epoch);
   }
   const bool good = poll(
-      v, epoch, [&](int i) { return tid + i * kThreads < S.K; },
+      v, epoch, spin, [&](int i) { return tid + i * kThreads < S.K; },
       [&](int i) { return ll_get(S.x_ll + tid + i * kThreads); });
   if (S.pro == KH_GEMV_PRO_LAYERNORM) {
     // mean, then the variance of the centred values (every thread takes part
@@ -455,7 +464,8 @@ __device__ __forceinline__ bool acquire_x(const CStage &S, const Hot &hot, const
 // lane / dh (HPI = 64 / dh heads per round), lane % dh = d; the base-2
 // online softmax of the attention kernels (exponentials against 0 while no
 // score is finite; a fully masked row gives NaN as in eager).
-__device__ __forceinline__ bool attend(const CStage &S, const ChainDyn &dyn, uint32_t epoch, float *xs) {
+__device__ __forceinline__ bool attend(const CStage &S, const ChainDyn &dyn, uint32_t epoch, int64_t spin,
+                                       float *xs) {
   constexpr float kLog2e = 1.4426950408889634f;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int dh = S.att_dh, hpi = 64 / dh, sub = lane / dh, d = lane % dh;
@@ -492,7 +502,7 @@ __device__ __forceinline__ bool attend(const CStage &S, const ChainDyn &dyn, uin
       kv[3 * r + 2] = wq[r];
     }
     good = poll(
-               kv, epoch, [&](int i) { return on[i / 3]; },
+               kv, epoch, spin, [&](int i) { return on[i / 3]; },
                [&](int i) {
                  const int r = i / 3;
                  if (i % 3 == 0) return word(kp, (int64_t)h[r] * S.k_s0 + (int64_t)j * S.k_s1 + d, S.k_shift);
@@ -547,6 +557,7 @@ __global__ __launch_bounds__(kBlock) void gemv_chain_kernel(const CStage *st, in
     st = st_lds;
   }
   const uint32_t epoch = __hip_atomic_load(&state->epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+  const int64_t spin = __hip_atomic_load(&state->spin, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const bool storer = wave == kWaves;
   if (tid == 0) alive = 1;
   if (storer && lane == 0) ll_put(&state->started[blockIdx.x], (uint64_t)epoch << 32 | blockIdx.x);
@@ -563,7 +574,14 @@ __global__ __launch_bounds__(kBlock) void gemv_chain_kernel(const CStage *st, in
       if (S.pro == KH_GEMV_PRO_LAYERNORM)
         for (int i = 0; i < kLnBarriers; ++i) __syncthreads();
       __syncthreads();                                 // B2
-      if (!alive) break;
+      if (!alive) {
+        // a wait of this workgroup gave up at stage s: NaN for every column
+        // it owes from stage s on, so no other workgroup waits for them and
+        // everything computed from them is NaN
+        for (int s2 = s; s2 < n_stages; ++s2)
+          if ((int)blockIdx.x * kWaves < st[s2].N) store_outputs(hot_of(st[s2], dyn), nwaves, lane, epoch, outs, true);
+        break;
+      }
       __syncthreads();                                 // B3
       store_outputs(hot_of(S, dyn), nwaves, lane, epoch, outs);   // `outs` is rewritten only after the next B2
     }
@@ -581,14 +599,15 @@ __global__ __launch_bounds__(kBlock) void gemv_chain_kernel(const CStage *st, in
     Carry cr;
     prefetch(hot, gw, nwaves, lane, cr);
     __syncthreads();                                   // B1: the previous stage's reads of xs are done
-    const bool good = S.pro == KH_GEMV_PRO_ATTN ? attend(S, dyn, epoch, xs) : acquire_x(S, hot, dyn, epoch, xs, red);
+    const bool good =
+        S.pro == KH_GEMV_PRO_ATTN ? attend(S, dyn, epoch, spin, xs) : acquire_x(S, hot, dyn, epoch, spin, xs, red);
     if (!good) alive = 0;
     __syncthreads();                                   // B2
     if (!alive) {
       if (tid == 0) atomicAdd(&state->timeouts, 1ull);
       break;
     }
-    compute(hot, gw, nwaves, lane, epoch, cr, xs, outs, state);
+    compute(hot, gw, nwaves, lane, epoch, cr, xs, outs, state, spin);
     __syncthreads();                                   // B3
   }
   if (blockIdx.x == 0 && wave == 0) {
@@ -708,7 +727,8 @@ class GemvChain final : public Chain {
           (e = hipMalloc(&d_state, sizeof(ChainState))) != hipSuccess ||
           (e = hipMalloc(&d_stages, st.size() * sizeof(CStage))) != hipSuccess ||
           (e = hipMemset(d_ll, 0, std::max<int64_t>(1, words) * sizeof(uint64_t))) != hipSuccess ||
-          (e = hipMemset(d_state, 0, sizeof(ChainState))) != hipSuccess) {
+          (e = hipMemset(d_state, 0, sizeof(ChainState))) != hipSuccess ||
+          (e = hipMemcpy(&d_state->spin, &kSpinTicks, sizeof(int64_t), hipMemcpyHostToDevice)) != hipSuccess) {
         (void)hipGetLastError();
         err = std::string("chain state: ") + hipGetErrorString(e);
         return KH_ERR_HIP;
@@ -780,6 +800,12 @@ class GemvChain final : public Chain {
     hipLaunchKernelGGL(gemv_chain_kernel, dim3(groups), dim3(kBlock), 0, stream, d_stages, (int)st.size(), dyn,
                        d_state);
     return hipGetLastError();
+  }
+
+  int set_spin(int64_t ticks) override {
+    if (!d_state) return KH_OK;
+    return hipMemcpy(&d_state->spin, &ticks, sizeof(ticks), hipMemcpyHostToDevice) == hipSuccess ? KH_OK
+                                                                                                 : KH_ERR_HIP;
   }
 
   int timeouts(unsigned long long *out) override {

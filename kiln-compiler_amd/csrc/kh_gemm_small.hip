@@ -30,15 +30,21 @@
 // LayerNorm prologue (LN, fp32; a LayerNorm whose only consumer is this
 // product's A operand): A is the LayerNorm's input x; the lowering folds
 // gamma into B (B' = gamma * B) and provides g = column sums of B' and
-// c = beta . B. With x0 a row's first value,
-//     LayerNorm(x) . B = rstd * ((x - x0) . B' - (mean - x0) * g) + c,
-// so A fragments enter the MFMAs as x - x0 (the shift keeps the correction
-// term small whatever the row's mean) and the row statistics come from the
+// c = beta . B. With s a shift near the row's mean,
+//     LayerNorm(x) . B = rstd * ((x - s) . B' - (mean - s) * g) + c,
+// so A fragments enter the MFMAs as x - s and the row statistics come from the
 // same fragments as the K loop streams them: each lane merges the mean and
 // the sum of squared deviations of its 8-value chunks (Chan's pairwise
 // update), lanes and then waves merge theirs in a fixed order, and the
-// epilogue applies the formula before the tape. The LayerNorm's launch and
-// its output's round trip through memory go away; A is read once.
+// epilogue applies the formula before the tape. The rounding error of the
+// accumulated (x - s) . B' and of the correction grows with |mean - s| /
+// std, so s is the mean of the row's first 32 values (every wave of the
+// workgroup computes it in the same order, so they all use the same s): a
+// row whose first value is an outlier (x[0] = 200 over N(0, 1) values)
+// would make the row's first value a shift about 27 standard deviations
+// from the mean, the sample mean about one. The LayerNorm's launch and its
+// output's round trip through memory go away; A is read once (plus the 128
+// bytes of the shift, an L2 hit).
 // K must be a positive multiple of 32 and the operands' spans below 2^29
 // elements (the host checks both).
 #include <algorithm>
@@ -169,13 +175,22 @@ __global__ __launch_bounds__(64 * WK) void gemm_small_kernel(const GemmArgs a) {
   auto part = [](const float4 &v, int j) { return j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w; };
 
   for (int p = 0; p < NS - 1 && p < n_steps; ++p) issue(p);
-  // LN: the row's first value (the shift) and this lane's running (count,
-  // mean, M2) of x - x0 per row of the tile
+  // LN: the shift s (the mean of the row's first 32 values: lane group g
+  // sums values 8g .. 8g+7, the four groups' sums are added by two xor
+  // shuffles, which gives every lane of the row the same bits) and this
+  // lane's running (count, mean, M2) of x - s per row of the tile
   float ln_x0[FM], ln_n[FM], ln_mean[FM], ln_m2[FM];
   if constexpr (LN) {
 #pragma unroll
     for (int fm = 0; fm < FM; ++fm) {
-      ln_x0[fm] = Ab[(int64_t)min(m0 + fm * MT + li, a.M - 1) * a.sa_m];
+      const float *row = Ab + (int64_t)min(m0 + fm * MT + li, a.M - 1) * a.sa_m + 8 * g;
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = row[e];
+      float t = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+      t += __shfl_xor(t, 16, 64);
+      t += __shfl_xor(t, 32, 64);
+      ln_x0[fm] = t * 0.03125f;
       ln_n[fm] = 0.0f, ln_mean[fm] = 0.0f, ln_m2[fm] = 0.0f;
     }
   }
@@ -334,7 +349,7 @@ __global__ __launch_bounds__(64 * WK) void gemm_small_kernel(const GemmArgs a) {
     const int valid = min(4, a.N - n);
     if constexpr (LN) {
       // the row's statistics over all of K (waves merged in order), then
-      // rstd * (sum - (mean - x0) * g) + c
+      // rstd * (sum - (mean - s) * g) + c
       float4 st = ln_part[0][m - m0];
 #pragma unroll
       for (int w = 1; w < WK; ++w) {

@@ -57,6 +57,8 @@ class Chain {
   virtual int bind(void *const *consts, int n_consts, void *arena, std::string &err) = 0;
   virtual hipError_t launch(void *const *inputs, int n_in, void *const *outputs, int n_out, hipStream_t stream) = 0;
   virtual int timeouts(unsigned long long *out) = 0;
+  // Wall-clock ticks (100 MHz) each wait may take; < 0: every wait gives up.
+  virtual int set_spin(int64_t ticks) = 0;
 };
 
 // The chains of a plan's launches (only GEMV launches marked KH_GEMV_CHAIN

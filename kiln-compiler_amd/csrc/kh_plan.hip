@@ -228,6 +228,11 @@ extern "C" {
 
 int kh_version(void) { return KH_ABI_VERSION; }
 
+#ifndef KH_BUILD_ID
+#define KH_BUILD_ID "unversioned"
+#endif
+const char *kh_build_id(void) { return KH_BUILD_ID; }
+
 int kh_abi_sizes(size_t *sizes4) {
   if (!sizes4) return fail(KH_ERR_INVALID, "null argument");
   sizes4[0] = sizeof(kh_launch);
@@ -365,6 +370,13 @@ int kh_plan_chain_timeouts(kh_plan *plan, uint64_t *timeouts) {
     if (c->timeouts(&n) != KH_OK) return fail(KH_ERR_HIP, "reading a chain's state");
     *timeouts += n;
   }
+  return KH_OK;
+}
+
+int kh_plan_chain_spin(kh_plan *plan, int64_t ticks) {
+  if (!plan) return fail(KH_ERR_INVALID, "null plan");
+  for (auto &c : plan->chains)
+    if (c->set_spin(ticks) != KH_OK) return fail(KH_ERR_HIP, "writing a chain's state");
   return KH_OK;
 }
 

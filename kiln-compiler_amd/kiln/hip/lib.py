@@ -90,6 +90,7 @@ def load():
     vp, ip, i32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int32
     sig = {
         "kh_version": (ip, []),
+        "kh_build_id": (ctypes.c_char_p, []),
         "kh_abi_sizes": (ip, [ctypes.POINTER(ctypes.c_size_t)]),
         "kh_last_error": (ctypes.c_char_p, []),
         "kh_init": (ip, [ip]),
@@ -109,6 +110,7 @@ def load():
                               ctypes.POINTER(ctypes.c_double)]),
         "kh_plan_chains": (ip, [vp, ctypes.POINTER(ctypes.c_int32), ip, ctypes.POINTER(ip)]),
         "kh_plan_chain_timeouts": (ip, [vp, ctypes.POINTER(ctypes.c_uint64)]),
+        "kh_plan_chain_spin": (ip, [vp, ctypes.c_int64]),
         "kh_plan_destroy": (ip, [vp]),
     }
     for name, (res, args) in sig.items():
@@ -125,11 +127,12 @@ def load():
     return lib
 
 
-EXPORTED = ("kh_version", "kh_abi_sizes", "kh_last_error", "kh_init", "kh_device_info", "kh_gemm_config_count", "kh_gemm_config",
+EXPORTED = ("kh_version", "kh_build_id", "kh_abi_sizes", "kh_last_error", "kh_init", "kh_device_info", "kh_gemm_config_count", "kh_gemm_config",
             "kh_plan_create", "kh_plan_workspace_bytes", "kh_plan_bind", "kh_plan_run", "kh_plan_run_noalloc",
             "kh_plan_run_host",
             "kh_plan_run_one",
             "kh_plan_capture", "kh_plan_replay", "kh_plan_time", "kh_plan_chains", "kh_plan_chain_timeouts",
+            "kh_plan_chain_spin",
             "kh_plan_destroy")
 
 
@@ -156,6 +159,11 @@ def gemm_configs() -> list:
         check(lib.kh_gemm_config(i, buf), "kh_gemm_config")
         out.append(tuple(buf))
     return out
+
+
+def build_id() -> str:
+    """Digest of the sources the loaded library was built from."""
+    return load().kh_build_id().decode()
 
 
 def device_info():
@@ -233,10 +241,16 @@ class Plan:
         return [tuple(buf[3 * i:3 * i + 3]) for i in range(n.value)]
 
     def chain_timeouts(self) -> int:
-        """Waits inside the plan's chains that gave up (none expected); synchronises the device."""
+        """Waits inside the plan's chains that gave up, over the plan's life
+        (none expected); synchronises the device."""
         n = ctypes.c_uint64()
         check(self.lib.kh_plan_chain_timeouts(self.handle, ctypes.byref(n)), "kh_plan_chain_timeouts")
         return n.value
+
+    def set_chain_spin(self, ticks: int):
+        """Bound on each chain wait in 100 MHz ticks (default 2,000,000 = 20 ms);
+        negative: every wait gives up at once (tests drive the give-up path)."""
+        check(self.lib.kh_plan_chain_spin(self.handle, int(ticks)), "kh_plan_chain_spin")
 
     def __del__(self):
         h = getattr(self, "handle", None)

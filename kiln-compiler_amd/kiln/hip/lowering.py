@@ -176,7 +176,7 @@ def _encode(tape: _Tape, slot, desc: kl.LaunchDesc, ref_offset=0):
 # ----------------------------------------------------------------------------------
 
 class _Lowerer:
-    def __init__(self, graph: Graph, precision: str, matmul_config, gemv_chains: bool = True):
+    def __init__(self, graph: Graph, precision: str, matmul_config, gemv_chains: bool = False):
         self.g = graph
         self.gemv_chains = gemv_chains
         self.layouts = compute_layouts(graph)
@@ -1150,7 +1150,7 @@ class _Lowerer:
         return self.program
 
 
-def lower_graph(graph: Graph, precision: str = "fp32", matmul_config=None, gemv_chains: bool = True) -> Program:
+def lower_graph(graph: Graph, precision: str = "fp32", matmul_config=None, gemv_chains: bool = False) -> Program:
     """Fused, buffer-assigned, memory-planned graph -> Program (launch list).
     gemv_chains: mark one-row matmuls KH_GEMV_CHAIN, so the library may run
     consecutive ones as one persistent launch."""

@@ -44,7 +44,8 @@ _fingerprint = None
 
 
 def backend_fingerprint() -> str:
-    """Digest of the code that turns a graph into a plan."""
+    """Digest of the code that turns a graph into a plan and of the library
+    build that reads the plan's descriptors (kh_build_id)."""
     global _fingerprint
     if _fingerprint is None:
         h = hashlib.sha256()
@@ -54,7 +55,8 @@ def backend_fingerprint() -> str:
                 h.update((here / name).read_bytes())
             except OSError:
                 h.update(b"missing " + name.encode())
-        h.update(repr((kl.ABI_VERSION, kl.ctypes.sizeof(kl.LaunchDesc), tuple(kl.gemm_configs()))).encode())
+        h.update(repr((kl.ABI_VERSION, kl.ctypes.sizeof(kl.LaunchDesc), tuple(kl.gemm_configs()),
+                       kl.build_id())).encode())
         _fingerprint = h.hexdigest()
     return _fingerprint
 

@@ -181,6 +181,13 @@ class HIPExecutable:
         # GPT-2 block, T = 128: 0.051 against 0.063 ms). Both run the same
         # kernels in the same order, so results are bit for bit the same.
         self.mode = None      # "graph" | "direct" once chosen
+        # persistent GEMV chains bound on the GPU: a wait inside one that gives
+        # up leaves NaN in every output computed from it and is counted; the
+        # count is read (one device synchronisation) after the first call and
+        # after every call in debug mode
+        self.has_chains = any(active for _, _, active in self.plan.chains())
+        self._chain_timeouts = 0
+        self._chain_checked = False
 
     # -- inputs ---------------------------------------------------------------------------
 
@@ -258,13 +265,31 @@ class HIPExecutable:
                 best[name] = min(best[name], start.elapsed_time(stop))
         return "direct" if best["direct"] < best["graph"] else "graph"
 
+    def check_chains(self):
+        """RuntimeError if a wait inside one of the plan's persistent GEMV
+        chains gave up since the last check (its outputs are NaN-poisoned)."""
+        if not self.has_chains:
+            return
+        count = self.plan.chain_timeouts()
+        new, self._chain_timeouts = count - self._chain_timeouts, count
+        if new:
+            raise RuntimeError(f"a persistent GEMV chain gave up {new} wait(s) (another stream's or process's "
+                               f"work kept its workgroups from running together?); the outputs of this call are "
+                               f"NaN from the stage that gave up on: compile with gemv_chains=False")
+
     def __call__(self, *inputs):
         inputs = self._prepare(inputs)
-        if not self.use_cuda_graphs or torch.cuda.is_current_stream_capturing():
-            return self._direct(inputs)   # also inside a caller's own stream capture
-        if self.mode is None:
-            self.mode = self._choose_mode(inputs)
-        return self._direct(inputs) if self.mode == "direct" else self._replay(inputs)
+        capturing = torch.cuda.is_current_stream_capturing()
+        if not self.use_cuda_graphs or capturing:
+            out = self._direct(inputs)   # also inside a caller's own stream capture
+        else:
+            if self.mode is None:
+                self.mode = self._choose_mode(inputs)
+            out = self._direct(inputs) if self.mode == "direct" else self._replay(inputs)
+        if self.has_chains and not capturing and (self.debug or not self._chain_checked):
+            self._chain_checked = True
+            self.check_chains()
+        return out
 
     def profile(self, *inputs, iters=20):
         """[(launch name, GPU ms per launch)], each launch timed natively."""

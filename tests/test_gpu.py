@@ -101,6 +101,32 @@ def test_matches_without_graphs(name):
     check(fn, *xs, cuda_graphs=False)
 
 
+EXP_EXTREMES = [[-200.0, -87.0, -10.0, 0.0, 1e-6, 10.0, 80.0, float("-inf")]]
+
+
+@pytest.mark.parametrize("graphs", [True, False], ids=["graph", "direct"])
+def test_exp_extremes(graphs):
+    # the reference's known-answer case (tests/test_compile.py:50-52 there):
+    # underflow to 0 (-200, -inf), the smallest normal range (-87), 1 + tiny,
+    # and 80 near the fp32 overflow edge, at rtol 1e-5 / atol 1e-30 - through
+    # the elementwise tape (KH_OP_EXP) and the softmax row kernel, whose
+    # exponentials are exp2((v - max) * log2 e): relative error about
+    # |v - max| * 1.2e-7, so the row is also checked scaled by 0.1 (shifted
+    # arguments down to -28)
+    x = torch.tensor(EXP_EXTREMES)
+    c = check(torch.exp, x, rtol=1e-5, atol=1e-30, cuda_graphs=graphs)
+    assert c.report.lowering["families"] == {"elementwise": 1}
+    for fn in (lambda t: F.softmax(t, -1), lambda t: F.softmax(t * 0.1, -1)):
+        c = check(fn, x, rtol=1e-5, atol=1e-30, cuda_graphs=graphs)
+        assert c.report.lowering["families"] == {"row": 1}
+    # the same values in a 4096-wide row (the one-wave fast path holds the
+    # row in registers) and fused after an elementwise op
+    wide = torch.randn(3, 4096) * 4
+    wide[:, :8] = x
+    check(lambda t: torch.exp(t - 1.0), wide, rtol=1e-5, atol=1e-30, cuda_graphs=graphs)
+    check(lambda t: F.softmax(t * 0.1, -1), wide, rtol=1e-5, atol=1e-30, cuda_graphs=graphs)
+
+
 @pytest.mark.parametrize("fn", [torch.nn.LayerNorm(10000).eval(), lambda x: F.softmax(x, -1),
                                 lambda x: F.softmax(x + MASK, -1)], ids=["layernorm", "softmax", "masked"])
 def test_long_rows_are_chunked(fn):
@@ -385,12 +411,19 @@ def test_layernorm_prologue_on_every_small_m_configuration(tile):
     # sums and beta . W as column constants); the LayerNorm has no launch of
     # its own. Ragged M / N, K from one step to the longest prologue row
     # (1024), with and without affine parameters, rows with mean 3 and with
-    # mean 100 (std 1: the shift by the row's first value keeps the result
-    # exact to fp32 rounding); repeated launches agree bit for bit
+    # mean 100 (std 1), and rows whose first value is an outlier (20 or 200
+    # over N(0, 1) values: a shift by the row's first value would sit 3-27
+    # standard deviations from the mean and cost the fp32 sums up to
+    # log2(27) bits); repeated launches agree bit for bit
     cfg = lambda *_: {"tile": tile, "splitk": 1}
-    for m, n, k, affine, loc, sd in ((77, 133, 32, True, 3.0, 2.0), (300, 452, 256, False, 3.0, 2.0),
-                                     (128, 200, 768, True, 3.0, 2.0), (40, 64, 1024, True, 3.0, 2.0),
-                                     (64, 96, 768, True, 100.0, 1.0)):
+    for m, n, k, affine, loc, sd, first in ((77, 133, 32, True, 3.0, 2.0, None),
+                                            (300, 452, 256, False, 3.0, 2.0, None),
+                                            (128, 200, 768, True, 3.0, 2.0, None),
+                                            (40, 64, 1024, True, 3.0, 2.0, None),
+                                            (64, 96, 768, True, 100.0, 1.0, None),
+                                            (64, 768, 768, True, 0.0, 1.0, 20.0),
+                                            (64, 768, 768, True, 0.0, 1.0, 200.0),
+                                            (50, 96, 256, False, 0.0, 1.0, -200.0)):
         torch.manual_seed(m + k)
         ln = torch.nn.LayerNorm(k, elementwise_affine=affine)
         if affine:
@@ -401,6 +434,8 @@ def test_layernorm_prologue_on_every_small_m_configuration(tile):
         model = torch.nn.Sequential(ln, lin).eval()
         fn = lambda t, res: model(t) + res
         x, r = loc + sd * torch.randn(m, k), torch.randn(m, n)
+        if first is not None:
+            x[:, 0] = first
         c = kiln.compile(fn, (x, r), device="cuda", cuda_graphs=False, gpu_matmul_config=cfg)
         summaries = [l.summary for l in c._exe.program.launches]
         assert len(summaries) == 1 and f"tile {tile} " in summaries[0] and "prologue: layernorm" in summaries[0]

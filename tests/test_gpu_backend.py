@@ -1,11 +1,14 @@
 """torch.compile(backend=kiln.backend) on the MI355X: results match eager
 PyTorch at the reference's tolerances (rtol 1e-4, atol 1e-5;
-tests/test_compile.py:108-116 there), and weights stay runtime inputs."""
+tests/test_compile.py:108-116 there) - and the GPT-2 block also the float64
+C oracle - and weights stay runtime inputs."""
 
+import numpy as np
 import pytest
 import torch
 
 import kiln
+import oracle
 from models.transformer import Block, gpt2_init_
 
 pytestmark = pytest.mark.gpu
@@ -46,5 +49,10 @@ def test_gpt2_block_compiles_for_the_gpu(T):
     compiled = torch.compile(model, backend=kiln.backend, dynamic=False)
     x = torch.randn(T, 768, device="cuda")
     with torch.no_grad():
-        torch.testing.assert_close(compiled(x), model(x), rtol=1e-4, atol=1e-5)
+        got = compiled(x)
+        torch.testing.assert_close(got, model(x), rtol=1e-4, atol=1e-5)
     assert kiln.stats == {"compiled": 1, "fallback": 0}
+    # and against the float64 C oracle of the block
+    params = {k: v.detach().cpu().numpy() for k, v in model.state_dict().items()}
+    ref = oracle.block(x.cpu().numpy(), params, 12)
+    np.testing.assert_allclose(got.cpu().numpy(), ref, rtol=1e-4, atol=1e-5)

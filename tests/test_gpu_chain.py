@@ -109,3 +109,43 @@ def test_chain_launch_timing_covers_every_launch():
     assert len(per_launch) == 9 and all(row[-1] > 0 for row in per_launch)
     assert torch.equal(c(x.cuda()), c(x.cuda()))
     assert c._exe.plan.chain_timeouts() == 0
+
+
+@pytest.mark.parametrize("debug", [False, True], ids=["first-call", "debug"])
+def test_chain_give_up_is_loud(debug):
+    # The host makes every bounded wait inside the chain give up at once (a
+    # negative spin bound: no wait is attempted, every kernel exits normally).
+    # Each workgroup then stores NaN as the outputs it owes, so everything
+    # computed from the chain is NaN, and the runtime raises instead of
+    # returning those outputs; with the bound restored the plan is correct
+    # again.
+    model = _stack(2, 128, 4)
+    x = torch.randn(1, 128)
+    c, plain = _chained(model, x, debug=debug)
+    exe = c._exe
+    assert exe.has_chains
+    xd = x.cuda()
+    ref = plain(xd)
+    torch.testing.assert_close(c(xd), ref, rtol=RTOL, atol=ATOL)   # the first call's check passes
+    exe.plan.set_chain_spin(-1)
+    if debug:
+        with pytest.raises(RuntimeError, match="gave up"):
+            c(xd)
+    out = exe._direct(exe._prepare([xd]))[0]
+    torch.cuda.synchronize()
+    assert bool(torch.isnan(out).all())
+    with pytest.raises(RuntimeError, match="gave up"):
+        exe.check_chains()
+    exe.plan.set_chain_spin(2_000_000)
+    torch.testing.assert_close(exe._direct(exe._prepare([xd]))[0], ref, rtol=RTOL, atol=ATOL)
+    exe.check_chains()                                           # nothing new gave up
+    torch.testing.assert_close(c(xd), ref, rtol=RTOL, atol=ATOL)
+
+
+def test_chain_give_up_raises_at_first_call():
+    model = _stack(2, 128, 4)
+    x = torch.randn(1, 128)
+    c = kiln.compile(model, (x,), device="cuda", gemv_chains=True, cuda_graphs=False)
+    c._exe.plan.set_chain_spin(-1)
+    with pytest.raises(RuntimeError, match="gave up"):
+        c(x.cuda())

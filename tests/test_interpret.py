@@ -130,6 +130,32 @@ def test_layernorm_prologue_through_a_row_reshape(shape, perm, fused):
     assert ("prologue: layernorm" in src) == fused and ("layernorm rows" in src) != fused
 
 
+def test_exp_extremes():
+    # the reference's known-answer case (tests/test_compile.py:50-52 there)
+    # through the elementwise tape and the softmax row pass
+    x = torch.tensor([[-200.0, -87.0, -10.0, 0.0, 1e-6, 10.0, 80.0, float("-inf")]])
+    for fn in (torch.exp, lambda t: F.softmax(t, -1), lambda t: F.softmax(t * 0.1, -1)):
+        check(fn, x, rtol=1e-5, atol=1e-30)
+
+
+@pytest.mark.parametrize("first", [20.0, 200.0, -200.0])
+def test_layernorm_prologue_rows_with_an_outlier_first_value(first):
+    # rows of N(0, 1) values whose first value is an outlier: the folded
+    # constants (gamma * W, its column sums, beta . W) stand for the same
+    # LayerNorm -> Linear whatever the row's spread
+    torch.manual_seed(7)
+    ln = torch.nn.LayerNorm(256)
+    with torch.no_grad():
+        ln.weight.copy_(1 + 0.1 * torch.randn(256))
+        ln.bias.copy_(0.1 * torch.randn(256))
+    lin = gpt2_init_(torch.nn.Linear(256, 96), seed=1)
+    model = torch.nn.Sequential(ln, lin).eval()
+    x = torch.randn(40, 256)
+    x[:, 0] = first
+    c = check(model, x)
+    assert "prologue: layernorm" in open(c.report.lowering["source"]).read()
+
+
 @pytest.mark.parametrize("precision", ["bf16", "bf16x3"])
 def test_bf16_products_round_as_the_mfma_variants(precision):
     torch.manual_seed(0)

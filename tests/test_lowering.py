@@ -21,6 +21,7 @@ from kiln.passes.manager import PassManager
 from models.transformer import Block, Stack
 
 HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "kiln_hip.h")
+PKG_ROOT = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "kiln-compiler_amd")
 
 
 def lowered(fn, *xs, fuse_attention=False, **opts):
@@ -43,6 +44,19 @@ def test_library_exports_every_header_symbol():
     for name in declared:
         assert hasattr(lib, name), name
     assert lib.kh_version() == kl.ABI_VERSION
+
+
+def test_library_build_id_is_the_tree_digest():
+    # kh_build_id (part of the stored-plan key) is the digest of the sources
+    # the library was built from: a library built from other sources gives
+    # other plan keys
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location("kiln_hip_build", os.path.join(PKG_ROOT, "build.py"))
+    build = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(build)
+    assert kl.build_id() == build.source_digest()
+    assert len(kl.build_id()) == 32
 
 
 def test_struct_sizes_match_the_library():
