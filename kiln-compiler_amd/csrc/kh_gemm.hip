@@ -898,7 +898,8 @@ struct TileCfg {
   int bm, bn, bk, wm, wn, wk, mt, kind, stages, prec;  // kind 1: register-staged loads; 3: LDS-copy pipeline;
                                                        // 4: skinny-M direct loads ([N][K] B); 5: one
                                                        // workgroup per CU, A and B K-contiguous ([N][K] B);
-                                                       // 6: small tiles, waves split K ([N][K] B)
+                                                       // 6: small tiles, waves split K ([N][K] B); 7: bf16,
+                                                       // 64-deep steps, one tile per workgroup ([N][K] B)
 };
 
 // Configurations by id. Ids 0-7: the copy pipeline (BK = 32, MFMA
@@ -1039,6 +1040,9 @@ constexpr TileCfg kConfigs[] = {
   {bm, bn, 32, wm, wn, 1, 16, 5, ns, prec == 1 ? KH_PREC_BF16 : KH_PREC_BF16X3},
     KH_GEMM_NT_BF16_CONFIGS(KH_CFGNTB_ROW)
 #undef KH_CFGNTB_ROW
+#define KH_CFGBF_ROW(id, bm, bn, wm, wn, ns) {bm, bn, 64, wm, wn, 1, 16, 7, ns, KH_PREC_BF16},
+    KH_GEMM_BF_CONFIGS(KH_CFGBF_ROW)
+#undef KH_CFGBF_ROW
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 
@@ -1052,6 +1056,7 @@ constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
 int tile_group(const TileCfg &t, int tiles_m) {
   const int lds = t.kind == 6   ? 4 * t.stages * t.bk * (t.bm + t.bn) * t.wk   // (fp32 bound)
                   : t.kind == 5 ? 4 * t.stages * t.bk * (t.bm + t.bn)   // (fp32 bound)
+                  : t.kind == 7 ? t.stages * t.bk * (4 * t.bm + 2 * t.bn)
                   : t.kind == 3 ? 4 * t.stages * (t.bm * t.bk + (t.prec == KH_PREC_FP32 ? t.bk * t.bn
                                                                  : t.bn * t.bk / 2 * (t.prec == KH_PREC_BF16X3 ? 2 : 1)))
                               : 8 * (t.bm * (t.bk + 4) + t.bn * (t.bk + 2));
@@ -1066,6 +1071,7 @@ int tile_group(const TileCfg &t, int tiles_m) {
 
 hipError_t launch_config(int id, const GemmArgs &a, dim3 grid, hipStream_t stream) {
   if (kConfigs[id].kind == 5) return launch_gemm_nt(id, a, grid, stream);
+  if (kConfigs[id].kind == 7) return launch_gemm_bf(id, a, grid, stream);
   if (kConfigs[id].kind == 6) return launch_gemm_small(id, a, grid, stream);
   switch (id) {
 #define KH_CFGS_CASE(cid, bm, bn, wk, depth)                                                            \
@@ -1319,8 +1325,8 @@ std::unique_ptr<Op> make_gemm(const kh_launch &L, std::string &err, bool &unsupp
   match_direct_epilogue(L, a);
   // LayerNorm prologue (cfg[4] = 1; fp32 small-M configurations holding at
   // most 4 rows per wave, K <= kLnMaxK): A is the LayerNorm's input x and
-  // the product is rstd * ((x - x0) . B - (mean - x0) * g) + c per row (x0
-  // the row's first value, mean = sum(x) * fparams[0], rstd = rsqrt(sum((x -
+  // the product is rstd * ((x - s) . B - (mean - s) * g) + c per row (s the
+  // mean of the row's first 32 values, mean = sum(x) * fparams[0], rstd = rsqrt(sum((x -
   // mean)^2) * fparams[1] + fparams[2])), i.e. LayerNorm(x) . B with the
   // LayerNorm's gamma folded into B: g = refs[cfg[5]] (column sums of B) and
   // c = refs[cfg[6]] (beta . B before the folding; -1: none), both with
@@ -1368,18 +1374,19 @@ std::unique_ptr<Op> make_gemm(const kh_launch &L, std::string &err, bool &unsupp
     }
     op->b_vec_layout = true;
   }
-  if (t.kind == 4 || t.kind == 5 || t.kind == 6) {
+  if (t.kind == 4 || t.kind == 5 || t.kind == 6 || t.kind == 7) {
     // skinny-M direct loads / K-contiguous pipelines: A row-major with unit K
     // stride, B the [batch][N][K] copy, both read as whole 16-byte pieces; K
     // is not split across workgroups (and is a positive whole number of
-    // 32-deep steps for kinds 5 and 6)
+    // steps, 32 or 64 deep, for kinds 5 and 6)
     const kh_ref &ra = L.refs[0], &rb = L.refs[1];
-    const bool steps = t.kind == 5 || t.kind == 6;
+    const bool steps = t.kind == 5 || t.kind == 6 || t.kind == 7;
+    const int step = steps ? t.bk : 4;
     op->b_vec_layout = a.sb_k == 1 && rb.offset % 4 == 0 && a.sb_n % 4 == 0 && a.sb_b % 4 == 0 && a.sb_n >= K;
-    if (!op->a_vec_layout || !op->b_vec_layout || K % (steps ? 32 : 4) || (steps && K == 0) || ra.offset % 4) {
+    if (!op->a_vec_layout || !op->b_vec_layout || K % step || (steps && K == 0) || ra.offset % 4) {
       err = "matmul: configuration " + std::to_string(cfg) +
             " needs A [.., M, K] and B [batch][N][K] with unit K stride, 16-byte aligned rows and K a " +
-            (steps ? std::string("positive multiple of 32") : std::string("multiple of 4"));
+            (steps ? "positive multiple of " + std::to_string(step) : std::string("multiple of 4"));
       return nullptr;
     }
     // buffer-load byte offsets are 32-bit (and must stay below the

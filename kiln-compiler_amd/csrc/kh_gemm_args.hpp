@@ -155,8 +155,21 @@ inline hipError_t launch_splitk_reduce(const GemmArgs &a, int cus, hipStream_t s
   X(93, 128, 192, 2, 2, 3, 2)      \
   X(94, 128, 128, 2, 4, 3, 2)
 
+// Configurations of the bf16 kernel with 64-deep K steps (kind 7,
+// kh_gemm_bf.hip; K a multiple of 64, one tile per workgroup): id, BM x BN,
+// waves WM x WN, stages NS.
+#define KH_GEMM_BF_CONFIGS(X) \
+  X(95, 128, 192, 2, 4, 2)             \
+  X(96, 64, 192, 2, 4, 3)              \
+  X(97, 64, 128, 2, 4, 3)              \
+  X(98, 64, 96, 2, 2, 3)               \
+  X(99, 64, 64, 2, 2, 3)               \
+  X(100, 128, 96, 2, 2, 3)
+
 // Launch configuration `id` of kind 5 (hipErrorInvalidValue for another id).
 hipError_t launch_gemm_nt(int id, const GemmArgs &a, dim3 grid, hipStream_t stream);
+// Launch configuration `id` of kind 7 (hipErrorInvalidValue for another id).
+hipError_t launch_gemm_bf(int id, const GemmArgs &a, dim3 grid, hipStream_t stream);
 
 // Longest row a small-M GEMM's LayerNorm prologue takes.
 constexpr int kLnMaxK = 1024;

@@ -1,0 +1,241 @@
+// kh_gemm_bf.hip - bf16-input matmul with 64-deep K steps (configuration
+// kind 7): C[b] = epilogue(A[b] @ B[b]) with A [.., M, K] fp32 K-contiguous,
+// rounded to bf16 as its fragments are read, and B the bf16 [batch][N][K']
+// copy of a constant (the arithmetic of the other bf16 GEMMs: bf16 inputs,
+// fp32 accumulation).
+//
+// Same contract as the rest of the matmul family (the reference's tl.dot
+// kernel with fused epilogue, kiln/gpu/codegen.py:484-530). A bf16 MFMA step
+// is 16x shorter than an fp32 one, so at one K step per stage of 32 values
+// (kinds 3 and 5) a step's copy wait and barrier cost more than its matrix
+// work. Here:
+//   * a stage holds 64 K values: A rows of 64 floats (16 chunks of 16 bytes,
+//     chunk c of row r at c ^ swz_rows<16>(r)) and bf16 B rows of 64 values
+//     (8 chunks, chunk c of row n at c ^ swz_a(n)), copied with 128-bit
+//     global_load_lds (no VGPRs, no VALU); NS stages in a ring, the copies
+//     of step s + NS - 1 issued right after the barrier of step s;
+//   * a step is two 32-deep halves; in half k2 lane (row li, group g) reads
+//     K values 32 k2 + 8g .. 32 k2 + 8g + 7 of its A rows (two 128-bit
+//     reads, rounded to bf16) and of its B rows (one 128-bit read), and each
+//     16 x 16 output block takes one v_mfma_f32_16x16x32_bf16;
+//   * one tile per workgroup and no persistence: the hardware runs two
+//     workgroups of the smaller tiles per CU, so one's copy latency hides
+//     under the other's MFMAs;
+//   * the epilogue stages the accumulators of 16 rows at a time through the
+//     ring (free once the main loop is done) and reads, computes and writes
+//     row-contiguous groups of 4 columns with 128-bit accesses: bias /
+//     residual / activation directly, other tapes through the tape
+//     interpreter.
+// Measured against the 32-deep K-contiguous kernel on 2048x3072x768 (bf16
+// weights, fp32 activations): 27.5 -> ~20 us per product.
+// K must be a positive multiple of 64 and the operands' spans below 2^29
+// elements (the host checks both).
+#include <algorithm>
+
+#include "kh_common.hpp"
+#include "kh_gemm_args.hpp"
+#include "kh_gemm_dev.hpp"
+#include "kh_internal.hpp"
+
+namespace kh {
+namespace {
+
+template <int BM, int BN, int WM, int WN, int NS, bool TAPE>
+__global__ __launch_bounds__(64 * WM * WN) void gemm_bf_kernel(const GemmArgs a) {
+  constexpr int BK = 64, MT = 16, kWaves = WM * WN;
+  constexpr int TM = BM / WM, TN = BN / WN, FM = TM / MT, FN = TN / MT;
+  constexpr int A_BYTES = BM * BK * 4, STAGE = A_BYTES + BN * BK * 2;   // bytes
+  constexpr int A_PW = BM * 16 / 64 / kWaves, B_PW = BN * 8 / 64 / kWaves, COPIES = A_PW + B_PW;
+  constexpr int CS = TN + 4;   // epilogue staging row stride (floats, 16-byte aligned rows)
+  static_assert(TM % MT == 0 && TN % MT == 0, "wave tile of whole MFMA blocks");
+  static_assert((BM * 16) % (64 * kWaves) == 0 && (BN * 8) % (64 * kWaves) == 0, "copy mapping");
+  static_assert(NS >= 2 && NS <= 4 && (NS - 2) * COPIES < 64, "ring depth / vmcnt range");
+  static_assert(NS * STAGE <= 160 * 1024 && kWaves * MT * CS * 4 <= NS * STAGE, "LDS: ring, staging inside it");
+  __shared__ float4 ring4[NS * STAGE / 16];
+  char *ring = reinterpret_cast<char *>(ring4);
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  const int wm = wave / WN, wn = wave % WN, li = lane & 15, g = lane >> 4;
+  const int bidx = blockIdx.y;
+  int tm, tn;
+  tile_coords(blockIdx.x, a, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  const float *Ab = a.A + (int64_t)bidx * a.sa_b;
+  const __bf16 *Bb = reinterpret_cast<const __bf16 *>(a.B) + (int64_t)bidx * a.sb_b;
+
+  // per-lane copy sources: byte offsets from the step's first K column (rows
+  // past M / N clamped to the last one; their results are never stored)
+  uint32_t a_off[A_PW], b_off[B_PW];
+#pragma unroll
+  for (int i = 0; i < A_PW; ++i) {
+    const int p = (wave * A_PW + i) * 64 + lane, r = p / 16;
+    a_off[i] = (uint32_t)(min(m0 + r, a.M - 1) * (int)a.sa_m + ((p % 16) ^ swz_rows<16>(r)) * 4) * 4u;
+  }
+#pragma unroll
+  for (int i = 0; i < B_PW; ++i) {
+    const int p = (wave * B_PW + i) * 64 + lane, r = p / 8;
+    b_off[i] = (uint32_t)(min(n0 + r, a.N - 1) * (int)a.sb_n + ((p % 8) ^ swz_a(r)) * 8) * 2u;
+  }
+  const int n_steps = a.K / BK;   // the host checks K % 64 == 0 and K > 0
+  auto issue = [&](int step) {
+    const float *ab = uniform_ptr(Ab + step * BK);
+    const float *bb = uniform_ptr(reinterpret_cast<const float *>(Bb + step * BK));
+    const uint32_t lds = (uint32_t)(uintptr_t)(lds_void_t *)(ring + (step % NS) * STAGE);
+#pragma unroll
+    for (int i = 0; i < A_PW; ++i) copy_to_lds<4>(ab, a_off[i], lds + (wave_u * A_PW + i) * 1024);
+#pragma unroll
+    for (int i = 0; i < B_PW; ++i) copy_to_lds<4>(bb, b_off[i], lds + A_BYTES + (wave_u * B_PW + i) * 1024);
+  };
+  // fragment byte offsets within a stage, per 32-deep half k2
+  int fa[FM][2][2], fb[FN][2];
+#pragma unroll
+  for (int fm = 0; fm < FM; ++fm) {
+    const int r = wm * TM + fm * MT + li;
+#pragma unroll
+    for (int k2 = 0; k2 < 2; ++k2)
+#pragma unroll
+      for (int q = 0; q < 2; ++q) fa[fm][k2][q] = r * 256 + ((8 * k2 + 2 * g + q) ^ swz_rows<16>(r)) * 16;
+  }
+#pragma unroll
+  for (int fn = 0; fn < FN; ++fn) {
+    const int r = wn * TN + fn * MT + li;
+#pragma unroll
+    for (int k2 = 0; k2 < 2; ++k2) fb[fn][k2] = A_BYTES + r * 128 + ((4 * k2 + g) ^ swz_a(r)) * 16;
+  }
+  f32x4 acc[FM][FN];
+#pragma unroll
+  for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn) acc[fm][fn] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int p = 0; p < NS - 1 && p < n_steps; ++p) issue(p);
+  // direct epilogue: operand pointers, strides and layouts, read from the
+  // kernel arguments here (scalar loads whose indices are themselves loaded:
+  // issued at the end of the tile they would be two dependent memory round
+  // trips in front of the first store, ~2 us per tile)
+  const bool has_b = a.d_bias >= 0, has_r = a.d_res >= 0;
+  const int jb = has_b ? a.d_bias : 0, jr = has_r ? a.d_res : 0, jo = TAPE ? 0 : a.d_out;
+  const float *pb = a.eptr[jb] + (int64_t)bidx * a.estride[jb][0];
+  const float *pr = a.eptr[jr] + (int64_t)bidx * a.estride[jr][0];
+  float *po = a.eptr[jo] + (int64_t)bidx * a.estride[jo][0];
+  const int64_t sbn = a.estride[jb][2], srm = a.estride[jr][1], srn = a.estride[jr][2];
+  const int64_t som = a.estride[jo][1], son = a.estride[jo][2];
+  const bool vb = a.e_vec_mask >> jb & 1, vr = a.e_vec_mask >> jr & 1, vo = a.e_vec_mask >> jo & 1;
+  const int act = a.d_act, M = a.M, N = a.N;
+  for (int s = 0; s < n_steps; ++s) {
+    // this wave's copies of step s landed (the copies of `later` steps were
+    // issued after them), then every wave's: the barrier also says that every
+    // wave is done reading stage s - 1, whose slot the next copies refill
+    const int later = min(NS - 2, n_steps - 1 - s);
+    if (later <= 0) wait_vmcnt<0>();
+    else if (later == 1) wait_vmcnt<COPIES>();
+    else wait_vmcnt<2 * COPIES>();
+    stage_barrier();
+    if (s + NS - 1 < n_steps) issue(s + NS - 1);
+    const char *st = ring + (s % NS) * STAGE;
+#pragma unroll
+    for (int k2 = 0; k2 < 2; ++k2) {
+      bf16x8 xa[FM], xb[FN];
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm) {
+        const float4 lo = *reinterpret_cast<const float4 *>(st + fa[fm][k2][0]);
+        const float4 hi = *reinterpret_cast<const float4 *>(st + fa[fm][k2][1]);
+        xa[fm][0] = (__bf16)lo.x, xa[fm][1] = (__bf16)lo.y, xa[fm][2] = (__bf16)lo.z, xa[fm][3] = (__bf16)lo.w;
+        xa[fm][4] = (__bf16)hi.x, xa[fm][5] = (__bf16)hi.y, xa[fm][6] = (__bf16)hi.z, xa[fm][7] = (__bf16)hi.w;
+      }
+#pragma unroll
+      for (int fn = 0; fn < FN; ++fn) xb[fn] = *reinterpret_cast<const bf16x8 *>(st + fb[fn][k2]);
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+        for (int fn = 0; fn < FN; ++fn)
+          acc[fm][fn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xa[fm], xb[fn], acc[fm][fn], 0, 0, 0);
+    }
+  }
+
+  // epilogue: 16-row blocks of the wave tile through the wave's slice of the
+  // ring (its own, and LDS operations of one wave complete in order)
+  __syncthreads();   // every wave's fragment reads of the ring are done
+  float *Cw = reinterpret_cast<float *>(ring) + wave * MT * CS;
+  const int row0 = m0 + wm * TM, col0 = n0 + wn * TN;
+#pragma unroll
+  for (int fm = 0; fm < FM; ++fm) {
+#pragma unroll
+    for (int fn = 0; fn < FN; ++fn)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) Cw[(4 * g + i) * CS + fn * MT + li] = acc[fm][fn][i];
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int q = lane; q < MT * TN / 4; q += 64) {
+      const int r = q / (TN / 4), c = (q % (TN / 4)) * 4;
+      const int m = row0 + fm * MT + r, n = col0 + c;
+      if (m < M && n < N) {
+        const float4 p = *reinterpret_cast<const float4 *>(Cw + r * CS + c);
+        const int valid = min(4, N - n);
+        if constexpr (TAPE) {
+          Vec<4> v;
+          v.v[0] = p.x, v.v[1] = p.y, v.v[2] = p.z, v.v[3] = p.w;
+          run_epilogue(a, bidx, m, n, valid, v);
+        } else {
+          // out = act((acc [+ bias]) [+ res]), in the tape's order
+          float v[4] = {p.x, p.y, p.z, p.w};
+          if (has_b) {
+            if (vb && valid == 4) {
+              const float4 t = *reinterpret_cast<const float4 *>(pb + n);
+              v[0] += t.x, v[1] += t.y, v[2] += t.z, v[3] += t.w;
+            } else {
+              for (int i = 0; i < valid; ++i) v[i] += pb[(int64_t)(n + i) * sbn];
+            }
+          }
+          if (has_r) {
+            const float *rr = pr + (int64_t)m * srm;
+            if (vr && valid == 4) {
+              const float4 t = *reinterpret_cast<const float4 *>(rr + n);
+              v[0] = t.x + v[0], v[1] = t.y + v[1], v[2] = t.z + v[2], v[3] = t.w + v[3];
+            } else {
+              for (int i = 0; i < valid; ++i) v[i] = rr[(int64_t)(n + i) * srn] + v[i];
+            }
+          }
+          if (act == KH_OP_GELU_TANH) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = op_gelu_tanh(v[i]);
+          } else if (act == KH_OP_GELU_ERF) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = op_gelu_erf(v[i]);
+          } else if (act == KH_OP_RELU) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = v[i] != v[i] ? v[i] : fmaxf(v[i], 0.0f);
+          }
+          float *o = po + (int64_t)m * som;
+          if (vo && valid == 4) {
+            *reinterpret_cast<float4 *>(o + n) = make_float4(v[0], v[1], v[2], v[3]);
+          } else {
+            for (int i = 0; i < valid; ++i) o[(int64_t)(n + i) * son] = v[i];
+          }
+        }
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+}
+
+}  // namespace
+
+hipError_t launch_gemm_bf(int id, const GemmArgs &a, dim3 grid, hipStream_t stream) {
+  switch (id) {
+#define KH_CFGBF_CASE(cid, bm, bn, wm, wn, ns)                                                                 \
+  case cid:                                                                                                    \
+    if (a.direct)                                                                                              \
+      hipLaunchKernelGGL((gemm_bf_kernel<bm, bn, wm, wn, ns, false>), grid, dim3(64 * wm * wn), 0, stream, a); \
+    else                                                                                                       \
+      hipLaunchKernelGGL((gemm_bf_kernel<bm, bn, wm, wn, ns, true>), grid, dim3(64 * wm * wn), 0, stream, a);  \
+    break;
+    KH_GEMM_BF_CONFIGS(KH_CFGBF_CASE)
+#undef KH_CFGBF_CASE
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace kh

@@ -155,6 +155,13 @@ TILES = {
     92: (128, 256, 32, 2, 4, 1, 16),
     93: (128, 192, 32, 2, 2, 1, 16),
     94: (128, 128, 32, 2, 4, 1, 16),
+    # the bf16 K-contiguous kernel with 64-deep K steps (K a multiple of 64)
+    95: (128, 192, 64, 2, 4, 1, 16),
+    96: (64, 192, 64, 2, 4, 1, 16),
+    97: (64, 128, 64, 2, 4, 1, 16),
+    98: (64, 96, 64, 2, 2, 1, 16),
+    99: (64, 64, 64, 2, 2, 1, 16),
+    100: (128, 96, 64, 2, 2, 1, 16),
 }
 # configurations of the skinny-M kernel: A row-major with unit K stride and
 # K % 4 == 0, B a constant read through its [batch][N][K] copy, no split-K;
@@ -163,7 +170,7 @@ TILES = {
 SKINNY = frozenset(range(47, 55))
 # configurations of the K-contiguous pipeline: A as for the skinny kernel, B
 # the [batch][N][K] copy of a constant, K a multiple of 32, no split-K
-K_CONTIGUOUS = frozenset(range(55, 65)) | frozenset(range(87, 95))
+K_CONTIGUOUS = frozenset(range(55, 65)) | frozenset(range(87, 101))
 # configurations of the small-M kernel: as the K-contiguous pipeline (B the
 # [batch][N][K] copy, K a positive multiple of 32, no split-K), for products
 # with at most SMALL_M_MAX rows
@@ -173,12 +180,13 @@ SMALL_M_MAX = 1024
 NK_B = SKINNY | K_CONTIGUOUS | SMALL_M
 SKINNY_DEPTH = {47: 8, 48: 4, 49: 8, 50: 4, 51: 4, 52: 8, 53: 4, 54: 8}
 SKINNY_TURNS = 4
-# input precision of each configuration: 15-20, 34-41, 75-79, 84-85 and 87-91
+# input precision of each configuration: 15-20, 34-41, 75-79, 84-85, 87-91 and 95-100
 # bf16 (A rounded in the kernel, B a bf16 copy of a constant), 26-31, 42-45,
 # 80-83, 86 and 92-94 three-pass bf16
 # (allow_tf32: A and B split into bf16 hi + lo, three products), the others
 # fp32
 PRECISION = {t: ("bf16" if 15 <= t <= 20 or 34 <= t <= 41 or 75 <= t <= 79 or t in (84, 85) or 87 <= t <= 91
+                 or 95 <= t <= 100
                  else "bf16x3" if 26 <= t <= 31 or 42 <= t <= 45 or 80 <= t <= 83 or t == 86 or 92 <= t <= 94
                  else "fp32")
              for t in TILES}
@@ -193,7 +201,8 @@ OCCUPANCY = {0: 2, 1: 2, 2: 3, 3: 2, 4: 4, 5: 2, 6: 1, 7: 1, 8: 4, 9: 4, 10: 4, 
              55: 1, 56: 1, 57: 1, 58: 1, 59: 1, 60: 1, 61: 1, 62: 1, 63: 1, 64: 1,
              65: 2, 66: 3, 67: 3, 68: 1, 69: 2, 70: 1, 71: 2, 72: 1, 73: 1, 74: 4,
              75: 4, 76: 2, 77: 3, 78: 3, 79: 4, 80: 3, 81: 2, 82: 2, 83: 4, 84: 2, 85: 1, 86: 2,
-             87: 1, 88: 1, 89: 1, 90: 1, 91: 1, 92: 1, 93: 1, 94: 1}
+             87: 1, 88: 1, 89: 1, 90: 1, 91: 1, 92: 1, 93: 1, 94: 1,
+             95: 1, 96: 1, 97: 1, 98: 1, 99: 1, 100: 1}
 EFFICIENCY = {0: 0.62, 1: 0.6, 2: 0.62, 3: 0.58, 4: 0.66, 5: 0.62, 6: 0.67, 7: 0.55,
               8: 0.55, 9: 0.55, 10: 0.5, 11: 0.5, 12: 0.45, 13: 0.5, 14: 0.55,
               15: 0.15, 16: 0.15, 17: 0.15, 18: 0.15, 19: 0.15, 20: 0.15,
@@ -206,7 +215,8 @@ EFFICIENCY = {0: 0.62, 1: 0.6, 2: 0.62, 3: 0.58, 4: 0.66, 5: 0.62, 6: 0.67, 7: 0
               65: 0.5, 66: 0.5, 67: 0.45, 68: 0.5, 69: 0.5, 70: 0.5, 71: 0.45, 72: 0.5, 73: 0.5, 74: 0.45,
               75: 0.12, 76: 0.12, 77: 0.12, 78: 0.12, 79: 0.1, 80: 0.25, 81: 0.25, 82: 0.25, 83: 0.2,
               84: 0.1, 85: 0.12, 86: 0.2,
-              87: 0.2, 88: 0.2, 89: 0.2, 90: 0.2, 91: 0.2, 92: 0.35, 93: 0.35, 94: 0.35}
+              87: 0.2, 88: 0.2, 89: 0.2, 90: 0.2, 91: 0.2, 92: 0.35, 93: 0.35, 94: 0.35,
+              95: 0.3, 96: 0.28, 97: 0.26, 98: 0.26, 99: 0.25, 100: 0.26}
 # MFMA rate of a CU relative to fp32, per precision
 RATE = {"fp32": 1.0, "bf16": 16.0, "bf16x3": 16.0 / 3}
 CU_MFLOP_PER_US = 0.614          # fp32 MFMA: 256 flop/clk/CU at 2.4 GHz
@@ -249,7 +259,7 @@ def k_major_fits(m, k, tile) -> bool:
         return skinny_fits(m, k, tile)
     if tile in SMALL_M and m > SMALL_M_MAX:
         return False
-    return k % 32 == 0 and k > 0
+    return k % TILES[tile][2] == 0 and k > 0
 
 
 def fits(tile, m, n, k) -> bool:

@@ -108,9 +108,11 @@ def test_k_contiguous_bf16_tiles_walk_several_tiles(tile):
     # than CUs (each workgroup walks several, the next tile's first stages
     # issued before the current epilogue) with ragged edges, fewer steps than
     # ring stages and many steps; direct epilogue (bias + residual) and the
-    # tape epilogue (a scale); repeated calls agree bit for bit
+    # tape epilogue (a scale); repeated calls agree bit for bit. K is a
+    # whole number of the tile's K steps (32 or 64 deep)
     cfg = lambda *_: {"tile": tile, "splitk": 1}
-    for m, n, k in ((4200, 2600, 64), (4200, 2600, 160), (300, 452, 768)):
+    deep = autotune.TILES[tile][2]
+    for m, n, k in ((4200, 2600, 64), (4200, 2600, 5 * deep), (300, 452, 768)):
         torch.manual_seed(m + k)
         lin = gpt2_init_(torch.nn.Linear(k, n), seed=k).eval()
         x, r = torch.randn(m, k), torch.randn(m, n)
@@ -127,9 +129,9 @@ def test_k_contiguous_bf16_tiles_walk_several_tiles(tile):
             assert torch.equal(c(*args), out)
     # batched constant weights: each batch reads its own slice of the copy
     torch.manual_seed(tile)
-    model = _Batched(torch.randn(3, 96, 50) * 0.1).eval()
+    model = _Batched(torch.randn(3, 3 * deep, 50) * 0.1).eval()
     w = model.w.detach()
-    x = torch.randn(3, 300, 96)
+    x = torch.randn(3, 300, 3 * deep)
     c = kiln.compile(model, (x,), device="cuda", matmul_precision="bf16", gpu_matmul_config=cfg)
     assert f"tile {tile} splitk 1" in c._exe.program.launches[0].summary
     ref = np.stack([r16(x[i].numpy()) @ r16(w[i].numpy()) for i in range(3)]) * 0.5
