@@ -5,9 +5,13 @@
 Headline (the timed steps): one GPT-2-small block (pre-LN, d 768, 12 heads,
 causal, fp32, random init N(0, 0.02), LN gamma 1 / beta 0, seeded input
 [T, 768] ~ N(0, 1)) compiled by kiln.compile(device="cuda", autotune=True);
-a step is one call as a user makes it (copy input in, one hipGraph replay of
-the 11-launch plan, clone output out). `value` = ms per step, averaged over
-exactly K steps between synchronisations, after W warm-up steps.
+a step is one call as a user makes it, with the input already in HBM: the
+plan's launches run on the caller's tensors ("direct"), or the input is
+copied into the static buffers, the captured hipGraph is replayed and the
+output cloned ("graph"), whichever the executable's first call measured
+faster (config.call_mode says which; the block sweep reports both paths at
+every T). `value` = ms per step, averaged over exactly K steps between
+synchronisations, after W warm-up steps.
 
 Also reported (outside the timed steps, and run before them so the timed
 steps see a GPU whose clocks are up): block latency at 128/512/1024/2048
@@ -16,10 +20,10 @@ and the per-call memory of each, the GEMM sweep in TFLOP/s, the fused
 memory-bound ops in GB/s (hot = same buffers, as the reference times them;
 cold = buffers rotated over > 512 MiB so the 256 MiB Infinity Cache cannot
 hold them), the 12-layer stack, the roofline of the block's dominant kernel,
-and the CPU baseline: eager PyTorch CPU fp32 running the headline block on
-this host at one thread and at all the cores the process may use (best of 3,
-the reference's bench_block.py method), with the C oracle (float64, one
-thread) as a separately labelled line.
+and the CPU baseline: the C oracle (the port of the reference's algorithm,
+float64, one thread) on the headline block, with eager PyTorch CPU fp32 on the
+same block at one thread and at all the cores the process may use (best of
+3, the reference's bench_block.py method) as separately labelled lines.
 """
 
 from __future__ import annotations
@@ -478,6 +482,11 @@ def block_sweep(tokens, autotune, inductor=True):
             e_ms = ms_per_call(lambda: model(x))
             c._exe.replay_only()
             replay_ms = min(events_ms(c._exe.replay_only, 20) for _ in range(5))
+            # both call paths end to end: copy in + replay + clone out, and the
+            # launches straight on the caller's tensors
+            ready = c._exe._prepare((x,))
+            graph_e2e_ms = ms_per_call(lambda: c._exe._replay(ready))
+            direct_ms = ms_per_call(lambda: c._exe._direct(ready))
         kiln_mib = c.report.arena_bytes / 2**20 + peak_mib(c, x)
         eager_mib = peak_mib(model, x)
         ind_ms = inductor_ms(model, x, "reduce-overhead") if inductor else None
@@ -489,14 +498,26 @@ def block_sweep(tokens, autotune, inductor=True):
             tf_err = ((ct(x).double() - ref64).abs().max() / ref64.abs().max()).item()
             assert tf_err <= 5e-5, f"block T={T} allow_tf32: error {tf_err:.2e} of the output scale"
             tf_ms = ms_per_call(lambda: ct(x))
+        # the bf16-input / fp32-accumulate variant (matmul_precision="bf16"):
+        # reported beside, with its error against float64
+        cb = kiln.compile(model, (x,), device="cuda", autotune=autotune, matmul_precision="bf16")
+        with torch.no_grad():
+            bf_err = ((cb(x).double() - ref64).abs().max() / ref64.abs().max()).item()
+            assert bf_err <= 2e-2, f"block T={T} bf16: error {bf_err:.2e} of the output scale"
+            bf_ms = ms_per_call(lambda: cb(x))
         out[str(T)] = {"kiln_ms": round(k_ms, 4), "eager_ms": round(e_ms, 4), "replay_ms": round(replay_ms, 4),
+                       "call_mode": c._exe.mode, "graph_e2e_ms": round(graph_e2e_ms, 4),
+                       "direct_ms": round(direct_ms, 4), "launches": c.report.lowering["launches"],
                        "inductor_ms": round(ind_ms, 4) if ind_ms else None,
                        "speedup": round(e_ms / k_ms, 3), "tflops": round(block_flops(T) / k_ms / 1e9, 2),
                        "arena_mib": round(c.report.arena_bytes / 2**20, 2),
                        "kiln_mib": round(kiln_mib, 2), "eager_mib": round(eager_mib, 2),
-                       "allow_tf32_ms": round(tf_ms, 4), "allow_tf32_error_of_scale": float(f"{tf_err:.2e}")}
-        log(f"block T={T}: kiln {k_ms:.4f} ms (replay {replay_ms:.4f}), eager {e_ms:.4f} ms, "
-            f"inductor {ind_ms if ind_ms else float('nan'):.4f} ms, allow_tf32 {tf_ms:.4f} ms, "
+                       "allow_tf32_ms": round(tf_ms, 4), "allow_tf32_error_of_scale": float(f"{tf_err:.2e}"),
+                       "bf16_ms": round(bf_ms, 4), "bf16_error_of_scale": float(f"{bf_err:.2e}"),
+                       "bf16_launches": cb.report.lowering["launches"]}
+        log(f"block T={T}: kiln {k_ms:.4f} ms ({c._exe.mode}; graph path {graph_e2e_ms:.4f}, direct {direct_ms:.4f}, "
+            f"replay alone {replay_ms:.4f}), eager {e_ms:.4f} ms, "
+            f"inductor {ind_ms if ind_ms else float('nan'):.4f} ms, allow_tf32 {tf_ms:.4f} ms, bf16 {bf_ms:.4f} ms, "
             f"MiB kiln {kiln_mib:.1f} / eager {eager_mib:.1f}")
     return out
 
@@ -638,14 +659,29 @@ def fused_ops():
             c._exe.run_into([xs[i]], [ys[i]])
 
         cold = graph_ms(step, repeats=n, rounds=3)
+        # a device copy of the same shape (the same bytes read and written,
+        # one launch), hot and cold the same way: what any single launch of
+        # this size can reach on this box
+        copy_hot = graph_ms(lambda: y.copy_(x))
+
+        def copy_step():
+            i = state["i"] % n
+            state["i"] += 1
+            ys[i].copy_(xs[i])
+
+        copy_cold = graph_ms(copy_step, repeats=n, rounds=3)
         with torch.no_grad():
             eager = graph_ms(lambda: fn(x))
         out[name] = {"kiln_hot_us": round(hot * 1e3, 2), "kiln_cold_us": round(cold * 1e3, 2),
                      "eager_hot_us": round(eager * 1e3, 2),
+                     "copy_hot_us": round(copy_hot * 1e3, 2), "copy_cold_us": round(copy_cold * 1e3, 2),
                      "hot_gbs": round(nbytes / hot / 1e6, 1), "cold_gbs": round(nbytes / cold / 1e6, 1),
-                     "cold_hbm_frac": round(nbytes / cold / 1e6 / HBM_PEAK_GBS, 3), "bytes": nbytes}
+                     "cold_hbm_frac": round(nbytes / cold / 1e6 / HBM_PEAK_GBS, 3),
+                     "cold_of_copy": round(copy_cold / cold, 3), "hot_of_copy": round(copy_hot / hot, 3),
+                     "bytes": nbytes}
         log(f"{name}: hot {hot * 1e3:.2f} us ({nbytes / hot / 1e6:.0f} GB/s), cold {cold * 1e3:.2f} us "
-            f"({nbytes / cold / 1e6:.0f} GB/s), eager {eager * 1e3:.2f} us")
+            f"({nbytes / cold / 1e6:.0f} GB/s, {copy_cold / cold:.2f} of a copy's {copy_cold * 1e3:.2f} us), "
+            f"eager {eager * 1e3:.2f} us")
         del xs, ys
         torch.cuda.empty_cache()
     # the same kernels at 1.5 GiB of traffic per call (six times the Infinity
@@ -743,13 +779,14 @@ def cpu_ms_per_call(fn, x, min_time=1.0):
 
 
 def cpu_baseline(T, oracle_line=True):
-    """Eager PyTorch CPU fp32 on the headline block (same weights and input as
-    the GPU run) at 1 thread (the reference's convention,
-    benchmarks/bench_block.py:61) and at every core this process may use
-    (capped by OMP_NUM_THREADS, the box's CPU share). The reference's own CPU
-    path (MLIR -> LLVM JIT) cannot be built here: no MLIR bindings, an empty
-    LLVM pin, a network-only build script. The C oracle (float64, one thread)
-    is timed once as a separately labelled line."""
+    """The C oracle (oracle/kiln_oracle.c: the CPU port of the reference's
+    algorithm for the block, float64 naive loops, one thread) on the headline
+    block with the GPU run's weights and input, twice (~12 s): the `port`
+    baseline. Beside it, eager PyTorch CPU fp32 on the same block at 1 thread
+    (the reference's convention, benchmarks/bench_block.py:61) and at every
+    core this process may use (capped by OMP_NUM_THREADS, the box's CPU
+    share). The reference's own CPU path (MLIR -> LLVM JIT) cannot be built
+    here: no MLIR bindings, an empty LLVM pin, a network-only build script."""
     import torch
 
     from models.transformer import Block, gpt2_init_
@@ -769,22 +806,29 @@ def cpu_baseline(T, oracle_line=True):
     finally:
         torch.set_num_threads(before)
     log(f"cpu baseline: eager PyTorch CPU fp32 block T={T}: {one:.1f} ms at 1 thread, {many:.1f} ms at {cores}")
-    out = {"value": round(many, 2), "unit": "ms", "cores": cores, "kind": "port",
-           "impl": "eager PyTorch CPU fp32 (torch " + torch.__version__ + ")",
-           "cpu_model": cpu_model(),
-           "sample": f"one full GPT-2-small block forward at T={T} (the headline workload, same seeded weights and "
-                     f"input), best of 3 rounds after calibration (reference benchmarks/bench_block.py:41-54)",
-           "single_thread": {"value": round(one, 2), "unit": "ms", "cores": 1},
+    eager = {"value": round(many, 2), "unit": "ms", "cores": cores,
+             "impl": "eager PyTorch CPU fp32 (torch " + torch.__version__ + ")",
+             "sample": f"one full GPT-2-small block forward at T={T}, best of 3 rounds after calibration "
+                       f"(reference benchmarks/bench_block.py:41-54)",
+             "single_thread": {"value": round(one, 2), "unit": "ms", "cores": 1}}
+    out = {"value": None, "unit": "ms", "cores": 1, "kind": "port",
+           "impl": "oracle/kiln_oracle.c: the C port of the reference's block algorithm, float64 naive loops",
+           "cpu_model": cpu_model(), "eager_pytorch_cpu": eager,
            "reference_cpu_path": "unavailable: MLIR Python bindings absent, LLVM pin empty, network-only build"}
     if oracle_line:
         import oracle
 
         params = {k: v.numpy() for k, v in model.state_dict().items()}
         oracle.lib()
-        t0 = time.perf_counter()
-        oracle.block(x.numpy(), params, 12)
-        out["oracle_port"] = {"value": round((time.perf_counter() - t0) * 1e3, 1), "unit": "ms", "cores": 1,
-                              "impl": "oracle/kiln_oracle.c, float64 naive loops (the parity checker)"}
+        runs = []
+        for _ in range(2):
+            t0 = time.perf_counter()
+            oracle.block(x.numpy(), params, 12)
+            runs.append((time.perf_counter() - t0) * 1e3)
+        out["value"] = round(min(runs), 1)
+        out["sample"] = (f"one full GPT-2-small block forward at T={T} (the headline workload, same seeded weights and "
+                         f"input), best of {len(runs)} runs ({sum(runs) / 1e3:.1f} s of CPU work)")
+        log(f"cpu baseline: C oracle (float64, 1 thread) block T={T}: {out['value']:.1f} ms")
     return out
 
 
@@ -836,7 +880,8 @@ def main():
         "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "fp32", "data": "synthetic (seeded N(0,1) input, random-init N(0,0.02) weights)",
         "config": {"workload": f"gpt2_small_block_T{args.tokens}", "tokens": args.tokens, "d_model": 768,
-                   "heads": 12, "parallelism": "none (1 GPU)"},
+                   "heads": 12, "parallelism": "none (1 GPU)", "call_mode": compiled._exe.mode,
+                   "launches": compiled.report.lowering["launches"]},
         "roofline": roofline, "cpu_baseline": cpu,
         "device": info, "per_launch_ms": {n: round(t, 5) for n, t in prof}, **extra,
     }

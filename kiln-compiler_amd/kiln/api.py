@@ -45,7 +45,8 @@ class Options:
     cuda_graphs: bool = True     # replay the whole plan as one hipGraph
     gpu_matmul_config: object = None  # fn(graph, kernel) -> {"tile": id, "splitk": s}, overrides tuning
     matmul_precision: str = "fp32"    # GEMM inputs: "fp32" | "bf16" (fp32 accumulate) | "bf16x3"
-    debug: bool = False          # NaN-poison the arena, synchronise after every run
+    debug: bool = False          # launch by launch: NaN-poison each arena buffer before the launch that first
+                                 # writes it, canaries between buffers checked after every launch
     fused_attention: bool = True # scores -> softmax -> (x V) as one launch (needs fusion)
     plan_cache: bool = True      # reuse plans lowered earlier for the same graph and settings
     gemv_chains: bool = False    # consecutive one-row matmuls (decode) as one persistent launch (measured
@@ -121,8 +122,12 @@ def build_passes(options: Options, tuner=None) -> list:
         pipeline += [FreezeParameters(), ConstantFold(), *[type(p)() for p in cleanup]]
     pipeline.append(DCE())
     pipeline.append(Fusion() if options.fusion else OneOpPerKernel())
-    pipeline += [BufferAssignment(), MemoryPlan(reuse=options.memory_plan)]
+    pipeline += [BufferAssignment(), MemoryPlan(reuse=options.memory_plan, guard=DEBUG_GUARD_BYTES if options.debug else 0)]
     return pipeline
+
+
+# canary bytes after every arena buffer in debug builds (Options.debug)
+DEBUG_GUARD_BYTES = 256
 
 
 def compile_graph(graph: Graph, options: Options | None = None):

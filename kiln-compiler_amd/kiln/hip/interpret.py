@@ -57,7 +57,24 @@ class HostExecutable:
         self.weight_bytes = sum(int(c.nbytes) for c in self.constants)
         self.arena_bytes = arena_bytes
         self.arena = np.full(max(arena_bytes, 256) // 4, np.nan, dtype=np.float32)
-        self.plan.bind([_ptr(c) for c in self.constants], _ptr(self.arena), None, 0)
+        consts = [_ptr(c) for c in self.constants]
+        self.plan.bind(consts, _ptr(self.arena), None, 0)
+        self.guards = None
+        if debug:
+            # launch by launch (one single-launch plan each), NaN poison and
+            # canaries as on the device (kiln/hip/debug.py)
+            from kiln.api import DEBUG_GUARD_BYTES
+            from kiln.hip.debug import ArenaGuards, numpy_ops
+
+            self.guards = ArenaGuards(program, DEBUG_GUARD_BYTES)
+            if self.guards.words_needed() > self.arena.size:
+                raise RuntimeError("debug: the arena has no room for its buffers' guards (stale plan?)")
+            self._guard_ops = numpy_ops(self.arena.view(np.int32))
+            self._single = []
+            for launch in program.launches:
+                one = kl.Plan([launch.desc])
+                one.bind(consts, _ptr(self.arena), None, 0)
+                self._single.append(one)
 
     def _prepare(self, inputs):
         if len(inputs) != len(self.input_shapes):
@@ -73,5 +90,13 @@ class HostExecutable:
     def __call__(self, *inputs):
         ins = self._prepare(inputs)
         outs = [np.full(s, np.nan, dtype=np.float32) for s in self.output_shapes]
-        self.plan.run_host([_ptr(a) for a in ins], [_ptr(a) for a in outs])
+        in_ptrs, out_ptrs = [_ptr(a) for a in ins], [_ptr(a) for a in outs]
+        if self.guards is None:
+            self.plan.run_host(in_ptrs, out_ptrs)
+        else:
+            fill, differs = self._guard_ops
+            for i, one in enumerate(self._single):
+                self.guards.before(i, fill)
+                one.run_host(in_ptrs, out_ptrs)
+                self.guards.after(i, differs)
         return [torch.from_numpy(o) for o in outs]

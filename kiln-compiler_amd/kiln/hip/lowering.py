@@ -65,6 +65,11 @@ class Program:
     # element offset, strides over (b, k, n), batch, K, N); today the bf16
     # [batch][N][K'] copies of GEMM B operands (kiln/hip/bf16.py)
     derived: dict = field(default_factory=dict)
+    # arena buffers: (label, byte offset, bytes, first launch, last launch)
+    # - the launches during which the buffer holds a live value (written by
+    # the first, read up to the last); the debug runtime poisons a buffer
+    # before its first launch and checks the canary after it while it lives
+    arena_buffers: list = field(default_factory=list)
 
     @property
     def source(self) -> str:
@@ -1147,6 +1152,17 @@ class _Lowerer:
                 self.lower_reduction(k)
             else:
                 self.lower_elementwise(k)
+        from kiln.passes.memory_plan import live_ranges
+
+        kernel_index = {k.name: i for i, k in enumerate(self.g.kernels)}
+        launch_kernel = [kernel_index.get(launch.kernel, -1) for launch in self.program.launches]
+        for v, (kf, kl_) in live_ranges(self.g).items():
+            live = [i for i, ki in enumerate(launch_kernel) if kf <= ki <= kl_]
+            if live:
+                label = f"{self.g.kernels[kf].name} {v.node.op} {list(v.shape)}"
+                self.program.arena_buffers.append((label, int(v.node.attrs.get("offset", 0)), int(v.type.nbytes),
+                                                   live[0], live[-1]))
+        self.program.arena_buffers.sort(key=lambda b: b[1])
         return self.program
 
 

@@ -31,7 +31,7 @@ from pathlib import Path
 
 from kiln.hip import lib as kl
 
-FORMAT = 2
+FORMAT = 3
 
 
 def cache_dir() -> Path:
@@ -102,6 +102,7 @@ def save(key: str, program, autotune_log=()) -> Path:
     record = {
         "format": FORMAT, "key": key, "precision": program.precision, "consts": list(program.consts),
         "derived": {name: list(recipe) for name, recipe in program.derived.items()},
+        "arena_buffers": [list(b) for b in program.arena_buffers],
         "launches": [{"name": l.name, "kernel": l.kernel, "family": l.family, "summary": l.summary,
                       "flops": l.flops, "bytes": l.bytes,
                       "desc": base64.b64encode(bytes(l.desc)).decode()} for l in program.launches],
@@ -139,7 +140,9 @@ def load(key: str):
                                    kl.LaunchDesc.from_buffer_copy(raw), item["summary"], int(item["flops"]),
                                    int(item["bytes"])))
         program = Program(launches=launches, consts=list(record["consts"]), precision=record["precision"],
-                          derived={name: _recipe(r) for name, r in record["derived"].items()})
+                          derived={name: _recipe(r) for name, r in record["derived"].items()},
+                          arena_buffers=[(str(b[0]), int(b[1]), int(b[2]), int(b[3]), int(b[4]))
+                                         for b in record.get("arena_buffers", [])])
         log = [dict(e, shape=tuple(e["shape"]), source="cache") for e in record.get("autotune", [])]
         return program, log
     except (OSError, ValueError, KeyError, TypeError, IndexError):

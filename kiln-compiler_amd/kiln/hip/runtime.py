@@ -170,7 +170,17 @@ class HIPExecutable:
         self.constants = [torch.from_numpy(h).to(self.device) for h in host]
         self.plan.bind([c.data_ptr() for c in self.constants], self.arena.data_ptr(),
                        self.workspace.data_ptr() if ws else None, ws)
+        self.guards = None
         if debug:
+            # launch by launch, NaN poison and canaries (kiln/hip/debug.py)
+            from kiln.api import DEBUG_GUARD_BYTES
+            from kiln.hip.debug import ArenaGuards, torch_ops
+
+            self.guards = ArenaGuards(program, DEBUG_GUARD_BYTES)
+            words = self.arena[: self.arena.numel() // 4 * 4].view(torch.int32)
+            if self.guards.words_needed() > words.numel():
+                raise RuntimeError("debug: the arena has no room for its buffers' guards (stale plan?)")
+            self._guard_ops = torch_ops(words)
             self.arena.view(torch.float32)[: self.arena.numel() // 4].fill_(float("nan"))
         self._static = None   # (inputs, outputs) the hipGraph was captured over
         # with hipGraphs on, calls take graph replay (inputs copied in, outputs
@@ -210,9 +220,16 @@ class HIPExecutable:
 
     def run_into(self, inputs, outputs):
         """One plan run on caller buffers (device, fp32, contiguous)."""
-        self.plan.run([t.data_ptr() for t in inputs], [t.data_ptr() for t in outputs], current_stream_handle())
-        if self.debug:
+        ins, outs = [t.data_ptr() for t in inputs], [t.data_ptr() for t in outputs]
+        if self.guards is None:
+            self.plan.run(ins, outs, current_stream_handle())
+            return
+        fill, differs = self._guard_ops
+        for i in range(len(self.kernel_names)):
+            self.guards.before(i, fill)
+            self.plan.run_one(i, ins, outs, current_stream_handle())
             torch.cuda.synchronize()
+            self.guards.after(i, differs)
 
     def _graph_buffers(self):
         if self._static is None:
@@ -280,8 +297,8 @@ class HIPExecutable:
     def __call__(self, *inputs):
         inputs = self._prepare(inputs)
         capturing = torch.cuda.is_current_stream_capturing()
-        if not self.use_cuda_graphs or capturing:
-            out = self._direct(inputs)   # also inside a caller's own stream capture
+        if not self.use_cuda_graphs or capturing or self.debug:
+            out = self._direct(inputs)   # also inside a caller's own stream capture; debug runs launch by launch
         else:
             if self.mode is None:
                 self.mode = self._choose_mode(inputs)

@@ -10,7 +10,10 @@ tests/test_memory_plan.py:42-51):
   * buffers are placed one by one, largest first (equal sizes: the earlier
     writer first), each at the lowest 64-byte-aligned offset where it
     overlaps no already placed buffer that is busy at the same time;
-  * ``reuse=False`` places them end to end instead (the ablation baseline).
+  * ``reuse=False`` places them end to end instead (the ablation baseline);
+  * ``guard`` (debug builds; 0 otherwise) reserves that many more bytes after
+    each buffer's aligned size, so no two buffers abut: the runtime fills the
+    gap with a canary and checks it after every launch.
 
 On the MI355X the arena is one device allocation, and the fixed offsets are
 what let a whole compiled graph be captured once and replayed as a hipGraph.
@@ -78,15 +81,16 @@ def _lowest_gap(size: int, taken) -> int:
 class MemoryPlan(Pass):
     name = "memory-plan"
 
-    def __init__(self, reuse: bool = True):
+    def __init__(self, reuse: bool = True, guard: int = 0):
         self.reuse = reuse
+        self.guard = align(guard)
 
     def run(self, graph: Graph):
         ranges = live_ranges(graph)
         placements = []   # (offset, size, busy interval)
         end = 0
         for v in sorted(ranges, key=lambda v: (-v.type.nbytes, ranges[v][0])):
-            size, busy = align(v.type.nbytes), ranges[v]
+            size, busy = align(v.type.nbytes) + self.guard, ranges[v]
             if self.reuse:
                 offset = _lowest_gap(size, [(o, o + s) for o, s, b in placements if overlaps(b, busy)])
             else:

@@ -101,6 +101,26 @@ def test_matches_without_graphs(name):
     check(fn, *xs, cuda_graphs=False)
 
 
+@pytest.mark.parametrize("T", [16, 128])
+def test_debug_mode_matches_the_plain_plan(T):
+    # Options(debug=True) runs the same kernels launch by launch with NaN
+    # poison before each arena buffer's first write and canaries between
+    # buffers checked after every launch: a correct plan passes the checks
+    # and gives bit for bit the result of the plain plan
+    torch.manual_seed(0)
+    model = gpt2_init_(Block(768, 12, T), seed=0).eval()
+    x = torch.randn(T, 768)
+    c = kiln.compile(model, (x,), device="cuda", debug=True)
+    plain = kiln.compile(model, (x,), device="cuda")
+    assert c._exe.guards is not None and c._exe.program.arena_buffers
+    xd = x.cuda()
+    out = c(xd)
+    assert torch.equal(out, plain(xd))
+    params = {k: v.numpy() for k, v in model.state_dict().items()}
+    np.testing.assert_allclose(out.cpu().numpy(), oracle.block(x.numpy(), params, 12), rtol=RTOL, atol=ATOL)
+    assert torch.equal(c(xd), out)
+
+
 EXP_EXTREMES = [[-200.0, -87.0, -10.0, 0.0, 1e-6, 10.0, 80.0, float("-inf")]]
 
 

@@ -244,3 +244,65 @@ def test_gemv_chain_needs_the_whole_previous_output():
     x = torch.randn(1, 96)
     assert check(half, x, gemv_chains=True).report.lowering["gemv_chains"] == []
     assert check(whole, x, gemv_chains=True).report.lowering["gemv_chains"] == [(0, 2)]
+
+
+def test_debug_mode_runs_launch_by_launch_against_the_oracle():
+    # Options(debug=True): guards between arena buffers, NaN poison before
+    # each buffer's first write, canaries checked after every launch; a
+    # correct plan passes them and gives the oracle's result
+    torch.manual_seed(0)
+    model = gpt2_init_(Block(128, 4, 16), seed=0).eval()
+    x = torch.randn(16, 128)
+    c = kiln.compile(model, (x,), device="cuda", debug=True)
+    plain = kiln.compile(model, (x,), device="cuda")
+    assert c.report.arena_bytes > plain.report.arena_bytes   # the guards take room
+    assert c._exe.program.arena_buffers
+    params = {k: v.numpy() for k, v in model.state_dict().items()}
+    np.testing.assert_allclose(c(x).numpy(), oracle.block(x.numpy(), params, 4), rtol=RTOL, atol=ATOL)
+
+
+def _debug_exe(program, c):
+    from kiln.hip.interpret import HostExecutable
+
+    exe = c._exe
+    return HostExecutable(program, c.report.arena_bytes, c.graph.constants, exe.input_shapes, exe.output_shapes,
+                          debug=True)
+
+
+def test_debug_mode_catches_a_write_past_a_buffer():
+    # plant a mistake in the plan (CPU): the first launch's store moved 8
+    # floats along the arena, so it writes into the next guard bytes
+    import copy
+
+    from kiln.hip import lib as kl
+
+    fn = lambda t: torch.exp(t * 2.0) + 1.0
+    x = torch.randn(4, 64)
+    c = kiln.compile(fn, (x,), device="cuda", fusion=False, debug=True)
+    np.testing.assert_allclose(c(x).numpy(), fn(x).numpy(), rtol=RTOL, atol=ATOL)
+    program = copy.deepcopy(c._exe.program)
+    d = program.launches[0].desc
+    store = [j for j in range(d.n_refs) if d.refs[j].base == kl.BASE_ARENA]
+    assert len(store) == 1
+    d.refs[store[0]].offset += 8
+    with pytest.raises(RuntimeError, match="wrote past the end of arena buffer"):
+        _debug_exe(program, c)(x)
+
+
+def test_debug_mode_poisons_a_buffer_read_before_it_is_written():
+    # plant a mistake in the plan (CPU): the second launch reads its input 8
+    # floats early, from bytes no launch of this call has written (the guard
+    # and the previous buffer's tail): NaN reaches the output
+    import copy
+
+    from kiln.hip import lib as kl
+
+    fn = lambda t: torch.exp(t * 2.0) + 1.0
+    x = torch.randn(4, 64)
+    c = kiln.compile(fn, (x,), device="cuda", fusion=False, debug=True)
+    program = copy.deepcopy(c._exe.program)
+    d = program.launches[1].desc
+    load = [j for j in range(d.n_refs) if d.refs[j].base == kl.BASE_ARENA]
+    d.refs[load[0]].offset += 64            # one row further (elements): the last row reads the guard
+    out = _debug_exe(program, c)(x)[0].numpy()
+    assert np.isnan(out[-1]).all() and np.isfinite(out[:-1]).all()
