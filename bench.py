@@ -63,11 +63,14 @@ def parse():
     p.add_argument("--no-inductor", action="store_true", help="skip the torch.compile column of the block sweep")
     p.add_argument("--counter-probe", metavar="JSON",
                    help="run only the dispatch sequence the rocprofv3 --pmc passes count (a copy of known size, "
-                        "then every launch of the block plans, a bf16 GEMM and torch's GEMMs, each repeated) and "
-                        "write its map to JSON")
+                        "then every launch of the block plans, a bf16 GEMM and torch's GEMMs, the fused ops, the "
+                        "12-layer decode and the bf16 block, each repeated) and write its map to JSON")
     p.add_argument("--traffic-report", nargs=3, metavar=("PROBE_JSON", "FETCH_DIR", "WRITE_DIR"),
                    help="turn the FETCH_SIZE and WRITE_SIZE counter passes over --counter-probe into the "
                         "per-launch HBM traffic summary (no GPU needed); --tokens picks the block")
+    p.add_argument("--traffic-groups", metavar="PREFIX",
+                   help="with --traffic-report: the probe groups whose label starts with PREFIX (e.g. c2_, "
+                        "decode12, bf16_T2048) instead of one block's launches")
     p.add_argument("--counter-report", nargs="+", metavar="PROBE_JSON DIR",
                    help="turn SQ counter passes over --counter-probe into the per-launch MFMA utilisation, "
                         "wait and LDS summary (no GPU needed)")
@@ -238,9 +241,11 @@ def counter_probe(args):
     COPY_BYTES (the calibration kernel: it reads and writes exactly COPY_BYTES),
     then groups, each a one-element fill (the group marker) followed by one
     launch PROBE_REPS times: every launch of the block plan at each of
-    PROBE_TOKENS, the bf16-input GEMM of PROBE_GEMM (nn.Linear with bias), and
+    PROBE_TOKENS, the bf16-input GEMM of PROBE_GEMM (nn.Linear with bias),
     torch's own fp32 and bf16 products of the same shape (hipBLASLt) for
-    comparison. A launch may issue several kernels (split-K issues two), so
+    comparison, the BASELINE fused ops (bias + GELU, LayerNorm, softmax), every
+    launch of the 12-layer decode (one-row GEMVs) and of the bf16 block at
+    T = 2048. A launch may issue several kernels (split-K issues two), so
     groups are cut at the markers. Writes the map from groups to launches as
     JSON."""
     import torch
@@ -284,6 +289,28 @@ def counter_probe(args):
         groups.append({"group": label, "name": label, "kernel": "torch", "summary": f"F.linear {m}x{n}x{k}",
                        "flops": flops, "bytes": nbytes})
         runs.append(fn)
+    # the BASELINE fused memory-bound ops (their launches' algorithmic bytes
+    # are the table's: inputs and parameters read once, outputs written once)
+    torch.manual_seed(0)
+    bias = torch.randn(3072, device="cuda")
+    ln = torch.nn.LayerNorm(768).eval().cuda()
+    for label, fn, shape in (("c2_bias_gelu_2048x3072", lambda t: F.gelu(t + bias, approximate="tanh"), (2048, 3072)),
+                             ("c2_layernorm_2048x768", ln, (2048, 768)),
+                             ("c2_softmax_12x512x512", lambda t: F.softmax(t * 0.125, -1), (12, 512, 512))):
+        xt = torch.randn(*shape, device="cuda")
+        plan_groups(label, kiln.compile(fn, (xt,), device="cuda", cuda_graphs=False), xt)
+    # the 12-layer decode: 49 one-row launches (GEMVs with their prologues)
+    from models.transformer import Stack
+
+    torch.manual_seed(0)
+    stack = gpt2_init_(Stack(12, 768, 12, 1), seed=0).eval().cuda()
+    x1 = torch.randn(1, 768, device="cuda")
+    plan_groups("decode12", kiln.compile(stack, (x1,), device="cuda", autotune=not args.no_autotune,
+                                         cuda_graphs=False), x1)
+    # the bf16 block at T = 2048 (bf16 GEMMs, fp32 attention and rows)
+    model, x = make_block(2048)
+    plan_groups("bf16_T2048", kiln.compile(model, (x,), device="cuda", autotune=not args.no_autotune,
+                                           matmul_precision="bf16"), x)
     torch.cuda.synchronize()
     with torch.no_grad():
         for _ in range(PROBE_REPS):
@@ -356,12 +383,13 @@ def _median(reps, counter, which=0):
     return statistics.median(r[counter][which] for r in reps)
 
 
-def traffic_report(probe_json, fetch_dir, write_dir, prefix=None):
+def traffic_report(probe_json, fetch_dir, write_dir, prefix=None, groups_prefix=None):
     """Per-launch HBM bytes: each group's median counter value (KiB per launch,
     summed over the kernels a launch issues) scaled by the copy calibration
     (COPY_BYTES / the copy's median). FETCH_SIZE and WRITE_SIZE count L2
     misses to the fabric, so a re-read served by the Infinity Cache counts.
-    With `prefix` (e.g. "T2048"), only that block's launches, by launch name."""
+    With `prefix` (e.g. "T2048"), only that block's launches, by launch name;
+    with `groups_prefix` (e.g. "c2_"), the groups whose label starts with it."""
     with open(probe_json) as f:
         probe = json.load(f)
     med = {}
@@ -375,6 +403,8 @@ def traffic_report(probe_json, fetch_dir, write_dir, prefix=None):
              f"WRITE_SIZE {med['WRITE_SIZE'][0]:.1f} KiB; scale fetch {f_scale:.4f}, write {w_scale:.4f}"]
     for i, l in enumerate(probe["groups"]):
         if prefix and not l["group"].startswith(prefix + "/"):
+            continue
+        if groups_prefix and not l["group"].startswith(groups_prefix):
             continue
         fb = med["FETCH_SIZE"][1 + i] * 1024 * f_scale
         wb = med["WRITE_SIZE"][1 + i] * 1024 * w_scale
@@ -835,7 +865,10 @@ def cpu_baseline(T, oracle_line=True):
 def main():
     args = parse()
     if args.traffic_report:
-        traffic_report(*args.traffic_report, prefix=f"T{args.tokens}")
+        if args.traffic_groups:
+            traffic_report(*args.traffic_report, groups_prefix=args.traffic_groups)
+        else:
+            traffic_report(*args.traffic_report, prefix=f"T{args.tokens}")
         return
     if args.counter_report:
         counter_report(args.counter_report[0], args.counter_report[1:])

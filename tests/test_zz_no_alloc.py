@@ -75,3 +75,53 @@ def test_noalloc_rejects_plans_beyond_its_array():
     rc = plan.lib.kh_plan_run_noalloc(plan.handle, null, 1, null, 1, None)
     assert rc == kl.ERR_CAPACITY
     assert b"16777216" in plan.lib.kh_last_error()
+
+
+def _captured_noalloc(plan, ins, out):
+    """kh_plan_run_noalloc recorded into a torch CUDA graph: a device
+    allocation during the call would fail the capture."""
+    lib = kl.load()
+    in_arr, out_arr = kl.pointer_array([t.data_ptr() for t in ins]), kl.pointer_array([out.data_ptr()])
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+            kl.check(lib.kh_plan_run_noalloc(plan.handle, in_arr, len(ins), out_arr, 1, stream),
+                     "kh_plan_run_noalloc")
+    torch.cuda.current_stream().wait_stream(side)
+    return graph, (in_arr, out_arr)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", ["split-k", "decode-chain"])
+def test_noalloc_run_captures_into_a_graph(case):
+    # the promise of the entry point: it allocates nothing, so it can be
+    # captured; each replay (with the program's own eager work between
+    # replays) matches kh_plan_run bit for bit
+    from models.transformer import Stack, gpt2_init_
+
+    if case == "split-k":
+        compiled, xs = _split_k_program(128, 768, 3072, 6)
+        shape = (128, 768)
+    else:
+        torch.manual_seed(0)
+        model = gpt2_init_(Stack(2, 128, 4, 1), seed=0).eval()
+        xs = (torch.randn(1, 128),)
+        compiled = kiln.compile(model, xs, device="cuda", cuda_graphs=False, gemv_chains=True)
+        assert compiled.report.lowering["gemv_chains"]
+        shape = (1, 128)
+    print(f"noalloc capture: {case}", flush=True)
+    plan = _unbound_workspace_plan(compiled)
+    expected = compiled(*xs)
+    ins = [x.to("cuda").contiguous() for x in xs]
+    out = torch.full(shape, float("nan"), device="cuda")
+    graph, keep = _captured_noalloc(plan, ins, out)
+    for _ in range(3):
+        out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, expected)
+        _ = (ins[0] * 2.0).sum().item()   # eager work between replays
+    assert plan.chain_timeouts() == 0
