@@ -62,12 +62,13 @@ constexpr int kBufferFlags = 0x00020000;
 
 struct AttnArgs {
   const float *q, *k, *v;
-  float *o;
+  float *o;                // (a bf16 array when o16)
   const float *mask;
   int64_t q_b, q_t, k_b, k_t, v_b, v_t, o_b, o_t, m_b, m_q, m_k;
   int32_t batch, tq, tk, n_qblocks;
   int32_t mask_mode, scale_mode;
   float scale;
+  int32_t o16;             // the output is bf16 (its consumer is a bf16 matmul)
 };
 
 // Exchange between the two lane halves (lanes l and l ^ 32): returns
@@ -283,7 +284,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
       acc.z += o_part[u][qr][d + 2] * e, acc.w += o_part[u][qr][d + 3] * e;
     }
     acc.x /= l, acc.y /= l, acc.z /= l, acc.w /= l;
-    *reinterpret_cast<float4 *>(a.o + b * a.o_b + (int64_t)(q0 + qr) * a.o_t + d) = acc;
+    const int64_t at = b * a.o_b + (int64_t)(q0 + qr) * a.o_t + d;
+    if (a.o16) store_bf16x4(a.o, at, acc.x, acc.y, acc.z, acc.w);
+    else *reinterpret_cast<float4 *>(a.o + at) = acc;
   }
 }
 
@@ -353,7 +356,7 @@ class AttnOp final : public Op {
     a.q = ptrs[0], a.k = ptrs[1], a.v = ptrs[2], a.o = ptrs[3];
     a.mask = a.mask_mode == KH_ATTN_MASK_ADD ? ptrs[4] : nullptr;
     for (int j = 0; j < 4; ++j)
-      if (reinterpret_cast<uintptr_t>(ptrs[j]) & 15) return hipErrorInvalidValue;
+      if (reinterpret_cast<uintptr_t>(ptrs[j]) & (j == 3 && a.o16 ? 7 : 15)) return hipErrorInvalidValue;
     if (a.batch == 0 || a.tq == 0) return hipSuccess;
     if (rows) {
       const dim3 g((unsigned)((a.batch * a.tq + 3) / 4));
@@ -478,6 +481,15 @@ std::unique_ptr<Op> make_attn(const kh_launch &L, std::string &err, bool &unsupp
     return nullptr;
   }
   op->grid = dim3((unsigned)std::max<int64_t>(1, n_groups));
+  // a bf16 output (the head-merged result read only by a bf16 matmul): the
+  // output ref only, and not on the few-query kernel
+  const uint32_t m16 = bf16_refs(L);
+  if (m16 && (m16 != 1u << 3 || op->rows)) {
+    unsupported = true;
+    err = "attention: bf16 storage only for the output of the blocked kernel";
+    return nullptr;
+  }
+  a.o16 = m16 ? 1 : 0;
   return op;
 }
 

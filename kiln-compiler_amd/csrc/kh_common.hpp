@@ -53,6 +53,16 @@ __device__ __forceinline__ void store_stream(float *p, float x, float y, float z
   __builtin_nontemporal_store(v, reinterpret_cast<f32x4_t *>(p));
 }
 
+// Four values rounded to bf16 (nearest even, as every bf16 input of the
+// matmul family is rounded) and stored as one 64-bit write at element `i` of
+// the bf16 array `p`: the output of a producer whose only consumer is a bf16
+// matmul.
+__device__ __forceinline__ void store_bf16x4(void *p, int64_t i, float x, float y, float z, float w) {
+  typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+  const bf16x4_t v = {(__bf16)x, (__bf16)y, (__bf16)z, (__bf16)w};
+  *reinterpret_cast<bf16x4_t *>(static_cast<__bf16 *>(p) + i) = v;
+}
+
 // ---------------------------------------------------------------------------
 // wave64 all-reductions: DPP within rows of 16 lanes, then cross-row swizzles.
 template <int CTRL>

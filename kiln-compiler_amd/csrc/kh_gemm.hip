@@ -1422,6 +1422,28 @@ std::unique_ptr<Op> make_gemm(const kh_launch &L, std::string &err, bool &unsupp
       cfg_run = kFallbackConfig;
     }
   }
+  // bf16 storage (cfg[7]): A and / or the direct epilogue's output, on the
+  // bf16 kernel with 64-deep steps only
+  const uint32_t m16 = bf16_refs(L);
+  if (m16) {
+    const bool a16 = m16 & 1u, o16 = a.direct && (m16 >> (2 + a.d_out) & 1u);
+    const uint32_t known = (a16 ? 1u : 0u) | (o16 ? 1u << (2 + a.d_out) : 0u);
+    if (t.kind != 7 || m16 != known || a.pro != KH_GEMV_PRO_NONE) {
+      unsupported = true;
+      err = "matmul: bf16 storage only for A and a direct epilogue's output on a 64-deep bf16 configuration";
+      return nullptr;
+    }
+    if (a16 && (a.sa_k != 1 || a.sa_m % 8 || a.sa_b % 8 || L.refs[0].offset % 8)) {
+      err = "matmul: a bf16 A operand needs unit K stride and 16-byte aligned rows";
+      return nullptr;
+    }
+    if (o16 && (a.estride[a.d_out][2] != 1 || a.estride[a.d_out][1] % 4 || a.estride[a.d_out][0] % 4 ||
+                L.refs[2 + a.d_out].offset % 4)) {
+      err = "matmul: a bf16 output needs unit N stride and 8-byte aligned rows";
+      return nullptr;
+    }
+    a.a16 = a16 ? 1 : 0, a.o16 = o16 ? 1 : 0;
+  }
   const TileCfg &tr = kConfigs[cfg_run];
   a.tiles_m = (int)((M + tr.bm - 1) / tr.bm);
   a.tiles_n = (int)((N + tr.bn - 1) / tr.bn);

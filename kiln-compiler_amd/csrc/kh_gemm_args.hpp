@@ -36,6 +36,9 @@ struct GemmArgs {
   // modes, scale
   int32_t att_q, att_mask, att_tk, att_dh, att_mask_mode, att_scale_mode;
   float att_scale;
+  // bf16 storage (kind 7 only): A holds bf16 values (its strides count bf16
+  // elements); the direct epilogue's output is written as bf16
+  int32_t a16, o16;
 };
 
 // Run the epilogue tape for columns [n, n + valid) of output row (b, m);

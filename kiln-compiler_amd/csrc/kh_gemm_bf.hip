@@ -28,6 +28,13 @@
 //     interpreter.
 // Measured against the 32-deep K-contiguous kernel on 2048x3072x768 (bf16
 // weights, fp32 activations): 27.5 -> ~20 us per product.
+// bf16 storage (ABF; a.a16): when the producer of A wrote it as bf16 (a
+// LayerNorm, attention or another product whose only consumer is this one),
+// A rows are 64 bf16 values per stage (8 chunks, like B's), half the bytes
+// copied and one 128-bit fragment read per half step with no rounding (the
+// same bits: the producer rounded to nearest even as the fragment read
+// does). a.o16: the direct epilogue writes its output as bf16 for a
+// consumer that reads it that way.
 // K must be a positive multiple of 64 and the operands' spans below 2^29
 // elements (the host checks both).
 #include <algorithm>
@@ -40,15 +47,16 @@
 namespace kh {
 namespace {
 
-template <int BM, int BN, int WM, int WN, int NS, bool TAPE>
+template <int BM, int BN, int WM, int WN, int NS, bool TAPE, bool ABF>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_bf_kernel(const GemmArgs a) {
   constexpr int BK = 64, MT = 16, kWaves = WM * WN;
   constexpr int TM = BM / WM, TN = BN / WN, FM = TM / MT, FN = TN / MT;
-  constexpr int A_BYTES = BM * BK * 4, STAGE = A_BYTES + BN * BK * 2;   // bytes
-  constexpr int A_PW = BM * 16 / 64 / kWaves, B_PW = BN * 8 / 64 / kWaves, COPIES = A_PW + B_PW;
+  constexpr int ACH = ABF ? 8 : 16;                                      // 16-byte chunks per A row and stage
+  constexpr int A_BYTES = BM * ACH * 16, STAGE = A_BYTES + BN * BK * 2;  // bytes
+  constexpr int A_PW = BM * ACH / 64 / kWaves, B_PW = BN * 8 / 64 / kWaves, COPIES = A_PW + B_PW;
   constexpr int CS = TN + 4;   // epilogue staging row stride (floats, 16-byte aligned rows)
   static_assert(TM % MT == 0 && TN % MT == 0, "wave tile of whole MFMA blocks");
-  static_assert((BM * 16) % (64 * kWaves) == 0 && (BN * 8) % (64 * kWaves) == 0, "copy mapping");
+  static_assert((BM * ACH) % (64 * kWaves) == 0 && (BN * 8) % (64 * kWaves) == 0, "copy mapping");
   static_assert(NS >= 2 && NS <= 4 && (NS - 2) * COPIES < 64, "ring depth / vmcnt range");
   static_assert(NS * STAGE <= 160 * 1024 && kWaves * MT * CS * 4 <= NS * STAGE, "LDS: ring, staging inside it");
   __shared__ float4 ring4[NS * STAGE / 16];
@@ -61,7 +69,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_bf_kernel(const GemmArgs a)
   int tm, tn;
   tile_coords(blockIdx.x, a, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
-  const float *Ab = a.A + (int64_t)bidx * a.sa_b;
+  // A in its element type: fp32, or bf16 (ABF)
+  const char *Ab = reinterpret_cast<const char *>(a.A) + (int64_t)bidx * a.sa_b * (ABF ? 2 : 4);
   const __bf16 *Bb = reinterpret_cast<const __bf16 *>(a.B) + (int64_t)bidx * a.sb_b;
 
   // per-lane copy sources: byte offsets from the step's first K column (rows
@@ -69,8 +78,9 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_bf_kernel(const GemmArgs a)
   uint32_t a_off[A_PW], b_off[B_PW];
 #pragma unroll
   for (int i = 0; i < A_PW; ++i) {
-    const int p = (wave * A_PW + i) * 64 + lane, r = p / 16;
-    a_off[i] = (uint32_t)(min(m0 + r, a.M - 1) * (int)a.sa_m + ((p % 16) ^ swz_rows<16>(r)) * 4) * 4u;
+    const int p = (wave * A_PW + i) * 64 + lane, r = p / ACH;
+    a_off[i] = ABF ? (uint32_t)(min(m0 + r, a.M - 1) * (int)a.sa_m + ((p % 8) ^ swz_a(r)) * 8) * 2u
+                   : (uint32_t)(min(m0 + r, a.M - 1) * (int)a.sa_m + ((p % 16) ^ swz_rows<16>(r)) * 4) * 4u;
   }
 #pragma unroll
   for (int i = 0; i < B_PW; ++i) {
@@ -79,7 +89,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_bf_kernel(const GemmArgs a)
   }
   const int n_steps = a.K / BK;   // the host checks K % 64 == 0 and K > 0
   auto issue = [&](int step) {
-    const float *ab = uniform_ptr(Ab + step * BK);
+    const float *ab = uniform_ptr(reinterpret_cast<const float *>(Ab + step * BK * (ABF ? 2 : 4)));
     const float *bb = uniform_ptr(reinterpret_cast<const float *>(Bb + step * BK));
     const uint32_t lds = (uint32_t)(uintptr_t)(lds_void_t *)(ring + (step % NS) * STAGE);
 #pragma unroll
@@ -95,7 +105,9 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_bf_kernel(const GemmArgs a)
 #pragma unroll
     for (int k2 = 0; k2 < 2; ++k2)
 #pragma unroll
-      for (int q = 0; q < 2; ++q) fa[fm][k2][q] = r * 256 + ((8 * k2 + 2 * g + q) ^ swz_rows<16>(r)) * 16;
+      for (int q = 0; q < 2; ++q)
+        fa[fm][k2][q] = ABF ? r * 128 + ((4 * k2 + g) ^ swz_a(r)) * 16
+                            : r * 256 + ((8 * k2 + 2 * g + q) ^ swz_rows<16>(r)) * 16;
   }
 #pragma unroll
   for (int fn = 0; fn < FN; ++fn) {
@@ -122,7 +134,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_bf_kernel(const GemmArgs a)
   const int64_t sbn = a.estride[jb][2], srm = a.estride[jr][1], srn = a.estride[jr][2];
   const int64_t som = a.estride[jo][1], son = a.estride[jo][2];
   const bool vb = a.e_vec_mask >> jb & 1, vr = a.e_vec_mask >> jr & 1, vo = a.e_vec_mask >> jo & 1;
-  const int act = a.d_act, M = a.M, N = a.N;
+  const int act = a.d_act, M = a.M, N = a.N, o16 = a.o16;
+  __bf16 *po16 = reinterpret_cast<__bf16 *>(a.eptr[jo]) + (int64_t)bidx * a.estride[jo][0];
   for (int s = 0; s < n_steps; ++s) {
     // this wave's copies of step s landed (the copies of `later` steps were
     // issued after them), then every wave's: the barrier also says that every
@@ -139,10 +152,14 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_bf_kernel(const GemmArgs a)
       bf16x8 xa[FM], xb[FN];
 #pragma unroll
       for (int fm = 0; fm < FM; ++fm) {
-        const float4 lo = *reinterpret_cast<const float4 *>(st + fa[fm][k2][0]);
-        const float4 hi = *reinterpret_cast<const float4 *>(st + fa[fm][k2][1]);
-        xa[fm][0] = (__bf16)lo.x, xa[fm][1] = (__bf16)lo.y, xa[fm][2] = (__bf16)lo.z, xa[fm][3] = (__bf16)lo.w;
-        xa[fm][4] = (__bf16)hi.x, xa[fm][5] = (__bf16)hi.y, xa[fm][6] = (__bf16)hi.z, xa[fm][7] = (__bf16)hi.w;
+        if constexpr (ABF) {
+          xa[fm] = *reinterpret_cast<const bf16x8 *>(st + fa[fm][k2][0]);
+        } else {
+          const float4 lo = *reinterpret_cast<const float4 *>(st + fa[fm][k2][0]);
+          const float4 hi = *reinterpret_cast<const float4 *>(st + fa[fm][k2][1]);
+          xa[fm][0] = (__bf16)lo.x, xa[fm][1] = (__bf16)lo.y, xa[fm][2] = (__bf16)lo.z, xa[fm][3] = (__bf16)lo.w;
+          xa[fm][4] = (__bf16)hi.x, xa[fm][5] = (__bf16)hi.y, xa[fm][6] = (__bf16)hi.z, xa[fm][7] = (__bf16)hi.w;
+        }
       }
 #pragma unroll
       for (int fn = 0; fn < FN; ++fn) xb[fn] = *reinterpret_cast<const bf16x8 *>(st + fb[fn][k2]);
@@ -207,11 +224,19 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_bf_kernel(const GemmArgs a)
 #pragma unroll
             for (int i = 0; i < 4; ++i) v[i] = v[i] != v[i] ? v[i] : fmaxf(v[i], 0.0f);
           }
-          float *o = po + (int64_t)m * som;
-          if (vo && valid == 4) {
-            *reinterpret_cast<float4 *>(o + n) = make_float4(v[0], v[1], v[2], v[3]);
+          if (o16) {
+            if (valid == 4) {
+              store_bf16x4(po16, (int64_t)m * som + n, v[0], v[1], v[2], v[3]);
+            } else {
+              for (int i = 0; i < valid; ++i) po16[(int64_t)m * som + n + i] = (__bf16)v[i];
+            }
           } else {
-            for (int i = 0; i < valid; ++i) o[(int64_t)(n + i) * son] = v[i];
+            float *o = po + (int64_t)m * som;
+            if (vo && valid == 4) {
+              *reinterpret_cast<float4 *>(o + n) = make_float4(v[0], v[1], v[2], v[3]);
+            } else {
+              for (int i = 0; i < valid; ++i) o[(int64_t)(n + i) * son] = v[i];
+            }
           }
         }
       }
@@ -224,12 +249,16 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_bf_kernel(const GemmArgs a)
 
 hipError_t launch_gemm_bf(int id, const GemmArgs &a, dim3 grid, hipStream_t stream) {
   switch (id) {
-#define KH_CFGBF_CASE(cid, bm, bn, wm, wn, ns)                                                                 \
-  case cid:                                                                                                    \
-    if (a.direct)                                                                                              \
-      hipLaunchKernelGGL((gemm_bf_kernel<bm, bn, wm, wn, ns, false>), grid, dim3(64 * wm * wn), 0, stream, a); \
-    else                                                                                                       \
-      hipLaunchKernelGGL((gemm_bf_kernel<bm, bn, wm, wn, ns, true>), grid, dim3(64 * wm * wn), 0, stream, a);  \
+#define KH_CFGBF_CASE(cid, bm, bn, wm, wn, ns)                                                                     \
+  case cid:                                                                                                        \
+    if (a.direct && a.a16)                                                                                         \
+      hipLaunchKernelGGL((gemm_bf_kernel<bm, bn, wm, wn, ns, false, true>), grid, dim3(64 * wm * wn), 0, stream, a); \
+    else if (a.direct)                                                                                             \
+      hipLaunchKernelGGL((gemm_bf_kernel<bm, bn, wm, wn, ns, false, false>), grid, dim3(64 * wm * wn), 0, stream, a); \
+    else if (a.a16)                                                                                                \
+      hipLaunchKernelGGL((gemm_bf_kernel<bm, bn, wm, wn, ns, true, true>), grid, dim3(64 * wm * wn), 0, stream, a);  \
+    else                                                                                                           \
+      hipLaunchKernelGGL((gemm_bf_kernel<bm, bn, wm, wn, ns, true, false>), grid, dim3(64 * wm * wn), 0, stream, a); \
     break;
     KH_GEMM_BF_CONFIGS(KH_CFGBF_CASE)
 #undef KH_CFGBF_CASE

@@ -22,6 +22,7 @@
 #include <string>
 #include <vector>
 
+#include "kh_internal.hpp"
 #include "kh_semantics.hpp"
 #include "kiln_hip.h"
 
@@ -75,6 +76,29 @@ inline float bf16_value(uint16_t bits) {
   return y;
 }
 
+inline uint16_t bf16_bits(float x) {
+  uint32_t u;
+  std::memcpy(&u, &x, 4);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);   // NaN stays (quiet) NaN
+  return (uint16_t)((u + (((u >> 16) & 1u) + 0x7FFFu)) >> 16);
+}
+
+// Operand j at element `off`: fp32, or bf16 when the launch stores it as
+// bf16 (kh_launch.cfg[7]), read widened and written rounded to nearest even
+// as the kernels do.
+struct Operands {
+  float *const *p;
+  uint32_t m16;
+  Operands(const kh_launch &L, float *const *ptrs) : p(ptrs), m16(bf16_refs(L)) {}
+  float ld(int j, int64_t off) const {
+    return (m16 >> j & 1) ? bf16_value(reinterpret_cast<const uint16_t *>(p[j])[off]) : p[j][off];
+  }
+  void st(int j, int64_t off, float v) const {
+    if (m16 >> j & 1) reinterpret_cast<uint16_t *>(p[j])[off] = bf16_bits(v);
+    else p[j][off] = v;
+  }
+};
+
 // Runs tape[begin, end) on `slot` at one element. load(j) / store(j, v) read
 // and write operand j at that element; reduce(insn, v) handles RSUM / RMAX.
 // Returns the mask of slots the range wrote.
@@ -115,6 +139,7 @@ void host_ew(const kh_launch &L, float *const *p) {
 // -- rows -----------------------------------------------------------------------------
 
 void host_row(const kh_launch &L, float *const *p) {
+  const Operands mem(L, p);
   const int rank = L.rank;
   const int64_t inner = rank > 0 ? L.shape[rank - 1] : 1;
   int64_t row_shape[KH_MAX_RANK];
@@ -134,8 +159,8 @@ void host_row(const kh_launch &L, float *const *p) {
         idx[rank - 1] = c;
         float *slot = &cols[(size_t)c * KH_NREGS];
         vec_written |= run_tape(
-            L, P.vec_begin, P.vec_end, slot, [&](int j) { return p[j][offset_of(L.refs[j], idx, rank)]; },
-            [&](int j, float v) { p[j][offset_of(L.refs[j], idx, rank)] = v; },
+            L, P.vec_begin, P.vec_end, slot, [&](int j) { return mem.ld(j, offset_of(L.refs[j], idx, rank)); },
+            [&](int j, float v) { mem.st(j, offset_of(L.refs[j], idx, rank), v); },
             [&](const kh_insn &in, float x) {
               acc[in.dst] = in.op == KH_OP_RSUM ? acc[in.dst] + x : nan_max(acc[in.dst], x);
             });
@@ -154,8 +179,8 @@ void host_row(const kh_launch &L, float *const *p) {
         if (P.acc_mask >> s & 1) row[s] = acc[s], uniform |= 1u << s;
       idx[rank - 1] = 0;
       uniform |= run_tape(
-          L, P.post_begin, P.post_end, row, [&](int j) { return p[j][offset_of(L.refs[j], idx, rank - 1)]; },
-          [&](int j, float v) { p[j][offset_of(L.refs[j], idx, rank - 1)] = v; }, [](const kh_insn &, float) {});
+          L, P.post_begin, P.post_end, row, [&](int j) { return mem.ld(j, offset_of(L.refs[j], idx, rank - 1)); },
+          [&](int j, float v) { mem.st(j, offset_of(L.refs[j], idx, rank - 1), v); }, [](const kh_insn &, float) {});
       for (int64_t c = 0; c < std::max<int64_t>(inner, 1); ++c)
         for (int s = 0; s < KH_NREGS; ++s)
           if (uniform >> s & 1) cols[(size_t)c * KH_NREGS + s] = row[s];
@@ -220,7 +245,8 @@ void host_attn(const kh_launch &L, float *const *p) {
       attend(tk, dh, L.cfg[1], L.fparams[0], L.cfg[0], i, p[0] + b * Q.strides[0] + i * Q.strides[1], Q.strides[2],
              p[1] + b * K.strides[0], K.strides[1], K.strides[2], p[2] + b * V.strides[0], V.strides[1], V.strides[2],
              mask, mask ? L.refs[4].strides[2] : 0, out.data());
-      for (int64_t d = 0; d < dh; ++d) p[3][b * O.strides[0] + i * O.strides[1] + d * O.strides[2]] = (float)out[d];
+      for (int64_t d = 0; d < dh; ++d)
+        Operands(L, p).st(3, b * O.strides[0] + i * O.strides[1] + d * O.strides[2], (float)out[d]);
     }
 }
 
@@ -249,7 +275,8 @@ void a_row(const kh_launch &L, float *const *p, int64_t b, int64_t m, std::vecto
     }
     return;
   }
-  for (int64_t k = 0; k < K; ++k) row[(size_t)k] = p[0][b * A.strides[0] + m * A.strides[1] + k * A.strides[2]];
+  const Operands mem(L, p);
+  for (int64_t k = 0; k < K; ++k) row[(size_t)k] = mem.ld(0, b * A.strides[0] + m * A.strides[1] + k * A.strides[2]);
   if (L.cfg[4] == KH_GEMV_PRO_LAYERNORM) {
     double sum = 0.0;
     for (int64_t k = 0; k < K; ++k) sum += row[(size_t)k];
@@ -298,9 +325,10 @@ void host_matmul(const kh_launch &L, float *const *p) {
         const int c_ref = L.family == KH_FAM_GEMM && L.cfg[4] == KH_GEMV_PRO_LAYERNORM ? L.cfg[6] : -1;
         if (c_ref >= 0) acc += (double)p[c_ref][offset_of(L.refs[c_ref], idx, 3)];
         slot[0] = (float)acc;
+        const Operands mem(L, p);
         run_tape(
-            L, 0, L.n_insns, slot, [&](int j) { return p[j][offset_of(L.refs[j], idx, 3)]; },
-            [&](int j, float v) { p[j][offset_of(L.refs[j], idx, 3)] = v; }, [](const kh_insn &, float) {});
+            L, 0, L.n_insns, slot, [&](int j) { return mem.ld(j, offset_of(L.refs[j], idx, 3)); },
+            [&](int j, float v) { mem.st(j, offset_of(L.refs[j], idx, 3), v); }, [](const kh_insn &, float) {});
       }
     }
 }

@@ -66,6 +66,14 @@ class Chain {
 std::vector<std::unique_ptr<Chain>> find_chains(const std::vector<kh_launch> &desc,
                                                 const std::vector<std::unique_ptr<Op>> &ops);
 
+// bf16 storage (cfg[7] of a ROW, ATTN or GEMM launch): bit j set means ref j
+// holds bf16 values, its offset and strides counted in bf16 elements. Each
+// family's factory accepts it only where its kernel reads or writes bf16.
+inline uint32_t bf16_refs(const kh_launch &L) {
+  const bool fam = L.family == KH_FAM_ROW || L.family == KH_FAM_ATTN || L.family == KH_FAM_GEMM;
+  return fam ? (uint32_t)L.cfg[7] & ((1u << KH_MAX_REFS) - 1) : 0u;
+}
+
 // Each factory returns nullptr and sets `err` when the descriptor is invalid or
 // unsupported; `unsupported` distinguishes the two for the status code.
 std::unique_ptr<Op> make_ew(const kh_launch &L, std::string &err, bool &unsupported);

@@ -189,7 +189,8 @@ int resolve(const kh_plan *p, int i, void *const *inputs, int n_in, void *const 
       default: return fail(KH_ERR_INVALID, "bad operand base");
     }
     if (base == nullptr) return fail(KH_ERR_INVALID, std::string("null device pointer for an operand of ") + L.name);
-    ptrs[j] = static_cast<float *>(base) + r.offset;
+    ptrs[j] = (kh::bf16_refs(L) >> j & 1) ? reinterpret_cast<float *>(static_cast<uint16_t *>(base) + r.offset)
+                                         : static_cast<float *>(base) + r.offset;
   }
   return KH_OK;
 }

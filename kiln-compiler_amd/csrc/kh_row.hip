@@ -33,10 +33,11 @@ struct LnArgs {
   const float *x;
   const float *gamma;   // may be null
   const float *beta;    // may be null
-  float *out;
+  float *out;           // (a bf16 array when out16)
   int64_t x_rs, out_rs; // row strides (elements)
   uint32_t rows, inner;
   float inv_n1, inv_n2, eps;
+  int32_t out16;        // the output is bf16 (its consumer is a bf16 matmul)
 };
 
 // One row per wave and no grid-stride loop: the grid covers every row, so
@@ -71,7 +72,6 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const LnArgs a) {
       }
     }
     const float rstd = rsqrtf(wave_sum(s2) * a.inv_n2 + a.eps);
-    float *o = a.out + (int64_t)row * a.out_rs;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const uint32_t c = (i * 64 + lane) * 4;
@@ -85,7 +85,8 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const LnArgs a) {
           const float4 b = *reinterpret_cast<const float4 *>(a.beta + c);
           y.x += b.x, y.y += b.y, y.z += b.z, y.w += b.w;
         }
-        store_stream(o + c, y.x, y.y, y.z, y.w);
+        if (a.out16) store_bf16x4(a.out, (int64_t)row * a.out_rs + c, y.x, y.y, y.z, y.w);
+        else store_stream(a.out + (int64_t)row * a.out_rs + c, y.x, y.y, y.z, y.w);
       }
     }
   }
@@ -416,6 +417,7 @@ std::unique_ptr<Op> make_row(const kh_launch &L, std::string &err, bool &unsuppo
   }
   const Device &dev = current_device();
   const int nv = pick_nv(inner);
+  const uint32_t m16 = bf16_refs(L);
 
   if (L.variant == KH_ROW_LAYERNORM || L.variant == KH_ROW_SOFTMAX) {
     // refs: [x, (gamma), (beta)] loads, then the output; cfg[4] = 1 if gamma, cfg[5] = 1 if beta.
@@ -435,8 +437,20 @@ std::unique_ptr<Op> make_row(const kh_launch &L, std::string &err, bool &unsuppo
         op->args.rows = (uint32_t)rows, op->args.inner = (uint32_t)inner;
         op->args.inv_n1 = L.fparams[0], op->args.inv_n2 = L.fparams[1], op->args.eps = L.fparams[2];
         op->grid = (int)std::max<int64_t>(1, std::min<int64_t>((rows + 3) / 4, (int64_t)1 << 30));
+        // a bf16 output: only the output, 8-byte aligned rows of 4-value groups
+        if (m16 && (m16 != 1u << out || L.refs[out].offset % 4 || rs[out] % 4)) {
+          unsupported = true;
+          err = "row: bf16 storage only for a LayerNorm's output with 4-aligned rows";
+          return nullptr;
+        }
+        op->args.out16 = m16 ? 1 : 0;
         return op;
       }
+    }
+    if (m16) {
+      unsupported = true;
+      err = "row: bf16 storage only for the one-wave LayerNorm kernel";
+      return nullptr;
     }
     if (ok && L.variant == KH_ROW_SOFTMAX) {
       ok = L.n_refs == 2 && vec_ok(L, 0, rs[0]) && vec_ok(L, 1, rs[1]);
@@ -453,6 +467,11 @@ std::unique_ptr<Op> make_row(const kh_launch &L, std::string &err, bool &unsuppo
     // Not eligible for the fast path: the tape in the descriptor is complete, run it generically.
   }
 
+  if (m16) {
+    unsupported = true;
+    err = "row: bf16 storage only for the one-wave LayerNorm kernel";
+    return nullptr;
+  }
   auto op = std::make_unique<RowOp>();
   RowArgs &a = op->args;
   a.n_refs = L.n_refs;

@@ -171,6 +171,10 @@ SKINNY = frozenset(range(47, 55))
 # configurations of the K-contiguous pipeline: A as for the skinny kernel, B
 # the [batch][N][K] copy of a constant, K a multiple of 32, no split-K
 K_CONTIGUOUS = frozenset(range(55, 65)) | frozenset(range(87, 101))
+# the bf16 configurations with 64-deep K steps (kind 7): they also read A as
+# bf16 when its producer stores it that way (kiln/hip/lowering.py,
+# plan_bf16_storage)
+BF16_A = frozenset(range(95, 101))
 # configurations of the small-M kernel: as the K-contiguous pipeline (B the
 # [batch][N][K] copy, K a positive multiple of 32, no split-K), for products
 # with at most SMALL_M_MAX rows

@@ -186,6 +186,7 @@ class _Lowerer:
         self.gemv_chains = gemv_chains
         self.layouts = compute_layouts(graph)
         self.users = graph.users()
+        self.bf16_buffers = set()   # arena buffers held as bf16 (plan_bf16_storage)
         self.precision = precision
         self.matmul_config = matmul_config
         self.program = Program(precision=precision)
@@ -217,6 +218,102 @@ class _Lowerer:
             assert byte_offset % 4 == 0
             return byte_offset // 4 + lay.offset
         return lay.offset
+
+    def stored_bf16(self, v) -> bool:
+        """Is v's storage an arena buffer held as bf16 (see plan_bf16_storage)?"""
+        lay = self.layouts.get(v)
+        return lay is not None and lay.base[0] == "arena" and lay.base[1] in self.bf16_buffers
+
+    def as_bf16(self, r, v):
+        """Ref r of v re-expressed over v's bf16 storage: the offset in bf16
+        elements (the buffer's byte offset / 2 + v's view offset); strides
+        count elements either way."""
+        lay = self.layouts[v]
+        r.offset = lay.base[1].node.attrs.get("offset", 0) // 2 + lay.offset
+        return r
+
+    def plan_bf16_storage(self):
+        """bf16 plans: arena buffers that are the A operand of exactly one
+        bf16 product on the 64-deep configurations (which read A as bf16) and
+        are written by a launch that can round its output to bf16 - the
+        one-wave LayerNorm, the blocked attention kernel, or another such
+        product with a bias [+ GELU / ReLU] epilogue - are stored as bf16: the
+        producer rounds once (to nearest even, as the product would at each
+        fragment read), the product copies half the bytes and rounds nothing.
+        Results are the same bits as with fp32 storage."""
+        out = set()
+        if self.precision != "bf16":
+            return out
+        readers = {}
+        for k in self.g.kernels:
+            for n in k.nodes:
+                for v in n.inputs:
+                    lay = self.layouts.get(v)
+                    if lay is not None and lay.base[0] == "arena" and v.node not in set(k.nodes):
+                        readers.setdefault(lay.base[1], set()).add(k)
+        for k in self.g.kernels:
+            if k.kind != "matmul" or self.is_gemv(k) or k in self.prologue:
+                continue
+            mm = next(n for n in k.nodes if n.op == "matmul")
+            a = mm.inputs[0]
+            cfg, prec = self.matmul_choice(k)
+            if prec != "bf16" or int(cfg.get("tile", -1)) not in autotune.BF16_A:
+                continue
+            lay = self.layouts.get(a)
+            if lay is None or lay.base[0] != "arena" or lay.offset != 0 or lay.strides[-1] != 1:
+                continue
+            buf = lay.base[1]
+            kk = a.shape[-1]
+            if kk % 8 or any(st % 8 for st, ext in zip(lay.strides[:-1], lay.shape[:-1]) if ext > 1):
+                continue
+            if readers.get(buf) != {k} or buf in self.g.results:
+                continue
+            producer = self.g.kernel_of(buf.node)
+            if producer is not None and self._rounds_to_bf16(producer, buf):
+                out.add(buf)
+        return out
+
+    def _rounds_to_bf16(self, k, buf) -> bool:
+        """Can kernel k write its output `buf` as bf16?"""
+        outs = kernel_outputs(self.g, k, self.users)
+        if k.kind == "attention":
+            from kiln.hip.attention import match_kernel
+
+            m = match_kernel(self.g, k)
+            return (m is not None and self.layouts[m.result].base == ("arena", buf) and m.q.shape[1] > 4
+                    and all(st % 4 == 0 for st in self.layouts[m.result].strides[:-1]))
+        if outs != [buf]:
+            return False
+        if k.kind == "reduction":
+            reds = [n for n in k.nodes if n.op.startswith("reduce_")]
+            if not reds or not all(is_row_reduction(n) for n in reds):
+                return False
+            members = set(k.nodes)
+            externals = []
+            for n in k.nodes:
+                for v in n.inputs:
+                    if (v.node not in members or v.node is None) and not self.is_imm(v) and v not in externals:
+                        externals.append(v)
+            variant = self._row_pattern(k, reds, outs, externals)[0]
+            inner = buf.shape[-1]
+            return variant == kl.ROW_LAYERNORM and inner % 4 == 0 and inner <= 4096
+        if k.kind == "matmul" and not self.is_gemv(k) and k not in self.prologue:
+            cfg, prec = self.matmul_choice(k)
+            if prec != "bf16" or int(cfg.get("tile", -1)) not in autotune.BF16_A:
+                return False
+            mm = next(n for n in k.nodes if n.op == "matmul")
+            rest = [n for n in k.nodes if n is not mm]
+            ops_ = [n.op for n in rest]
+            if ops_ not in (["add"], ["add", "gelu"], ["add", "relu"]):
+                return False
+            bias = rest[0].inputs[1] if rest[0].inputs[0] is mm.out else rest[0].inputs[0]
+            chain_ok = rest[0].inputs[0] is mm.out or rest[0].inputs[1] is mm.out
+            if len(rest) == 2:
+                chain_ok = chain_ok and rest[1].inputs[0] is rest[0].out
+            n_cols = mm.out.shape[-1]
+            return (chain_ok and rest[-1].out is buf and bias.type.rank >= 1 and bias.shape[-1] == n_cols
+                    and all(s == 1 for s in bias.shape[:-1]) and n_cols % 4 == 0)
+        return False
 
     def ref(self, v, space):
         """kh_ref for value v read over iteration space `space` (right-aligned
@@ -457,12 +554,18 @@ class _Lowerer:
             ref_of[v] = len(refs)
             refs.append(self.ref(v, shape))
         out_ref = {}
+        bf16_mask = 0
         for v in outs:
             out_ref[v] = len(refs)
-            refs.append(self.ref(v, shape))
+            r = self.ref(v, shape)
+            if self.stored_bf16(v):
+                r = self.as_bf16(r, v)
+                bf16_mask |= 1 << out_ref[v]
+            refs.append(r)
         self._check_refs(refs)
 
         d = self.new_desc(kl.FAM_ROW, "row", k, shape)
+        d.cfg[7] = bf16_mask
         for j, r in enumerate(refs):
             d.refs[j] = r
         d.n_refs = len(refs)
@@ -561,6 +664,9 @@ class _Lowerer:
         d.n_passes = len(t.segments)
         nbytes = 4 * (sum(math.prod(v.shape) for v in externals) + sum(math.prod(v.shape) for v in outs))
         kind = {kl.ROW_LAYERNORM: "layernorm", kl.ROW_SOFTMAX: "softmax"}.get(variant, "generic")
+        if bf16_mask:
+            kind += " out:bf16"
+            nbytes -= 2 * sum(math.prod(v.shape) for v in outs)
         self.add(d, k, f"{kind} rows {list(rows)} x {inner}, {len(t.segments)} passes"
                        f"{'' if single else ' (chunked)'}: {' '.join(n.op for n in k.nodes)}", nbytes=nbytes)
 
@@ -656,6 +762,9 @@ class _Lowerer:
             d.variant = kl.GEMV_CHAIN   # the library may run it in a persistent chain with its GEMV neighbours
         d.gemm[0], d.gemm[1], d.gemm[2], d.gemm[3] = batch, m, n, kk
         d.refs[0] = ref3(a_src, (batch, m, kk), lay=pro[4] if pro else None)
+        if not pro and self.stored_bf16(a):
+            d.refs[0] = self.as_bf16(d.refs[0], a)
+            d.cfg[7] |= 1
         k_major = not gemv and int(cfg.get("tile", -1)) in autotune.NK_B
         nk = (gemv and self.layouts[b].base[0] == "const" and kk % 4 == 0) or k_major
         derived_b = prec in ("bf16", "bf16x3") or nk
@@ -679,7 +788,11 @@ class _Lowerer:
         out_ref = {}
         for v in outs:
             out_ref[v] = len(refs)
-            refs.append(ref3(v, space3))
+            r = ref3(v, space3)
+            if self.stored_bf16(v):
+                r = self.as_bf16(r, v)
+                d.cfg[7] |= 1 << (2 + out_ref[v])
+            refs.append(r)
         pro_refs = []
         attn_work = None
         if gemv and k in self.attn_prologue:
@@ -751,6 +864,12 @@ class _Lowerer:
         summary += f" tile {d.cfg[1]} splitk {d.cfg[2]}"
         if prec != "fp32":
             summary += f" {prec}"
+        if d.cfg[7] & 1:
+            summary += " A:bf16"
+            nbytes -= 2 * math.prod(a.shape)
+        if any(self.stored_bf16(v) for v in outs):
+            summary += " out:bf16"
+            nbytes -= 2 * math.prod(out_shape)
         if pro:
             summary += " prologue: layernorm"
             nbytes += 4 * kk * len(pro_refs)
@@ -1112,6 +1231,9 @@ class _Lowerer:
             r.offset = self.element_offset(v)
             for i in range(3):
                 r.strides[i] = st[i]
+            if j == 3 and self.stored_bf16(v):
+                r = self.as_bf16(r, v)
+                d.cfg[7] |= 1 << 3
             d.refs[j] = r
         d.n_refs = 4
         mode = kl.ATTN_MASK_NONE
@@ -1130,6 +1252,9 @@ class _Lowerer:
         what = {kl.ATTN_MASK_NONE: "no mask", kl.ATTN_MASK_CAUSAL: "causal", kl.ATTN_MASK_ADD: "additive mask"}[mode]
         scale = {kl.ATTN_SCALE_NONE: "", kl.ATTN_SCALE_MUL: f", scores * {m.scale:g}",
                  kl.ATTN_SCALE_DIV: f", scores / {m.scale:g}"}[m.scale_mode]
+        if d.cfg[7]:
+            scale += ", out:bf16"
+            nbytes -= 2 * batch * dh * tq
         self.add(d, k, f"{batch} heads x {tq} queries x {tk} keys, head dim {dh}, {what}{scale}",
                  flops=flops, nbytes=nbytes)
 
@@ -1141,6 +1266,7 @@ class _Lowerer:
                 if ops.kind(n.op) not in ("elementwise", "reduction", "matmul") and k.kind != "attention":
                     raise NotImplementedError(f"GPU backend: unexpected op '{n.op}' in a kernel")
         fused = self.find_ln_prologues() | self.find_attn_prologues()
+        self.bf16_buffers = self.plan_bf16_storage()
         for k in self.g.kernels:
             if k in fused:
                 continue

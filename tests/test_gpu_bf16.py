@@ -211,3 +211,29 @@ def test_gpt2_block_bf16(T):
         eager = model(x).numpy()
     close_to_scale(out, ref, CHAINED)
     stated(out, eager)
+
+
+@pytest.mark.parametrize("T", [512, 2048])
+def test_bf16_storage_gives_the_same_bits_on_the_block(T, monkeypatch):
+    # the GPT-2 block with bf16 products (shipped table): producers whose only
+    # reader is a 64-deep bf16 product store their outputs as bf16 (rounded
+    # to nearest even, the rounding the product does at every fragment read),
+    # so the result is bit for bit the one of the same plan with fp32 storage
+    from kiln.hip import lowering
+
+    torch.manual_seed(0)
+    model = gpt2_init_(Block(768, 12, T), seed=0).eval()
+    x = torch.randn(T, 768)
+    c = kiln.compile(model, (x,), device="cuda", matmul_precision="bf16")
+    summaries = [l.summary for l in c._exe.program.launches]
+    print(f"bf16 storage T={T}: " + " | ".join(summaries), flush=True)
+    assert any("A:bf16" in s for s in summaries)
+    xd = x.cuda()
+    got = c(xd)
+    monkeypatch.setattr(lowering._Lowerer, "plan_bf16_storage", lambda self: set())
+    plain = kiln.compile(model, (x,), device="cuda", matmul_precision="bf16", plan_cache=False)
+    assert not any("A:bf16" in l.summary for l in plain._exe.program.launches)
+    assert torch.equal(got, plain(xd))
+    with torch.no_grad():
+        eager = model(x).cuda()
+    assert float((got - eager).abs().max()) <= STATED * float(eager.abs().max())

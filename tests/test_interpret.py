@@ -306,3 +306,49 @@ def test_debug_mode_poisons_a_buffer_read_before_it_is_written():
     d.refs[load[0]].offset += 64            # one row further (elements): the last row reads the guard
     out = _debug_exe(program, c)(x)[0].numpy()
     assert np.isnan(out[-1]).all() and np.isfinite(out[:-1]).all()
+
+
+def _no_bf16_storage(monkeypatch):
+    from kiln.hip import lowering
+
+    monkeypatch.setattr(lowering._Lowerer, "plan_bf16_storage", lambda self: set())
+
+
+def test_bf16_storage_between_producers_and_products_gives_the_same_bits(monkeypatch):
+    # bf16 plans on the 64-deep product configurations: the LayerNorms, the
+    # attention and the MLP-up product round their outputs to bf16 when a
+    # bf16 product is their only reader; the products read them as bf16. The
+    # rounding is the one the products would do at every fragment read, so
+    # the result is bit for bit the one of the same plan with fp32 storage
+    torch.manual_seed(0)
+    model = gpt2_init_(Block(128, 4, 16), seed=0).eval()
+    x = torch.randn(16, 128)
+    cfg = lambda *_: {"tile": 99, "splitk": 1}
+    c = kiln.compile(model, (x,), device="cuda", matmul_precision="bf16", gpu_matmul_config=cfg)
+    summaries = [l.summary for l in c._exe.program.launches]
+    assert sum("A:bf16" in s for s in summaries) == 4, summaries
+    assert sum("out:bf16" in s for s in summaries) == 4, summaries   # 2 LayerNorms, attention, MLP up
+    got = c(x)
+    _no_bf16_storage(monkeypatch)
+    plain = kiln.compile(model, (x,), device="cuda", matmul_precision="bf16", gpu_matmul_config=cfg)
+    assert not any("bf16" in s.split("bf16", 1)[-1] for s in [l.summary for l in plain._exe.program.launches])
+    assert torch.equal(got, plain(x))
+    with torch.no_grad():
+        eager = model(x)
+    assert float((got - eager).abs().max()) <= 2e-2 * float(eager.abs().max())
+
+
+def test_bf16_storage_needs_a_single_bf16_reader():
+    # a LayerNorm output that is also a graph result stays fp32
+    torch.manual_seed(1)
+    ln = torch.nn.LayerNorm(128)
+    lin = gpt2_init_(torch.nn.Linear(128, 64), seed=1)
+
+    def fn(t):
+        y = ln(t)
+        return lin(y), y
+
+    x = torch.randn(32, 128)
+    c = kiln.compile(fn, (x,), device="cuda", matmul_precision="bf16",
+                     gpu_matmul_config=lambda *_: {"tile": 99, "splitk": 1})
+    assert not any("bf16" in l.summary.replace("tile 99 splitk 1 bf16", "") for l in c._exe.program.launches)
