@@ -16,9 +16,12 @@
  * Conventions
  *   - Every function returns KH_OK (0) or a KH_ERR_* code; kh_last_error()
  *     returns a thread-local message for the last failure.
- *   - The library allocates no user-visible device memory. Arena, constants,
- *     inputs, outputs and the workspace are device pointers owned by the
- *     caller (torch tensors) and borrowed for the plan's lifetime.
+ *   - Arena, constants, inputs, outputs and the workspace are device pointers
+ *     owned by the caller (torch tensors) and borrowed for the plan's
+ *     lifetime. The library's own device memory: a 16 MiB array per GPU for
+ *     kh_plan_run_noalloc's split-K partials, and the device state of
+ *     persistent GEMV chains, allocated by kh_plan_bind and freed by
+ *     kh_plan_destroy.
  *   - Kernels are launched on the hipStream_t the caller passes (torch's
  *     current stream), so ordering with the caller's own work is preserved.
  *   - A plan is not reentrant: calls share one arena and one workspace
@@ -176,6 +179,14 @@ typedef struct kh_pass {
  *        ADD: s + refs[4] (strides over (b, query, key)); out = softmax(s) V.
  *        cfg[2] = waves per workgroup splitting the keys (0: library picks).
  * cfg[] holds the family configuration (GEMM: tile id, split-K, precision).
+ * bf16 storage (ROW, ATTN, GEMM): bit j of cfg[7] says refs[j] holds bf16
+ * values (round to nearest even), its offset and strides counted in bf16
+ * elements. Accepted only where a kernel implements it, else
+ * KH_ERR_UNSUPPORTED: the output of the one-wave LayerNorm (offset and row
+ * stride multiples of 4), the output of the blocked attention kernel (refs[3],
+ * 8-element aligned rows), and on the bf16 configurations 95-100 of a GEMM the
+ * A operand (bit 0; unit K stride, rows 8-element aligned) and the output ref
+ * of a direct epilogue (its bit; unit N stride, rows 4-element aligned).
  */
 typedef struct kh_launch {
   int32_t family;
