@@ -11,7 +11,7 @@
 // work. Here:
 //   * a stage holds 64 K values: A rows of 64 floats (16 chunks of 16 bytes,
 //     chunk c of row r at c ^ swz_rows<16>(r)) and bf16 B rows of 64 values
-//     (8 chunks, chunk c of row n at c ^ swz_a(n)), copied with 128-bit
+//     (8 chunks, chunk c of row n at c ^ swz_h64(n)), copied with 128-bit
 //     global_load_lds (no VGPRs, no VALU); NS stages in a ring, the copies
 //     of step s + NS - 1 issued right after the barrier of step s;
 //   * a step is two 32-deep halves; in half k2 lane (row li, group g) reads
@@ -27,7 +27,13 @@
 //     residual / activation directly, other tapes through the tape
 //     interpreter.
 // Measured against the 32-deep K-contiguous kernel on 2048x3072x768 (bf16
-// weights, fp32 activations): 27.5 -> ~20 us per product.
+// weights, fp32 activations): 27.5 -> 23.1 us per product; 18.6 us with bf16
+// A. Where its time goes (the same product at K = 64 .. 3072): a one-step
+// product takes ~10 us, half of it the epilogue's output stores, and each
+// further 64-deep step ~0.74 us, bound by the copies into LDS (~15 TB/s over
+// all CUs from L2); without its MFMAs or its fragment reads a step is barely
+// shorter, and a deeper ring or a barrier in the middle of the step does not
+// shorten it.
 // bf16 storage (ABF; a.a16): when the producer of A wrote it as bf16 (a
 // LayerNorm, attention or another product whose only consumer is this one),
 // A rows are 64 bf16 values per stage (8 chunks, like B's), half the bytes
@@ -47,6 +53,7 @@
 namespace kh {
 namespace {
 
+
 template <int BM, int BN, int WM, int WN, int NS, bool TAPE, bool ABF>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_bf_kernel(const GemmArgs a) {
   constexpr int BK = 64, MT = 16, kWaves = WM * WN;
@@ -55,7 +62,9 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_bf_kernel(const GemmArgs a)
   constexpr int A_BYTES = BM * ACH * 16, STAGE = A_BYTES + BN * BK * 2;  // bytes
   constexpr int A_PW = BM * ACH / 64 / kWaves, B_PW = BN * 8 / 64 / kWaves, COPIES = A_PW + B_PW;
   constexpr int CS = TN + 4;   // epilogue staging row stride (floats, 16-byte aligned rows)
+  constexpr int QJ = MT * TN / 4 / 64;   // epilogue column groups per lane and 16-row block
   static_assert(TM % MT == 0 && TN % MT == 0, "wave tile of whole MFMA blocks");
+  static_assert((MT * TN / 4) % 64 == 0, "16-row blocks of whole 64-lane column-group rounds");
   static_assert((BM * ACH) % (64 * kWaves) == 0 && (BN * 8) % (64 * kWaves) == 0, "copy mapping");
   static_assert(NS >= 2 && NS <= 4 && (NS - 2) * COPIES < 64, "ring depth / vmcnt range");
   static_assert(NS * STAGE <= 160 * 1024 && kWaves * MT * CS * 4 <= NS * STAGE, "LDS: ring, staging inside it");
@@ -79,13 +88,13 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_bf_kernel(const GemmArgs a)
 #pragma unroll
   for (int i = 0; i < A_PW; ++i) {
     const int p = (wave * A_PW + i) * 64 + lane, r = p / ACH;
-    a_off[i] = ABF ? (uint32_t)(min(m0 + r, a.M - 1) * (int)a.sa_m + ((p % 8) ^ swz_a(r)) * 8) * 2u
+    a_off[i] = ABF ? (uint32_t)(min(m0 + r, a.M - 1) * (int)a.sa_m + ((p % 8) ^ swz_h64(r)) * 8) * 2u
                    : (uint32_t)(min(m0 + r, a.M - 1) * (int)a.sa_m + ((p % 16) ^ swz_rows<16>(r)) * 4) * 4u;
   }
 #pragma unroll
   for (int i = 0; i < B_PW; ++i) {
     const int p = (wave * B_PW + i) * 64 + lane, r = p / 8;
-    b_off[i] = (uint32_t)(min(n0 + r, a.N - 1) * (int)a.sb_n + ((p % 8) ^ swz_a(r)) * 8) * 2u;
+    b_off[i] = (uint32_t)(min(n0 + r, a.N - 1) * (int)a.sb_n + ((p % 8) ^ swz_h64(r)) * 8) * 2u;
   }
   const int n_steps = a.K / BK;   // the host checks K % 64 == 0 and K > 0
   auto issue = [&](int step) {
@@ -106,14 +115,14 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_bf_kernel(const GemmArgs a)
     for (int k2 = 0; k2 < 2; ++k2)
 #pragma unroll
       for (int q = 0; q < 2; ++q)
-        fa[fm][k2][q] = ABF ? r * 128 + ((4 * k2 + g) ^ swz_a(r)) * 16
+        fa[fm][k2][q] = ABF ? r * 128 + ((4 * k2 + g) ^ swz_h64(r)) * 16
                             : r * 256 + ((8 * k2 + 2 * g + q) ^ swz_rows<16>(r)) * 16;
   }
 #pragma unroll
   for (int fn = 0; fn < FN; ++fn) {
     const int r = wn * TN + fn * MT + li;
 #pragma unroll
-    for (int k2 = 0; k2 < 2; ++k2) fb[fn][k2] = A_BYTES + r * 128 + ((4 * k2 + g) ^ swz_a(r)) * 16;
+    for (int k2 = 0; k2 < 2; ++k2) fb[fn][k2] = A_BYTES + r * 128 + ((4 * k2 + g) ^ swz_h64(r)) * 16;
   }
   f32x4 acc[FM][FN];
 #pragma unroll
@@ -121,11 +130,15 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_bf_kernel(const GemmArgs a)
 #pragma unroll
     for (int fn = 0; fn < FN; ++fn) acc[fm][fn] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int p = 0; p < NS - 1 && p < n_steps; ++p) issue(p);
   // direct epilogue: operand pointers, strides and layouts, read from the
   // kernel arguments here (scalar loads whose indices are themselves loaded:
   // issued at the end of the tile they would be two dependent memory round
-  // trips in front of the first store, ~2 us per tile)
+  // trips in front of the first store, ~2 us per tile). Lane l handles the
+  // column groups (l + 64 j) % (TN / 4), j < QJ, of every 16-row block: its
+  // bias values are loaded here, before the first copies (so the copies'
+  // vmcnt waits never count them), and its residual values at the start of
+  // the last K step (one memory latency under that step's MFMAs instead of
+  // one per 16-row block in the epilogue: ~2 us per tile each).
   const bool has_b = a.d_bias >= 0, has_r = a.d_res >= 0;
   const int jb = has_b ? a.d_bias : 0, jr = has_r ? a.d_res : 0, jo = TAPE ? 0 : a.d_out;
   const float *pb = a.eptr[jb] + (int64_t)bidx * a.estride[jb][0];
@@ -136,6 +149,29 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_bf_kernel(const GemmArgs a)
   const bool vb = a.e_vec_mask >> jb & 1, vr = a.e_vec_mask >> jr & 1, vo = a.e_vec_mask >> jo & 1;
   const int act = a.d_act, M = a.M, N = a.N, o16 = a.o16;
   __bf16 *po16 = reinterpret_cast<__bf16 *>(a.eptr[jo]) + (int64_t)bidx * a.estride[jo][0];
+  const int row0 = m0 + wm * TM, col0 = n0 + wn * TN;
+  float4 bias_v[QJ];
+#pragma unroll
+  for (int j = 0; j < QJ; ++j) {
+    const int n = col0 + ((lane + 64 * j) % (TN / 4)) * 4;
+    bias_v[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (!TAPE && has_b && vb && n + 4 <= N) bias_v[j] = *reinterpret_cast<const float4 *>(pb + n);
+  }
+  float4 res_v[FM][QJ];
+  auto load_residual = [&]() {
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+      for (int j = 0; j < QJ; ++j) {
+        const int q = lane + 64 * j, m = row0 + fm * MT + q / (TN / 4), n = col0 + (q % (TN / 4)) * 4;
+        res_v[fm][j] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (!TAPE && has_r && vr && m < M && n + 4 <= N)
+          res_v[fm][j] = *reinterpret_cast<const float4 *>(pr + (int64_t)m * srm + n);
+      }
+  };
+
+  for (int p = 0; p < NS - 1 && p < n_steps; ++p) issue(p);
+
   for (int s = 0; s < n_steps; ++s) {
     // this wave's copies of step s landed (the copies of `later` steps were
     // issued after them), then every wave's: the barrier also says that every
@@ -146,6 +182,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_bf_kernel(const GemmArgs a)
     else wait_vmcnt<2 * COPIES>();
     stage_barrier();
     if (s + NS - 1 < n_steps) issue(s + NS - 1);
+    if (s == n_steps - 1) load_residual();   // no copy wait follows
     const char *st = ring + (s % NS) * STAGE;
 #pragma unroll
     for (int k2 = 0; k2 < 2; ++k2) {
@@ -171,11 +208,11 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_bf_kernel(const GemmArgs a)
     }
   }
 
+
   // epilogue: 16-row blocks of the wave tile through the wave's slice of the
   // ring (its own, and LDS operations of one wave complete in order)
   __syncthreads();   // every wave's fragment reads of the ring are done
   float *Cw = reinterpret_cast<float *>(ring) + wave * MT * CS;
-  const int row0 = m0 + wm * TM, col0 = n0 + wn * TN;
 #pragma unroll
   for (int fm = 0; fm < FM; ++fm) {
 #pragma unroll
@@ -184,8 +221,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_bf_kernel(const GemmArgs a)
       for (int i = 0; i < 4; ++i) Cw[(4 * g + i) * CS + fn * MT + li] = acc[fm][fn][i];
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
-    for (int q = lane; q < MT * TN / 4; q += 64) {
-      const int r = q / (TN / 4), c = (q % (TN / 4)) * 4;
+    for (int j = 0; j < QJ; ++j) {
+      const int q = lane + 64 * j, r = q / (TN / 4), c = (q % (TN / 4)) * 4;
       const int m = row0 + fm * MT + r, n = col0 + c;
       if (m < M && n < N) {
         const float4 p = *reinterpret_cast<const float4 *>(Cw + r * CS + c);
@@ -199,7 +236,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_bf_kernel(const GemmArgs a)
           float v[4] = {p.x, p.y, p.z, p.w};
           if (has_b) {
             if (vb && valid == 4) {
-              const float4 t = *reinterpret_cast<const float4 *>(pb + n);
+              const float4 t = bias_v[j];
               v[0] += t.x, v[1] += t.y, v[2] += t.z, v[3] += t.w;
             } else {
               for (int i = 0; i < valid; ++i) v[i] += pb[(int64_t)(n + i) * sbn];
@@ -208,7 +245,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_bf_kernel(const GemmArgs a)
           if (has_r) {
             const float *rr = pr + (int64_t)m * srm;
             if (vr && valid == 4) {
-              const float4 t = *reinterpret_cast<const float4 *>(rr + n);
+              const float4 t = res_v[fm][j];
               v[0] = t.x + v[0], v[1] = t.y + v[1], v[2] = t.z + v[2], v[3] = t.w + v[3];
             } else {
               for (int i = 0; i < valid; ++i) v[i] = rr[(int64_t)(n + i) * srn] + v[i];
