@@ -377,17 +377,27 @@ def _usable(entry) -> bool:
     return isinstance(entry, dict) and isinstance(entry.get("config"), dict)
 
 
-def _linear_graph(batch, m, n, k, weight, bias):
+def _linear_graph(batch, m, n, k, weight, bias, a16=False):
     """What a candidate is timed on: an nn.Linear as the frontend imports and
     freezes it - activations [.., M, K] times a constant [K, N] weight, the
-    bias added in the GEMM epilogue."""
+    bias added in the GEMM epilogue. a16: the activations are a LayerNorm's
+    output (without affine parameters), which a bf16 plan stores as bf16 for
+    the configurations that read A that way - the A operand of every bf16
+    product of a transformer block."""
     from kiln.ir import Graph, TensorType
 
     g = Graph("matmul")
     x = g.add_arg(TensorType(((batch,) if batch > 1 else ()) + (m, k)), "a")
+    if a16:
+        from kiln.frontend.fx_import import _Builder, expand_layer_norm
+
+        x = expand_layer_norm(_Builder(g), x, 1, None, None, LN_EPS)[0]
     product = g.add_node("matmul", [x, g.constant(weight, "b")])
     g.results = [g.add_node("add", [product, g.constant(bias, "bias")])]
     return g
+
+
+LN_EPS = 1e-5
 
 
 class _Trial:
@@ -399,6 +409,10 @@ class _Trial:
         self.ins = [t.data_ptr() for t in inputs]
         self.outs = [output.data_ptr()]
         self.best = float("inf")
+        # the product's own launches (a LayerNorm in front of it is not timed)
+        names = [launch.name for launch in exe.program.launches]
+        mm = [i for i, name in enumerate(names) if "matmul" in name]
+        self.index = mm[0] if len(names) > 1 and len(mm) == 1 else -1
 
     @property
     def key(self):
@@ -407,7 +421,8 @@ class _Trial:
     def measure(self, repeats, rounds):
         from kiln.hip.runtime import current_stream_handle
 
-        t = self.exe.plan.time(self.ins, self.outs, current_stream_handle(), repeats=repeats, rounds=rounds)
+        t = self.exe.plan.time(self.ins, self.outs, current_stream_handle(), index=self.index, repeats=repeats,
+                               rounds=rounds)
         self.best = min(self.best, t)
         return t
 
@@ -442,32 +457,38 @@ class GPUAutotuner:
         except OSError as err:
             warnings.warn(f"Kiln: couldn't write the GPU autotune cache ({err})")
 
-    def config_for(self, graph, kernel):
+    def config_for(self, graph, kernel, a16=False):
         """The configuration for ``kernel``'s matmul: cached, shipped, or
-        measured now (and cached). Every answer is logged."""
+        measured now (and cached). Every answer is logged. a16 (bf16 only):
+        the plan can store the product's A operand as bf16 (its producer
+        rounds it), so candidates are timed that way and keyed apart."""
         batch, m, n, k = matmul_shape(kernel)
-        key = f"{self.device_key()}|{self.precision}|{batch}x{m}x{n}x{k}"
+        a16 = bool(a16) and self.precision == "bf16"
+        key = f"{self.device_key()}|{self.precision}{'+a16' if a16 else ''}|{batch}x{m}x{n}x{k}"
         for source, table in (("cache", self._cache), ("shipped", self._shipped)):
             if _usable(table.get(key)):
                 entry = table[key]
                 break
         else:
             source = "tuned"
-            entry = self.tune(batch, m, n, k, default_config_for(batch, m, n, k, precision=self.precision))
+            entry = self.tune(batch, m, n, k, default_config_for(batch, m, n, k, precision=self.precision), a16=a16)
             if entry["candidates"]:
                 self._remember(key, entry)
-        self.log.append({"shape": (batch, m, n, k), "source": source, **entry})
+        self.log.append({"shape": (batch, m, n, k), "source": source, **({"a16": True} if a16 else {}), **entry})
         return dict(entry["config"])
 
-    def _build(self, config, batch, m, n, k, weight, bias):
+    # the lowering may pass a16 (a user's fn(graph, kernel) gets two arguments)
+    config_for.accepts_a16 = True
+
+    def _build(self, config, batch, m, n, k, weight, bias, a16=False):
         from kiln.api import Options, compile_graph
 
         options = Options(device="cuda", cuda_graphs=False, matmul_precision=self.precision,
                           gpu_matmul_config=lambda *_: dict(config))
-        exe, _ = compile_graph(_linear_graph(batch, m, n, k, weight, bias), options)
+        exe, _ = compile_graph(_linear_graph(batch, m, n, k, weight, bias, a16), options)
         return exe
 
-    def _trials(self, batch, m, n, k, configs):
+    def _trials(self, batch, m, n, k, configs, a16=False):
         """Build every configuration and keep those whose result matches
         float64; returns (trials, reasons for the rejected ones)."""
         import torch
@@ -479,14 +500,17 @@ class GPUAutotuner:
         x = torch.randn(*lead, m, k, generator=gen)
         w = torch.randn(*lead, k, n, generator=gen) / math.sqrt(k)
         bias = torch.randn(n, generator=gen) * 0.02
-        exact = x.double() @ w.double() + bias.double()
+        a = x.double()
+        if a16:
+            a = (a - a.mean(-1, keepdim=True)) / (a.var(-1, unbiased=False, keepdim=True) + LN_EPS).sqrt()
+        exact = a @ w.double() + bias.double()
         scale = float(exact.abs().max()) or 1.0
         tolerance = 1e-4 if self.precision == "fp32" else 2e-2
         x_dev = x.to(device())
         trials, rejected = [], []
         for config in configs:
             try:
-                exe = self._build(config, batch, m, n, k, w.numpy(), bias.numpy())
+                exe = self._build(config, batch, m, n, k, w.numpy(), bias.numpy(), a16)
                 (out,) = exe(x_dev)
                 err = float((out.double().cpu() - exact).abs().max()) / scale
             except Exception as failure:  # noqa: BLE001 - a candidate that fails is dropped, never fatal
@@ -499,10 +523,10 @@ class GPUAutotuner:
                 rejected.append(f"{config}: relative error {err:.1e}")
         return trials, rejected
 
-    def tune(self, batch, m, n, k, default):
+    def tune(self, batch, m, n, k, default, a16=False):
         started = time.perf_counter()
         configs = [default] + [c for c in candidates(batch, m, n, k, precision=self.precision) if c != default]
-        trials, rejected = self._trials(batch, m, n, k, configs)
+        trials, rejected = self._trials(batch, m, n, k, configs, a16)
         if not trials:
             warnings.warn(f"Kiln: no GEMM config passed for {batch}x{m}x{n}x{k}; keeping the default. "
                           + "; ".join(rejected[:3]))

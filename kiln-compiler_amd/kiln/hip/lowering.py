@@ -244,34 +244,53 @@ class _Lowerer:
         out = set()
         if self.precision != "bf16":
             return out
-        readers = {}
-        for k in self.g.kernels:
-            for n in k.nodes:
-                for v in n.inputs:
-                    lay = self.layouts.get(v)
-                    if lay is not None and lay.base[0] == "arena" and v.node not in set(k.nodes):
-                        readers.setdefault(lay.base[1], set()).add(k)
         for k in self.g.kernels:
             if k.kind != "matmul" or self.is_gemv(k) or k in self.prologue:
                 continue
-            mm = next(n for n in k.nodes if n.op == "matmul")
-            a = mm.inputs[0]
             cfg, prec = self.matmul_choice(k)
             if prec != "bf16" or int(cfg.get("tile", -1)) not in autotune.BF16_A:
                 continue
-            lay = self.layouts.get(a)
-            if lay is None or lay.base[0] != "arena" or lay.offset != 0 or lay.strides[-1] != 1:
-                continue
-            buf = lay.base[1]
-            kk = a.shape[-1]
-            if kk % 8 or any(st % 8 for st, ext in zip(lay.strides[:-1], lay.shape[:-1]) if ext > 1):
-                continue
-            if readers.get(buf) != {k} or buf in self.g.results:
-                continue
-            producer = self.g.kernel_of(buf.node)
-            if producer is not None and self._rounds_to_bf16(producer, buf):
+            buf = self.a16_buffer(k)
+            if buf is not None:
                 out.add(buf)
         return out
+
+    def _arena_readers(self):
+        """arena buffer -> the kernels that read it"""
+        if not hasattr(self, "_readers"):
+            self._readers = {}
+            for k in self.g.kernels:
+                members = set(k.nodes)
+                for n in k.nodes:
+                    for v in n.inputs:
+                        lay = self.layouts.get(v)
+                        if lay is not None and lay.base[0] == "arena" and v.node not in members:
+                            self._readers.setdefault(lay.base[1], set()).add(k)
+        return self._readers
+
+    def a16_buffer(self, k):
+        """The arena buffer of matmul kernel k's A operand if it can be stored
+        as bf16 for a product that reads A that way: A is the whole buffer,
+        K-contiguous with 16-byte aligned rows, read by k alone, not a graph
+        result, and written by a launch that can round its output to bf16.
+        Otherwise None. (Whether k reads A as bf16 depends on its tile; this
+        does not ask.)"""
+        if self.precision != "bf16" or k.kind != "matmul" or k in self.prologue:
+            return None
+        mm = next(n for n in k.nodes if n.op == "matmul")
+        a, b = mm.inputs
+        if a.shape[-2] == 1 or self.layouts[b].base[0] != "const":
+            return None
+        lay = self.layouts.get(a)
+        if lay is None or lay.base[0] != "arena" or lay.offset != 0 or lay.strides[-1] != 1:
+            return None
+        buf = lay.base[1]
+        if a.shape[-1] % 8 or any(st % 8 for st, ext in zip(lay.strides[:-1], lay.shape[:-1]) if ext > 1):
+            return None
+        if self._arena_readers().get(buf) != {k} or buf in self.g.results:
+            return None
+        producer = self.g.kernel_of(buf.node)
+        return buf if producer is not None and self._rounds_to_bf16(producer, buf) else None
 
     def _rounds_to_bf16(self, k, buf) -> bool:
         """Can kernel k write its output `buf` as bf16?"""
@@ -901,7 +920,11 @@ class _Lowerer:
         """(configuration, precision) of matmul kernel k, asked once per kernel."""
         if k not in self._cfg:
             mm = next(n for n in k.nodes if n.op == "matmul")
-            cfg = dict(self.matmul_config(self.g, k))
+            if getattr(self.matmul_config, "accepts_a16", False) and self.a16_buffer(k) is not None:
+                # the tuner times this product reading A as bf16, as the plan can store it
+                cfg = dict(self.matmul_config(self.g, k, a16=True))
+            else:
+                cfg = dict(self.matmul_config(self.g, k))
             prec = cfg.get("precision", self.precision)
             if prec in ("bf16", "bf16x3") and self.layouts[mm.inputs[1]].base[0] != "const":
                 # bf16 inputs need B as a build-time bf16 copy of a constant; a

@@ -5,8 +5,9 @@
 Runs the measured autotuner (kiln.hip.autotune.GPUAutotuner, no cache, no
 shipped table) on one MI355X for every GEMM shape of the GPT-2-small block at
 T = 128, 512, 1024 and 2048 tokens, the 12-layer stack and the benchmark GEMM
-sweep, in fp32 and bf16, and writes the winners keyed like the on-disk cache
-(device|CUs|precision|BxMxNxK). The table is what makes a plan the same on
+sweep, in fp32 and bf16 (the block products also as "bf16+a16": timed reading a
+bf16 A operand, as a bf16 plan stores it), and writes the winners keyed like
+the on-disk cache (device|CUs|precision|BxMxNxK). The table is what makes a plan the same on
 every MI355X: compiled models look their shapes up there before measuring.
 """
 
@@ -17,6 +18,12 @@ import json
 import sys
 
 from kiln.hip import autotune
+
+# block products (qkv, attention projection, MLP up, MLP down) at each token
+# count: in a bf16 plan their A operands come from a LayerNorm, the attention
+# or the MLP-up product, which store them as bf16 for the configurations that
+# read A that way ("bf16+a16" entries)
+BLOCK = sorted((t, n, k) for t in (128, 512, 1024, 2048) for n, k in ((2304, 768), (768, 768), (3072, 768), (768, 3072)))
 
 SHAPES = sorted({
     # GPT-2 block: qkv, attention projection, MLP up, MLP down, at each token count
@@ -47,24 +54,28 @@ def warm_up(seconds=1.0):
 def main(argv=None):
     p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     p.add_argument("--out", default=str(autotune.SHIPPED_PATH))
-    p.add_argument("--precision", nargs="+", choices=("fp32", "bf16", "bf16x3"), default=None,
+    p.add_argument("--precision", nargs="+", choices=("fp32", "bf16", "bf16+a16", "bf16x3"), default=None,
                    help="re-tune only these precisions and keep the table's other entries")
     p.add_argument("--max-m", type=int, default=None,
                    help="re-tune only shapes with at most this many rows and keep the table's other entries")
     args = p.parse_args(argv)
     warm_up()
     shapes = [s for s in SHAPES if args.max_m is None or s[0] <= args.max_m]
-    precisions = args.precision or ("fp32", "bf16", "bf16x3")
+    precisions = args.precision or ("fp32", "bf16", "bf16+a16", "bf16x3")
     table = {}
     if args.precision or args.max_m is not None:
         retuned = {(p_, f"1x{m}x{n}x{k}") for p_ in precisions for m, n, k in shapes}
         table = {key: v for key, v in autotune.shipped_configs().items()
                  if (key.split("|")[-2], key.split("|")[-1]) not in retuned}
     for precision in precisions:
-        tuner = autotune.GPUAutotuner(precision=precision, use_cache=False, use_shipped=False)
+        a16 = precision == "bf16+a16"
+        base = "bf16" if a16 else precision
+        tuner = autotune.GPUAutotuner(precision=base, use_cache=False, use_shipped=False)
         device = tuner.device_key()
         for m, n, k in shapes:
-            entry = tuner.tune(1, m, n, k, autotune.default_config_for(1, m, n, k, precision=precision))
+            if a16 and (m, n, k) not in BLOCK:
+                continue
+            entry = tuner.tune(1, m, n, k, autotune.default_config_for(1, m, n, k, precision=base), a16=a16)
             if entry["candidates"]:
                 table[f"{device}|{precision}|1x{m}x{n}x{k}"] = entry
             print(f"{precision} {m}x{n}x{k}: {entry['config']} {entry['tflops']} TFLOP/s", flush=True)

@@ -338,6 +338,30 @@ def test_bf16_storage_between_producers_and_products_gives_the_same_bits(monkeyp
     assert float((got - eager).abs().max()) <= 2e-2 * float(eager.abs().max())
 
 
+def test_tuner_is_asked_for_a16_exactly_where_a_can_be_stored_bf16():
+    # the block's four products have producers that can round A to bf16 (the
+    # LayerNorms, the attention, the MLP-up product): the tuner is asked to
+    # time them reading bf16 A; a Linear on a graph input is not
+    asked = []
+
+    def cfg(graph, kernel, a16=False):
+        asked.append((kernel.name, a16))
+        return {"tile": 99, "splitk": 1}
+
+    cfg.accepts_a16 = True
+    torch.manual_seed(0)
+    model = gpt2_init_(Block(128, 4, 16), seed=0).eval()
+    kiln.compile(model, (torch.randn(16, 128),), device="cuda", matmul_precision="bf16", gpu_matmul_config=cfg)
+    assert len(asked) == 4 and all(a16 for _, a16 in asked), asked
+    asked.clear()
+    kiln.compile(torch.nn.Linear(128, 64), (torch.randn(16, 128),), device="cuda", matmul_precision="bf16",
+                 gpu_matmul_config=cfg)
+    assert asked and not any(a16 for _, a16 in asked), asked
+    asked.clear()
+    kiln.compile(model, (torch.randn(16, 128),), device="cuda", gpu_matmul_config=cfg)   # fp32: never
+    assert asked and not any(a16 for _, a16 in asked), asked
+
+
 def test_bf16_storage_needs_a_single_bf16_reader():
     # a LayerNorm output that is also a graph result stays fp32
     torch.manual_seed(1)
