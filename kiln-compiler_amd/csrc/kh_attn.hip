@@ -40,6 +40,9 @@
 //     memory;
 //   * workgroups are issued longest-first (causal rows near the end of the
 //     sequence have the most key blocks);
+//   * grids that 32-query blocks leave short of work (under 1.5 workgroups
+//     per CU: the GPT-2 block up to T = 512) run attn16_kernel, 16 queries
+//     per workgroup on 16 x 16 MFMAs;
 //   * decode shapes (at most 4 queries over at most 64 keys) run a separate
 //     kernel with one wave per query row (attn_rows_kernel).
 #include <algorithm>
@@ -54,6 +57,7 @@ namespace kh {
 namespace {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kQB = 32;  // queries per workgroup
 constexpr int kKB = 32;  // keys per block
@@ -290,6 +294,222 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
   }
 }
 
+// The same computation with 16 queries per workgroup on
+// v_mfma_f32_16x16x4_f32, for grids that 32-query blocks leave short of work
+// (a 32-key block costs a wave half the matrix-core time it costs above, and
+// a causal row's key blocks spread over twice the workgroups). Lane (li =
+// lane % 16, g = lane / 16):
+//   * S^T = K Q^T as two 16 x 16 tiles per 32-key block: lane (li, g) holds
+//     the scores of query li with keys 16 t + 4 g + r (tile t, register r);
+//     MFMA step j of a tile sums head-dimension element g * DH/4 + j of the
+//     four lane groups (the dot product is order-free), so each lane reads
+//     its Q and K row pieces as contiguous 128-bit loads;
+//   * the softmax max and sum over a query's 32 keys: 8 registers per lane,
+//     then the four lane groups (two xor shuffles, the same bits in all four);
+//   * O^T += V^T P^T: MFMA step (t, r) takes key 16 t + 4 g + r from lane
+//     group g, which is where that key's probability already is; lane (li,
+//     g) ends with head-dimension elements 16 d + 4 g .. + 3 of query li,
+//     written as one 128-bit store per 16-wide tile d.
+template <int DH, int NW, bool ADD>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) void attn16_kernel(const AttnArgs a) {
+  constexpr int QB = 16;       // queries per workgroup
+  constexpr int QS = DH / 4;   // head-dimension elements per lane group (MFMA steps of a score tile)
+  constexpr int DT = DH / 16;  // 16-wide tiles of the head dimension in O^T
+  __shared__ float o_part[NW][QB][DH + 4];
+  __shared__ float m_part[NW][QB], l_part[NW][QB];
+
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int li = lane & 15, g = lane >> 4;
+  const int b = blockIdx.x % a.batch;
+  const int qb = a.n_qblocks - 1 - (int)(blockIdx.x / a.batch);
+  const int q0 = qb * QB;
+  const int qi = q0 + li;
+  const bool q_ok = qi < a.tq;
+
+  constexpr float kLog2e = 1.4426950408889634f;
+  const float c_scale = a.scale_mode == KH_ATTN_SCALE_MUL   ? a.scale * kLog2e
+                        : a.scale_mode == KH_ATTN_SCALE_DIV ? kLog2e / a.scale
+                                                            : kLog2e;
+  float qf[QS];
+  {
+    const float *qp = a.q + b * a.q_b + (int64_t)min(qi, a.tq - 1) * a.q_t + g * QS;
+#pragma unroll
+    for (int j = 0; j < QS / 4; ++j) {
+      float4 t = *reinterpret_cast<const float4 *>(qp + 4 * j);
+      if (!q_ok) t = make_float4(0.f, 0.f, 0.f, 0.f);
+      qf[4 * j] = t.x * c_scale, qf[4 * j + 1] = t.y * c_scale;
+      qf[4 * j + 2] = t.z * c_scale, qf[4 * j + 3] = t.w * c_scale;
+    }
+  }
+
+  const bool causal = a.mask_mode == KH_ATTN_MASK_CAUSAL;
+  const int kend = causal ? min(a.tk, q0 + QB) : a.tk;
+  const int nkb = (kend + kKB - 1) / kKB;
+  const int lim = causal ? min(a.tk, qi + 1) : a.tk;
+
+  // buffer loads as in attn_kernel: key indices clamped to the last key
+  const uint32_t k_t4 = (uint32_t)a.k_t * 4, v_t4 = (uint32_t)a.v_t * 4;
+  const __amdgpu_buffer_rsrc_t k_res = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)(a.k + b * a.k_b), (short)0, (int)(((uint32_t)(a.tk - 1) * (uint32_t)a.k_t + DH) * 4), kBufferFlags);
+  const __amdgpu_buffer_rsrc_t v_res = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)(a.v + b * a.v_b), (short)0, (int)(((uint32_t)(a.tk - 1) * (uint32_t)a.v_t + DH) * 4), kBufferFlags);
+  const uint32_t k_last = (uint32_t)(a.tk - 1) * k_t4 + g * QS * 4;
+  const uint32_t v_last = (uint32_t)(a.tk - 1) * v_t4 + li * 4;
+  // K[16 t + li][g * QS ..] of key block kb, tile t
+  auto load_k = [&](int kb, float4 (&kf)[2][QS / 4]) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const uint32_t off = min((uint32_t)(kb * kKB + t * 16 + li) * k_t4 + g * QS * 4, k_last);
+#pragma unroll
+      for (int j = 0; j < QS / 4; ++j) {
+        const auto x = __builtin_amdgcn_raw_buffer_load_b128(k_res, off + 16 * j, 0, 0);
+        kf[t][j] = make_float4(__uint_as_float(x[0]), __uint_as_float(x[1]), __uint_as_float(x[2]), __uint_as_float(x[3]));
+      }
+    }
+  };
+  // V^T operand of MFMA step (t, r), tile d: V[16 t + 4 g + r][16 d + li]
+  auto load_v = [&](int kb, float (&vf)[8 * DT]) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const uint32_t off = min((uint32_t)(kb * kKB + t * 16 + 4 * g + r) * v_t4 + li * 4, v_last);
+#pragma unroll
+        for (int d = 0; d < DT; ++d)
+          vf[(t * 4 + r) * DT + d] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(v_res, off + 64 * d, 0, 0));
+      }
+  };
+  auto scores = [&](const float4 (&kc)[2][QS / 4], f32x4 (&s)[2]) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      s[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < QS / 4; ++j) {
+        s[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kc[t][j].x, qf[4 * j + 0], s[t], 0, 0, 0);
+        s[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kc[t][j].y, qf[4 * j + 1], s[t], 0, 0, 0);
+        s[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kc[t][j].z, qf[4 * j + 2], s[t], 0, 0, 0);
+        s[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(kc[t][j].w, qf[4 * j + 3], s[t], 0, 0, 0);
+      }
+    }
+  };
+
+  f32x4 oacc[DT];
+#pragma unroll
+  for (int d = 0; d < DT; ++d) oacc[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.0f;
+
+  // online softmax of one score block, as in attn_kernel (base-2 domain, a
+  // row with no finite score so far takes its exponentials against 0)
+  auto softmax = [&](f32x4 (&s)[2], int kb, auto masked) {
+    const int room = lim - kb * kKB - 4 * g;   // key(t, r) < lim  <=>  16 t + r < room
+    float mx = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float u = s[t][r];
+        if (ADD) {
+          const int key = min(kb * kKB + t * 16 + 4 * g + r, a.tk - 1);
+          u = fmaf(a.mask[b * a.m_b + (int64_t)min(qi, a.tq - 1) * a.m_q + (int64_t)key * a.m_k], kLog2e, u);
+        }
+        if (decltype(masked)::value) u = 16 * t + r < room ? u : -INFINITY;
+        s[t][r] = u;
+        mx = fmaxf(mx, u);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+    float sum = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        s[t][r] = __builtin_amdgcn_exp2f(s[t][r] - m_use);
+        sum += s[t][r];
+      }
+    sum += __shfl_xor(sum, 16);
+    sum += __shfl_xor(sum, 32);
+    l_run = fmaf(l_run, alpha, sum);
+    m_run = m_new;
+#pragma unroll
+    for (int d = 0; d < DT; ++d) oacc[d] *= alpha;
+  };
+  auto pv = [&](const float (&vf)[8 * DT], const f32x4 (&p)[2]) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int d = 0; d < DT; ++d)
+          oacc[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[(t * 4 + r) * DT + d], p[t][r], oacc[d], 0, 0, 0);
+  };
+
+  // the software pipeline of attn_kernel: K two blocks and V one block ahead
+  int kb = w;
+  if (kb < nkb) {
+    float4 kf[2][QS / 4];
+    float vf[8 * DT];
+    f32x4 s_cur[2], s_nxt[2];
+    load_k(kb, kf);
+    load_v(kb, vf);
+    scores(kf, s_cur);
+    load_k(min(kb + NW, nkb - 1), kf);
+    for (; kb + NW < nkb; kb += NW) {
+      scores(kf, s_nxt);
+      softmax(s_cur, kb, std::false_type{});
+      load_k(min(kb + 2 * NW, nkb - 1), kf);
+      pv(vf, s_cur);
+      load_v(kb + NW, vf);
+      s_cur[0] = s_nxt[0], s_cur[1] = s_nxt[1];
+#pragma unroll
+      for (int i = 0; i < 2 * QS; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
+      }
+#pragma unroll
+      for (int i = 0; i < 8 * DT; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
+        __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);  // VALU
+      }
+    }
+    softmax(s_cur, kb, std::true_type{});
+    pv(vf, s_cur);
+  }
+
+  // merge the NW key-split partials as in attn_kernel
+  if (g == 0) m_part[w][li] = m_run, l_part[w][li] = l_run;
+#pragma unroll
+  for (int d = 0; d < DT; ++d)
+    *reinterpret_cast<float4 *>(&o_part[w][li][d * 16 + 4 * g]) = make_float4(oacc[d][0], oacc[d][1], oacc[d][2], oacc[d][3]);
+  __syncthreads();
+  constexpr int kChunks = QB * DH / 4;
+  for (int c = threadIdx.x; c < kChunks; c += 64 * NW) {
+    const int qr = c / (DH / 4), d = (c % (DH / 4)) * 4;
+    if (q0 + qr >= a.tq) continue;
+    float mm = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < NW; ++u) mm = fmaxf(mm, m_part[u][qr]);
+    const float mu = mm == -INFINITY ? 0.0f : mm;
+    float l = 0.0f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int u = 0; u < NW; ++u) {
+      const float e = __builtin_amdgcn_exp2f(m_part[u][qr] - mu);
+      l += l_part[u][qr] * e;
+      acc.x += o_part[u][qr][d] * e, acc.y += o_part[u][qr][d + 1] * e;
+      acc.z += o_part[u][qr][d + 2] * e, acc.w += o_part[u][qr][d + 3] * e;
+    }
+    acc.x /= l, acc.y /= l, acc.z /= l, acc.w /= l;
+    const int64_t at = b * a.o_b + (int64_t)(q0 + qr) * a.o_t + d;
+    if (a.o16) store_bf16x4(a.o, at, acc.x, acc.y, acc.z, acc.w);
+    else *reinterpret_cast<float4 *>(a.o + at) = acc;
+  }
+}
+
 // Few-query attention (decode shapes: Tq <= kRowsMaxQ queries over at most
 // kRowsMaxK keys): one wave per (head, query), lane d holding head dimension
 // d (lanes DH.. idle for DH = 32). Each chunk of kRowKeys keys has its K and
@@ -349,6 +569,7 @@ class AttnOp final : public Op {
   AttnArgs args{};
   int dh = 64, nw = 4;
   bool rows = false;  // few-query kernel
+  bool q16 = false;   // 16 queries per workgroup (attn16_kernel)
   dim3 grid;
 
   hipError_t launch(float *const *ptrs, float *, hipStream_t stream) override {
@@ -367,6 +588,22 @@ class AttnOp final : public Op {
       else hipLaunchKernelGGL((attn_rows_kernel<32, false>), g, dim3(256), 0, stream, a);
       return hipGetLastError();
     }
+#define KH_ATTN16_LAUNCH(D, W)                                                                       \
+  if (q16 && dh == D && nw == W) {                                                                   \
+    if (a.mask_mode == KH_ATTN_MASK_ADD)                                                             \
+      hipLaunchKernelGGL((attn16_kernel<D, W, true>), grid, dim3(64 * W), 0, stream, a);            \
+    else                                                                                             \
+      hipLaunchKernelGGL((attn16_kernel<D, W, false>), grid, dim3(64 * W), 0, stream, a);           \
+    return hipGetLastError();                                                                        \
+  }
+    KH_ATTN16_LAUNCH(64, 8)
+    KH_ATTN16_LAUNCH(64, 4)
+    KH_ATTN16_LAUNCH(64, 2)
+    KH_ATTN16_LAUNCH(64, 1)
+    KH_ATTN16_LAUNCH(32, 4)
+    KH_ATTN16_LAUNCH(32, 2)
+    KH_ATTN16_LAUNCH(32, 1)
+#undef KH_ATTN16_LAUNCH
 #define KH_ATTN_LAUNCH(D, W)                                                                         \
   if (dh == D && nw == W) {                                                                          \
     if (a.mask_mode == KH_ATTN_MASK_ADD)                                                             \
@@ -451,7 +688,17 @@ std::unique_ptr<Op> make_attn(const kh_launch &L, std::string &err, bool &unsupp
   if (mask_mode == KH_ATTN_MASK_ADD)
     a.m_b = L.refs[4].strides[0], a.m_q = L.refs[4].strides[1], a.m_k = L.refs[4].strides[2];
   a.mask_mode = mask_mode, a.scale_mode = scale_mode, a.scale = L.fparams[0];
-  a.n_qblocks = (int)((tq + kQB - 1) / kQB);
+  // queries per workgroup (cfg[3]: 0 = library picks, 16 or 32)
+  const int qpw = L.cfg[3];
+  if (qpw != 0 && qpw != 16 && qpw != 32) {
+    err = "attention: queries per workgroup must be 0, 16 or 32";
+    return nullptr;
+  }
+  // 16 when 32-query blocks would give under 1.5 workgroups per CU (measured
+  // on the GPT-2 block, 12 heads causal: T = 128 6.2 -> 4.7 us, 512 13.5 ->
+  // 11.4 us; from T = 1024 on the 32-query kernel is faster)
+  op->q16 = qpw == 16 || (qpw == 0 && 2 * batch * ((tq + kQB - 1) / kQB) < 3ll * current_device().cus);
+  a.n_qblocks = (int)((tq + (op->q16 ? 16 : kQB) - 1) / (op->q16 ? 16 : kQB));
   op->dh = (int)dh;
   // key-split waves per workgroup: enough workgroups x waves to cover the GPU
   int nw = L.cfg[2];
@@ -465,6 +712,9 @@ std::unique_ptr<Op> make_attn(const kh_launch &L, std::string &err, bool &unsupp
     // the grid is under three workgroups per CU (T = 1024 .. 1536: 20% faster)
     nw = groups >= 16ll * current_device().cus ? 2 : 4;
     if (nw == 4 && visited >= 16 && groups < 3ll * current_device().cus && dh == 64) nw = 8;
+    // 16-query blocks: four waves, eight from 8 visited key blocks (T = 512:
+    // 12.3 -> 11.4 us)
+    if (op->q16) nw = visited >= 8 && dh == 64 ? 8 : 4;
     if (kblocks < nw) nw = kblocks >= 2 ? 2 : 1;
   }
   if (nw != 1 && nw != 2 && nw != 4 && !(nw == 8 && dh == 64)) {

@@ -187,7 +187,11 @@ class _GpuBuild:
         config_for, source_name, tuner = self.config_source()
         key = None
         if self.options.plan_cache and source_name is not None:
+            from kiln.hip import lowering
+
             source = source_name + "|gemv-chains" if self.options.gemv_chains else source_name
+            if lowering.ATTN_QUERIES:
+                source += f"|attention-q{lowering.ATTN_QUERIES}"
             key = plans.plan_key(str(self.graph), self.precision, source, kl.device_info())
             stored = plans.load(key)
             if stored is not None:

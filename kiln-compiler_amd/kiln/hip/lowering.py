@@ -37,6 +37,10 @@ from kiln.passes.buffers import Layout, compute_layouts, kernel_inputs, kernel_o
 from kiln.passes.fusion import is_row_reduction
 
 ROW_SINGLE_CHUNK = 1024   # rows up to this length are held in registers (workgroup x 4)
+# queries per workgroup of the blocked attention kernel (kh_launch.cfg[3]):
+# 0 lets the library pick (16 for grids that 32-query blocks leave short of
+# work); 16 or 32 forces one
+ATTN_QUERIES = 0
 
 _UNARY_OP = {"neg": "neg", "exp": "exp", "tanh": "tanh", "sigmoid": "sigmoid", "relu": "relu",
              "rsqrt": "rsqrt", "sqrt": "sqrt", "erf": "erf", "copy": "mov"}
@@ -1267,6 +1271,7 @@ class _Lowerer:
                 d.refs[4] = self.ref(m.mask, (batch, tq, tk))
                 d.n_refs = 5
         d.cfg[0], d.cfg[1] = mode, m.scale_mode
+        d.cfg[3] = ATTN_QUERIES
         d.fparams[0] = m.scale
         causal = mode == kl.ATTN_MASK_CAUSAL
         pairs = sum(min(tk, i + 1) for i in range(tq)) if causal else tq * tk

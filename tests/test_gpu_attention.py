@@ -23,6 +23,16 @@ from test_gpu import ATOL, RTOL, as_tuple, imported
 pytestmark = pytest.mark.gpu
 
 
+@pytest.fixture(params=[0, 16, 32], ids=["q-auto", "q16", "q32"])
+def queries(request, monkeypatch):
+    """Queries per workgroup of the blocked kernel: the library's choice, or
+    forced to 16 (attn16_kernel) or 32."""
+    from kiln.hip import lowering
+
+    monkeypatch.setattr(lowering, "ATTN_QUERIES", request.param)
+    return request.param
+
+
 def n_attention(compiled):
     return sum(1 for l in compiled._exe.program.launches if l.family == kl.FAM_ATTN)
 
@@ -70,14 +80,14 @@ def qkv(b, tq, tk, d, seed=0):
 
 @pytest.mark.parametrize("T", [1, 5, 32, 77, 128, 200])
 @pytest.mark.parametrize("d", [32, 64])
-def test_causal(T, d):
+def test_causal(T, d, queries):
     mask = torch.full((T, T), float("-inf")).triu(1)
     c = compare(Attn(mask, scale=1 / math.sqrt(d)), *qkv(3, T, T, d, seed=T))
     assert "causal" in c._exe.program.source
 
 
 @pytest.mark.parametrize("tq, tk", [(1, 40), (50, 90), (64, 64), (33, 7)])
-def test_no_mask_cross_attention(tq, tk):
+def test_no_mask_cross_attention(tq, tk, queries):
     compare(Attn(None, scale=0.125), *qkv(2, tq, tk, 64, seed=tq + tk))
 
 
@@ -144,12 +154,12 @@ def test_decode_attention_as_gemv_prologue(tk, d, masked, prec):
         assert torch.equal(c(q, k, v), first)
 
 
-def test_divided_scale_and_no_head_merge():
+def test_divided_scale_and_no_head_merge(queries):
     c = compare(Attn(None, scale=8.0, divide=True, merge=False), *qkv(4, 70, 70, 64, seed=3))
     assert "scores / 8" in c._exe.program.source
 
 
-def test_additive_mask():
+def test_additive_mask(queries):
     g = torch.Generator().manual_seed(7)
     mask = torch.randn(45, 60, generator=g)
     mask[torch.rand(45, 60, generator=g) < 0.3] = float("-inf")
@@ -158,7 +168,7 @@ def test_additive_mask():
     assert "additive mask" in c._exe.program.source
 
 
-def test_fully_masked_rows_are_nan_as_in_eager():
+def test_fully_masked_rows_are_nan_as_in_eager(queries):
     mask = torch.zeros(20, 20)
     mask[3, :] = float("-inf")
     mask[11, :] = float("-inf")
