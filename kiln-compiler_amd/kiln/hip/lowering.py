@@ -887,7 +887,7 @@ class _Lowerer:
         summary += f" tile {d.cfg[1]} splitk {d.cfg[2]}"
         if prec != "fp32":
             summary += f" {prec}"
-        if d.cfg[7] & 1:
+        if not gemv and d.cfg[7] & 1:   # (a GEMV's cfg[7] is its attention prologue's key count)
             summary += " A:bf16"
             nbytes -= 2 * math.prod(a.shape)
         if any(self.stored_bf16(v) for v in outs):

@@ -225,6 +225,8 @@ def test_decode_attention_runs_as_the_projection_prologue():
     # ln_1 -> qkv, attention -> c_proj, ln_2 -> fc, proj: four GEMVs
     assert [kl.FAMILY_NAMES[l.family] for l in prog.launches] == ["gemv"] * 4
     assert "prologue: attention" in prog.launches[1].summary
+    # (cfg[7] counts the keys: the summary does not read it as bf16 storage)
+    assert not any("bf16" in l.summary for l in prog.launches)
     d = prog.launches[1].desc
     assert (d.cfg[0], d.cfg[4], d.cfg[7]) == (64, kl.GEMV_PRO_ATTN, 1)
     kl.Plan([l.desc for l in prog.launches])
