@@ -37,6 +37,12 @@ from kiln.passes.buffers import Layout, compute_layouts, kernel_inputs, kernel_o
 from kiln.passes.fusion import is_row_reduction
 
 ROW_SINGLE_CHUNK = 1024   # rows up to this length are held in registers (workgroup x 4)
+# rows up to which a LayerNorm runs as the prologue of the small-M GEMM that
+# reads it: the prologue's row statistics cost the GEMM time that grows with
+# the rows, the LayerNorm launch it saves ~3 us (GPT-2 block, whole call:
+# T = 128 0.0470 against 0.0496 ms, T = 256 0.0700 against 0.0713, T = 384
+# 0.0947 against 0.0922, T = 512 0.1030 against 0.1020)
+LN_PROLOGUE_MAX_ROWS = 256
 # queries per workgroup of the blocked attention kernel (kh_launch.cfg[3]):
 # 0 lets the library pick (16 for grids that 32-query blocks leave short of
 # work); 16 or 32 forces one
@@ -1064,7 +1070,7 @@ class _Lowerer:
         """Whether matmul kernel km can run a LayerNorm of x (gamma, beta:
         its parameters or None) as its prologue: an fp32 small-M configuration
         (B the [N][K] copy of a constant, A read with unit K stride) holding at
-        most 4 rows per wave, K <= 1024, x laid out like the A operand it
+        most 4 rows per wave, K <= 1024, at most LN_PROLOGUE_MAX_ROWS rows, x laid out like the A operand it
         replaces (`lay`: x's storage as [rows, K]), and gamma / beta constants
         (folded into build-time copies)."""
         cfg, prec = self.matmul_choice(km)
@@ -1074,7 +1080,7 @@ class _Lowerer:
         bm, wk = autotune.TILES[tile][0], autotune.TILES[tile][5]
         mm = next(n for n in km.nodes if n.op == "matmul")
         m, kk = mm.inputs[0].shape[-2], mm.inputs[0].shape[-1]
-        if bm % wk or bm > 4 * wk or kk > 1024:
+        if bm % wk or bm > 4 * wk or kk > 1024 or m > LN_PROLOGUE_MAX_ROWS:
             return False
         if not (self.skinny_ok(mm) and autotune.k_major_fits(m, kk, tile)):
             return False

@@ -437,7 +437,7 @@ def test_layernorm_prologue_on_every_small_m_configuration(tile):
     # log2(27) bits); repeated launches agree bit for bit
     cfg = lambda *_: {"tile": tile, "splitk": 1}
     for m, n, k, affine, loc, sd, first in ((77, 133, 32, True, 3.0, 2.0, None),
-                                            (300, 452, 256, False, 3.0, 2.0, None),
+                                            (250, 452, 256, False, 3.0, 2.0, None),
                                             (128, 200, 768, True, 3.0, 2.0, None),
                                             (40, 64, 1024, True, 3.0, 2.0, None),
                                             (64, 96, 768, True, 100.0, 1.0, None),

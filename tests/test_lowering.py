@@ -210,6 +210,20 @@ def test_bias_gelu_is_one_elementwise_launch_with_vector_operands():
     assert list(bias.strides[:2]) == [0, 1]
 
 
+def test_layernorm_prologue_only_up_to_its_row_limit():
+    # past LN_PROLOGUE_MAX_ROWS rows the LayerNorm keeps its own launch (the
+    # prologue's row statistics would cost the product more than the launch)
+    from kiln.hip import lowering
+
+    lim = lowering.LN_PROLOGUE_MAX_ROWS
+    for rows, fused in ((lim, True), (lim + 32, False)):
+        cfg = lambda *_: {"tile": 66, "splitk": 1}
+        g = import_exported(torch.export.export(_ln_linear().eval(), (torch.randn(rows, 64),)).run_decompositions())
+        PassManager(build_passes(Options())).run(g)
+        prog = lower_graph(g, matmul_config=cfg)
+        assert any("prologue: layernorm" in l.summary for l in prog.launches) == fused
+
+
 def test_stack_decode_plan():
     _, prog = lowered(Stack(12, 768, 12, 1), torch.randn(1, 768))
     # ln_1 and ln_2 of every layer run as the prologue of the qkv / fc GEMV;
