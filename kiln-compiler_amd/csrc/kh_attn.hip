@@ -315,7 +315,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
   constexpr int QB = 16;       // queries per workgroup
   constexpr int QS = DH / 4;   // head-dimension elements per lane group (MFMA steps of a score tile)
   constexpr int DT = DH / 16;  // 16-wide tiles of the head dimension in O^T
-  __shared__ float o_part[NW][QB][DH + 4];
+  __shared__ __attribute__((aligned(16))) float o_part[NW][QB][DH + 4];   // (128-bit stores: 16-byte rows)
   __shared__ float m_part[NW][QB], l_part[NW][QB];
 
   const int lane = threadIdx.x & 63;
