@@ -213,6 +213,33 @@ def test_gpt2_block_bf16(T):
     stated(out, eager)
 
 
+@pytest.mark.parametrize("queries", [16, 32])
+def test_bf16_attention_output_on_both_query_blocks(queries, monkeypatch):
+    # every product on a 64-deep bf16 configuration, so the attention (16 or
+    # 32 queries per workgroup, ragged T) writes its head-merged output as
+    # bf16 for the projection: the same bits as the plan with fp32 storage
+    from kiln.hip import lowering
+
+    monkeypatch.setattr(lowering, "ATTN_QUERIES", queries)
+    T = 200
+    torch.manual_seed(3)
+    model = gpt2_init_(Block(768, 12, T), seed=3).eval()
+    x = torch.randn(T, 768)
+    cfg = lambda *_: {"tile": 99, "splitk": 1}
+    c = kiln.compile(model, (x,), device="cuda", matmul_precision="bf16", gpu_matmul_config=cfg)
+    summaries = [l.summary for l in c._exe.program.launches]
+    assert any("heads" in s and "out:bf16" in s for s in summaries), summaries
+    xd = x.cuda()
+    got = c(xd)
+    monkeypatch.setattr(lowering._Lowerer, "plan_bf16_storage", lambda self: set())
+    plain = kiln.compile(model, (x,), device="cuda", matmul_precision="bf16", gpu_matmul_config=cfg)
+    assert not any("bf16" in s.split("bf16", 1)[-1] for s in [l.summary for l in plain._exe.program.launches])
+    assert torch.equal(got, plain(xd))
+    with torch.no_grad():
+        eager = model(x).cuda()
+    assert float((got - eager).abs().max()) <= STATED * float(eager.abs().max())
+
+
 @pytest.mark.parametrize("T", [512, 2048])
 def test_bf16_storage_gives_the_same_bits_on_the_block(T, monkeypatch):
     # the GPT-2 block with bf16 products (shipped table): producers whose only
