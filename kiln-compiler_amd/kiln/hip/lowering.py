@@ -893,6 +893,8 @@ class _Lowerer:
         summary += f" tile {d.cfg[1]} splitk {d.cfg[2]}"
         if prec != "fp32":
             summary += f" {prec}"
+        if prec == "bf16":   # B read as its bf16 copy (the three-pass copy holds 2 bf16 per weight)
+            nbytes -= 2 * math.prod(b.shape)
         if not gemv and d.cfg[7] & 1:   # (a GEMV's cfg[7] is its attention prologue's key count)
             summary += " A:bf16"
             nbytes -= 2 * math.prod(a.shape)

@@ -224,6 +224,20 @@ def test_layernorm_prologue_only_up_to_its_row_limit():
         assert any("prologue: layernorm" in l.summary for l in prog.launches) == fused
 
 
+@pytest.mark.parametrize("prec, b_bytes", [("fp32", 4), ("bf16", 2), ("bf16x3", 4)])
+def test_matmul_launch_bytes_count_the_weight_copy_read(prec, b_bytes):
+    # algorithmic bytes of a Linear: A, the bias and the output in fp32, the
+    # weights as the copy the kernel reads (bf16: 2 bytes a weight; the
+    # three-pass copy holds two bf16 per weight)
+    m, k, n = 64, 96, 80
+    g = import_exported(torch.export.export(torch.nn.Linear(k, n).eval(), (torch.randn(m, k),)).run_decompositions())
+    PassManager(build_passes(Options())).run(g)
+    prog = lower_graph(g, precision=prec, matmul_config=lambda *_: {"tile": autotune.default_config_for(
+        1, m, n, k, precision=prec)["tile"], "splitk": 1})
+    (launch,) = prog.launches
+    assert launch.bytes == 4 * (m * k + n + m * n) + b_bytes * k * n
+
+
 def test_stack_decode_plan():
     _, prog = lowered(Stack(12, 768, 12, 1), torch.randn(1, 768))
     # ln_1 and ln_2 of every layer run as the prologue of the qkv / fc GEMV;
