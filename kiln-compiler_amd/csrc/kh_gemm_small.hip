@@ -283,8 +283,9 @@ __global__ __launch_bounds__(64 * WK) void gemm_small_kernel(const GemmArgs a) {
   }
   wait_vmcnt<0>();   // (no copy of this wave is outstanding past here)
 
-  // direct epilogue: this thread's first output group's operands, loaded
-  // before the partial tiles are summed
+  // this thread's first output group's operands (the direct epilogue's bias
+  // and residual, the LN prologue's g and c), loaded before the partial
+  // tiles are summed so their latency overlaps the reduction
   constexpr int GROUPS = BM * BN / 4;
   const int q0 = threadIdx.x;
   auto group_mn = [&](int q, int &m, int &n) {
@@ -298,14 +299,18 @@ __global__ __launch_bounds__(64 * WK) void gemm_small_kernel(const GemmArgs a) {
     for (int i = 0; i < valid; ++i) v[i] = p[(int64_t)(n + i) * a.estride[j][2]];
     return make_float4(v[0], v[1], v[2], v[3]);
   };
-  float4 pre_b = make_float4(0.f, 0.f, 0.f, 0.f), pre_r = pre_b;
-  if (a.direct && q0 < GROUPS) {
+  float4 pre_b = make_float4(0.f, 0.f, 0.f, 0.f), pre_r = pre_b, pre_g = pre_b, pre_c = pre_b;
+  if ((a.direct || LN) && q0 < GROUPS) {
     int m, n;
     group_mn(q0, m, n);
     if (m < a.M && n < a.N) {
       const int valid = min(4, a.N - n);
-      if (a.d_bias >= 0) pre_b = load4(a.d_bias, m, n, valid);
-      if (a.d_res >= 0) pre_r = load4(a.d_res, m, n, valid);
+      if constexpr (LN) {   // the prologue's column vectors g and c
+        pre_g = load4(a.pro_g, m, n, valid);
+        if (a.pro_b >= 0) pre_c = load4(a.pro_b, m, n, valid);
+      }
+      if (a.direct && a.d_bias >= 0) pre_b = load4(a.d_bias, m, n, valid);
+      if (a.direct && a.d_res >= 0) pre_r = load4(a.d_res, m, n, valid);
     }
   }
 
@@ -357,11 +362,11 @@ __global__ __launch_bounds__(64 * WK) void gemm_small_kernel(const GemmArgs a) {
         merge(st.x, st.y, st.z, o.x, o.y, o.z);
       }
       const float rstd = rsqrtf(st.z * a.pro_c2 + a.pro_eps), mu = st.y;
-      const float4 gs = load4(a.pro_g, m, n, valid);
+      const float4 gs = q == q0 ? pre_g : load4(a.pro_g, m, n, valid);
       sum.x = rstd * fmaf(-mu, gs.x, sum.x), sum.y = rstd * fmaf(-mu, gs.y, sum.y);
       sum.z = rstd * fmaf(-mu, gs.z, sum.z), sum.w = rstd * fmaf(-mu, gs.w, sum.w);
       if (a.pro_b >= 0) {   // the folded beta . B
-        const float4 c = load4(a.pro_b, m, n, valid);
+        const float4 c = q == q0 ? pre_c : load4(a.pro_b, m, n, valid);
         sum.x += c.x, sum.y += c.y, sum.z += c.z, sum.w += c.w;
       }
     }
