@@ -71,6 +71,10 @@ def parse():
     p.add_argument("--traffic-groups", metavar="PREFIX",
                    help="with --traffic-report: the probe groups whose label starts with PREFIX (e.g. c2_, "
                         "decode12, bf16_T2048) instead of one block's launches")
+    p.add_argument("--probes", action="store_true",
+                   help="run only the library's measurement probes and print their summary: the MFMA / VALU "
+                        "issue probe, and the attention kernel's per-workgroup timeline on the T = 2048 block "
+                        "shape (12 heads; also 4 heads, one workgroup per CU)")
     p.add_argument("--counter-report", nargs="+", metavar="PROBE_JSON DIR",
                    help="turn SQ counter passes over --counter-probe into the per-launch MFMA utilisation, "
                         "wait and LDS summary (no GPU needed)")
@@ -869,6 +873,82 @@ def cpu_baseline(T, oracle_line=True):
     return out
 
 
+def mfma_probe():
+    """Shader cycles per 32x32x2 fp32 MFMA per SIMD under the library's
+    kh_probe_mfma_valu: MFMA-only streams, then MFMAs with VALU work in the
+    same wave (one and two waves per SIMD)."""
+    import ctypes
+    from kiln.hip import lib as kl
+
+    lib = kl.load()
+    out = (ctypes.c_double * 2)()
+    log("MFMA / VALU issue probe (32x32x2 fp32 MFMA = 64 matrix-core cycles at full rate):")
+    log("  waves/SIMD chains group valu   cycles/MFMA   clock GHz")
+    for wps in (1, 2):
+        for c, g, v in ((1, 1, 0), (2, 1, 0), (1, 1, 1), (1, 1, 2), (1, 1, 4), (2, 1, 2), (4, 1, 2), (8, 1, 2),
+                        (1, 4, 8), (1, 8, 16), (2, 8, 16), (1, 32, 64)):
+            kl.check(lib.kh_probe_mfma_valu(c, g, v, wps, out), "kh_probe_mfma_valu")
+            log(f"  {wps:10d} {c:6d} {g:5d} {v:4d} {out[0]:13.1f} {out[1]:11.3f}")
+
+
+def attention_timeline():
+    """Per-workgroup timeline of the 32-query attention kernel on the GPT-2
+    block's T = 2048 operands (the QKV product's [T, 2304] output read as
+    q, k, v), from kh_probe_attn_timeline: makespan, per-block cycles of the
+    longest workgroups, the shader clock, how many workgroups ran per CU and
+    when the CUs went idle."""
+    import ctypes
+    import numpy as np
+    import torch
+    from kiln.hip import lib as kl
+
+    lib = kl.load()
+    T, DH = 2048, 64
+    torch.manual_seed(0)
+    qkv = torch.randn(T, 3 * 768, device="cuda")
+    out = torch.empty(T, 768, device="cuda")
+    st = (ctypes.c_int64 * 8)(DH, 2304, DH, 2304, DH, 2304, DH, 768)
+    stream = torch.cuda.current_stream().cuda_stream
+    log("attention timeline (kh_probe_attn_timeline, causal, head dim 64, GPT-2 QKV layout):")
+    for heads, nw in ((12, 4), (12, 8), (4, 4), (4, 8)):
+        nq = (T + 31) // 32
+        rec = torch.zeros(heads * nq * nw * 8, dtype=torch.int64, device="cuda")
+        q, k, v = qkv[:, :768], qkv[:, 768:1536], qkv[:, 1536:]
+        for _ in range(20):  # the last run's records are kept
+            kl.check(lib.kh_probe_attn_timeline(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), heads, T,
+                                                T, st, nw, 0.125, rec.data_ptr(), stream), "kh_probe_attn_timeline")
+        torch.cuda.synchronize()
+        r = rec.cpu().numpy().reshape(heads * nq, nw, 8).view(np.uint64).astype(np.float64)
+        t0, t1, t2 = r[:, :, 0].min(1), r[:, :, 1], r[:, :, 2].max(1)
+        base = t0.min()
+        span = (t2.max() - base) * 0.01
+        blocks = r[:, :, 7].max(1)
+        ghz = (r[:, :, 4] - r[:, :, 3]) / ((r[:, :, 2] - r[:, :, 0]) * 10.0)
+        hw = r[:, 0, 5].astype(np.int64)
+        cu_id = (r[:, 0, 6].astype(np.int64) & 15) * 4096 + ((hw >> 13) & 7) * 512 + ((hw >> 12) & 1) * 256 + ((hw >> 8) & 15)
+        longest = blocks >= blocks.max() - 1
+        dur = (t2 - t0) * 0.01
+        cyc = ((r[:, :, 4] - r[:, :, 3]).max(1))[longest] / blocks[longest]
+        per_cu = {}
+        idle = {}
+        for g in range(len(t0)):
+            per_cu[cu_id[g]] = per_cu.get(cu_id[g], 0) + 1
+            idle[cu_id[g]] = max(idle.get(cu_id[g], 0.0), (t2[g] - base) * 0.01)
+        counts = {}
+        for n in per_cu.values():
+            counts[n] = counts.get(n, 0) + 1
+        iv = np.array(sorted(idle.values()))
+        grid = np.linspace(0, span, 9)
+        active = [int(((t0 - base) * 0.01 <= t).sum() - ((t2 - base) * 0.01 <= t).sum()) for t in grid]
+        log(f"  {heads} heads, {nw} waves per workgroup: {len(t0)} workgroups on {len(per_cu)} CUs, makespan "
+            f"{span:.1f} us, shader clock median {np.median(ghz):.2f} GHz")
+        log(f"    longest workgroups ({int(blocks.max())} key blocks per wave): {np.median(dur[longest]):.1f} us, "
+            f"{np.median(cyc):.0f} shader cycles per key block per wave (64 MFMAs = 4096 matrix-core cycles)")
+        log(f"    workgroups per CU: {dict(sorted(counts.items()))}; CUs idle from {iv.min():.1f} us (first), "
+            f"{np.median(iv):.1f} (median), {iv.max():.1f} (last)")
+        log("    workgroups running: " + "  ".join(f"{t:.0f}us:{n}" for t, n in zip(grid, active)))
+
+
 def main():
     args = parse()
     if args.traffic_report:
@@ -895,6 +975,10 @@ def main():
 
     if args.counter_probe:
         counter_probe(args)
+        return
+    if args.probes:
+        mfma_probe()
+        attention_timeline()
         return
     torch.manual_seed(0)
     info = kl.device_info() if kl.load() else {}

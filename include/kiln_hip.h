@@ -311,6 +311,34 @@ int kh_plan_chain_timeouts(kh_plan *plan, uint64_t *timeouts);
 int kh_plan_chain_spin(kh_plan *plan, int64_t ticks);
 int kh_plan_destroy(kh_plan *plan);
 
+/*
+ * Measurement probes. No counterpart in the reference (its kernels are
+ * generated and it measures them only by wall time, kiln/gpu/runtime.py
+ * 93-132); these measure what bounds the hand-written attention kernel.
+ *
+ * kh_probe_attn_timeline: one run of the 32-query attention kernel (head
+ * dimension 64, causal, scores * scale, `waves` = 4 or 8 key-split waves per
+ * workgroup) over q, k, v and out given as in an ATTN launch (strides8 =
+ * q, k, v, out {head, row} element strides), built with timestamps: rec
+ * receives 8 uint64 per wave of every workgroup (workgroup g, wave w at
+ * rec + 8 (g * waves + w)): start, loop end and end on the 100 MHz wall
+ * clock, shader clock at start and end, the hardware's HW_ID and XCC_ID
+ * words, and the key blocks the wave processed. rec must hold
+ * 8 * waves * batch * ceil(tq / 32) words. Launches on `stream`.
+ *
+ * kh_probe_mfma_valu: shader cycles per 32x32x2 fp32 MFMA per SIMD
+ * (out2[0]) and the shader clock in GHz (out2[1]) when each SIMD runs
+ * waves_per_simd (1 or 2) waves that issue MFMAs in groups of `group`
+ * back-to-back over `chains` independent accumulators, each group followed
+ * by `valu` independent fp32 FMAs (timed from the first start to the last end
+ * of the waves of one CU). Combinations offered (chains, group,
+ * valu): (1,1,0) (2,1,0) (1,1,1) (1,1,2) (1,1,4) (2,1,2) (4,1,2) (8,1,2)
+ * (1,4,8) (1,8,16) (2,8,16) (1,32,64). Allocates and synchronises the device.
+ */
+int kh_probe_attn_timeline(const float *q, const float *k, const float *v, float *out, int batch, int tq, int tk,
+                           const int64_t *strides8, int waves, float scale, uint64_t *rec, void *stream);
+int kh_probe_mfma_valu(int chains, int group, int valu, int waves_per_simd, double *out2);
+
 #ifdef __cplusplus
 }
 #endif

@@ -73,6 +73,7 @@ struct AttnArgs {
   int32_t mask_mode, scale_mode;
   float scale;
   int32_t o16;             // the output is bf16 (its consumer is a bf16 matmul)
+  uint64_t *rec;           // timeline probe only: 8 words per wave (kh_probe_attn_timeline)
 };
 
 // Exchange between the two lane halves (lanes l and l ^ 32): returns
@@ -83,8 +84,12 @@ __device__ __forceinline__ float2 halves(float x) {
   return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
-template <int DH, int NW, bool ADD>
+// REC (the timeline probe only): each wave also records its start, loop-end
+// and end times, the shader clock and the CU it ran on.
+template <int DH, int NW, bool ADD, bool REC = false>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) void attn_kernel(const AttnArgs a) {
+  uint64_t rec_t0 = 0, rec_c0 = 0;
+  if constexpr (REC) rec_t0 = __builtin_amdgcn_s_memrealtime(), rec_c0 = __builtin_amdgcn_s_memtime();
   constexpr int NT = DH / 32;  // 32-wide tiles of the head dimension in O^T
   constexpr int QS = DH / 2;   // head-dim elements per lane half (= MFMA steps of S^T)
   __shared__ float o_part[NW][kQB][DH + 4];
@@ -263,6 +268,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     pv(vf, s_cur);
   }
 
+  uint64_t rec_t1 = 0;
+  if constexpr (REC) rec_t1 = __builtin_amdgcn_s_memrealtime();
   // merge the NW key-split partials: o = sum_w 2^(m_w - M) o_w / sum_w 2^(m_w - M) l_w
   if (half == 0) m_part[w][col] = m_run, l_part[w][col] = l_run;
 #pragma unroll
@@ -291,6 +298,17 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     const int64_t at = b * a.o_b + (int64_t)(q0 + qr) * a.o_t + d;
     if (a.o16) store_bf16x4(a.o, at, acc.x, acc.y, acc.z, acc.w);
     else *reinterpret_cast<float4 *>(a.o + at) = acc;
+  }
+  if constexpr (REC) {
+    const uint64_t t2 = __builtin_amdgcn_s_memrealtime(), c2 = __builtin_amdgcn_s_memtime();
+    uint32_t hw, xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    if (lane == 0) {
+      uint64_t *r = a.rec + ((int64_t)blockIdx.x * NW + w) * 8;
+      r[0] = rec_t0, r[1] = rec_t1, r[2] = t2, r[3] = rec_c0, r[4] = c2;
+      r[5] = hw, r[6] = xcc, r[7] = w < nkb ? (uint64_t)((nkb - w + NW - 1) / NW) : 0;
+    }
   }
 }
 
@@ -741,6 +759,34 @@ std::unique_ptr<Op> make_attn(const kh_launch &L, std::string &err, bool &unsupp
   }
   a.o16 = m16 ? 1 : 0;
   return op;
+}
+
+hipError_t probe_attn_timeline(const float *q, const float *k, const float *v, float *o, int batch, int tq, int tk,
+                               const int64_t *st, int nw, float scale, uint64_t *rec, hipStream_t stream,
+                               std::string &err) {
+  if (!q || !k || !v || !o || !st || !rec || batch <= 0 || tq <= 0 || tk <= 0 || (nw != 4 && nw != 8)) {
+    err = "attention timeline: null operand, empty shape or waves not 4 or 8";
+    return hipErrorInvalidValue;
+  }
+  const float *base[4] = {q, k, v, o};
+  for (int j = 0; j < 4; ++j) {
+    const int64_t rows = j == 0 || j == 3 ? tq : tk;
+    const int64_t span = (int64_t)(batch - 1) * st[2 * j] + (rows - 1) * st[2 * j + 1] + 64;
+    if ((reinterpret_cast<uintptr_t>(base[j]) & 15) || st[2 * j] < 0 || st[2 * j + 1] < 0 || st[2 * j] % 4 ||
+        st[2 * j + 1] % 4 || span >= (1ll << 30)) {
+      err = "attention timeline: operands need 16-byte aligned rows and spans under 2^30 elements";
+      return hipErrorInvalidValue;
+    }
+  }
+  AttnArgs a{};
+  a.q = q, a.k = k, a.v = v, a.o = o, a.mask = nullptr, a.rec = rec;
+  a.q_b = st[0], a.q_t = st[1], a.k_b = st[2], a.k_t = st[3], a.v_b = st[4], a.v_t = st[5], a.o_b = st[6], a.o_t = st[7];
+  a.batch = batch, a.tq = tq, a.tk = tk, a.n_qblocks = (tq + kQB - 1) / kQB;
+  a.mask_mode = KH_ATTN_MASK_CAUSAL, a.scale_mode = KH_ATTN_SCALE_MUL, a.scale = scale;
+  const dim3 grid((unsigned)(batch * a.n_qblocks));
+  if (nw == 4) hipLaunchKernelGGL((attn_kernel<64, 4, false, true>), grid, dim3(256), 0, stream, a);
+  else hipLaunchKernelGGL((attn_kernel<64, 8, false, true>), grid, dim3(512), 0, stream, a);
+  return hipGetLastError();
 }
 
 }  // namespace kh

@@ -90,6 +90,12 @@ bool run_launch_host(const kh_launch &L, float *const *ptrs, std::string &err);
 int gemm_config_count();
 bool gemm_config(int id, int32_t out8[8]);
 
+// Measurement probes (kh_probe_attn_timeline, kh_probe_mfma_valu).
+hipError_t probe_attn_timeline(const float *q, const float *k, const float *v, float *o, int batch, int tq, int tk,
+                               const int64_t *strides8, int nw, float scale, uint64_t *rec, hipStream_t stream,
+                               std::string &err);
+hipError_t probe_mfma_valu(int chains, int group, int valu, int waves_per_simd, double out2[2], std::string &err);
+
 // Shared descriptor checks.
 // Facts about a validated tape range.
 struct TapeInfo {

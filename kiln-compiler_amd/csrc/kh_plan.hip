@@ -528,4 +528,22 @@ int kh_plan_destroy(kh_plan *plan) {
   return KH_OK;
 }
 
+int kh_probe_attn_timeline(const float *q, const float *k, const float *v, float *out, int batch, int tq, int tk,
+                           const int64_t *strides8, int waves, float scale, uint64_t *rec, void *stream) {
+  std::string err;
+  const hipError_t e = kh::probe_attn_timeline(q, k, v, out, batch, tq, tk, strides8, waves, scale, rec,
+                                               (hipStream_t)stream, err);
+  if (e == hipErrorInvalidValue && !err.empty()) return fail(KH_ERR_INVALID, err);
+  if (e != hipSuccess) return kh::hip_fail(e, "kh_probe_attn_timeline");
+  return KH_OK;
+}
+
+int kh_probe_mfma_valu(int chains, int group, int valu, int waves_per_simd, double *out2) {
+  std::string err;
+  const hipError_t e = kh::probe_mfma_valu(chains, group, valu, waves_per_simd, out2, err);
+  if (e == hipErrorInvalidValue && !err.empty()) return fail(KH_ERR_INVALID, err);
+  if (e != hipSuccess) return fail(KH_ERR_HIP, err.empty() ? std::string("kh_probe_mfma_valu") : err);
+  return KH_OK;
+}
+
 }  // extern "C"

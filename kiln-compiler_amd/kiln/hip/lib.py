@@ -112,6 +112,9 @@ def load():
         "kh_plan_chain_timeouts": (ip, [vp, ctypes.POINTER(ctypes.c_uint64)]),
         "kh_plan_chain_spin": (ip, [vp, ctypes.c_int64]),
         "kh_plan_destroy": (ip, [vp]),
+        "kh_probe_attn_timeline": (ip, [vp, vp, vp, vp, ip, ip, ip, ctypes.POINTER(ctypes.c_int64), ip,
+                                        ctypes.c_float, vp, vp]),
+        "kh_probe_mfma_valu": (ip, [ip, ip, ip, ip, ctypes.POINTER(ctypes.c_double)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -133,7 +136,7 @@ EXPORTED = ("kh_version", "kh_build_id", "kh_abi_sizes", "kh_last_error", "kh_in
             "kh_plan_run_one",
             "kh_plan_capture", "kh_plan_replay", "kh_plan_time", "kh_plan_chains", "kh_plan_chain_timeouts",
             "kh_plan_chain_spin",
-            "kh_plan_destroy")
+            "kh_plan_destroy", "kh_probe_attn_timeline", "kh_probe_mfma_valu")
 
 
 def check(rc: int, what: str = ""):
