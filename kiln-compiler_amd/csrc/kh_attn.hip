@@ -768,6 +768,10 @@ hipError_t probe_attn_timeline(const float *q, const float *k, const float *v, f
     err = "attention timeline: null operand, empty shape or waves not 4 or 8";
     return hipErrorInvalidValue;
   }
+  if (tq >= (1 << 24) || tk >= (1 << 24) || (int64_t)batch * ((tq + kQB - 1) / kQB) >= (1ll << 31)) {
+    err = "attention timeline: sizes out of range";
+    return hipErrorInvalidValue;
+  }
   const float *base[4] = {q, k, v, o};
   for (int j = 0; j < 4; ++j) {
     const int64_t rows = j == 0 || j == 3 ? tq : tk;
