@@ -178,7 +178,11 @@ typedef struct kh_pass {
  *        s / fparams[0], then (cfg[0]) CAUSAL: -inf where key > query, or
  *        ADD: s + refs[4] (strides over (b, query, key)); out = softmax(s) V.
  *        cfg[2] = waves per workgroup splitting the keys (0: library picks),
- *        cfg[3] = queries per workgroup (0: library picks, 16 or 32).
+ *        cfg[3] = queries per workgroup (0: library picks, 16 or 32),
+ *        cfg[5] = products precision: 0 fp32; 1 bf16 inputs (q and k for the
+ *        scores, the softmax weights and v for the weighted sum rounded to
+ *        bf16, round to nearest even; scores, softmax and accumulation
+ *        fp32).
  * cfg[] holds the family configuration (GEMM: tile id, split-K, precision).
  * bf16 storage (ROW, ATTN, GEMM): bit j of cfg[7] says refs[j] holds bf16
  * values (round to nearest even), its offset and strides counted in bf16

@@ -58,6 +58,7 @@ namespace {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kQB = 32;  // queries per workgroup
 constexpr int kKB = 32;  // keys per block
@@ -76,6 +77,14 @@ struct AttnArgs {
   uint64_t *rec;           // timeline probe only: 8 words per wave (kh_probe_attn_timeline)
 };
 
+// Eight fp32 values rounded to bf16 (round to nearest even), an MFMA operand.
+__device__ __forceinline__ bf16x8 pack_bf16x8(const float4 &x, const float4 &y) {
+  bf16x8 r;
+  r[0] = (__bf16)x.x, r[1] = (__bf16)x.y, r[2] = (__bf16)x.z, r[3] = (__bf16)x.w;
+  r[4] = (__bf16)y.x, r[5] = (__bf16)y.y, r[6] = (__bf16)y.z, r[7] = (__bf16)y.w;
+  return r;
+}
+
 // Exchange between the two lane halves (lanes l and l ^ 32): returns
 // (x[l & 31], x[32 + (l & 31)]), the low half's value first in every lane,
 // so a combine of the two is the same in both halves. One v_permlane32_swap.
@@ -84,9 +93,22 @@ __device__ __forceinline__ float2 halves(float x) {
   return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
+// BF: bf16 products (plans whose matrix products take bf16 inputs): Q and K
+// rounded to bf16 (round to nearest even) for the scores, the probabilities
+// and V for P.V, on v_mfma_f32_32x32x16_bf16; the scale, mask, softmax and
+// accumulation stay fp32. The accumulator layouts are those of the fp32
+// MFMAs, so everything but the operands is shared:
+//   * S^T: MFMA c (16-wide chunk c of the head dimension) takes from lane
+//     (col, half) K[key col] and Q[query col] elements 16 c + 8 half .. + 7;
+//   * O^T += V^T P^T: MFMA (c, t) covers keys 16 c .. 16 c + 15 of the
+//     block, K slot j of lane half h being key 16 c + 8 (j / 4) + 4 h + j % 4
+//     - the keys of the lane's score registers 8 c .. 8 c + 7 - so a lane's B
+//     operand is its own probabilities and its A operand the V values the
+//     fp32 path loads for those registers;
+//   * K and V are loaded as fp32 and rounded when an MFMA operand is formed.
 // REC (the timeline probe only): each wave also records its start, loop-end
 // and end times, the shader clock and the CU it ran on.
-template <int DH, int NW, bool ADD, bool REC = false>
+template <int DH, int NW, bool ADD, bool BF = false, bool REC = false>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) void attn_kernel(const AttnArgs a) {
   uint64_t rec_t0 = 0, rec_c0 = 0;
   if constexpr (REC) rec_t0 = __builtin_amdgcn_s_memrealtime(), rec_c0 = __builtin_amdgcn_s_memtime();
@@ -112,8 +134,17 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
   const float c_scale = a.scale_mode == KH_ATTN_SCALE_MUL   ? a.scale * kLog2e
                         : a.scale_mode == KH_ATTN_SCALE_DIV ? kLog2e / a.scale
                                                             : kLog2e;
-  float qf[QS];
-  {
+  float qf[BF ? 1 : QS];
+  bf16x8 qh[BF ? DH / 16 : 1];   // (bf16 products: Q as it is, the scale applied to the scores)
+  if constexpr (BF) {
+    const float *qp = a.q + b * a.q_b + (int64_t)min(qi, a.tq - 1) * a.q_t + 8 * half;
+#pragma unroll
+    for (int c = 0; c < DH / 16; ++c) {
+      float4 x = *reinterpret_cast<const float4 *>(qp + 16 * c), y = *reinterpret_cast<const float4 *>(qp + 16 * c + 4);
+      if (!q_ok) x = make_float4(0.f, 0.f, 0.f, 0.f), y = x;
+      qh[c] = pack_bf16x8(x, y);
+    }
+  } else {
     const float *qp = a.q + b * a.q_b + (int64_t)min(qi, a.tq - 1) * a.q_t + half * QS;
 #pragma unroll
     for (int j = 0; j < QS / 4; ++j) {
@@ -140,13 +171,16 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
       (void *)(a.k + b * a.k_b), (short)0, (int)(((uint32_t)(a.tk - 1) * (uint32_t)a.k_t + DH) * 4), kBufferFlags);
   const __amdgpu_buffer_rsrc_t v_res = __builtin_amdgcn_make_buffer_rsrc(
       (void *)(a.v + b * a.v_b), (short)0, (int)(((uint32_t)(a.tk - 1) * (uint32_t)a.v_t + DH) * 4), kBufferFlags);
-  const uint32_t k_last = (uint32_t)(a.tk - 1) * k_t4 + half * QS * 4;
+  // a lane's K elements: fp32 products half * QS .. + QS - 1; bf16 products
+  // 16 c + 8 half .. + 7 of every chunk c (kf[2 c], kf[2 c + 1])
+  const uint32_t k_lane = BF ? half * 32 : half * QS * 4;
+  const uint32_t k_last = (uint32_t)(a.tk - 1) * k_t4 + k_lane;
   const uint32_t v_last = (uint32_t)(a.tk - 1) * v_t4 + col * 4;
   auto load_k = [&](int kb, float4 (&kf)[QS / 4]) {
-    const uint32_t off = min((uint32_t)(kb * kKB + col) * k_t4 + half * QS * 4, k_last);
+    const uint32_t off = min((uint32_t)(kb * kKB + col) * k_t4 + k_lane, k_last);
 #pragma unroll
     for (int j = 0; j < QS / 4; ++j) {
-      const auto x = __builtin_amdgcn_raw_buffer_load_b128(k_res, off + 16 * j, 0, 0);
+      const auto x = __builtin_amdgcn_raw_buffer_load_b128(k_res, off + (BF ? 64 * (j / 2) + 16 * (j % 2) : 16 * j), 0, 0);
       kf[j] = make_float4(__uint_as_float(x[0]), __uint_as_float(x[1]), __uint_as_float(x[2]), __uint_as_float(x[3]));
     }
   };
@@ -168,6 +202,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     f32x16 s;
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[r] = 0.0f;
+    if constexpr (BF) {
+#pragma unroll
+      for (int c = 0; c < DH / 16; ++c)
+        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pack_bf16x8(kc[2 * c], kc[2 * c + 1]), qh[c], s, 0, 0, 0);
+      return s;
+    }
 #pragma unroll
     for (int j = 0; j < QS / 4; ++j) {
       s = __builtin_amdgcn_mfma_f32_32x32x2f32(kc[j].x, qf[4 * j + 0], s, 0, 0, 0);
@@ -195,7 +235,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     float mx = -INFINITY;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      float u = s[r];
+      float u = BF ? s[r] * c_scale : s[r];
       if (ADD) {
         const int key = min(kb * kKB + half * 4 + (r >> 2) * 8 + (r & 3), a.tk - 1);
         u = fmaf(a.mask[b * a.m_b + (int64_t)min(qi, a.tq - 1) * a.m_q + (int64_t)key * a.m_k], kLog2e, u);
@@ -224,6 +264,21 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
   };
   // O^T += V^T P^T, key order permuted to match the score registers
   auto pv = [&](const float (&vf)[16 * NT], const f32x16 &p) {
+    if constexpr (BF) {
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const bf16x8 pb = pack_bf16x8(make_float4(p[8 * c], p[8 * c + 1], p[8 * c + 2], p[8 * c + 3]),
+                                      make_float4(p[8 * c + 4], p[8 * c + 5], p[8 * c + 6], p[8 * c + 7]));
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          const float *v8 = vf + 8 * c * NT + t;
+          const bf16x8 va = pack_bf16x8(make_float4(v8[0], v8[NT], v8[2 * NT], v8[3 * NT]),
+                                        make_float4(v8[4 * NT], v8[5 * NT], v8[6 * NT], v8[7 * NT]));
+          oacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb, oacc[t], 0, 0, 0);
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int r = 0; r < 16; ++r)
 #pragma unroll
@@ -250,18 +305,21 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
       pv(vf, s_cur);
       load_v(kb + NW, vf);
       s_cur = s_nxt;
-      // issue order: each score MFMA of the next block followed by softmax
-      // VALU work, then each P.V MFMA followed by a load and its addressing
+      // issue order (fp32 products): each score MFMA of the next block
+      // followed by softmax VALU work, then each P.V MFMA followed by a load
+      // and its addressing
+      if constexpr (!BF) {
 #pragma unroll
-      for (int i = 0; i < 32; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
-      }
+        for (int i = 0; i < 32; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
+        }
 #pragma unroll
-      for (int i = 0; i < 32; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
-        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
+        for (int i = 0; i < 32; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
+          __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
+        }
       }
     }
     softmax(s_cur, kb, std::true_type{});
@@ -528,6 +586,218 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
   }
 }
 
+// The 16-query computation with bf16 products (plans whose matrix products
+// run bf16 inputs with fp32 accumulation): Q and K rounded to bf16 (round to
+// nearest even) for the scores, the probabilities and V rounded to bf16 for
+// P.V, on v_mfma_f32_16x16x32_bf16; the scale, the mask, the softmax and the
+// accumulation stay fp32. Lane (li, g) layout as in attn16_kernel:
+//   * S^T tile t (16 keys) is one MFMA per 32-wide chunk c of the head
+//     dimension: lane (li, g) gives K[16 t + li] and Q[li] elements
+//     32 c + 8 g .. + 7, and holds the scores of query li with keys
+//     16 t + 4 g + r (register r), the layout the softmax of attn16_kernel
+//     works on;
+//   * O^T += V^T P^T is one MFMA per 16-wide head-dimension tile d over all
+//     32 keys of a block: K slot j of lane group g is key 16 (j / 4) + 4 g +
+//     j % 4, so a lane's B operand is its own 8 probabilities and its A
+//     operand V[that key][16 d + li];
+//   * K and V are loaded as fp32 (the operands of the launch are fp32) and
+//     converted when the MFMA operands are formed, so a load is not waited
+//     for before its block is reached.
+template <int DH, int NW, bool ADD>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) void attnbf_kernel(const AttnArgs a) {
+  constexpr int QB = 16;       // queries per workgroup
+  constexpr int QC = DH / 32;  // 32-wide chunks of the head dimension (K steps of a score MFMA)
+  constexpr int DT = DH / 16;  // 16-wide tiles of the head dimension in O^T
+  __shared__ __attribute__((aligned(16))) float o_part[NW][QB][DH + 4];
+  __shared__ float m_part[NW][QB], l_part[NW][QB];
+
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int li = lane & 15, g = lane >> 4;
+  const int b = blockIdx.x % a.batch;
+  const int qb = a.n_qblocks - 1 - (int)(blockIdx.x / a.batch);
+  const int q0 = qb * QB;
+  const int qi = q0 + li;
+  const bool q_ok = qi < a.tq;
+
+  constexpr float kLog2e = 1.4426950408889634f;
+  // applied to the fp32 scores (the products see Q as it is)
+  const float c_scale = a.scale_mode == KH_ATTN_SCALE_MUL   ? a.scale * kLog2e
+                        : a.scale_mode == KH_ATTN_SCALE_DIV ? kLog2e / a.scale
+                                                            : kLog2e;
+  auto pack8 = [](const float4 &x, const float4 &y) {
+    bf16x8 r;
+    r[0] = (__bf16)x.x, r[1] = (__bf16)x.y, r[2] = (__bf16)x.z, r[3] = (__bf16)x.w;
+    r[4] = (__bf16)y.x, r[5] = (__bf16)y.y, r[6] = (__bf16)y.z, r[7] = (__bf16)y.w;
+    return r;
+  };
+  bf16x8 qh[QC];
+  {
+    const float *qp = a.q + b * a.q_b + (int64_t)min(qi, a.tq - 1) * a.q_t + 8 * g;
+#pragma unroll
+    for (int c = 0; c < QC; ++c) {
+      float4 x = *reinterpret_cast<const float4 *>(qp + 32 * c), y = *reinterpret_cast<const float4 *>(qp + 32 * c + 4);
+      if (!q_ok) x = make_float4(0.f, 0.f, 0.f, 0.f), y = x;
+      qh[c] = pack8(x, y);
+    }
+  }
+
+  const bool causal = a.mask_mode == KH_ATTN_MASK_CAUSAL;
+  const int kend = causal ? min(a.tk, q0 + QB) : a.tk;
+  const int nkb = (kend + kKB - 1) / kKB;
+  const int lim = causal ? min(a.tk, qi + 1) : a.tk;
+
+  // buffer loads as in attn_kernel: key indices clamped to the last key
+  const uint32_t k_t4 = (uint32_t)a.k_t * 4, v_t4 = (uint32_t)a.v_t * 4;
+  const __amdgpu_buffer_rsrc_t k_res = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)(a.k + b * a.k_b), (short)0, (int)(((uint32_t)(a.tk - 1) * (uint32_t)a.k_t + DH) * 4), kBufferFlags);
+  const __amdgpu_buffer_rsrc_t v_res = __builtin_amdgcn_make_buffer_rsrc(
+      (void *)(a.v + b * a.v_b), (short)0, (int)(((uint32_t)(a.tk - 1) * (uint32_t)a.v_t + DH) * 4), kBufferFlags);
+  const uint32_t k_last = (uint32_t)(a.tk - 1) * k_t4 + g * 32;
+  const uint32_t v_last = (uint32_t)(a.tk - 1) * v_t4 + li * 4;
+  // K[16 t + li][32 c + 8 g .. + 7] of key block kb: kf[t][c][0..1]
+  auto load_k = [&](int kb, float4 (&kf)[2][QC][2]) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const uint32_t off = min((uint32_t)(kb * kKB + t * 16 + li) * k_t4 + g * 32, k_last);
+#pragma unroll
+      for (int c = 0; c < QC; ++c)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const auto x = __builtin_amdgcn_raw_buffer_load_b128(k_res, off + 128 * c + 16 * h, 0, 0);
+          kf[t][c][h] = make_float4(__uint_as_float(x[0]), __uint_as_float(x[1]), __uint_as_float(x[2]),
+                                    __uint_as_float(x[3]));
+        }
+    }
+  };
+  // V^T operand of tile d, K slot j = 4 t + r: V[16 t + 4 g + r][16 d + li]
+  auto load_v = [&](int kb, float (&vf)[8 * DT]) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const uint32_t off = min((uint32_t)(kb * kKB + t * 16 + 4 * g + r) * v_t4 + li * 4, v_last);
+#pragma unroll
+        for (int d = 0; d < DT; ++d)
+          vf[(t * 4 + r) * DT + d] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(v_res, off + 64 * d, 0, 0));
+      }
+  };
+  auto scores = [&](const float4 (&kf)[2][QC][2], f32x4 (&s)[2]) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      s[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < QC; ++c)
+        s[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pack8(kf[t][c][0], kf[t][c][1]), qh[c], s[t], 0, 0, 0);
+    }
+  };
+
+  f32x4 oacc[DT];
+#pragma unroll
+  for (int d = 0; d < DT; ++d) oacc[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.0f;
+
+  // online softmax of one score block as in attn16_kernel, the scale applied
+  // here; the probabilities' fp32 sum is the normaliser
+  auto softmax = [&](f32x4 (&s)[2], int kb, auto masked) {
+    const int room = lim - kb * kKB - 4 * g;   // key(t, r) < lim  <=>  16 t + r < room
+    float mx = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float u = s[t][r] * c_scale;
+        if (ADD) {
+          const int key = min(kb * kKB + t * 16 + 4 * g + r, a.tk - 1);
+          u = fmaf(a.mask[b * a.m_b + (int64_t)min(qi, a.tq - 1) * a.m_q + (int64_t)key * a.m_k], kLog2e, u);
+        }
+        if (decltype(masked)::value) u = 16 * t + r < room ? u : -INFINITY;
+        s[t][r] = u;
+        mx = fmaxf(mx, u);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+    float sum = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        s[t][r] = __builtin_amdgcn_exp2f(s[t][r] - m_use);
+        sum += s[t][r];
+      }
+    sum += __shfl_xor(sum, 16);
+    sum += __shfl_xor(sum, 32);
+    l_run = fmaf(l_run, alpha, sum);
+    m_run = m_new;
+#pragma unroll
+    for (int d = 0; d < DT; ++d) oacc[d] *= alpha;
+  };
+  auto pv = [&](const float (&vf)[8 * DT], const f32x4 (&p)[2]) {
+    const bf16x8 pb = pack8(make_float4(p[0][0], p[0][1], p[0][2], p[0][3]), make_float4(p[1][0], p[1][1], p[1][2], p[1][3]));
+#pragma unroll
+    for (int d = 0; d < DT; ++d) {
+      bf16x8 va;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) va[j] = (__bf16)vf[j * DT + d];
+      oacc[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb, oacc[d], 0, 0, 0);
+    }
+  };
+
+  // the software pipeline of attn16_kernel: K two blocks and V one block ahead
+  int kb = w;
+  if (kb < nkb) {
+    float4 kf[2][QC][2];
+    float vf[8 * DT];
+    f32x4 s_cur[2], s_nxt[2];
+    load_k(kb, kf);
+    load_v(kb, vf);
+    scores(kf, s_cur);
+    load_k(min(kb + NW, nkb - 1), kf);
+    for (; kb + NW < nkb; kb += NW) {
+      scores(kf, s_nxt);
+      softmax(s_cur, kb, std::false_type{});
+      load_k(min(kb + 2 * NW, nkb - 1), kf);
+      pv(vf, s_cur);
+      load_v(kb + NW, vf);
+      s_cur[0] = s_nxt[0], s_cur[1] = s_nxt[1];
+    }
+    softmax(s_cur, kb, std::true_type{});
+    pv(vf, s_cur);
+  }
+
+  // merge the NW key-split partials as in attn_kernel
+  if (g == 0) m_part[w][li] = m_run, l_part[w][li] = l_run;
+#pragma unroll
+  for (int d = 0; d < DT; ++d)
+    *reinterpret_cast<float4 *>(&o_part[w][li][d * 16 + 4 * g]) = make_float4(oacc[d][0], oacc[d][1], oacc[d][2], oacc[d][3]);
+  __syncthreads();
+  constexpr int kChunks = QB * DH / 4;
+  for (int c = threadIdx.x; c < kChunks; c += 64 * NW) {
+    const int qr = c / (DH / 4), d = (c % (DH / 4)) * 4;
+    if (q0 + qr >= a.tq) continue;
+    float mm = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < NW; ++u) mm = fmaxf(mm, m_part[u][qr]);
+    const float mu = mm == -INFINITY ? 0.0f : mm;
+    float l = 0.0f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int u = 0; u < NW; ++u) {
+      const float e = __builtin_amdgcn_exp2f(m_part[u][qr] - mu);
+      l += l_part[u][qr] * e;
+      acc.x += o_part[u][qr][d] * e, acc.y += o_part[u][qr][d + 1] * e;
+      acc.z += o_part[u][qr][d + 2] * e, acc.w += o_part[u][qr][d + 3] * e;
+    }
+    acc.x /= l, acc.y /= l, acc.z /= l, acc.w /= l;
+    const int64_t at = b * a.o_b + (int64_t)(q0 + qr) * a.o_t + d;
+    if (a.o16) store_bf16x4(a.o, at, acc.x, acc.y, acc.z, acc.w);
+    else *reinterpret_cast<float4 *>(a.o + at) = acc;
+  }
+}
+
 // Few-query attention (decode shapes: Tq <= kRowsMaxQ queries over at most
 // kRowsMaxK keys): one wave per (head, query), lane d holding head dimension
 // d (lanes DH.. idle for DH = 32). Each chunk of kRowKeys keys has its K and
@@ -588,6 +858,7 @@ class AttnOp final : public Op {
   int dh = 64, nw = 4;
   bool rows = false;  // few-query kernel
   bool q16 = false;   // 16 queries per workgroup (attn16_kernel)
+  bool bf = false;    // bf16 products (attn_kernel<..., BF> / attnbf_kernel)
   dim3 grid;
 
   hipError_t launch(float *const *ptrs, float *, hipStream_t stream) override {
@@ -606,6 +877,22 @@ class AttnOp final : public Op {
       else hipLaunchKernelGGL((attn_rows_kernel<32, false>), g, dim3(256), 0, stream, a);
       return hipGetLastError();
     }
+#define KH_ATTNBF_LAUNCH(D, W)                                                                       \
+  if (bf && q16 && dh == D && nw == W) {                                                             \
+    if (a.mask_mode == KH_ATTN_MASK_ADD)                                                             \
+      hipLaunchKernelGGL((attnbf_kernel<D, W, true>), grid, dim3(64 * W), 0, stream, a);            \
+    else                                                                                             \
+      hipLaunchKernelGGL((attnbf_kernel<D, W, false>), grid, dim3(64 * W), 0, stream, a);           \
+    return hipGetLastError();                                                                        \
+  }
+    KH_ATTNBF_LAUNCH(64, 8)
+    KH_ATTNBF_LAUNCH(64, 4)
+    KH_ATTNBF_LAUNCH(64, 2)
+    KH_ATTNBF_LAUNCH(64, 1)
+    KH_ATTNBF_LAUNCH(32, 4)
+    KH_ATTNBF_LAUNCH(32, 2)
+    KH_ATTNBF_LAUNCH(32, 1)
+#undef KH_ATTNBF_LAUNCH
 #define KH_ATTN16_LAUNCH(D, W)                                                                       \
   if (q16 && dh == D && nw == W) {                                                                   \
     if (a.mask_mode == KH_ATTN_MASK_ADD)                                                             \
@@ -624,10 +911,11 @@ class AttnOp final : public Op {
 #undef KH_ATTN16_LAUNCH
 #define KH_ATTN_LAUNCH(D, W)                                                                         \
   if (dh == D && nw == W) {                                                                          \
-    if (a.mask_mode == KH_ATTN_MASK_ADD)                                                             \
-      hipLaunchKernelGGL((attn_kernel<D, W, true>), grid, dim3(64 * W), 0, stream, a);              \
-    else                                                                                             \
-      hipLaunchKernelGGL((attn_kernel<D, W, false>), grid, dim3(64 * W), 0, stream, a);             \
+    const bool add = a.mask_mode == KH_ATTN_MASK_ADD;                                                \
+    if (bf && add) hipLaunchKernelGGL((attn_kernel<D, W, true, true>), grid, dim3(64 * W), 0, stream, a); \
+    else if (bf) hipLaunchKernelGGL((attn_kernel<D, W, false, true>), grid, dim3(64 * W), 0, stream, a); \
+    else if (add) hipLaunchKernelGGL((attn_kernel<D, W, true>), grid, dim3(64 * W), 0, stream, a);  \
+    else hipLaunchKernelGGL((attn_kernel<D, W, false>), grid, dim3(64 * W), 0, stream, a);         \
     return hipGetLastError();                                                                        \
   }
     KH_ATTN_LAUNCH(64, 8)
@@ -715,6 +1003,14 @@ std::unique_ptr<Op> make_attn(const kh_launch &L, std::string &err, bool &unsupp
   // 16 when 32-query blocks would give under 1.5 workgroups per CU (measured
   // on the GPT-2 block, 12 heads causal: T = 128 6.2 -> 4.7 us, 512 13.5 ->
   // 11.4 us; from T = 1024 on the 32-query kernel is faster)
+  // products precision (cfg[5]): 0 fp32, 1 bf16 inputs with fp32 accumulation
+  // (attn_kernel<..., BF> or, for 16 queries per workgroup, attnbf_kernel)
+  const int prec = L.cfg[5];
+  if (prec != 0 && prec != 1) {
+    err = "attention: products precision must be 0 (fp32) or 1 (bf16)";
+    return nullptr;
+  }
+  op->bf = prec == 1;
   op->q16 = qpw == 16 || (qpw == 0 && 2 * batch * ((tq + kQB - 1) / kQB) < 3ll * current_device().cus);
   a.n_qblocks = (int)((tq + (op->q16 ? 16 : kQB) - 1) / (op->q16 ? 16 : kQB));
   op->dh = (int)dh;
@@ -741,7 +1037,7 @@ std::unique_ptr<Op> make_attn(const kh_launch &L, std::string &err, bool &unsupp
   }
   op->nw = nw;
   // decode shapes (a few queries, a few keys): one wave per query row
-  op->rows = tq <= kRowsMaxQ && tk <= kRowsMaxK && L.cfg[2] <= 0 && batch * tq < (1ll << 31);
+  op->rows = !op->bf && tq <= kRowsMaxQ && tk <= kRowsMaxK && L.cfg[2] <= 0 && batch * tq < (1ll << 31);
   const int64_t n_groups = batch * (int64_t)a.n_qblocks;
   if (n_groups >= (1ll << 31)) {
     unsupported = true;
@@ -788,8 +1084,8 @@ hipError_t probe_attn_timeline(const float *q, const float *k, const float *v, f
   a.batch = batch, a.tq = tq, a.tk = tk, a.n_qblocks = (tq + kQB - 1) / kQB;
   a.mask_mode = KH_ATTN_MASK_CAUSAL, a.scale_mode = KH_ATTN_SCALE_MUL, a.scale = scale;
   const dim3 grid((unsigned)(batch * a.n_qblocks));
-  if (nw == 4) hipLaunchKernelGGL((attn_kernel<64, 4, false, true>), grid, dim3(256), 0, stream, a);
-  else hipLaunchKernelGGL((attn_kernel<64, 8, false, true>), grid, dim3(512), 0, stream, a);
+  if (nw == 4) hipLaunchKernelGGL((attn_kernel<64, 4, false, false, true>), grid, dim3(256), 0, stream, a);
+  else hipLaunchKernelGGL((attn_kernel<64, 8, false, false, true>), grid, dim3(512), 0, stream, a);
   return hipGetLastError();
 }
 

@@ -47,6 +47,8 @@ LN_PROLOGUE_MAX_ROWS = 256
 # 0 lets the library pick (16 for grids that 32-query blocks leave short of
 # work); 16 or 32 forces one
 ATTN_QUERIES = 0
+# the few-query attention kernel's largest query count (kRowsMaxQ in kh_attn.hip)
+ATTN_ROWS_MAX_Q = 4
 
 _UNARY_OP = {"neg": "neg", "exp": "exp", "tanh": "tanh", "sigmoid": "sigmoid", "relu": "relu",
              "rsqrt": "rsqrt", "sqrt": "sqrt", "erf": "erf", "copy": "mov"}
@@ -1280,6 +1282,12 @@ class _Lowerer:
                 d.n_refs = 5
         d.cfg[0], d.cfg[1] = mode, m.scale_mode
         d.cfg[3] = ATTN_QUERIES
+        # bf16 plans run the two products of attention on bf16 inputs too
+        # (fp32 accumulation and softmax); decode shapes keep the few-query
+        # kernel's fp32 products
+        bf_products = self.precision == "bf16" and tq > ATTN_ROWS_MAX_Q
+        if bf_products:
+            d.cfg[5] = 1
         d.fparams[0] = m.scale
         causal = mode == kl.ATTN_MASK_CAUSAL
         pairs = sum(min(tk, i + 1) for i in range(tq)) if causal else tq * tk
@@ -1288,6 +1296,8 @@ class _Lowerer:
         what = {kl.ATTN_MASK_NONE: "no mask", kl.ATTN_MASK_CAUSAL: "causal", kl.ATTN_MASK_ADD: "additive mask"}[mode]
         scale = {kl.ATTN_SCALE_NONE: "", kl.ATTN_SCALE_MUL: f", scores * {m.scale:g}",
                  kl.ATTN_SCALE_DIV: f", scores / {m.scale:g}"}[m.scale_mode]
+        if bf_products:
+            scale += ", products:bf16"
         if d.cfg[7]:
             scale += ", out:bf16"
             nbytes -= 2 * batch * dh * tq

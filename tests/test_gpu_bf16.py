@@ -188,7 +188,9 @@ def test_activation_product_stays_fp32():
 
 def _bf16_reference_block(model):
     """float64 copy of the block whose Linear layers see bf16-rounded inputs
-    and weights - the computation the bf16 variant performs."""
+    and weights, and whose attention products see bf16-rounded q, k (scores)
+    and softmax weights, v (weighted sum) - the computation the bf16 variant
+    performs."""
     ref = copy.deepcopy(model).double()
     for mod in ref.modules():
         if isinstance(mod, torch.nn.Linear):
@@ -196,6 +198,18 @@ def _bf16_reference_block(model):
                 mod.weight.copy_(torch.from_numpy(r16(mod.weight.float().numpy())))
             mod.register_forward_pre_hook(
                 lambda m, args: (torch.from_numpy(r16(args[0].float().numpy())),))
+    rt = lambda t: torch.from_numpy(r16(t.float().numpy()))
+
+    def attn(x):
+        T, C = x.shape
+        q, k, v = ref.c_attn(x).split(C, dim=1)
+        hd = C // ref.nh
+        q, k, v = (t.reshape(T, ref.nh, hd).transpose(0, 1) for t in (q, k, v))
+        att = (rt(q) @ rt(k).transpose(-2, -1)) * (1.0 / hd ** 0.5) + ref.mask[:T, :T]
+        y = (rt(F.softmax(att, dim=-1)) @ rt(v)).transpose(0, 1).reshape(T, C)
+        return ref.c_proj(y)
+
+    ref.attn = attn
     return ref
 
 
@@ -264,3 +278,103 @@ def test_bf16_storage_gives_the_same_bits_on_the_block(T, monkeypatch):
     with torch.no_grad():
         eager = model(x).cuda()
     assert float((got - eager).abs().max()) <= STATED * float(eager.abs().max())
+
+
+# -- attention with bf16 products ------------------------------------------------------------
+
+@pytest.fixture(params=[0, 16, 32], ids=["q-auto", "q16", "q32"])
+def queries(request, monkeypatch):
+    """Queries per workgroup of the blocked kernel: the library's choice, or
+    forced to 16 (attnbf_kernel) or 32 (attn_kernel with bf16 products)."""
+    from kiln.hip import lowering
+
+    monkeypatch.setattr(lowering, "ATTN_QUERIES", request.param)
+    return request.param
+
+
+class _Attn(torch.nn.Module):
+    """softmax(q k^T * scale + mask) v over [B, T, D] inputs."""
+
+    def __init__(self, mask=None, scale=0.125):
+        super().__init__()
+        self.scale = scale
+        if mask is not None:
+            self.register_buffer("mask", mask)
+        else:
+            self.mask = None
+
+    def forward(self, q, k, v):
+        s = (q @ k.transpose(-2, -1)) * self.scale
+        if self.mask is not None:
+            s = s + self.mask
+        return F.softmax(s, dim=-1) @ v
+
+
+def _bf16_attention_reference(q, k, v, scale, mask):
+    """The unfused computation with bf16 products: q, k rounded for the
+    scores, the normalised softmax weights and v rounded for the weighted sum,
+    everything else float64."""
+    s = r16(q.numpy()) @ r16(k.numpy()).transpose(0, 2, 1) * scale
+    if mask is not None:
+        s = s + mask.numpy().astype(np.float64)
+    with np.errstate(invalid="ignore"):
+        e = np.exp(s - s.max(-1, keepdims=True))
+        p = e / e.sum(-1, keepdims=True)
+    return r16(p.astype(np.float32)) @ r16(v.numpy())
+
+
+def _check_bf16_attention(model, q, k, v, mask):
+    c = kiln.compile(model, (q, k, v), device="cuda", matmul_precision="bf16")
+    summaries = [l.summary for l in c._exe.program.launches]
+    assert any("heads" in s and "products:bf16" in s for s in summaries), summaries
+    got = c(q.cuda(), k.cuda(), v.cuda()).cpu().numpy().astype(np.float64)
+    ref = _bf16_attention_reference(q, k, v, model.scale, mask)
+    # the kernel rounds the running-max-relative probabilities, the reference
+    # the normalised ones: each weight within 2^-9 of its value in both, so
+    # the outputs agree to 2^-8 of the largest |v|
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    tol = 2.0 ** -8 * float(np.abs(v.numpy()).max()) + 1e-5
+    err = float(np.abs(got[~nan] - ref[~nan]).max()) if (~nan).any() else 0.0
+    assert err <= tol, f"max error {err:.2e} > {tol:.2e}"
+    with torch.no_grad():
+        eager = model(q, k, v).numpy().astype(np.float64)
+    np.testing.assert_allclose(got[~nan], eager[~nan], rtol=STATED, atol=STATED * np.abs(eager[~nan]).max())
+    return c
+
+
+@pytest.mark.parametrize("T", [5, 77, 200, 512])
+@pytest.mark.parametrize("d", [32, 64])
+def test_bf16_attention_causal(T, d, queries):
+    g = torch.Generator().manual_seed(T + d)
+    q, k, v = (torch.randn(3, T, d, generator=g) for _ in range(3))
+    mask = torch.full((T, T), float("-inf")).triu(1)
+    _check_bf16_attention(_Attn(mask, 1 / d ** 0.5), q, k, v, mask)
+
+
+@pytest.mark.parametrize("tq, tk", [(50, 90), (33, 7), (64, 64), (130, 300)])
+def test_bf16_attention_cross(tq, tk, queries):
+    g = torch.Generator().manual_seed(tq * 7 + tk)
+    q, k, v = torch.randn(2, tq, 64, generator=g), torch.randn(2, tk, 64, generator=g), torch.randn(2, tk, 64, generator=g)
+    _check_bf16_attention(_Attn(None, 0.125), q, k, v, None)
+
+
+def test_bf16_attention_additive_mask_and_fully_masked_row(queries):
+    tq, tk = 40, 70
+    g = torch.Generator().manual_seed(11)
+    q, k, v = torch.randn(2, tq, 64, generator=g), torch.randn(2, tk, 64, generator=g), torch.randn(2, tk, 64, generator=g)
+    mask = torch.randn(tq, tk, generator=g)
+    mask[torch.rand(tq, tk, generator=g) < 0.3] = float("-inf")
+    mask[:, 0] = 0.0
+    mask[7, :] = float("-inf")          # a fully masked row: NaN, as in eager
+    _check_bf16_attention(_Attn(mask, 0.125), q, k, v, mask)
+
+
+def test_bf16_attention_keeps_fp32_products_on_decode_shapes():
+    g = torch.Generator().manual_seed(5)
+    q, k, v = torch.randn(4, 1, 64, generator=g), torch.randn(4, 40, 64, generator=g), torch.randn(4, 40, 64, generator=g)
+    c = kiln.compile(_Attn(None, 0.125), (q, k, v), device="cuda", matmul_precision="bf16")
+    assert not any("products:bf16" in l.summary for l in c._exe.program.launches)
+    with torch.no_grad():
+        eager = _Attn(None, 0.125)(q, k, v)
+    torch.testing.assert_close(c(q.cuda(), k.cuda(), v.cuda()).cpu(), eager, rtol=1e-4, atol=1e-5)

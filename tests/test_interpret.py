@@ -376,3 +376,33 @@ def test_bf16_storage_needs_a_single_bf16_reader():
     c = kiln.compile(fn, (x,), device="cuda", matmul_precision="bf16",
                      gpu_matmul_config=lambda *_: {"tile": 99, "splitk": 1})
     assert not any("bf16" in l.summary.replace("tile 99 splitk 1 bf16", "") for l in c._exe.program.launches)
+
+
+def test_bf16_attention_products_on_the_host():
+    # a bf16 plan's attention (cfg[5] = 1) on the host: q, k rounded to bf16
+    # for the scores (float64 sum, then the fp32 score and scale), the
+    # normalised weights and v rounded to bf16 for the weighted sum
+    class Attn(torch.nn.Module):
+        def __init__(self, mask):
+            super().__init__()
+            self.register_buffer("mask", mask)
+
+        def forward(self, q, k, v):
+            return F.softmax((q @ k.transpose(-2, -1)) * 0.125 + self.mask, dim=-1) @ v
+
+    T, d = 40, 64
+    g = torch.Generator().manual_seed(2)
+    q, k, v = (torch.randn(2, T, d, generator=g) for _ in range(3))
+    mask = torch.full((T, T), float("-inf")).triu(1)
+    c = kiln.compile(Attn(mask), (q, k, v), device="cuda", matmul_precision="bf16")
+    assert "products:bf16" in open(c.report.lowering["source"]).read()
+    r = lambda a: oracle.bf16_round(np.asarray(a, np.float32)).astype(np.float64)
+    s = (r(q.numpy()) @ r(k.numpy()).transpose(0, 2, 1)).astype(np.float32) * np.float32(0.125)
+    s = s.astype(np.float64) + mask.numpy()
+    e = np.exp(s - s.max(-1, keepdims=True))
+    w = r((e / e.sum(-1, keepdims=True)).astype(np.float32))
+    ref = w @ r(v.numpy())
+    np.testing.assert_allclose(c(q, k, v).numpy().astype(np.float64), ref, rtol=1e-6, atol=1e-7)
+    # decode shapes keep fp32 products
+    c1 = kiln.compile(Attn(mask[:1]), (q[:, :1], k, v), device="cuda", matmul_precision="bf16")
+    assert "products:bf16" not in open(c1.report.lowering["source"]).read()
