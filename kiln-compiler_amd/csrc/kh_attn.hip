@@ -1000,9 +1000,6 @@ std::unique_ptr<Op> make_attn(const kh_launch &L, std::string &err, bool &unsupp
     err = "attention: queries per workgroup must be 0, 16 or 32";
     return nullptr;
   }
-  // 16 when 32-query blocks would give under 1.5 workgroups per CU (measured
-  // on the GPT-2 block, 12 heads causal: T = 128 6.2 -> 4.7 us, 512 13.5 ->
-  // 11.4 us; from T = 1024 on the 32-query kernel is faster)
   // products precision (cfg[5]): 0 fp32, 1 bf16 inputs with fp32 accumulation
   // (attn_kernel<..., BF> or, for 16 queries per workgroup, attnbf_kernel)
   const int prec = L.cfg[5];
@@ -1011,7 +1008,14 @@ std::unique_ptr<Op> make_attn(const kh_launch &L, std::string &err, bool &unsupp
     return nullptr;
   }
   op->bf = prec == 1;
-  op->q16 = qpw == 16 || (qpw == 0 && 2 * batch * ((tq + kQB - 1) / kQB) < 3ll * current_device().cus);
+  // 16 when 32-query blocks would give under 1.5 workgroups per CU (measured
+  // on the GPT-2 block, 12 heads causal: T = 128 6.2 -> 4.7 us, 512 13.5 ->
+  // 11.4 us; from T = 1024 on the 32-query kernel is faster); with bf16
+  // products under half a workgroup per CU (T = 128 5.0 -> 4.1 us, 256 6.4 ->
+  // 5.9; T = 384 7.4 against 7.7-8.1, 512 8.5 against 9.5-10.6)
+  const int64_t groups32 = batch * ((tq + kQB - 1) / kQB);
+  op->q16 = qpw == 16 || (qpw == 0 && (op->bf ? 2 * groups32 < current_device().cus
+                                                : 2 * groups32 < 3ll * current_device().cus));
   a.n_qblocks = (int)((tq + (op->q16 ? 16 : kQB) - 1) / (op->q16 ? 16 : kQB));
   op->dh = (int)dh;
   // key-split waves per workgroup: enough workgroups x waves to cover the GPU
@@ -1029,6 +1033,11 @@ std::unique_ptr<Op> make_attn(const kh_launch &L, std::string &err, bool &unsupp
     // 16-query blocks: four waves, eight from 8 visited key blocks (T = 512:
     // 12.3 -> 11.4 us)
     if (op->q16) nw = visited >= 8 && dh == 64 ? 8 : 4;
+    // bf16 products, 32-query blocks: two waves up to 16 visited key blocks,
+    // four beyond (GPT-2 block: T = 512 8.5 against 8.9 / 10.7 us with 4 / 8,
+    // T = 1024 17.1 against 18.5 / 17.2, T = 1536 26.9 against 29.2 / 29.7 with
+    // 2 / 8, T = 2048 37.8 against 43.4 / 46.1)
+    else if (op->bf && groups < 16ll * current_device().cus) nw = visited <= 16 ? 2 : 4;
     if (kblocks < nw) nw = kblocks >= 2 ? 2 : 1;
   }
   if (nw != 1 && nw != 2 && nw != 4 && !(nw == 8 && dh == 64)) {
