@@ -106,9 +106,12 @@ __device__ __forceinline__ float2 halves(float x) {
 //     operand is its own probabilities and its A operand the V values the
 //     fp32 path loads for those registers;
 //   * K and V are loaded as fp32 and rounded when an MFMA operand is formed.
+// IN16 (with BF): q, k and v are stored as bf16 by their producer, so the
+// operands are loaded as bf16 (K as one 16-byte load per chunk, V as 16-bit
+// loads paired into MFMA operand words) and rounded by no one here.
 // REC (the timeline probe only): each wave also records its start, loop-end
 // and end times, the shader clock and the CU it ran on.
-template <int DH, int NW, bool ADD, bool BF = false, bool REC = false>
+template <int DH, int NW, bool ADD, bool BF = false, bool REC = false, bool IN16 = false>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) void attn_kernel(const AttnArgs a) {
   uint64_t rec_t0 = 0, rec_c0 = 0;
   if constexpr (REC) rec_t0 = __builtin_amdgcn_s_memrealtime(), rec_c0 = __builtin_amdgcn_s_memtime();
@@ -136,7 +139,15 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
                                                             : kLog2e;
   float qf[BF ? 1 : QS];
   bf16x8 qh[BF ? DH / 16 : 1];   // (bf16 products: Q as it is, the scale applied to the scores)
-  if constexpr (BF) {
+  static_assert(BF || !IN16, "bf16 storage of q, k, v comes with bf16 products");
+  if constexpr (IN16) {
+    const uint16_t *qp = reinterpret_cast<const uint16_t *>(a.q) + b * a.q_b + (int64_t)min(qi, a.tq - 1) * a.q_t + 8 * half;
+#pragma unroll
+    for (int c = 0; c < DH / 16; ++c) {
+      qh[c] = *reinterpret_cast<const bf16x8 *>(qp + 16 * c);
+      if (!q_ok) qh[c] = bf16x8{};
+    }
+  } else if constexpr (BF) {
     const float *qp = a.q + b * a.q_b + (int64_t)min(qi, a.tq - 1) * a.q_t + 8 * half;
 #pragma unroll
     for (int c = 0; c < DH / 16; ++c) {
@@ -166,21 +177,26 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
   // spans < 2^30 elements) and the column step as an immediate. Key indices
   // are clamped to the last key, so every load of a partial block stays
   // inside the operand (and the resource's extent bounds it as well).
-  const uint32_t k_t4 = (uint32_t)a.k_t * 4, v_t4 = (uint32_t)a.v_t * 4;
+  constexpr uint32_t ES = IN16 ? 2 : 4;   // bytes per q, k, v element
+  const uint32_t k_t4 = (uint32_t)a.k_t * ES, v_t4 = (uint32_t)a.v_t * ES;
   const __amdgpu_buffer_rsrc_t k_res = __builtin_amdgcn_make_buffer_rsrc(
-      (void *)(a.k + b * a.k_b), (short)0, (int)(((uint32_t)(a.tk - 1) * (uint32_t)a.k_t + DH) * 4), kBufferFlags);
+      (void *)(reinterpret_cast<const char *>(a.k) + b * a.k_b * ES), (short)0,
+      (int)(((uint32_t)(a.tk - 1) * (uint32_t)a.k_t + DH) * ES), kBufferFlags);
   const __amdgpu_buffer_rsrc_t v_res = __builtin_amdgcn_make_buffer_rsrc(
-      (void *)(a.v + b * a.v_b), (short)0, (int)(((uint32_t)(a.tk - 1) * (uint32_t)a.v_t + DH) * 4), kBufferFlags);
+      (void *)(reinterpret_cast<const char *>(a.v) + b * a.v_b * ES), (short)0,
+      (int)(((uint32_t)(a.tk - 1) * (uint32_t)a.v_t + DH) * ES), kBufferFlags);
   // a lane's K elements: fp32 products half * QS .. + QS - 1; bf16 products
-  // 16 c + 8 half .. + 7 of every chunk c (kf[2 c], kf[2 c + 1])
-  const uint32_t k_lane = BF ? half * 32 : half * QS * 4;
+  // 16 c + 8 half .. + 7 of every chunk c (kf[2 c], kf[2 c + 1]; bf16
+  // storage: kf[c], eight bf16)
+  const uint32_t k_lane = BF ? half * 8 * ES : half * QS * 4;
   const uint32_t k_last = (uint32_t)(a.tk - 1) * k_t4 + k_lane;
-  const uint32_t v_last = (uint32_t)(a.tk - 1) * v_t4 + col * 4;
+  const uint32_t v_last = (uint32_t)(a.tk - 1) * v_t4 + col * ES;
   auto load_k = [&](int kb, float4 (&kf)[QS / 4]) {
     const uint32_t off = min((uint32_t)(kb * kKB + col) * k_t4 + k_lane, k_last);
 #pragma unroll
-    for (int j = 0; j < QS / 4; ++j) {
-      const auto x = __builtin_amdgcn_raw_buffer_load_b128(k_res, off + (BF ? 64 * (j / 2) + 16 * (j % 2) : 16 * j), 0, 0);
+    for (int j = 0; j < (IN16 ? DH / 16 : QS / 4); ++j) {
+      const auto x = __builtin_amdgcn_raw_buffer_load_b128(
+          k_res, off + (IN16 ? 32 * j : BF ? 64 * (j / 2) + 16 * (j % 2) : 16 * j), 0, 0);
       kf[j] = make_float4(__uint_as_float(x[0]), __uint_as_float(x[1]), __uint_as_float(x[2]), __uint_as_float(x[3]));
     }
   };
@@ -188,13 +204,17 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
   // key0 + (r/4)*8 + half*4 + r%4, the key held in accumulator register r of
   // this lane half.
   auto load_v = [&](int kb, float (&vf)[16 * NT]) {
-    const uint32_t base = (uint32_t)(kb * kKB + half * 4) * v_t4 + col * 4;
+    const uint32_t base = (uint32_t)(kb * kKB + half * 4) * v_t4 + col * ES;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const uint32_t off = min(base + (uint32_t)((r >> 2) * 8 + (r & 3)) * v_t4, v_last);
 #pragma unroll
-      for (int t = 0; t < NT; ++t)
-        vf[r * NT + t] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(v_res, off + 128 * t, 0, 0));
+      for (int t = 0; t < NT; ++t) {
+        if constexpr (IN16)   // (the bf16 bits in the low half)
+          vf[r * NT + t] = __uint_as_float((uint32_t)__builtin_amdgcn_raw_buffer_load_b16(v_res, off + 64 * t, 0, 0));
+        else
+          vf[r * NT + t] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(v_res, off + 128 * t, 0, 0));
+      }
     }
   };
   // S^T block: register r of lane (col, half) = score of query col, key(r)
@@ -204,8 +224,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     for (int r = 0; r < 16; ++r) s[r] = 0.0f;
     if constexpr (BF) {
 #pragma unroll
-      for (int c = 0; c < DH / 16; ++c)
-        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(pack_bf16x8(kc[2 * c], kc[2 * c + 1]), qh[c], s, 0, 0, 0);
+      for (int c = 0; c < DH / 16; ++c) {
+        const bf16x8 k8 = IN16 ? __builtin_bit_cast(bf16x8, kc[c]) : pack_bf16x8(kc[2 * c], kc[2 * c + 1]);
+        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k8, qh[c], s, 0, 0, 0);
+      }
       return s;
     }
 #pragma unroll
@@ -272,8 +294,18 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
           const float *v8 = vf + 8 * c * NT + t;
-          const bf16x8 va = pack_bf16x8(make_float4(v8[0], v8[NT], v8[2 * NT], v8[3 * NT]),
-                                        make_float4(v8[4 * NT], v8[5 * NT], v8[6 * NT], v8[7 * NT]));
+          bf16x8 va;
+          if constexpr (IN16) {
+            uint4 w;
+            w.x = __float_as_uint(v8[0]) | (__float_as_uint(v8[NT]) << 16);
+            w.y = __float_as_uint(v8[2 * NT]) | (__float_as_uint(v8[3 * NT]) << 16);
+            w.z = __float_as_uint(v8[4 * NT]) | (__float_as_uint(v8[5 * NT]) << 16);
+            w.w = __float_as_uint(v8[6 * NT]) | (__float_as_uint(v8[7 * NT]) << 16);
+            va = __builtin_bit_cast(bf16x8, w);
+          } else {
+            va = pack_bf16x8(make_float4(v8[0], v8[NT], v8[2 * NT], v8[3 * NT]),
+                             make_float4(v8[4 * NT], v8[5 * NT], v8[6 * NT], v8[7 * NT]));
+          }
           oacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb, oacc[t], 0, 0, 0);
         }
       }
@@ -859,6 +891,7 @@ class AttnOp final : public Op {
   bool rows = false;  // few-query kernel
   bool q16 = false;   // 16 queries per workgroup (attn16_kernel)
   bool bf = false;    // bf16 products (attn_kernel<..., BF> / attnbf_kernel)
+  bool in16 = false;  // q, k, v stored as bf16 (attn_kernel<..., BF, ..., IN16>)
   dim3 grid;
 
   hipError_t launch(float *const *ptrs, float *, hipStream_t stream) override {
@@ -912,7 +945,9 @@ class AttnOp final : public Op {
 #define KH_ATTN_LAUNCH(D, W)                                                                         \
   if (dh == D && nw == W) {                                                                          \
     const bool add = a.mask_mode == KH_ATTN_MASK_ADD;                                                \
-    if (bf && add) hipLaunchKernelGGL((attn_kernel<D, W, true, true>), grid, dim3(64 * W), 0, stream, a); \
+    if (in16 && add) hipLaunchKernelGGL((attn_kernel<D, W, true, true, false, true>), grid, dim3(64 * W), 0, stream, a); \
+    else if (in16) hipLaunchKernelGGL((attn_kernel<D, W, false, true, false, true>), grid, dim3(64 * W), 0, stream, a); \
+    else if (bf && add) hipLaunchKernelGGL((attn_kernel<D, W, true, true>), grid, dim3(64 * W), 0, stream, a); \
     else if (bf) hipLaunchKernelGGL((attn_kernel<D, W, false, true>), grid, dim3(64 * W), 0, stream, a); \
     else if (add) hipLaunchKernelGGL((attn_kernel<D, W, true>), grid, dim3(64 * W), 0, stream, a);  \
     else hipLaunchKernelGGL((attn_kernel<D, W, false>), grid, dim3(64 * W), 0, stream, a);         \
@@ -962,9 +997,12 @@ std::unique_ptr<Op> make_attn(const kh_launch &L, std::string &err, bool &unsupp
     err = "attention: head dimension must be 32 or 64";
     return nullptr;
   }
+  const uint32_t m16 = bf16_refs(L);
   for (int j = 0; j < 4; ++j) {
     const kh_ref &r = L.refs[j];
-    if (r.strides[2] != 1 || !aligned4(r.offset) || !aligned4(r.strides[0]) || !aligned4(r.strides[1])) {
+    // 16-byte aligned rows: 4 fp32 or (bf16 storage of q, k, v) 8 bf16 elements
+    const int64_t al = j < 3 && (m16 >> j & 1) ? 8 : 4;
+    if (r.strides[2] != 1 || r.offset % al || r.strides[0] % al || r.strides[1] % al) {
       unsupported = true;
       err = "attention: q, k, v and out need unit head-dim stride and 16-byte aligned rows";
       return nullptr;
@@ -1014,8 +1052,15 @@ std::unique_ptr<Op> make_attn(const kh_launch &L, std::string &err, bool &unsupp
   // products under half a workgroup per CU (T = 128 5.0 -> 4.1 us, 256 6.4 ->
   // 5.9; T = 384 7.4 against 7.7-8.1, 512 8.5 against 9.5-10.6)
   const int64_t groups32 = batch * ((tq + kQB - 1) / kQB);
-  op->q16 = qpw == 16 || (qpw == 0 && (op->bf ? 2 * groups32 < current_device().cus
-                                                : 2 * groups32 < 3ll * current_device().cus));
+  // q, k, v stored as bf16 (all three, with bf16 products): the 32-query kernel
+  op->in16 = (m16 & 7u) != 0;
+  if ((m16 & ~0xFu) || (op->in16 && ((m16 & 7u) != 7u || !op->bf || qpw == 16))) {
+    unsupported = true;
+    err = "attention: bf16 storage of q, k, v needs all three, bf16 products and 32 queries per workgroup";
+    return nullptr;
+  }
+  op->q16 = !op->in16 && (qpw == 16 || (qpw == 0 && (op->bf ? 2 * groups32 < current_device().cus
+                                                              : 2 * groups32 < 3ll * current_device().cus)));
   a.n_qblocks = (int)((tq + (op->q16 ? 16 : kQB) - 1) / (op->q16 ? 16 : kQB));
   op->dh = (int)dh;
   // key-split waves per workgroup: enough workgroups x waves to cover the GPU
@@ -1046,7 +1091,7 @@ std::unique_ptr<Op> make_attn(const kh_launch &L, std::string &err, bool &unsupp
   }
   op->nw = nw;
   // decode shapes (a few queries, a few keys): one wave per query row
-  op->rows = !op->bf && tq <= kRowsMaxQ && tk <= kRowsMaxK && L.cfg[2] <= 0 && batch * tq < (1ll << 31);
+  op->rows = !op->bf && !op->in16 && tq <= kRowsMaxQ && tk <= kRowsMaxK && L.cfg[2] <= 0 && batch * tq < (1ll << 31);
   const int64_t n_groups = batch * (int64_t)a.n_qblocks;
   if (n_groups >= (1ll << 31)) {
     unsupported = true;
@@ -1054,15 +1099,14 @@ std::unique_ptr<Op> make_attn(const kh_launch &L, std::string &err, bool &unsupp
     return nullptr;
   }
   op->grid = dim3((unsigned)std::max<int64_t>(1, n_groups));
-  // a bf16 output (the head-merged result read only by a bf16 matmul): the
-  // output ref only, and not on the few-query kernel
-  const uint32_t m16 = bf16_refs(L);
-  if (m16 && (m16 != 1u << 3 || op->rows)) {
+  // a bf16 output (the head-merged result read only by a bf16 matmul): not
+  // on the few-query kernel
+  if ((m16 >> 3 & 1) && op->rows) {
     unsupported = true;
     err = "attention: bf16 storage only for the output of the blocked kernel";
     return nullptr;
   }
-  a.o16 = m16 ? 1 : 0;
+  a.o16 = m16 >> 3 & 1;
   return op;
 }
 

@@ -240,10 +240,25 @@ void attend(int64_t tk, int64_t dh, int scale_mode, float scale, int mask_mode, 
   }
 }
 
-void host_attn(const kh_launch &L, float *const *p) {
+void host_attn(const kh_launch &L, float *const *p0) {
   const int64_t batch = L.gemm[0], tq = L.gemm[1], tk = L.gemm[2], dh = L.gemm[3];
   const kh_ref &Q = L.refs[0], &K = L.refs[1], &V = L.refs[2], &O = L.refs[3];
   std::vector<double> out((size_t)dh);
+  // q, k, v stored as bf16: widened copies of the elements the refs reach
+  std::vector<float> wide[3];
+  float *p[KH_MAX_REFS];
+  for (int j = 0; j < KH_MAX_REFS; ++j) p[j] = p0[j];
+  const uint32_t m16 = bf16_refs(L);
+  for (int j = 0; j < 3; ++j) {
+    if (!(m16 >> j & 1)) continue;
+    const kh_ref &r = L.refs[j];
+    const int64_t rows = j == 0 ? tq : tk;
+    const int64_t span = (batch - 1) * r.strides[0] + (rows - 1) * r.strides[1] + (dh - 1) * r.strides[2] + 1;
+    wide[j].resize((size_t)std::max<int64_t>(span, 0));
+    const uint16_t *src = reinterpret_cast<const uint16_t *>(p0[j]);
+    for (int64_t i = 0; i < span; ++i) wide[j][(size_t)i] = bf16_value(src[i]);
+    p[j] = wide[j].data();
+  }
   for (int64_t b = 0; b < batch; ++b)
     for (int64_t i = 0; i < tq; ++i) {
       const float *mask = L.cfg[0] == KH_ATTN_MASK_ADD ? p[4] + b * L.refs[4].strides[0] + i * L.refs[4].strides[1]

@@ -257,6 +257,11 @@ class _Lowerer:
         if self.precision != "bf16":
             return out
         for k in self.g.kernels:
+            if k.kind == "attention":
+                buf = self.qkv16_buffer(k)
+                if buf is not None:
+                    out.add(buf)
+                continue
             if k.kind != "matmul" or self.is_gemv(k) or k in self.prologue:
                 continue
             cfg, prec = self.matmul_choice(k)
@@ -303,6 +308,34 @@ class _Lowerer:
             return None
         producer = self.g.kernel_of(buf.node)
         return buf if producer is not None and self._rounds_to_bf16(producer, buf) else None
+
+    def qkv16_buffer(self, k):
+        """The arena buffer holding attention kernel k's q, k and v if it can
+        be stored as bf16: the attention runs bf16 products on the 32-query
+        kernel (more than a few queries, not forced to 16 per workgroup), q, k
+        and v are views of that one buffer with unit head-dim stride and
+        16-byte aligned rows in bf16, k reads it alone, and its producer can
+        round its output to bf16 (the rounding the products do when they form
+        their operands, so the bits do not change). Otherwise None."""
+        from kiln.hip.attention import match_kernel, operand_strides
+
+        m = match_kernel(self.g, k)
+        strides = operand_strides(m, self.layouts) if m is not None else None
+        if strides is None or m.q.shape[1] <= ATTN_ROWS_MAX_Q or ATTN_QUERIES == 16:
+            return None
+        bufs = set()
+        for v, (_, st) in zip((m.q, m.k, m.v), strides):
+            lay = self.layouts.get(v)
+            if lay is None or lay.base[0] != "arena" or st[2] != 1 or st[0] % 8 or st[1] % 8 or lay.offset % 8:
+                return None
+            bufs.add(lay.base[1])
+        if len(bufs) != 1:
+            return None
+        buf = bufs.pop()
+        if self._arena_readers().get(buf) != {k} or buf in self.g.results:
+            return None
+        producer = self.g.kernel_of(buf.node)
+        return buf if producer is not None and producer.kind == "matmul" and self._rounds_to_bf16(producer, buf) else None
 
     def _rounds_to_bf16(self, k, buf) -> bool:
         """Can kernel k write its output `buf` as bf16?"""
@@ -1268,9 +1301,9 @@ class _Lowerer:
             r.offset = self.element_offset(v)
             for i in range(3):
                 r.strides[i] = st[i]
-            if j == 3 and self.stored_bf16(v):
+            if self.stored_bf16(v):   # the output, or (all three) q, k, v
                 r = self.as_bf16(r, v)
-                d.cfg[7] |= 1 << 3
+                d.cfg[7] |= 1 << j
             d.refs[j] = r
         d.n_refs = 4
         mode = kl.ATTN_MASK_NONE
@@ -1298,7 +1331,10 @@ class _Lowerer:
                  kl.ATTN_SCALE_DIV: f", scores / {m.scale:g}"}[m.scale_mode]
         if bf_products:
             scale += ", products:bf16"
-        if d.cfg[7]:
+        if d.cfg[7] & 7:
+            scale += ", qkv:bf16"
+            nbytes -= 2 * batch * dh * (tq + 2 * tk)
+        if d.cfg[7] & 8:
             scale += ", out:bf16"
             nbytes -= 2 * batch * dh * tq
         self.add(d, k, f"{batch} heads x {tq} queries x {tk} keys, head dim {dh}, {what}{scale}",

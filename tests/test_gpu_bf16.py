@@ -243,6 +243,9 @@ def test_bf16_attention_output_on_both_query_blocks(queries, monkeypatch):
     c = kiln.compile(model, (x,), device="cuda", matmul_precision="bf16", gpu_matmul_config=cfg)
     summaries = [l.summary for l in c._exe.program.launches]
     assert any("heads" in s and "out:bf16" in s for s in summaries), summaries
+    # with 32 queries per workgroup the QKV product also writes q, k, v as
+    # bf16 for the attention's bf16 products
+    assert any("heads" in s and "qkv:bf16" in s for s in summaries) == (queries == 32), summaries
     xd = x.cuda()
     got = c(xd)
     monkeypatch.setattr(lowering._Lowerer, "plan_bf16_storage", lambda self: set())

@@ -317,9 +317,10 @@ def _no_bf16_storage(monkeypatch):
 def test_bf16_storage_between_producers_and_products_gives_the_same_bits(monkeypatch):
     # bf16 plans on the 64-deep product configurations: the LayerNorms, the
     # attention and the MLP-up product round their outputs to bf16 when a
-    # bf16 product is their only reader; the products read them as bf16. The
-    # rounding is the one the products would do at every fragment read, so
-    # the result is bit for bit the one of the same plan with fp32 storage
+    # bf16 product is their only reader, and the QKV product rounds q, k, v
+    # for the attention's bf16 products; the readers take them as bf16. The
+    # rounding is the one the readers would do when they form their operands,
+    # so the result is bit for bit the one of the same plan with fp32 storage
     torch.manual_seed(0)
     model = gpt2_init_(Block(128, 4, 16), seed=0).eval()
     x = torch.randn(16, 128)
@@ -327,7 +328,8 @@ def test_bf16_storage_between_producers_and_products_gives_the_same_bits(monkeyp
     c = kiln.compile(model, (x,), device="cuda", matmul_precision="bf16", gpu_matmul_config=cfg)
     summaries = [l.summary for l in c._exe.program.launches]
     assert sum("A:bf16" in s for s in summaries) == 4, summaries
-    assert sum("out:bf16" in s for s in summaries) == 4, summaries   # 2 LayerNorms, attention, MLP up
+    assert sum("out:bf16" in s for s in summaries) == 5, summaries   # 2 LayerNorms, QKV, attention, MLP up
+    assert any("heads" in s and "qkv:bf16" in s for s in summaries), summaries
     got = c(x)
     _no_bf16_storage(monkeypatch)
     plain = kiln.compile(model, (x,), device="cuda", matmul_precision="bf16", gpu_matmul_config=cfg)
