@@ -189,7 +189,9 @@ typedef struct kh_pass {
  * elements. Accepted only where a kernel implements it, else
  * KH_ERR_UNSUPPORTED: the output of the one-wave LayerNorm (offset and row
  * stride multiples of 4), the output of the blocked attention kernel (refs[3],
- * 8-element aligned rows), and on the bf16 configurations 95-100 of a GEMM the
+ * 8-element aligned rows) and its q, k, v together (refs[0..2], with bf16
+ * products, cfg[5] = 1, and 32 queries per workgroup; 16-byte aligned rows),
+ * and on the bf16 configurations 95-100 of a GEMM the
  * A operand (bit 0; unit K stride, rows 8-element aligned) and the output ref
  * of a direct epilogue (its bit; unit N stride, rows 4-element aligned).
  */
