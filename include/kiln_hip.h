@@ -182,7 +182,10 @@ typedef struct kh_pass {
  *        cfg[5] = products precision: 0 fp32; 1 bf16 inputs (q and k for the
  *        scores, the softmax weights and v for the weighted sum rounded to
  *        bf16, round to nearest even; scores, softmax and accumulation
- *        fp32).
+ *        fp32); 2 three-pass bf16 (each of those inputs split into hi =
+ *        bf16(x) and lo = bf16(x - hi), lo 0 for a non-finite hi, a product
+ *        taken as lo.hi + hi.lo + hi.hi; fp32 q, k, v and 32 queries per
+ *        workgroup).
  * cfg[] holds the family configuration (GEMM: tile id, split-K, precision).
  * bf16 storage (ROW, ATTN, GEMM): bit j of cfg[7] says refs[j] holds bf16
  * values (round to nearest even), its offset and strides counted in bf16

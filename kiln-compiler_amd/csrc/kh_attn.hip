@@ -85,6 +85,39 @@ __device__ __forceinline__ bf16x8 pack_bf16x8(const float4 &x, const float4 &y) 
   return r;
 }
 
+// Two fp32 values rounded to bf16 (nearest even) in one word, a's bits low.
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  bf16x2 r;
+  r[0] = (__bf16)a, r[1] = (__bf16)b;
+  return __builtin_bit_cast(uint32_t, r);
+}
+
+// Eight fp32 values as the two bf16 halves of the three-pass product:
+// hi = bf16(x), lo = bf16(x - hi) (the difference is exact in fp32; a
+// non-finite hi keeps lo 0), so x.y ~ x_lo y_hi + x_hi y_lo + x_hi y_hi with
+// the dropped x_lo y_lo ~2^-16 of the product. CHECK = false for values that
+// are finite or NaN (probabilities), where the hi part alone already decides
+// a NaN result.
+template <bool CHECK>
+__device__ __forceinline__ void split_bf16x8(const float4 &x, const float4 &y, bf16x8 &hi, bf16x8 &lo) {
+  const float v[8] = {x.x, x.y, x.z, x.w, y.x, y.y, y.z, y.w};
+  uint32_t h[4], l[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    h[e] = pack_bf16x2(v[2 * e], v[2 * e + 1]);
+    const float h0 = __uint_as_float(h[e] << 16), h1 = __uint_as_float(h[e] & 0xffff0000u);
+    float l0 = v[2 * e] - h0, l1 = v[2 * e + 1] - h1;
+    if constexpr (CHECK) {
+      l0 = __builtin_isfinite(h0) ? l0 : 0.0f;
+      l1 = __builtin_isfinite(h1) ? l1 : 0.0f;
+    }
+    l[e] = pack_bf16x2(l0, l1);
+  }
+  hi = __builtin_bit_cast(bf16x8, make_uint4(h[0], h[1], h[2], h[3]));
+  lo = __builtin_bit_cast(bf16x8, make_uint4(l[0], l[1], l[2], l[3]));
+}
+
 // Exchange between the two lane halves (lanes l and l ^ 32): returns
 // (x[l & 31], x[32 + (l & 31)]), the low half's value first in every lane,
 // so a combine of the two is the same in both halves. One v_permlane32_swap.
@@ -109,9 +142,13 @@ __device__ __forceinline__ float2 halves(float x) {
 // IN16 (with BF): q, k and v are stored as bf16 by their producer, so the
 // operands are loaded as bf16 (K as one 16-byte load per chunk, V as 16-bit
 // loads paired into MFMA operand words) and rounded by no one here.
+// X3 (with BF, fp32 storage): three-pass bf16 products (plans with
+// allow_tf32): each of q, k, the probabilities and v splits into bf16 hi and
+// lo parts (split_bf16x8) and a product is lo.hi + hi.lo + hi.hi, three MFMAs
+// where BF issues one.
 // REC (the timeline probe only): each wave also records its start, loop-end
 // and end times, the shader clock and the CU it ran on.
-template <int DH, int NW, bool ADD, bool BF = false, bool REC = false, bool IN16 = false>
+template <int DH, int NW, bool ADD, bool BF = false, bool REC = false, bool IN16 = false, bool X3 = false>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) void attn_kernel(const AttnArgs a) {
   uint64_t rec_t0 = 0, rec_c0 = 0;
   if constexpr (REC) rec_t0 = __builtin_amdgcn_s_memrealtime(), rec_c0 = __builtin_amdgcn_s_memtime();
@@ -139,7 +176,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
                                                             : kLog2e;
   float qf[BF ? 1 : QS];
   bf16x8 qh[BF ? DH / 16 : 1];   // (bf16 products: Q as it is, the scale applied to the scores)
+  bf16x8 ql[X3 ? DH / 16 : 1];   // (three-pass products: Q's lo part)
   static_assert(BF || !IN16, "bf16 storage of q, k, v comes with bf16 products");
+  static_assert(!X3 || (BF && !IN16), "three-pass products split fp32 q, k, v");
   if constexpr (IN16) {
     const uint16_t *qp = reinterpret_cast<const uint16_t *>(a.q) + b * a.q_b + (int64_t)min(qi, a.tq - 1) * a.q_t + 8 * half;
 #pragma unroll
@@ -153,7 +192,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     for (int c = 0; c < DH / 16; ++c) {
       float4 x = *reinterpret_cast<const float4 *>(qp + 16 * c), y = *reinterpret_cast<const float4 *>(qp + 16 * c + 4);
       if (!q_ok) x = make_float4(0.f, 0.f, 0.f, 0.f), y = x;
-      qh[c] = pack_bf16x8(x, y);
+      if constexpr (X3) split_bf16x8<true>(x, y, qh[c], ql[c]);
+      else qh[c] = pack_bf16x8(x, y);
     }
   } else {
     const float *qp = a.q + b * a.q_b + (int64_t)min(qi, a.tq - 1) * a.q_t + half * QS;
@@ -225,6 +265,14 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     if constexpr (BF) {
 #pragma unroll
       for (int c = 0; c < DH / 16; ++c) {
+        if constexpr (X3) {
+          bf16x8 kh, kl;
+          split_bf16x8<true>(kc[2 * c], kc[2 * c + 1], kh, kl);
+          s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kl, qh[c], s, 0, 0, 0);
+          s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh, ql[c], s, 0, 0, 0);
+          s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh, qh[c], s, 0, 0, 0);
+          continue;
+        }
         const bf16x8 k8 = IN16 ? __builtin_bit_cast(bf16x8, kc[c]) : pack_bf16x8(kc[2 * c], kc[2 * c + 1]);
         s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(k8, qh[c], s, 0, 0, 0);
       }
@@ -289,13 +337,22 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     if constexpr (BF) {
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
-        const bf16x8 pb = pack_bf16x8(make_float4(p[8 * c], p[8 * c + 1], p[8 * c + 2], p[8 * c + 3]),
-                                      make_float4(p[8 * c + 4], p[8 * c + 5], p[8 * c + 6], p[8 * c + 7]));
+        const float4 p0 = make_float4(p[8 * c], p[8 * c + 1], p[8 * c + 2], p[8 * c + 3]);
+        const float4 p1 = make_float4(p[8 * c + 4], p[8 * c + 5], p[8 * c + 6], p[8 * c + 7]);
+        bf16x8 pb, pl;
+        if constexpr (X3) split_bf16x8<false>(p0, p1, pb, pl);
+        else pb = pack_bf16x8(p0, p1);
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
           const float *v8 = vf + 8 * c * NT + t;
           bf16x8 va;
-          if constexpr (IN16) {
+          if constexpr (X3) {
+            bf16x8 vl;
+            split_bf16x8<true>(make_float4(v8[0], v8[NT], v8[2 * NT], v8[3 * NT]),
+                               make_float4(v8[4 * NT], v8[5 * NT], v8[6 * NT], v8[7 * NT]), va, vl);
+            oacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vl, pb, oacc[t], 0, 0, 0);
+            oacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pl, oacc[t], 0, 0, 0);
+          } else if constexpr (IN16) {
             uint4 w;
             w.x = __float_as_uint(v8[0]) | (__float_as_uint(v8[NT]) << 16);
             w.y = __float_as_uint(v8[2 * NT]) | (__float_as_uint(v8[3 * NT]) << 16);
@@ -892,6 +949,7 @@ class AttnOp final : public Op {
   bool q16 = false;   // 16 queries per workgroup (attn16_kernel)
   bool bf = false;    // bf16 products (attn_kernel<..., BF> / attnbf_kernel)
   bool in16 = false;  // q, k, v stored as bf16 (attn_kernel<..., BF, ..., IN16>)
+  bool x3 = false;    // three-pass bf16 products (attn_kernel<..., BF, ..., X3>)
   dim3 grid;
 
   hipError_t launch(float *const *ptrs, float *, hipStream_t stream) override {
@@ -945,7 +1003,9 @@ class AttnOp final : public Op {
 #define KH_ATTN_LAUNCH(D, W)                                                                         \
   if (dh == D && nw == W) {                                                                          \
     const bool add = a.mask_mode == KH_ATTN_MASK_ADD;                                                \
-    if (in16 && add) hipLaunchKernelGGL((attn_kernel<D, W, true, true, false, true>), grid, dim3(64 * W), 0, stream, a); \
+    if (x3 && add) hipLaunchKernelGGL((attn_kernel<D, W, true, true, false, false, true>), grid, dim3(64 * W), 0, stream, a); \
+    else if (x3) hipLaunchKernelGGL((attn_kernel<D, W, false, true, false, false, true>), grid, dim3(64 * W), 0, stream, a); \
+    else if (in16 && add) hipLaunchKernelGGL((attn_kernel<D, W, true, true, false, true>), grid, dim3(64 * W), 0, stream, a); \
     else if (in16) hipLaunchKernelGGL((attn_kernel<D, W, false, true, false, true>), grid, dim3(64 * W), 0, stream, a); \
     else if (bf && add) hipLaunchKernelGGL((attn_kernel<D, W, true, true>), grid, dim3(64 * W), 0, stream, a); \
     else if (bf) hipLaunchKernelGGL((attn_kernel<D, W, false, true>), grid, dim3(64 * W), 0, stream, a); \
@@ -1039,13 +1099,15 @@ std::unique_ptr<Op> make_attn(const kh_launch &L, std::string &err, bool &unsupp
     return nullptr;
   }
   // products precision (cfg[5]): 0 fp32, 1 bf16 inputs with fp32 accumulation
-  // (attn_kernel<..., BF> or, for 16 queries per workgroup, attnbf_kernel)
+  // (attn_kernel<..., BF> or, for 16 queries per workgroup, attnbf_kernel),
+  // 2 three-pass bf16 (attn_kernel<..., BF, ..., X3>, 32 queries per workgroup)
   const int prec = L.cfg[5];
-  if (prec != 0 && prec != 1) {
-    err = "attention: products precision must be 0 (fp32) or 1 (bf16)";
+  if (prec < 0 || prec > 2) {
+    err = "attention: products precision must be 0 (fp32), 1 (bf16) or 2 (three-pass bf16)";
     return nullptr;
   }
-  op->bf = prec == 1;
+  op->bf = prec >= 1;
+  op->x3 = prec == 2;
   // 16 when 32-query blocks would give under 1.5 workgroups per CU (measured
   // on the GPT-2 block, 12 heads causal: T = 128 6.2 -> 4.7 us, 512 13.5 ->
   // 11.4 us; from T = 1024 on the 32-query kernel is faster); with bf16
@@ -1059,7 +1121,12 @@ std::unique_ptr<Op> make_attn(const kh_launch &L, std::string &err, bool &unsupp
     err = "attention: bf16 storage of q, k, v needs all three, bf16 products and 32 queries per workgroup";
     return nullptr;
   }
-  op->q16 = !op->in16 && (qpw == 16 || (qpw == 0 && (op->bf ? 2 * groups32 < current_device().cus
+  if (op->x3 && ((m16 & 7u) || qpw == 16)) {
+    unsupported = true;
+    err = "attention: three-pass products split fp32 q, k, v on 32 queries per workgroup";
+    return nullptr;
+  }
+  op->q16 = !op->in16 && !op->x3 && (qpw == 16 || (qpw == 0 && (op->bf ? 2 * groups32 < current_device().cus
                                                               : 2 * groups32 < 3ll * current_device().cus)));
   a.n_qblocks = (int)((tq + (op->q16 ? 16 : kQB) - 1) / (op->q16 ? 16 : kQB));
   op->dh = (int)dh;
@@ -1078,6 +1145,11 @@ std::unique_ptr<Op> make_attn(const kh_launch &L, std::string &err, bool &unsupp
     // 16-query blocks: four waves, eight from 8 visited key blocks (T = 512:
     // 12.3 -> 11.4 us)
     if (op->q16) nw = visited >= 8 && dh == 64 ? 8 : 4;
+    // three-pass products: eight waves for grids of one to one and a half
+    // workgroups per CU, four otherwise (GPT-2 block: T = 768 15.8 / 16.9
+    // us with 8 / 4, T = 1024 20.9 / 22.8; T = 512 11.2 / 12.2 with 4 / 8,
+    // T = 1536 34.7 / 37.2, T = 2048 52.8 / 56.5; two waves 28-41% slower)
+    else if (op->x3) nw = groups >= current_device().cus && 2 * groups <= 3ll * current_device().cus && dh == 64 ? 8 : 4;
     // bf16 products, 32-query blocks: two waves up to 16 visited key blocks,
     // four beyond (GPT-2 block: T = 512 8.5 against 8.9 / 10.7 us with 4 / 8,
     // T = 1024 17.1 against 18.5 / 17.2, T = 1536 26.9 against 29.2 / 29.7 with

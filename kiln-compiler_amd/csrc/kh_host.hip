@@ -213,14 +213,23 @@ void host_red(const kh_launch &L, float *const *p) {
 // unfused attention whose matmuls take bf16 inputs).
 void attend(int64_t tk, int64_t dh, int scale_mode, float scale, int mask_mode, int64_t query,
             const float *q, int64_t q_sd, const float *k, int64_t k_sj, int64_t k_sd, const float *v, int64_t v_sj,
-            int64_t v_sd, const float *mask, int64_t mask_sj, double *out, bool bf = false) {
-  auto in = [bf](float x) { return bf ? bf16_round(x) : x; };
+            int64_t v_sd, const float *mask, int64_t mask_sj, double *out, int prec = 0) {
+  // one product of the two matmuls: fp32 inputs, bf16-rounded inputs, or the
+  // three-pass sum lo.hi + hi.lo + hi.hi of the bf16 halves (a non-finite hi
+  // keeps lo 0)
+  auto prod = [prec](float x, float y) -> double {
+    if (prec == 0) return (double)x * (double)y;
+    const float xh = bf16_round(x), yh = bf16_round(y);
+    if (prec == 1) return (double)xh * (double)yh;
+    const float xl = std::isfinite(xh) ? bf16_round(x - xh) : 0.0f, yl = std::isfinite(yh) ? bf16_round(y - yh) : 0.0f;
+    return (double)xl * yh + (double)xh * yl + (double)xh * yh;
+  };
   std::vector<double> s((size_t)tk);
   double m = -INFINITY;
   for (int64_t j = 0; j < tk; ++j) {
     float dot = 0.0f;
     double acc = 0.0;
-    for (int64_t d = 0; d < dh; ++d) acc += (double)in(q[d * q_sd]) * (double)in(k[j * k_sj + d * k_sd]);
+    for (int64_t d = 0; d < dh; ++d) acc += prod(q[d * q_sd], k[j * k_sj + d * k_sd]);
     dot = (float)acc;
     if (scale_mode == KH_ATTN_SCALE_MUL) dot *= scale;
     if (scale_mode == KH_ATTN_SCALE_DIV) dot /= scale;
@@ -231,12 +240,13 @@ void attend(int64_t tk, int64_t dh, int scale_mode, float scale, int mask_mode, 
   }
   double l = 0.0;
   for (int64_t j = 0; j < tk; ++j) l += (s[j] = std::exp(s[j] - m));
-  if (bf)
-    for (int64_t j = 0; j < tk; ++j) s[j] = bf16_round((float)(s[j] / l));
+  // bf16 and three-pass products take the normalised weights in fp32, as the
+  // unfused softmax hands them to its matmul
   for (int64_t d = 0; d < dh; ++d) {
     double acc = 0.0;
-    for (int64_t j = 0; j < tk; ++j) acc += s[j] * (double)in(v[j * v_sj + d * v_sd]);
-    out[d] = bf ? acc : acc / l;
+    for (int64_t j = 0; j < tk; ++j)
+      acc += prec ? prod((float)(s[j] / l), v[j * v_sj + d * v_sd]) : s[j] * (double)v[j * v_sj + d * v_sd];
+    out[d] = prec ? acc : acc / l;
   }
 }
 
@@ -265,7 +275,7 @@ void host_attn(const kh_launch &L, float *const *p0) {
                                                        : nullptr;
       attend(tk, dh, L.cfg[1], L.fparams[0], L.cfg[0], i, p[0] + b * Q.strides[0] + i * Q.strides[1], Q.strides[2],
              p[1] + b * K.strides[0], K.strides[1], K.strides[2], p[2] + b * V.strides[0], V.strides[1], V.strides[2],
-             mask, mask ? L.refs[4].strides[2] : 0, out.data(), L.cfg[5] == 1);
+             mask, mask ? L.refs[4].strides[2] : 0, out.data(), L.cfg[5]);
       for (int64_t d = 0; d < dh; ++d)
         Operands(L, p).st(3, b * O.strides[0] + i * O.strides[1] + d * O.strides[2], (float)out[d]);
     }

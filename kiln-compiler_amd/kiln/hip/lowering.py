@@ -49,6 +49,13 @@ LN_PROLOGUE_MAX_ROWS = 256
 ATTN_QUERIES = 0
 # the few-query attention kernel's largest query count (kRowsMaxQ in kh_attn.hip)
 ATTN_ROWS_MAX_Q = 4
+# three-pass plans (allow_tf32) run attention's two products as three-pass
+# bf16 on the 32-query kernel where its grid has at least this many
+# workgroups (GPT-2 block, 12 heads causal: T = 512 11.9 -> 11.2 us, 1024
+# 25.5 -> 20.9, 2048 66.7 -> 52.8); smaller grids keep fp32 products on the
+# 16-query kernel, which is faster there (T = 256 6.8 against 7.9 us, T = 128
+# 5.2 against 5.8)
+ATTN_X3_MIN_GROUPS = 192
 
 _UNARY_OP = {"neg": "neg", "exp": "exp", "tanh": "tanh", "sigmoid": "sigmoid", "relu": "relu",
              "rsqrt": "rsqrt", "sqrt": "sqrt", "erf": "erf", "copy": "mov"}
@@ -1316,11 +1323,16 @@ class _Lowerer:
         d.cfg[0], d.cfg[1] = mode, m.scale_mode
         d.cfg[3] = ATTN_QUERIES
         # bf16 plans run the two products of attention on bf16 inputs too
-        # (fp32 accumulation and softmax); decode shapes keep the few-query
+        # (fp32 accumulation and softmax), three-pass plans on three-pass bf16
+        # where the grid is large enough; decode shapes keep the few-query
         # kernel's fp32 products
         bf_products = self.precision == "bf16" and tq > ATTN_ROWS_MAX_Q
+        x3_products = (self.precision == "bf16x3" and tq > ATTN_ROWS_MAX_Q and ATTN_QUERIES != 16
+                       and batch * -(-tq // 32) >= ATTN_X3_MIN_GROUPS)
         if bf_products:
             d.cfg[5] = 1
+        if x3_products:
+            d.cfg[5] = 2
         d.fparams[0] = m.scale
         causal = mode == kl.ATTN_MASK_CAUSAL
         pairs = sum(min(tk, i + 1) for i in range(tq)) if causal else tq * tk
@@ -1331,6 +1343,8 @@ class _Lowerer:
                  kl.ATTN_SCALE_DIV: f", scores / {m.scale:g}"}[m.scale_mode]
         if bf_products:
             scale += ", products:bf16"
+        if x3_products:
+            scale += ", products:bf16x3"
         if d.cfg[7] & 7:
             scale += ", qkv:bf16"
             nbytes -= 2 * batch * dh * (tq + 2 * tk)

@@ -131,7 +131,7 @@ def test_k_contiguous_bf16x3_tiles_walk_several_tiles(tile):
     close_to_scale(c(x).cpu().numpy(), ref, SPLIT_EXACT)
 
 
-@pytest.mark.parametrize("T", [128, 512])
+@pytest.mark.parametrize("T", [128, 512, 2048])
 def test_gpt2_block_allow_tf32(T):
     torch.manual_seed(0)
     model = gpt2_init_(Block(768, 12, T), seed=0).eval()
@@ -142,3 +142,123 @@ def test_gpt2_block_allow_tf32(T):
     with torch.no_grad():
         ref = model.double()(x.double()).numpy()
     close_to_scale(out, ref, FP32_CLASS)
+
+
+# -- attention with three-pass products ---------------------------------------------------------
+# Three-pass plans run attention's two products on the same splits: q, k for
+# the scores, the probabilities and v for the weighted sum (hi.lo + lo.hi +
+# hi.hi, fp32 accumulation, scale, mask and softmax fp32), on the 32-query
+# kernel where its grid has at least lowering.ATTN_X3_MIN_GROUPS workgroups
+# (the tests below lower that bar to 0 to reach ragged and small shapes).
+
+class _Attn(torch.nn.Module):
+    """softmax(q k^T * scale + mask) v over [B, T, D] inputs."""
+
+    def __init__(self, mask=None, scale=0.125):
+        super().__init__()
+        self.scale = scale
+        if mask is not None:
+            self.register_buffer("mask", mask)
+        else:
+            self.mask = None
+
+    def forward(self, q, k, v):
+        s = (q @ k.transpose(-2, -1)) * self.scale
+        if self.mask is not None:
+            s = s + self.mask
+        return torch.softmax(s, dim=-1) @ v
+
+
+def _three_pass_attention_reference(q, k, v, scale, mask):
+    """The unfused computation with three-pass products: the scores from the
+    splits of q and k, the normalised softmax weights (fp32) and v split for
+    the weighted sum, everything else float64."""
+    qh, ql = split(q.numpy())
+    kh, kl = split(k.numpy())
+    kt = lambda a: a.transpose(0, 2, 1)
+    s = (ql @ kt(kh) + qh @ kt(kl) + qh @ kt(kh)) * scale
+    if mask is not None:
+        s = s + mask.numpy().astype(np.float64)
+    with np.errstate(invalid="ignore"):
+        e = np.exp(s - s.max(-1, keepdims=True))
+        p = (e / e.sum(-1, keepdims=True)).astype(np.float32)
+    ph, pl = split(p)
+    vh, vl = split(v.numpy())
+    return pl @ vh + ph @ vl + ph @ vh
+
+
+@pytest.fixture
+def x3_everywhere(monkeypatch):
+    from kiln.hip import lowering
+
+    monkeypatch.setattr(lowering, "ATTN_X3_MIN_GROUPS", 0)
+
+
+def _check_x3_attention(model, q, k, v, mask, expect=True):
+    c = kiln.compile(model, (q, k, v), device="cuda", allow_tf32=True)
+    summaries = [l.summary for l in c._exe.program.launches]
+    assert any("heads" in s for s in summaries), summaries
+    assert any("products:bf16x3" in s for s in summaries) == expect, summaries
+    got = c(q.cuda(), k.cuda(), v.cuda()).cpu().numpy().astype(np.float64)
+    nan = np.isnan(_three_pass_attention_reference(q, k, v, model.scale, mask))
+    assert np.array_equal(np.isnan(got), nan)
+    # the kernel splits the running-max-relative probabilities, the reference
+    # the normalised ones: each weight's split is within ~2^-16 of it in both
+    ref = _three_pass_attention_reference(q, k, v, model.scale, mask)
+    tol = 2.0 ** -15 * float(np.abs(v.numpy()).max()) + 1e-6
+    err = float(np.abs(got[~nan] - ref[~nan]).max()) if (~nan).any() else 0.0
+    assert err <= tol, f"max error {err:.2e} > {tol:.2e}"
+    # and fp32-class against float64 of the unsplit inputs
+    with torch.no_grad():
+        f64 = model.double()(q.double(), k.double(), v.double()).numpy()
+    model.float()
+    close_to_scale(got[~nan], f64[~nan], FP32_CLASS)
+    return c
+
+
+@pytest.mark.parametrize("T", [5, 77, 200, 512])
+@pytest.mark.parametrize("d", [32, 64])
+def test_x3_attention_causal(T, d, x3_everywhere):
+    g = torch.Generator().manual_seed(T + d)
+    q, k, v = (torch.randn(3, T, d, generator=g) for _ in range(3))
+    mask = torch.full((T, T), float("-inf")).triu(1)
+    _check_x3_attention(_Attn(mask, 1 / d ** 0.5), q, k, v, mask)
+
+
+@pytest.mark.parametrize("tq, tk", [(50, 90), (33, 7), (64, 64), (130, 300)])
+def test_x3_attention_cross(tq, tk, x3_everywhere):
+    g = torch.Generator().manual_seed(tq * 7 + tk)
+    q, k, v = torch.randn(2, tq, 64, generator=g), torch.randn(2, tk, 64, generator=g), torch.randn(2, tk, 64, generator=g)
+    _check_x3_attention(_Attn(None, 0.125), q, k, v, None)
+
+
+def test_x3_attention_additive_mask_and_fully_masked_row(x3_everywhere):
+    tq, tk = 40, 70
+    g = torch.Generator().manual_seed(11)
+    q, k, v = torch.randn(2, tq, 64, generator=g), torch.randn(2, tk, 64, generator=g), torch.randn(2, tk, 64, generator=g)
+    mask = torch.randn(tq, tk, generator=g)
+    mask[torch.rand(tq, tk, generator=g) < 0.3] = float("-inf")
+    mask[:, 0] = 0.0
+    mask[7, :] = float("-inf")          # a fully masked row: NaN, as in eager
+    _check_x3_attention(_Attn(mask, 0.125), q, k, v, mask)
+
+
+@pytest.mark.parametrize("heads, T, expect", [(12, 512, True), (12, 1024, True), (12, 256, False), (3, 2048, True)])
+def test_x3_attention_by_grid_size(heads, T, expect):
+    # the library default: three-pass products from 192 query blocks of 32 on
+    # (eight waves per workgroup at T = 1024, four at 512 and 2048), fp32
+    # products on the 16-query kernel below
+    g = torch.Generator().manual_seed(heads + T)
+    q, k, v = (torch.randn(heads, T, 64, generator=g) for _ in range(3))
+    mask = torch.full((T, T), float("-inf")).triu(1)
+    _check_x3_attention(_Attn(mask, 0.125), q, k, v, mask, expect=expect)
+
+
+def test_x3_attention_keeps_fp32_products_on_decode_shapes(x3_everywhere):
+    g = torch.Generator().manual_seed(5)
+    q, k, v = torch.randn(4, 1, 64, generator=g), torch.randn(4, 40, 64, generator=g), torch.randn(4, 40, 64, generator=g)
+    c = kiln.compile(_Attn(None, 0.125), (q, k, v), device="cuda", allow_tf32=True)
+    assert not any("products:bf16" in l.summary for l in c._exe.program.launches)
+    with torch.no_grad():
+        eager = _Attn(None, 0.125)(q, k, v)
+    torch.testing.assert_close(c(q.cuda(), k.cuda(), v.cuda()).cpu(), eager, rtol=1e-4, atol=1e-5)

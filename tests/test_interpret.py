@@ -408,3 +408,48 @@ def test_bf16_attention_products_on_the_host():
     # decode shapes keep fp32 products
     c1 = kiln.compile(Attn(mask[:1]), (q[:, :1], k, v), device="cuda", matmul_precision="bf16")
     assert "products:bf16" not in open(c1.report.lowering["source"]).read()
+
+
+def test_three_pass_attention_products_on_the_host(monkeypatch):
+    # a three-pass plan's attention (cfg[5] = 2) on the host: q, k split into
+    # bf16 hi = rn(x) and lo = rn(x - hi) for the scores (lo.hi + hi.lo + hi.hi
+    # summed in float64, then the fp32 score and scale), the normalised
+    # weights and v split the same way for the weighted sum
+    from kiln.hip import lowering
+
+    class Attn(torch.nn.Module):
+        def __init__(self, mask):
+            super().__init__()
+            self.register_buffer("mask", mask)
+
+        def forward(self, q, k, v):
+            return F.softmax((q @ k.transpose(-2, -1)) * 0.125 + self.mask, dim=-1) @ v
+
+    T, d = 40, 64
+    g = torch.Generator().manual_seed(3)
+    q, k, v = (torch.randn(2, T, d, generator=g) for _ in range(3))
+    mask = torch.full((T, T), float("-inf")).triu(1)
+    # two query blocks of 32: under the library's grid bar, so fp32 products
+    c0 = kiln.compile(Attn(mask), (q[:1], k[:1], v[:1]), device="cuda", allow_tf32=True)
+    assert "products:bf16" not in open(c0.report.lowering["source"]).read()
+    monkeypatch.setattr(lowering, "ATTN_X3_MIN_GROUPS", 0)
+    c = kiln.compile(Attn(mask), (q, k, v), device="cuda", matmul_precision="bf16x3")
+    assert "products:bf16x3" in open(c.report.lowering["source"]).read()
+
+    def split(a):
+        a = np.asarray(a, np.float32)
+        hi = oracle.bf16_round(a)
+        lo = oracle.bf16_round(np.where(np.isfinite(hi), a - hi, 0.0).astype(np.float32))
+        return hi.astype(np.float64), lo.astype(np.float64)
+
+    (qh, ql), (kh, kl), (vh, vl) = split(q.numpy()), split(k.numpy()), split(v.numpy())
+    kt = lambda a: a.transpose(0, 2, 1)
+    s = (ql @ kt(kh) + qh @ kt(kl) + qh @ kt(kh)).astype(np.float32) * np.float32(0.125)
+    s = s.astype(np.float64) + mask.numpy()
+    e = np.exp(s - s.max(-1, keepdims=True))
+    wh, wl = split((e / e.sum(-1, keepdims=True)).astype(np.float32))
+    ref = wl @ vh + wh @ vl + wh @ vh
+    got = c(q, k, v).numpy().astype(np.float64)
+    np.testing.assert_allclose(got, ref, rtol=1e-6, atol=1e-7)
+    # a dropped cross term would move the result by ~1e-3 of its scale
+    assert np.abs(got - (wh @ vh)).max() > 1e-5
