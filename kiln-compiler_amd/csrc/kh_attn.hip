@@ -106,7 +106,10 @@ __device__ __forceinline__ void split_bf16x8(const float4 &x, const float4 &y, b
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     h[e] = pack_bf16x2(v[2 * e], v[2 * e + 1]);
-    const float h0 = __uint_as_float(h[e] << 16), h1 = __uint_as_float(h[e] & 0xffff0000u);
+    // the two halves as fp32 (a byte permute for the low one, which the
+    // compiler would otherwise recompute with a second conversion)
+    const float h0 = __uint_as_float(__builtin_amdgcn_perm(h[e], h[e], 0x01000c0cu));
+    const float h1 = __uint_as_float(h[e] & 0xffff0000u);
     float l0 = v[2 * e] - h0, l1 = v[2 * e + 1] - h1;
     if constexpr (CHECK) {
       l0 = __builtin_isfinite(h0) ? l0 : 0.0f;
