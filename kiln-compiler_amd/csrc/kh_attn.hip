@@ -85,42 +85,6 @@ __device__ __forceinline__ bf16x8 pack_bf16x8(const float4 &x, const float4 &y) 
   return r;
 }
 
-// Two fp32 values rounded to bf16 (nearest even) in one word, a's bits low.
-__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-  bf16x2 r;
-  r[0] = (__bf16)a, r[1] = (__bf16)b;
-  return __builtin_bit_cast(uint32_t, r);
-}
-
-// Eight fp32 values as the two bf16 halves of the three-pass product:
-// hi = bf16(x), lo = bf16(x - hi) (the difference is exact in fp32; a
-// non-finite hi keeps lo 0), so x.y ~ x_lo y_hi + x_hi y_lo + x_hi y_hi with
-// the dropped x_lo y_lo ~2^-16 of the product. CHECK = false for values that
-// are finite or NaN (probabilities), where the hi part alone already decides
-// a NaN result.
-template <bool CHECK>
-__device__ __forceinline__ void split_bf16x8(const float4 &x, const float4 &y, bf16x8 &hi, bf16x8 &lo) {
-  const float v[8] = {x.x, x.y, x.z, x.w, y.x, y.y, y.z, y.w};
-  uint32_t h[4], l[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    h[e] = pack_bf16x2(v[2 * e], v[2 * e + 1]);
-    // the two halves as fp32 (a byte permute for the low one, which the
-    // compiler would otherwise recompute with a second conversion)
-    const float h0 = __uint_as_float(__builtin_amdgcn_perm(h[e], h[e], 0x01000c0cu));
-    const float h1 = __uint_as_float(h[e] & 0xffff0000u);
-    float l0 = v[2 * e] - h0, l1 = v[2 * e + 1] - h1;
-    if constexpr (CHECK) {
-      l0 = __builtin_isfinite(h0) ? l0 : 0.0f;
-      l1 = __builtin_isfinite(h1) ? l1 : 0.0f;
-    }
-    l[e] = pack_bf16x2(l0, l1);
-  }
-  hi = __builtin_bit_cast(bf16x8, make_uint4(h[0], h[1], h[2], h[3]));
-  lo = __builtin_bit_cast(bf16x8, make_uint4(l[0], l[1], l[2], l[3]));
-}
-
 // Exchange between the two lane halves (lanes l and l ^ 32): returns
 // (x[l & 31], x[32 + (l & 31)]), the low half's value first in every lane,
 // so a combine of the two is the same in both halves. One v_permlane32_swap.

@@ -198,4 +198,45 @@ __device__ __forceinline__ void exec_tape(const kh_insn *tape, int begin, int en
   }
 }
 
+// ---------------------------------------------------------------------------
+// bf16 operands of the matrix cores (round to nearest, ties to even).
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+
+// Two fp32 values as bf16 in one word, a's bits low (one v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  bf16x2_t r;
+  r[0] = (__bf16)a, r[1] = (__bf16)b;
+  return __builtin_bit_cast(uint32_t, r);
+}
+
+// Eight fp32 values as the two bf16 halves of a three-pass product:
+// hi = bf16(x), lo = bf16(x - hi) (the difference is exact in fp32; a
+// non-finite hi keeps lo 0), so x.y ~ x_lo y_hi + x_hi y_lo + x_hi y_hi with
+// the dropped x_lo y_lo ~2^-16 of the product. CHECK = false for values that
+// are finite or NaN (softmax probabilities), where the hi part alone already
+// makes a NaN result. Per pair of values: two conversions, a byte permute and
+// a mask to widen the hi halves back to fp32, two subtractions.
+template <bool CHECK>
+__device__ __forceinline__ void split_bf16x8(const float4 &x, const float4 &y, bf16x8_t &hi, bf16x8_t &lo) {
+  const float v[8] = {x.x, x.y, x.z, x.w, y.x, y.y, y.z, y.w};
+  uint32_t h[4], l[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    h[e] = pack_bf16x2(v[2 * e], v[2 * e + 1]);
+    // (the low half through a byte permute: the compiler would otherwise
+    // recompute it with a second conversion)
+    const float h0 = __uint_as_float(__builtin_amdgcn_perm(h[e], h[e], 0x01000c0cu));
+    const float h1 = __uint_as_float(h[e] & 0xffff0000u);
+    float l0 = v[2 * e] - h0, l1 = v[2 * e + 1] - h1;
+    if constexpr (CHECK) {
+      l0 = __builtin_isfinite(h0) ? l0 : 0.0f;
+      l1 = __builtin_isfinite(h1) ? l1 : 0.0f;
+    }
+    l[e] = pack_bf16x2(l0, l1);
+  }
+  hi = __builtin_bit_cast(bf16x8_t, make_uint4(h[0], h[1], h[2], h[3]));
+  lo = __builtin_bit_cast(bf16x8_t, make_uint4(l[0], l[1], l[2], l[3]));
+}
+
 }  // namespace kh

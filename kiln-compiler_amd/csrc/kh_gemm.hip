@@ -528,13 +528,9 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void gemm3_f32_kernel(const GemmAr
         bf16x8 ah[FM], al[FM], bh[FN], bl[FN];
 #pragma unroll
         for (int fm = 0; fm < FM; ++fm)
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            ah[fm][e] = (__bf16)af[fm][8 * j + e];
-            // the difference is exact in fp32; a non-finite hi part keeps lo 0
-            const float hv = (float)ah[fm][e];
-            al[fm][e] = (__bf16)(__builtin_isfinite(hv) ? af[fm][8 * j + e] - hv : 0.0f);
-          }
+          split_bf16x8<true>(make_float4(af[fm][8 * j], af[fm][8 * j + 1], af[fm][8 * j + 2], af[fm][8 * j + 3]),
+                             make_float4(af[fm][8 * j + 4], af[fm][8 * j + 5], af[fm][8 * j + 6], af[fm][8 * j + 7]),
+                             ah[fm], al[fm]);
 #pragma unroll
         for (int fn = 0; fn < FN; ++fn) {
           bh[fn] = *reinterpret_cast<const bf16x8 *>(st + b_off[fn][j]);

@@ -245,17 +245,14 @@ __global__ __launch_bounds__(64 * WK) void gemm_small_kernel(const GemmArgs a) {
     if constexpr (BF) {
       bf16x8 ah[FM], al[FM];
 #pragma unroll
-      for (int fm = 0; fm < FM; ++fm)
+      for (int fm = 0; fm < FM; ++fm) {
+        if constexpr (PREC == 2) {
+          split_bf16x8<true>(xa[fm][0], xa[fm][1], ah[fm], al[fm]);
+        } else {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float x = part(xa[fm][e / 4], e % 4);
-          ah[fm][e] = (__bf16)x;
-          if constexpr (PREC == 2) {
-            // the difference is exact in fp32; a non-finite hi part keeps lo 0
-            const float hv = (float)ah[fm][e];
-            al[fm][e] = (__bf16)(__builtin_isfinite(hv) ? x - hv : 0.0f);
-          }
+          for (int e = 0; e < 8; ++e) ah[fm][e] = (__bf16)part(xa[fm][e / 4], e % 4);
         }
+      }
 #pragma unroll
       for (int fm = 0; fm < FM; ++fm)
 #pragma unroll
