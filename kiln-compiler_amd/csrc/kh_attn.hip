@@ -77,14 +77,6 @@ struct AttnArgs {
   uint64_t *rec;           // timeline probe only: 8 words per wave (kh_probe_attn_timeline)
 };
 
-// Eight fp32 values rounded to bf16 (round to nearest even), an MFMA operand.
-__device__ __forceinline__ bf16x8 pack_bf16x8(const float4 &x, const float4 &y) {
-  bf16x8 r;
-  r[0] = (__bf16)x.x, r[1] = (__bf16)x.y, r[2] = (__bf16)x.z, r[3] = (__bf16)x.w;
-  r[4] = (__bf16)y.x, r[5] = (__bf16)y.y, r[6] = (__bf16)y.z, r[7] = (__bf16)y.w;
-  return r;
-}
-
 // Exchange between the two lane halves (lanes l and l ^ 32): returns
 // (x[l & 31], x[32 + (l & 31)]), the low half's value first in every lane,
 // so a combine of the two is the same in both halves. One v_permlane32_swap.
@@ -681,12 +673,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
   const float c_scale = a.scale_mode == KH_ATTN_SCALE_MUL   ? a.scale * kLog2e
                         : a.scale_mode == KH_ATTN_SCALE_DIV ? kLog2e / a.scale
                                                             : kLog2e;
-  auto pack8 = [](const float4 &x, const float4 &y) {
-    bf16x8 r;
-    r[0] = (__bf16)x.x, r[1] = (__bf16)x.y, r[2] = (__bf16)x.z, r[3] = (__bf16)x.w;
-    r[4] = (__bf16)y.x, r[5] = (__bf16)y.y, r[6] = (__bf16)y.z, r[7] = (__bf16)y.w;
-    return r;
-  };
+  auto pack8 = [](const float4 &x, const float4 &y) { return pack_bf16x8(x, y); };
   bf16x8 qh[QC];
   {
     const float *qp = a.q + b * a.q_b + (int64_t)min(qi, a.tq - 1) * a.q_t + 8 * g;
@@ -795,9 +782,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     const bf16x8 pb = pack8(make_float4(p[0][0], p[0][1], p[0][2], p[0][3]), make_float4(p[1][0], p[1][1], p[1][2], p[1][3]));
 #pragma unroll
     for (int d = 0; d < DT; ++d) {
-      bf16x8 va;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) va[j] = (__bf16)vf[j * DT + d];
+      const bf16x8 va = pack_bf16x8(make_float4(vf[d], vf[DT + d], vf[2 * DT + d], vf[3 * DT + d]),
+                                    make_float4(vf[4 * DT + d], vf[5 * DT + d], vf[6 * DT + d], vf[7 * DT + d]));
       oacc[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb, oacc[d], 0, 0, 0);
     }
   };

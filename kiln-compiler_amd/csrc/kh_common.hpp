@@ -210,6 +210,14 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   return __builtin_bit_cast(uint32_t, r);
 }
 
+// Eight fp32 values as one bf16 operand, one conversion per pair (element-wise
+// assignments into the vector can cost the compiler a second conversion and a
+// permute per pair).
+__device__ __forceinline__ bf16x8_t pack_bf16x8(const float4 &x, const float4 &y) {
+  return __builtin_bit_cast(bf16x8_t, make_uint4(pack_bf16x2(x.x, x.y), pack_bf16x2(x.z, x.w),
+                                                 pack_bf16x2(y.x, y.y), pack_bf16x2(y.z, y.w)));
+}
+
 // Eight fp32 values as the two bf16 halves of a three-pass product:
 // hi = bf16(x), lo = bf16(x - hi) (the difference is exact in fp32; a
 // non-finite hi keeps lo 0), so x.y ~ x_lo y_hi + x_hi y_lo + x_hi y_hi with

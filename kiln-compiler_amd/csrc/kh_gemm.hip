@@ -551,8 +551,8 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void gemm3_f32_kernel(const GemmAr
         bf16x8 a8[FM], b8[FN];
 #pragma unroll
         for (int fm = 0; fm < FM; ++fm)
-#pragma unroll
-          for (int e = 0; e < 8; ++e) a8[fm][e] = (__bf16)af[fm][8 * j + e];
+          a8[fm] = pack_bf16x8(make_float4(af[fm][8 * j], af[fm][8 * j + 1], af[fm][8 * j + 2], af[fm][8 * j + 3]),
+                               make_float4(af[fm][8 * j + 4], af[fm][8 * j + 5], af[fm][8 * j + 6], af[fm][8 * j + 7]));
 #pragma unroll
         for (int fn = 0; fn < FN; ++fn) b8[fn] = *reinterpret_cast<const bf16x8 *>(st + b_off[fn][j]);
 #pragma unroll

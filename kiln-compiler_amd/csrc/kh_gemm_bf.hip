@@ -194,8 +194,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_bf_kernel(const GemmArgs a)
         } else {
           const float4 lo = *reinterpret_cast<const float4 *>(st + fa[fm][k2][0]);
           const float4 hi = *reinterpret_cast<const float4 *>(st + fa[fm][k2][1]);
-          xa[fm][0] = (__bf16)lo.x, xa[fm][1] = (__bf16)lo.y, xa[fm][2] = (__bf16)lo.z, xa[fm][3] = (__bf16)lo.w;
-          xa[fm][4] = (__bf16)hi.x, xa[fm][5] = (__bf16)hi.y, xa[fm][6] = (__bf16)hi.z, xa[fm][7] = (__bf16)hi.w;
+          xa[fm] = pack_bf16x8(lo, hi);
         }
       }
 #pragma unroll

@@ -306,8 +306,7 @@ void gemm_nt_kernel(const GemmArgs a) {
           if constexpr (PREC == 2) {
             split_bf16x8<true>(xa[fm][0], xa[fm][1], ah[fm], al[fm]);
           } else {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) ah[fm][e] = (__bf16)part(xa[fm][e / 4], e % 4);
+            ah[fm] = pack_bf16x8(xa[fm][0], xa[fm][1]);
           }
         }
 #pragma unroll
