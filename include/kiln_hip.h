@@ -197,6 +197,14 @@ typedef struct kh_pass {
  * and on the bf16 configurations 95-100 of a GEMM the
  * A operand (bit 0; unit K stride, rows 8-element aligned) and the output ref
  * of a direct epilogue (its bit; unit N stride, rows 4-element aligned).
+ * Pair storage (ROW, ATTN, GEMM): bit 16 + j of cfg[7] says refs[j] holds each
+ * value x as one 32-bit word, bf16(x) in the low half and bf16(x - bf16(x))
+ * (0 for a non-finite bf16(x)) in the high half - the halves a three-pass
+ * product splits x into - addressed like fp32. Accepted for the output of the
+ * one-wave LayerNorm, the output of the blocked attention kernels and, with
+ * three-pass products (cfg[5] = 2), its q, k, v together, and on the
+ * three-pass GEMM configurations the A operand (bit 16) and the output of a
+ * direct epilogue without split-K.
  */
 typedef struct kh_launch {
   int32_t family;

@@ -74,6 +74,7 @@ struct AttnArgs {
   int32_t mask_mode, scale_mode;
   float scale;
   int32_t o16;             // the output is bf16 (its consumer is a bf16 matmul)
+  int32_t o_pair;          // the output is pair words (its consumer is a three-pass matmul)
   uint64_t *rec;           // timeline probe only: 8 words per wave (kh_probe_attn_timeline)
 };
 
@@ -104,10 +105,13 @@ __device__ __forceinline__ float2 halves(float x) {
 // X3 (with BF, fp32 storage): three-pass bf16 products (plans with
 // allow_tf32): each of q, k, the probabilities and v splits into bf16 hi and
 // lo parts (split_bf16x8) and a product is lo.hi + hi.lo + hi.hi, three MFMAs
-// where BF issues one.
+// where BF issues one. P3 (with X3): q, k and v are stored as pair words by
+// their producer (the two halves already made), so only the probabilities
+// are split here.
 // REC (the timeline probe only): each wave also records its start, loop-end
 // and end times, the shader clock and the CU it ran on.
-template <int DH, int NW, bool ADD, bool BF = false, bool REC = false, bool IN16 = false, bool X3 = false>
+template <int DH, int NW, bool ADD, bool BF = false, bool REC = false, bool IN16 = false, bool X3 = false,
+          bool P3 = false>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) void attn_kernel(const AttnArgs a) {
   uint64_t rec_t0 = 0, rec_c0 = 0;
   if constexpr (REC) rec_t0 = __builtin_amdgcn_s_memrealtime(), rec_c0 = __builtin_amdgcn_s_memtime();
@@ -138,6 +142,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
   bf16x8 ql[X3 ? DH / 16 : 1];   // (three-pass products: Q's lo part)
   static_assert(BF || !IN16, "bf16 storage of q, k, v comes with bf16 products");
   static_assert(!X3 || (BF && !IN16), "three-pass products split fp32 q, k, v");
+  static_assert(!P3 || X3, "pair-stored q, k, v come with three-pass products");
   if constexpr (IN16) {
     const uint16_t *qp = reinterpret_cast<const uint16_t *>(a.q) + b * a.q_b + (int64_t)min(qi, a.tq - 1) * a.q_t + 8 * half;
 #pragma unroll
@@ -151,7 +156,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     for (int c = 0; c < DH / 16; ++c) {
       float4 x = *reinterpret_cast<const float4 *>(qp + 16 * c), y = *reinterpret_cast<const float4 *>(qp + 16 * c + 4);
       if (!q_ok) x = make_float4(0.f, 0.f, 0.f, 0.f), y = x;
-      if constexpr (X3) split_bf16x8<true>(x, y, qh[c], ql[c]);
+      if constexpr (P3) unpair_bf16x8(x, y, qh[c], ql[c]);
+      else if constexpr (X3) split_bf16x8<true>(x, y, qh[c], ql[c]);
       else qh[c] = pack_bf16x8(x, y);
     }
   } else {
@@ -226,7 +232,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
       for (int c = 0; c < DH / 16; ++c) {
         if constexpr (X3) {
           bf16x8 kh, kl;
-          split_bf16x8<true>(kc[2 * c], kc[2 * c + 1], kh, kl);
+          if constexpr (P3) unpair_bf16x8(kc[2 * c], kc[2 * c + 1], kh, kl);
+          else split_bf16x8<true>(kc[2 * c], kc[2 * c + 1], kh, kl);
           s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kl, qh[c], s, 0, 0, 0);
           s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh, ql[c], s, 0, 0, 0);
           s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh, qh[c], s, 0, 0, 0);
@@ -307,8 +314,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
           bf16x8 va;
           if constexpr (X3) {
             bf16x8 vl;
-            split_bf16x8<true>(make_float4(v8[0], v8[NT], v8[2 * NT], v8[3 * NT]),
-                               make_float4(v8[4 * NT], v8[5 * NT], v8[6 * NT], v8[7 * NT]), va, vl);
+            const float4 v0 = make_float4(v8[0], v8[NT], v8[2 * NT], v8[3 * NT]);
+            const float4 v1 = make_float4(v8[4 * NT], v8[5 * NT], v8[6 * NT], v8[7 * NT]);
+            if constexpr (P3) unpair_bf16x8(v0, v1, va, vl);
+            else split_bf16x8<true>(v0, v1, va, vl);
             oacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vl, pb, oacc[t], 0, 0, 0);
             oacc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pl, oacc[t], 0, 0, 0);
           } else if constexpr (IN16) {
@@ -402,6 +411,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     }
     acc.x /= l, acc.y /= l, acc.z /= l, acc.w /= l;
     const int64_t at = b * a.o_b + (int64_t)(q0 + qr) * a.o_t + d;
+    if (a.o_pair) acc = make_float4(pair_word(acc.x), pair_word(acc.y), pair_word(acc.z), pair_word(acc.w));
     if (a.o16) store_bf16x4(a.o, at, acc.x, acc.y, acc.z, acc.w);
     else *reinterpret_cast<float4 *>(a.o + at) = acc;
   }
@@ -629,6 +639,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     }
     acc.x /= l, acc.y /= l, acc.z /= l, acc.w /= l;
     const int64_t at = b * a.o_b + (int64_t)(q0 + qr) * a.o_t + d;
+    if (a.o_pair) acc = make_float4(pair_word(acc.x), pair_word(acc.y), pair_word(acc.z), pair_word(acc.w));
     if (a.o16) store_bf16x4(a.o, at, acc.x, acc.y, acc.z, acc.w);
     else *reinterpret_cast<float4 *>(a.o + at) = acc;
   }
@@ -835,6 +846,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) vo
     }
     acc.x /= l, acc.y /= l, acc.z /= l, acc.w /= l;
     const int64_t at = b * a.o_b + (int64_t)(q0 + qr) * a.o_t + d;
+    if (a.o_pair) acc = make_float4(pair_word(acc.x), pair_word(acc.y), pair_word(acc.z), pair_word(acc.w));
     if (a.o16) store_bf16x4(a.o, at, acc.x, acc.y, acc.z, acc.w);
     else *reinterpret_cast<float4 *>(a.o + at) = acc;
   }
@@ -903,6 +915,7 @@ class AttnOp final : public Op {
   bool bf = false;    // bf16 products (attn_kernel<..., BF> / attnbf_kernel)
   bool in16 = false;  // q, k, v stored as bf16 (attn_kernel<..., BF, ..., IN16>)
   bool x3 = false;    // three-pass bf16 products (attn_kernel<..., BF, ..., X3>)
+  bool p3 = false;    // q, k, v stored as pair words (attn_kernel<..., X3, P3>)
   dim3 grid;
 
   hipError_t launch(float *const *ptrs, float *, hipStream_t stream) override {
@@ -956,7 +969,9 @@ class AttnOp final : public Op {
 #define KH_ATTN_LAUNCH(D, W)                                                                         \
   if (dh == D && nw == W) {                                                                          \
     const bool add = a.mask_mode == KH_ATTN_MASK_ADD;                                                \
-    if (x3 && add) hipLaunchKernelGGL((attn_kernel<D, W, true, true, false, false, true>), grid, dim3(64 * W), 0, stream, a); \
+    if (p3 && add) hipLaunchKernelGGL((attn_kernel<D, W, true, true, false, false, true, true>), grid, dim3(64 * W), 0, stream, a); \
+    else if (p3) hipLaunchKernelGGL((attn_kernel<D, W, false, true, false, false, true, true>), grid, dim3(64 * W), 0, stream, a); \
+    else if (x3 && add) hipLaunchKernelGGL((attn_kernel<D, W, true, true, false, false, true>), grid, dim3(64 * W), 0, stream, a); \
     else if (x3) hipLaunchKernelGGL((attn_kernel<D, W, false, true, false, false, true>), grid, dim3(64 * W), 0, stream, a); \
     else if (in16 && add) hipLaunchKernelGGL((attn_kernel<D, W, true, true, false, true>), grid, dim3(64 * W), 0, stream, a); \
     else if (in16) hipLaunchKernelGGL((attn_kernel<D, W, false, true, false, true>), grid, dim3(64 * W), 0, stream, a); \
@@ -1079,6 +1094,15 @@ std::unique_ptr<Op> make_attn(const kh_launch &L, std::string &err, bool &unsupp
     err = "attention: three-pass products split fp32 q, k, v on 32 queries per workgroup";
     return nullptr;
   }
+  // pair words (cfg[7] bits 16 + j): q, k, v together (three-pass products)
+  // and / or the output of a blocked kernel
+  const uint32_t mp = pair_refs(L);
+  op->p3 = (mp & 7u) != 0;
+  if ((mp & ~0xFu) || (op->p3 && ((mp & 7u) != 7u || !op->x3)) || (mp & m16)) {
+    unsupported = true;
+    err = "attention: pair storage of q, k, v needs all three and three-pass products; of the output, fp32 storage";
+    return nullptr;
+  }
   op->q16 = !op->in16 && !op->x3 && (qpw == 16 || (qpw == 0 && (op->bf ? 2 * groups32 < current_device().cus
                                                               : 2 * groups32 < 3ll * current_device().cus)));
   a.n_qblocks = (int)((tq + (op->q16 ? 16 : kQB) - 1) / (op->q16 ? 16 : kQB));
@@ -1132,6 +1156,12 @@ std::unique_ptr<Op> make_attn(const kh_launch &L, std::string &err, bool &unsupp
     return nullptr;
   }
   a.o16 = m16 >> 3 & 1;
+  if ((mp >> 3 & 1) && op->rows) {
+    unsupported = true;
+    err = "attention: pair storage only for the output of the blocked kernels";
+    return nullptr;
+  }
+  a.o_pair = mp >> 3 & 1;
   return op;
 }
 

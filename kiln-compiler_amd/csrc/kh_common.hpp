@@ -218,6 +218,29 @@ __device__ __forceinline__ bf16x8_t pack_bf16x8(const float4 &x, const float4 &y
                                                  pack_bf16x2(y.x, y.y), pack_bf16x2(y.z, y.w)));
 }
 
+// x as its pair word (see split_bf16x8): bf16(x) low, bf16(x - bf16(x)) high
+// (0 for a non-finite bf16(x)), returned as a float's bits for an fp32 store.
+__device__ __forceinline__ float pair_word(float x) {
+  const float hv = __uint_as_float(pack_bf16x2(x, x) & 0xffff0000u);
+  const float lo = __builtin_isfinite(hv) ? x - hv : 0.0f;
+  return __uint_as_float(pack_bf16x2(x, lo));
+}
+
+// Eight pair words (as stored by a pair-storing producer) as the hi and lo
+// operands split_bf16x8 would make of the values they hold.
+__device__ __forceinline__ void unpair_bf16x8(const float4 &x, const float4 &y, bf16x8_t &hi, bf16x8_t &lo) {
+  const uint32_t w[8] = {__float_as_uint(x.x), __float_as_uint(x.y), __float_as_uint(x.z), __float_as_uint(x.w),
+                         __float_as_uint(y.x), __float_as_uint(y.y), __float_as_uint(y.z), __float_as_uint(y.w)};
+  uint32_t h[4], l[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    h[e] = __builtin_amdgcn_perm(w[2 * e + 1], w[2 * e], 0x05040100u);
+    l[e] = __builtin_amdgcn_perm(w[2 * e + 1], w[2 * e], 0x07060302u);
+  }
+  hi = __builtin_bit_cast(bf16x8_t, make_uint4(h[0], h[1], h[2], h[3]));
+  lo = __builtin_bit_cast(bf16x8_t, make_uint4(l[0], l[1], l[2], l[3]));
+}
+
 // Eight fp32 values as the two bf16 halves of a three-pass product:
 // hi = bf16(x), lo = bf16(x - hi) (the difference is exact in fp32; a
 // non-finite hi keeps lo 0), so x.y ~ x_lo y_hi + x_hi y_lo + x_hi y_hi with

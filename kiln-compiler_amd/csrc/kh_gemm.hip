@@ -527,10 +527,12 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void gemm3_f32_kernel(const GemmAr
       for (int j = 0; j < KB; ++j) {
         bf16x8 ah[FM], al[FM], bh[FN], bl[FN];
 #pragma unroll
-        for (int fm = 0; fm < FM; ++fm)
-          split_bf16x8<true>(make_float4(af[fm][8 * j], af[fm][8 * j + 1], af[fm][8 * j + 2], af[fm][8 * j + 3]),
-                             make_float4(af[fm][8 * j + 4], af[fm][8 * j + 5], af[fm][8 * j + 6], af[fm][8 * j + 7]),
-                             ah[fm], al[fm]);
+        for (int fm = 0; fm < FM; ++fm) {
+          const float4 x0 = make_float4(af[fm][8 * j], af[fm][8 * j + 1], af[fm][8 * j + 2], af[fm][8 * j + 3]);
+          const float4 x1 = make_float4(af[fm][8 * j + 4], af[fm][8 * j + 5], af[fm][8 * j + 6], af[fm][8 * j + 7]);
+          if (a.a_pair) unpair_bf16x8(x0, x1, ah[fm], al[fm]);
+          else split_bf16x8<true>(x0, x1, ah[fm], al[fm]);
+        }
 #pragma unroll
         for (int fn = 0; fn < FN; ++fn) {
           bh[fn] = *reinterpret_cast<const bf16x8 *>(st + b_off[fn][j]);
@@ -658,6 +660,10 @@ __global__ __launch_bounds__(64 * WM * WN, 2) void gemm3_f32_kernel(const GemmAr
           if (a.d_act == KH_OP_GELU_TANH) v[i] = op_gelu_tanh(v[i]);
           else if (a.d_act == KH_OP_GELU_ERF) v[i] = op_gelu_erf(v[i]);
           else if (a.d_act == KH_OP_RELU) v[i] = v[i] != v[i] ? v[i] : fmaxf(v[i], 0.0f);
+        }
+        if (a.o_pair) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v[i] = pair_word(v[i]);
         }
         float *o = a.eptr[a.d_out] + (int64_t)bidx * a.estride[a.d_out][0] + (int64_t)m * a.estride[a.d_out][1];
         if ((a.e_vec_mask >> a.d_out & 1) && valid == 4) {
@@ -1450,6 +1456,23 @@ std::unique_ptr<Op> make_gemm(const kh_launch &L, std::string &err, bool &unsupp
   splitk = (int)std::max<int64_t>(1, (K + a.k_per_split - 1) / std::max(1, a.k_per_split));
   if (K == 0) splitk = 1, a.k_per_split = 0;
   a.splitk = splitk;
+  // pair storage (cfg[7] bits 16 + j): A and / or the direct epilogue's
+  // output, on the three-pass configurations (the kernels of kinds 3, 5 and
+  // 6, which split A fragments and write a direct epilogue's output)
+  const uint32_t mp = pair_refs(L);
+  if (mp) {
+    const bool ap = mp & 1u, op_ = a.direct && (mp >> (2 + a.d_out) & 1u);
+    const uint32_t known = (ap ? 1u : 0u) | (op_ ? 1u << (2 + a.d_out) : 0u);
+    const bool kind_ok = tr.kind == 3 || tr.kind == 5 || tr.kind == 6;
+    if (mp != known || m16 || cfg_run != cfg || t.prec != KH_PREC_BF16X3 || !kind_ok || a.pro != KH_GEMV_PRO_NONE ||
+        (op_ && a.splitk != 1)) {
+      unsupported = true;
+      err = "matmul: pair storage only for A and a direct epilogue's output of a three-pass configuration "
+            "(the output without split-K)";
+      return nullptr;
+    }
+    a.a_pair = ap ? 1 : 0, a.o_pair = op_ ? 1 : 0;
+  }
   const int64_t n_tiles = (int64_t)a.tiles_m * a.tiles_n;
   if (n_tiles >= (1ll << 31)) {
     unsupported = true;

@@ -39,6 +39,9 @@ struct GemmArgs {
   // bf16 storage (kind 7 only): A holds bf16 values (its strides count bf16
   // elements); the direct epilogue's output is written as bf16
   int32_t a16, o16;
+  // pair storage (three-pass configurations): A holds pair words; the direct
+  // epilogue writes its output as pair words
+  int32_t a_pair, o_pair;
 };
 
 // Run the epilogue tape for columns [n, n + valid) of output row (b, m);

@@ -246,6 +246,10 @@ void gemm_nt_kernel(const GemmArgs a) {
           }
 #pragma unroll
           for (int i = 0; i < 4; ++i) v[i] = act(v[i]);
+          if (a.o_pair) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = pair_word(v[i]);
+          }
           float *o = a.eptr[a.d_out] + (int64_t)bidx * a.estride[a.d_out][0] + (int64_t)m * a.estride[a.d_out][1];
           if ((a.e_vec_mask >> a.d_out & 1) && valid == 4) {
             *reinterpret_cast<float4 *>(o + n) = make_float4(v[0], v[1], v[2], v[3]);
@@ -304,7 +308,8 @@ void gemm_nt_kernel(const GemmArgs a) {
 #pragma unroll
         for (int fm = 0; fm < FM; ++fm) {
           if constexpr (PREC == 2) {
-            split_bf16x8<true>(xa[fm][0], xa[fm][1], ah[fm], al[fm]);
+            if (a.a_pair) unpair_bf16x8(xa[fm][0], xa[fm][1], ah[fm], al[fm]);
+            else split_bf16x8<true>(xa[fm][0], xa[fm][1], ah[fm], al[fm]);
           } else {
             ah[fm] = pack_bf16x8(xa[fm][0], xa[fm][1]);
           }

@@ -247,7 +247,8 @@ __global__ __launch_bounds__(64 * WK) void gemm_small_kernel(const GemmArgs a) {
 #pragma unroll
       for (int fm = 0; fm < FM; ++fm) {
         if constexpr (PREC == 2) {
-          split_bf16x8<true>(xa[fm][0], xa[fm][1], ah[fm], al[fm]);
+          if (a.a_pair) unpair_bf16x8(xa[fm][0], xa[fm][1], ah[fm], al[fm]);
+          else split_bf16x8<true>(xa[fm][0], xa[fm][1], ah[fm], al[fm]);
         } else {
           ah[fm] = pack_bf16x8(xa[fm][0], xa[fm][1]);
         }
@@ -383,6 +384,10 @@ __global__ __launch_bounds__(64 * WK) void gemm_small_kernel(const GemmArgs a) {
       if (a.d_act == KH_OP_GELU_TANH) v[i] = op_gelu_tanh(v[i]);
       else if (a.d_act == KH_OP_GELU_ERF) v[i] = op_gelu_erf(v[i]);
       else if (a.d_act == KH_OP_RELU) v[i] = v[i] != v[i] ? v[i] : fmaxf(v[i], 0.0f);
+    }
+    if (a.o_pair) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = pair_word(v[i]);
     }
     float *o = a.eptr[a.d_out] + (int64_t)bidx * a.estride[a.d_out][0] + (int64_t)m * a.estride[a.d_out][1];
     if ((a.e_vec_mask >> a.d_out & 1) && valid == 4) {

@@ -74,6 +74,16 @@ inline uint32_t bf16_refs(const kh_launch &L) {
   return fam ? (uint32_t)L.cfg[7] & ((1u << KH_MAX_REFS) - 1) : 0u;
 }
 
+// Pair storage (cfg[7] bit 16 + j of a ROW, ATTN or GEMM launch): ref j holds
+// each fp32 value x of a three-pass operand as one 32-bit word, bf16(x) in the
+// low half and bf16(x - bf16(x)) in the high half (0 for a non-finite
+// bf16(x)): the two halves a three-pass product splits x into, made once by
+// the producer. Offsets and strides count words, as for fp32.
+inline uint32_t pair_refs(const kh_launch &L) {
+  const bool fam = L.family == KH_FAM_ROW || L.family == KH_FAM_ATTN || L.family == KH_FAM_GEMM;
+  return fam ? ((uint32_t)L.cfg[7] >> 16) & ((1u << KH_MAX_REFS) - 1) : 0u;
+}
+
 // Each factory returns nullptr and sets `err` when the descriptor is invalid or
 // unsupported; `unsupported` distinguishes the two for the status code.
 std::unique_ptr<Op> make_ew(const kh_launch &L, std::string &err, bool &unsupported);

@@ -38,6 +38,7 @@ struct LnArgs {
   uint32_t rows, inner;
   float inv_n1, inv_n2, eps;
   int32_t out16;        // the output is bf16 (its consumer is a bf16 matmul)
+  int32_t out_pair;     // the output is pair words (its consumer is a three-pass matmul)
 };
 
 // One row per wave and no grid-stride loop: the grid covers every row, so
@@ -85,6 +86,7 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const LnArgs a) {
           const float4 b = *reinterpret_cast<const float4 *>(a.beta + c);
           y.x += b.x, y.y += b.y, y.z += b.z, y.w += b.w;
         }
+        if (a.out_pair) y = make_float4(pair_word(y.x), pair_word(y.y), pair_word(y.z), pair_word(y.w));
         if (a.out16) store_bf16x4(a.out, (int64_t)row * a.out_rs + c, y.x, y.y, y.z, y.w);
         else store_stream(a.out + (int64_t)row * a.out_rs + c, y.x, y.y, y.z, y.w);
       }
@@ -417,7 +419,7 @@ std::unique_ptr<Op> make_row(const kh_launch &L, std::string &err, bool &unsuppo
   }
   const Device &dev = current_device();
   const int nv = pick_nv(inner);
-  const uint32_t m16 = bf16_refs(L);
+  const uint32_t m16 = bf16_refs(L), mp = pair_refs(L);
 
   if (L.variant == KH_ROW_LAYERNORM || L.variant == KH_ROW_SOFTMAX) {
     // refs: [x, (gamma), (beta)] loads, then the output; cfg[4] = 1 if gamma, cfg[5] = 1 if beta.
@@ -444,12 +446,19 @@ std::unique_ptr<Op> make_row(const kh_launch &L, std::string &err, bool &unsuppo
           return nullptr;
         }
         op->args.out16 = m16 ? 1 : 0;
+        // pair words: only the output
+        if (mp && (mp != 1u << out || m16)) {
+          unsupported = true;
+          err = "row: pair storage only for a LayerNorm's output";
+          return nullptr;
+        }
+        op->args.out_pair = mp ? 1 : 0;
         return op;
       }
     }
-    if (m16) {
+    if (m16 || mp) {
       unsupported = true;
-      err = "row: bf16 storage only for the one-wave LayerNorm kernel";
+      err = "row: bf16 or pair storage only for the one-wave LayerNorm kernel";
       return nullptr;
     }
     if (ok && L.variant == KH_ROW_SOFTMAX) {
@@ -467,9 +476,9 @@ std::unique_ptr<Op> make_row(const kh_launch &L, std::string &err, bool &unsuppo
     // Not eligible for the fast path: the tape in the descriptor is complete, run it generically.
   }
 
-  if (m16) {
+  if (m16 || mp) {
     unsupported = true;
-    err = "row: bf16 storage only for the one-wave LayerNorm kernel";
+    err = "row: bf16 or pair storage only for the one-wave LayerNorm kernel";
     return nullptr;
   }
   auto op = std::make_unique<RowOp>();

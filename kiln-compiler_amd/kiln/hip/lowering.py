@@ -206,6 +206,7 @@ class _Lowerer:
         self.layouts = compute_layouts(graph)
         self.users = graph.users()
         self.bf16_buffers = set()   # arena buffers held as bf16 (plan_bf16_storage)
+        self.pair_buffers = set()   # arena buffers held as pair words (plan_pair_storage)
         self.precision = precision
         self.matmul_config = matmul_config
         self.program = Program(precision=precision)
@@ -243,6 +244,11 @@ class _Lowerer:
         lay = self.layouts.get(v)
         return lay is not None and lay.base[0] == "arena" and lay.base[1] in self.bf16_buffers
 
+    def stored_pairs(self, v) -> bool:
+        """Is v's storage an arena buffer held as pair words (see plan_pair_storage)?"""
+        lay = self.layouts.get(v)
+        return lay is not None and lay.base[0] == "arena" and lay.base[1] in self.pair_buffers
+
     def as_bf16(self, r, v):
         """Ref r of v re-expressed over v's bf16 storage: the offset in bf16
         elements (the buffer's byte offset / 2 + v's view offset); strides
@@ -278,6 +284,116 @@ class _Lowerer:
             if buf is not None:
                 out.add(buf)
         return out
+
+    def plan_pair_storage(self):
+        """Three-pass plans: arena buffers whose only reader splits every value
+        into bf16 hi and lo halves - the A operand of a three-pass product, or
+        the q, k and v of an attention with three-pass products - and whose
+        producer can write those halves itself (the one-wave LayerNorm, the
+        blocked attention kernel, a three-pass product with a bias [+ GELU /
+        ReLU] epilogue and no split-K) are stored as pair words (bf16(x) low,
+        bf16(x - bf16(x)) high): the producer splits each value once, the
+        reader only regroups halves. Results are the same bits as with fp32
+        storage."""
+        out = set()
+        if self.precision != "bf16x3":
+            return out
+        for k in self.g.kernels:
+            if k.kind == "attention":
+                buf = self.qkv_pair_buffer(k)
+            elif k.kind == "matmul" and not self.is_gemv(k) and k not in self.prologue:
+                buf = self.a_pair_buffer(k)
+            else:
+                buf = None
+            if buf is not None:
+                out.add(buf)
+        return out
+
+    def a_pair_buffer(self, k):
+        """The arena buffer of three-pass matmul kernel k's A operand if it can
+        be stored as pair words: A is the whole buffer with unit K stride, read
+        by k alone, not a graph result, and written by a launch that can store
+        pair words. Otherwise None."""
+        cfg, prec = self.matmul_choice(k)
+        if prec != "bf16x3":
+            return None
+        mm = next(n for n in k.nodes if n.op == "matmul")
+        a, b = mm.inputs
+        if a.shape[-2] == 1 or self.layouts[b].base[0] != "const":
+            return None
+        lay = self.layouts.get(a)
+        if lay is None or lay.base[0] != "arena" or lay.offset != 0 or lay.strides[-1] != 1:
+            return None
+        buf = lay.base[1]
+        if self._arena_readers().get(buf) != {k} or buf in self.g.results:
+            return None
+        producer = self.g.kernel_of(buf.node)
+        return buf if producer is not None and self._writes_pairs(producer, buf) else None
+
+    def qkv_pair_buffer(self, k):
+        """The arena buffer holding attention kernel k's q, k and v if it can
+        be stored as pair words: the attention runs three-pass products, q, k
+        and v are views of that one buffer, k reads it alone, and its producer
+        can store pair words. Otherwise None."""
+        from kiln.hip.attention import match_kernel, operand_strides
+
+        m = match_kernel(self.g, k)
+        strides = operand_strides(m, self.layouts) if m is not None else None
+        if strides is None or not self.x3_attention(m):
+            return None
+        bufs = set()
+        for v in (m.q, m.k, m.v):
+            lay = self.layouts.get(v)
+            if lay is None or lay.base[0] != "arena":
+                return None
+            bufs.add(lay.base[1])
+        if len(bufs) != 1:
+            return None
+        buf = bufs.pop()
+        if self._arena_readers().get(buf) != {k} or buf in self.g.results:
+            return None
+        producer = self.g.kernel_of(buf.node)
+        return buf if producer is not None and producer.kind == "matmul" and self._writes_pairs(producer, buf) else None
+
+    def x3_attention(self, m) -> bool:
+        """Does the attention matched as m run three-pass products (three-pass
+        plans, more than a few queries, a grid of at least ATTN_X3_MIN_GROUPS
+        32-query blocks)?"""
+        batch, tq, _ = m.q.shape
+        return (self.precision == "bf16x3" and tq > ATTN_ROWS_MAX_Q and ATTN_QUERIES != 16
+                and batch * -(-tq // 32) >= ATTN_X3_MIN_GROUPS)
+
+    def _writes_pairs(self, k, buf) -> bool:
+        """Can kernel k write its output `buf` as pair words?"""
+        if k.kind == "attention" or k.kind == "reduction":
+            # the blocked attention kernel and the one-wave LayerNorm: the
+            # same kernels that can store bf16
+            return self._rounds_to_bf16(k, buf, precision="bf16x3")
+        if k.kind != "matmul" or self.is_gemv(k) or k in self.prologue:
+            return False
+        if kernel_outputs(self.g, k, self.users) != [buf]:
+            return False
+        cfg, prec = self.matmul_choice(k)
+        tile = int(cfg.get("tile", -1))
+        if prec != "bf16x3" or (tile not in autotune.K_CONTIGUOUS | autotune.SMALL_M and int(cfg.get("splitk", 1)) > 1):
+            return False
+        return self._bias_act_epilogue(k, buf)
+
+    def _bias_act_epilogue(self, k, buf) -> bool:
+        """Is matmul kernel k's tape out = act(acc + bias), act none, GELU or
+        ReLU, with out = buf (the library's direct epilogue)?"""
+        mm = next(n for n in k.nodes if n.op == "matmul")
+        rest = [n for n in k.nodes if n is not mm]
+        ops_ = [n.op for n in rest]
+        if ops_ not in (["add"], ["add", "gelu"], ["add", "relu"]):
+            return False
+        bias = rest[0].inputs[1] if rest[0].inputs[0] is mm.out else rest[0].inputs[0]
+        chain_ok = rest[0].inputs[0] is mm.out or rest[0].inputs[1] is mm.out
+        if len(rest) == 2:
+            chain_ok = chain_ok and rest[1].inputs[0] is rest[0].out
+        n_cols = mm.out.shape[-1]
+        return (chain_ok and rest[-1].out is buf and bias.type.rank >= 1 and bias.shape[-1] == n_cols
+                and all(s == 1 for s in bias.shape[:-1]) and n_cols % 4 == 0)
 
     def _arena_readers(self):
         """arena buffer -> the kernels that read it"""
@@ -344,8 +460,10 @@ class _Lowerer:
         producer = self.g.kernel_of(buf.node)
         return buf if producer is not None and producer.kind == "matmul" and self._rounds_to_bf16(producer, buf) else None
 
-    def _rounds_to_bf16(self, k, buf) -> bool:
-        """Can kernel k write its output `buf` as bf16?"""
+    def _rounds_to_bf16(self, k, buf, precision="bf16") -> bool:
+        """Can kernel k write its output `buf` as bf16? (With precision
+        "bf16x3", only its LayerNorm and attention cases are asked, for pair
+        words, which the same kernels write.)"""
         outs = kernel_outputs(self.g, k, self.users)
         if k.kind == "attention":
             from kiln.hip.attention import match_kernel
@@ -368,22 +486,11 @@ class _Lowerer:
             variant = self._row_pattern(k, reds, outs, externals)[0]
             inner = buf.shape[-1]
             return variant == kl.ROW_LAYERNORM and inner % 4 == 0 and inner <= 4096
-        if k.kind == "matmul" and not self.is_gemv(k) and k not in self.prologue:
+        if k.kind == "matmul" and not self.is_gemv(k) and k not in self.prologue and precision == "bf16":
             cfg, prec = self.matmul_choice(k)
             if prec != "bf16" or int(cfg.get("tile", -1)) not in autotune.BF16_A:
                 return False
-            mm = next(n for n in k.nodes if n.op == "matmul")
-            rest = [n for n in k.nodes if n is not mm]
-            ops_ = [n.op for n in rest]
-            if ops_ not in (["add"], ["add", "gelu"], ["add", "relu"]):
-                return False
-            bias = rest[0].inputs[1] if rest[0].inputs[0] is mm.out else rest[0].inputs[0]
-            chain_ok = rest[0].inputs[0] is mm.out or rest[0].inputs[1] is mm.out
-            if len(rest) == 2:
-                chain_ok = chain_ok and rest[1].inputs[0] is rest[0].out
-            n_cols = mm.out.shape[-1]
-            return (chain_ok and rest[-1].out is buf and bias.type.rank >= 1 and bias.shape[-1] == n_cols
-                    and all(s == 1 for s in bias.shape[:-1]) and n_cols % 4 == 0)
+            return self._bias_act_epilogue(k, buf)
         return False
 
     def ref(self, v, space):
@@ -632,6 +739,8 @@ class _Lowerer:
             if self.stored_bf16(v):
                 r = self.as_bf16(r, v)
                 bf16_mask |= 1 << out_ref[v]
+            if self.stored_pairs(v):
+                bf16_mask |= 1 << (16 + out_ref[v])
             refs.append(r)
         self._check_refs(refs)
 
@@ -735,9 +844,11 @@ class _Lowerer:
         d.n_passes = len(t.segments)
         nbytes = 4 * (sum(math.prod(v.shape) for v in externals) + sum(math.prod(v.shape) for v in outs))
         kind = {kl.ROW_LAYERNORM: "layernorm", kl.ROW_SOFTMAX: "softmax"}.get(variant, "generic")
-        if bf16_mask:
+        if bf16_mask & 0xFFFF:
             kind += " out:bf16"
             nbytes -= 2 * sum(math.prod(v.shape) for v in outs)
+        if bf16_mask >> 16:
+            kind += " out:pairs"
         self.add(d, k, f"{kind} rows {list(rows)} x {inner}, {len(t.segments)} passes"
                        f"{'' if single else ' (chunked)'}: {' '.join(n.op for n in k.nodes)}", nbytes=nbytes)
 
@@ -836,6 +947,8 @@ class _Lowerer:
         if not pro and self.stored_bf16(a):
             d.refs[0] = self.as_bf16(d.refs[0], a)
             d.cfg[7] |= 1
+        if not pro and not gemv and self.stored_pairs(a):
+            d.cfg[7] |= 1 << 16
         k_major = not gemv and int(cfg.get("tile", -1)) in autotune.NK_B
         nk = (gemv and self.layouts[b].base[0] == "const" and kk % 4 == 0) or k_major
         derived_b = prec in ("bf16", "bf16x3") or nk
@@ -863,6 +976,8 @@ class _Lowerer:
             if self.stored_bf16(v):
                 r = self.as_bf16(r, v)
                 d.cfg[7] |= 1 << (2 + out_ref[v])
+            if self.stored_pairs(v):
+                d.cfg[7] |= 1 << (16 + 2 + out_ref[v])
             refs.append(r)
         pro_refs = []
         attn_work = None
@@ -943,6 +1058,10 @@ class _Lowerer:
         if any(self.stored_bf16(v) for v in outs):
             summary += " out:bf16"
             nbytes -= 2 * math.prod(out_shape)
+        if not gemv and d.cfg[7] >> 16 & 1:
+            summary += " A:pairs"
+        if any(self.stored_pairs(v) for v in outs):
+            summary += " out:pairs"
         if pro:
             summary += " prologue: layernorm"
             nbytes += 4 * kk * len(pro_refs)
@@ -1311,6 +1430,8 @@ class _Lowerer:
             if self.stored_bf16(v):   # the output, or (all three) q, k, v
                 r = self.as_bf16(r, v)
                 d.cfg[7] |= 1 << j
+            if self.stored_pairs(v):  # (pair words: addressed as fp32)
+                d.cfg[7] |= 1 << (16 + j)
             d.refs[j] = r
         d.n_refs = 4
         mode = kl.ATTN_MASK_NONE
@@ -1327,8 +1448,7 @@ class _Lowerer:
         # where the grid is large enough; decode shapes keep the few-query
         # kernel's fp32 products
         bf_products = self.precision == "bf16" and tq > ATTN_ROWS_MAX_Q
-        x3_products = (self.precision == "bf16x3" and tq > ATTN_ROWS_MAX_Q and ATTN_QUERIES != 16
-                       and batch * -(-tq // 32) >= ATTN_X3_MIN_GROUPS)
+        x3_products = self.x3_attention(m)
         if bf_products:
             d.cfg[5] = 1
         if x3_products:
@@ -1351,6 +1471,10 @@ class _Lowerer:
         if d.cfg[7] & 8:
             scale += ", out:bf16"
             nbytes -= 2 * batch * dh * tq
+        if d.cfg[7] >> 16 & 7:
+            scale += ", qkv:pairs"
+        if d.cfg[7] >> 16 & 8:
+            scale += ", out:pairs"
         self.add(d, k, f"{batch} heads x {tq} queries x {tk} keys, head dim {dh}, {what}{scale}",
                  flops=flops, nbytes=nbytes)
 
@@ -1363,6 +1487,7 @@ class _Lowerer:
                     raise NotImplementedError(f"GPU backend: unexpected op '{n.op}' in a kernel")
         fused = self.find_ln_prologues() | self.find_attn_prologues()
         self.bf16_buffers = self.plan_bf16_storage()
+        self.pair_buffers = self.plan_pair_storage()
         for k in self.g.kernels:
             if k in fused:
                 continue

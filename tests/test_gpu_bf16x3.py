@@ -262,3 +262,32 @@ def test_x3_attention_keeps_fp32_products_on_decode_shapes(x3_everywhere):
     with torch.no_grad():
         eager = _Attn(None, 0.125)(q, k, v)
     torch.testing.assert_close(c(q.cuda(), k.cuda(), v.cuda()).cpu(), eager, rtol=1e-4, atol=1e-5)
+
+
+@pytest.mark.parametrize("T", [256, 512, 1024, 2048])
+def test_pair_storage_gives_the_same_bits_on_the_block(T, monkeypatch):
+    # the GPT-2 block with allow_tf32 (shipped table): producers whose only
+    # reader splits each value into bf16 hi and lo halves (the three-pass
+    # products' A operands, the three-pass attention's q, k, v) store those
+    # halves as pair words, so the result is bit for bit the one of the same
+    # plan with fp32 storage
+    from kiln.hip import lowering
+
+    torch.manual_seed(0)
+    model = gpt2_init_(Block(768, 12, T), seed=0).eval()
+    x = torch.randn(T, 768)
+    c = kiln.compile(model, (x,), device="cuda", allow_tf32=True)
+    summaries = [l.summary for l in c._exe.program.launches]
+    print(f"pair storage T={T}: " + " | ".join(summaries), flush=True)
+    assert sum("A:pairs" in s for s in summaries) == 4
+    assert any("qkv:pairs" in s for s in summaries) == (T >= 512)
+    xd = x.cuda()
+    got = c(xd)
+    monkeypatch.setattr(lowering._Lowerer, "plan_pair_storage", lambda self: set())
+    plain = kiln.compile(model, (x,), device="cuda", allow_tf32=True, plan_cache=False)
+    assert not any("pairs" in l.summary for l in plain._exe.program.launches)
+    assert torch.equal(got, plain(xd))
+    with torch.no_grad():
+        f64 = model.double()(x.double()).numpy()
+    model.float()
+    close_to_scale(got.cpu().numpy(), f64, FP32_CLASS)

@@ -453,3 +453,29 @@ def test_three_pass_attention_products_on_the_host(monkeypatch):
     np.testing.assert_allclose(got, ref, rtol=1e-6, atol=1e-7)
     # a dropped cross term would move the result by ~1e-3 of its scale
     assert np.abs(got - (wh @ vh)).max() > 1e-5
+
+
+def test_pair_storage_in_three_pass_plans(monkeypatch):
+    # allow_tf32 plans store as pair words (bf16 hi and lo halves of each
+    # value) what only three-pass readers read: the LayerNorm outputs, the
+    # attention's q, k, v and output, the MLP-up output; the host runs them as
+    # fp32 storage, the same meaning
+    from kiln.hip import lowering
+
+    monkeypatch.setattr(lowering, "ATTN_X3_MIN_GROUPS", 0)
+    T = 64
+    model = gpt2_init_(Block(128, 4, T), seed=0).eval()
+    x = torch.randn(T, 128)
+    c = kiln.compile(model, (x,), device="cuda", allow_tf32=True)
+    summaries = [l.summary for l in c._exe.program.launches]
+    assert sum("A:pairs" in s for s in summaries) == 4, summaries
+    assert any("qkv:pairs" in s and "out:pairs" in s for s in summaries), summaries
+    assert sum("layernorm out:pairs" in s for s in summaries) == 2, summaries
+    got = c(x)
+    monkeypatch.setattr(lowering._Lowerer, "plan_pair_storage", lambda self: set())
+    plain = kiln.compile(model, (x,), device="cuda", allow_tf32=True, plan_cache=False)
+    assert not any("pairs" in l.summary for l in plain._exe.program.launches)
+    assert torch.equal(got, plain(x))
+    # bf16 and fp32 plans store nothing as pairs
+    c16 = kiln.compile(model, (x * 1.0,), device="cuda", matmul_precision="bf16", plan_cache=False)
+    assert not any("pairs" in l.summary for l in c16._exe.program.launches)
