@@ -75,6 +75,9 @@ def parse():
                    help="run only the library's measurement probes and print their summary: the MFMA / VALU "
                         "issue probe, and the attention kernel's per-workgroup timeline on the T = 2048 block "
                         "shape (12 heads; also 4 heads, one workgroup per CU)")
+    p.add_argument("--trace-summary", metavar="KERNEL_TRACE_CSV",
+                   help="summarise a rocprofv3 --kernel-trace CSV of a bench.py run: kiln kernels per kernel and "
+                        "grid, median and minimum duration (no GPU needed)")
     p.add_argument("--counter-report", nargs="+", metavar="PROBE_JSON DIR",
                    help="turn SQ counter passes over --counter-probe into the per-launch MFMA utilisation, "
                         "wait and LDS summary (no GPU needed)")
@@ -422,6 +425,40 @@ def traffic_report(probe_json, fetch_dir, write_dir, prefix=None, groups_prefix=
 SIMDS = 1024          # 256 CUs x 4 SIMDs
 SHADER_ARRAYS = 32    # 8 XCDs x 4 (rocprofv3 agent info: Array_Count)
 ENGINE_GHZ = 2.4
+
+
+def trace_summary(path, min_calls=20, width=58):
+    """Kiln kernels of a rocprofv3 kernel trace (run_kernel_trace.csv) per
+    kernel and grid (workgroups x threads): calls, median and minimum
+    duration in us. One kernel on one grid can serve two workloads (the same
+    tile on two shapes): a group whose sorted durations have a gap larger
+    than half its median, with at least min_calls on each side, is printed
+    as two rows, split at the largest gap."""
+    import csv
+    import re
+    import statistics
+
+    groups = {}
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            name = r["Kernel_Name"]
+            if "kh::" not in name:
+                continue
+            short = re.sub(r"\(kh::.*$", "", re.sub(r"^void kh::\(anonymous namespace\)::", "", name))
+            threads = int(r["Workgroup_Size_X"])
+            wg = int(r["Grid_Size_X"]) // max(1, threads)
+            us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+            groups.setdefault((short, wg, threads), []).append(us)
+    print(f"{'kernel':{width}s} {'workgroups x threads':>22s} {'calls':>6s} {'median_us':>10s} {'min_us':>8s}")
+    for (k, wg, th), v in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+        if len(v) < min_calls:
+            continue
+        v = sorted(v)
+        gap, i = max(((v[j + 1] - v[j], j) for j in range(len(v) - 1)), default=(0.0, 0))
+        split = gap > 0.5 * statistics.median(v) and min(i + 1, len(v) - i - 1) >= min_calls
+        for part in ([v[:i + 1], v[i + 1:]] if split else [v]):
+            print(f"{k[:width]:{width}s} {f'{wg} x {th}':>22s} {len(part):6d} {statistics.median(part):10.2f} "
+                  f"{min(part):8.2f}")
 
 
 def counter_report(probe_json, dirs):
@@ -959,6 +996,9 @@ def main():
         return
     if args.counter_report:
         counter_report(args.counter_report[0], args.counter_report[1:])
+        return
+    if args.trace_summary:
+        trace_summary(args.trace_summary)
         return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); this build has no multi-GPU path",

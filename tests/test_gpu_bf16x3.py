@@ -287,6 +287,11 @@ def test_pair_storage_gives_the_same_bits_on_the_block(T, monkeypatch):
     plain = kiln.compile(model, (x,), device="cuda", allow_tf32=True, plan_cache=False)
     assert not any("pairs" in l.summary for l in plain._exe.program.launches)
     assert torch.equal(got, plain(xd))
+    # non-finite activations too (a non-finite hi half keeps its lo half 0)
+    xn = xd.clone()
+    xn[3, 5], xn[11, 0] = float("inf"), float("-inf")
+    xn[7] = float("nan")
+    torch.testing.assert_close(c(xn), plain(xn), rtol=0, atol=0, equal_nan=True)
     with torch.no_grad():
         f64 = model.double()(x.double()).numpy()
     model.float()
