@@ -459,12 +459,18 @@ class GPUAutotuner:
 
     def config_for(self, graph, kernel, a16=False):
         """The configuration for ``kernel``'s matmul: cached, shipped, or
-        measured now (and cached). Every answer is logged. a16 (bf16 only):
-        the plan can store the product's A operand as bf16 (its producer
-        rounds it), so candidates are timed that way and keyed apart."""
+        measured now (and cached). Every answer is logged. a16: the plan can
+        store the product's A operand as bf16 (bf16: its producer rounds it)
+        or as pair words (bf16x3: its producer splits it), so candidates are
+        timed that way and keyed apart."""
         batch, m, n, k = matmul_shape(kernel)
-        a16 = bool(a16) and self.precision == "bf16"
+        a16 = bool(a16) and self.precision in ("bf16", "bf16x3")
         key = f"{self.device_key()}|{self.precision}{'+a16' if a16 else ''}|{batch}x{m}x{n}x{k}"
+        if a16 and self.precision == "bf16x3" and not any(_usable(t.get(key)) for t in (self._cache, self._shipped)):
+            # three-pass products reading pair-stored A: timed that way only
+            # ahead of time (tune_shipped), else the plain entry
+            a16 = False
+            key = f"{self.device_key()}|{self.precision}|{batch}x{m}x{n}x{k}"
         for source, table in (("cache", self._cache), ("shipped", self._shipped)):
             if _usable(table.get(key)):
                 entry = table[key]

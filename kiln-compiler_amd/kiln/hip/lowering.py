@@ -309,13 +309,16 @@ class _Lowerer:
                 out.add(buf)
         return out
 
-    def a_pair_buffer(self, k):
+    def a_pair_buffer(self, k, check_choice=True):
         """The arena buffer of three-pass matmul kernel k's A operand if it can
         be stored as pair words: A is the whole buffer with unit K stride, read
         by k alone, not a graph result, and written by a launch that can store
-        pair words. Otherwise None."""
-        cfg, prec = self.matmul_choice(k)
-        if prec != "bf16x3":
+        pair words. Otherwise None. (check_choice=False: before k's
+        configuration is chosen, for the tuner's keying, asking only that the
+        plan is three-pass.)"""
+        if self.precision != "bf16x3" or k in self.prologue:
+            return None
+        if check_choice and (self.is_gemv(k) or self.matmul_choice(k)[1] != "bf16x3"):
             return None
         mm = next(n for n in k.nodes if n.op == "matmul")
         a, b = mm.inputs
@@ -1093,8 +1096,9 @@ class _Lowerer:
         """(configuration, precision) of matmul kernel k, asked once per kernel."""
         if k not in self._cfg:
             mm = next(n for n in k.nodes if n.op == "matmul")
-            if getattr(self.matmul_config, "accepts_a16", False) and self.a16_buffer(k) is not None:
-                # the tuner times this product reading A as bf16, as the plan can store it
+            if getattr(self.matmul_config, "accepts_a16", False) and (
+                    self.a16_buffer(k) is not None or self.a_pair_buffer(k, check_choice=False) is not None):
+                # the tuner times this product reading A as bf16 / pair words, as the plan can store it
                 cfg = dict(self.matmul_config(self.g, k, a16=True))
             else:
                 cfg = dict(self.matmul_config(self.g, k))

@@ -22,7 +22,8 @@ from kiln.hip import autotune
 # block products (qkv, attention projection, MLP up, MLP down) at each token
 # count: in a bf16 plan their A operands come from a LayerNorm, the attention
 # or the MLP-up product, which store them as bf16 for the configurations that
-# read A that way ("bf16+a16" entries)
+# read A that way ("bf16+a16" entries); in a three-pass plan, as pair words
+# ("bf16x3+a16")
 BLOCK = sorted((t, n, k) for t in (128, 512, 1024, 2048) for n, k in ((2304, 768), (768, 768), (3072, 768), (768, 3072)))
 
 SHAPES = sorted({
@@ -54,22 +55,22 @@ def warm_up(seconds=1.0):
 def main(argv=None):
     p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     p.add_argument("--out", default=str(autotune.SHIPPED_PATH))
-    p.add_argument("--precision", nargs="+", choices=("fp32", "bf16", "bf16+a16", "bf16x3"), default=None,
+    p.add_argument("--precision", nargs="+", choices=("fp32", "bf16", "bf16+a16", "bf16x3", "bf16x3+a16"), default=None,
                    help="re-tune only these precisions and keep the table's other entries")
     p.add_argument("--max-m", type=int, default=None,
                    help="re-tune only shapes with at most this many rows and keep the table's other entries")
     args = p.parse_args(argv)
     warm_up()
     shapes = [s for s in SHAPES if args.max_m is None or s[0] <= args.max_m]
-    precisions = args.precision or ("fp32", "bf16", "bf16+a16", "bf16x3")
+    precisions = args.precision or ("fp32", "bf16", "bf16+a16", "bf16x3", "bf16x3+a16")
     table = {}
     if args.precision or args.max_m is not None:
         retuned = {(p_, f"1x{m}x{n}x{k}") for p_ in precisions for m, n, k in shapes}
         table = {key: v for key, v in autotune.shipped_configs().items()
                  if (key.split("|")[-2], key.split("|")[-1]) not in retuned}
     for precision in precisions:
-        a16 = precision == "bf16+a16"
-        base = "bf16" if a16 else precision
+        a16 = precision.endswith("+a16")
+        base = precision.split("+")[0]
         tuner = autotune.GPUAutotuner(precision=base, use_cache=False, use_shipped=False)
         device = tuner.device_key()
         for m, n, k in shapes:
