@@ -465,9 +465,9 @@ def test_shipped_tuning_table_is_consistent():
         arch, cus, precision, shape = key.split("|")
         b, m, n, k = map(int, shape.split("x"))
         tile = entry["config"]["tile"]
-        if precision.endswith("+a16"):      # timed reading a bf16 A operand
+        if precision.endswith("+a16"):      # timed reading a bf16 (bf16x3: pair-stored) A operand
             precision = precision[:-len("+a16")]
-            assert precision == "bf16" and m > 1
+            assert precision in ("bf16", "bf16x3") and m > 1
         if m == 1 and precision == "fp32":
             assert 0 <= tile <= 5          # GEMV workgroup variants
         else:
